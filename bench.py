@@ -1,0 +1,232 @@
+"""Benchmark: FP64-equivalent TFLOP/s of the Ozaki matmul on one MI355X.
+
+Workload (default): matmul(A, B, pipeline="ondevice", accumulation="fused",
+precision="high") with FP64 A, B of 8192 x 8192 x 8192, entries N(0,1) from
+RandomState(0) (A drawn first, then B), both resident in HBM before timing.
+A step is one full call: split + extraction of A and B, the fused 24-pair
+slice GEMM with the 2Sum accumulation, FP64 output and the non-finite check.
+
+Prints one JSON line with value = 2 M N K / t (TFLOP/s), plus
+  roofline      the fused GEMM kernel's BF16 MFMA rate (HIP events on the
+                stream it runs on) against the 2.5 PFLOP/s dense peak;
+  cpu_baseline  the oracle (NumPy restatement of matmul_numpy(pipeline=
+                "ondevice")) timed on this host at 4096^3;
+  rocblas_dgemm FP64 DGEMM of the same matrices (torch.matmul -> rocBLAS);
+  accuracy      max scaled error vs the oracle (same order, must be 0) and vs
+                FP64, on a subset of rows of the full-size product.
+"""
+
+import argparse
+import json
+import os
+import re
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+METRIC = ("FP64-equiv TFLOP/s (2MNK/t) 8192³ precision=high; "
+          "max scaled err vs ref")
+PEAK_BF16_TFLOPS = 2500.0
+PEAK_HBM_GBS = 8000.0
+PROFILE_TRAFFIC = ROOT / "profiles" / "gemm_allpairs_high_8192_traffic.md"
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--n", type=int, default=8192)
+    ap.add_argument("--precision", default="high")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-check", action="store_true")
+    return ap.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per GEMM launch from the committed rocprofv3 PMC summary."""
+    if not PROFILE_TRAFFIC.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", PROFILE_TRAFFIC.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(precision):
+    import oracle
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max((p.get("num_threads", 1) for p in threadpool_info()
+                       if p.get("user_api") == "blas"), default=1)
+    except Exception:
+        threads = os.cpu_count() or 1
+    n = 4096
+    rs = np.random.RandomState(0)
+    A, B = rs.randn(n, n), rs.randn(n, n)
+    log(f"cpu baseline: oracle matmul_numpy ondevice {precision} {n}^3")
+    t0 = time.perf_counter()
+    oracle.matmul_numpy(A, B, pipeline="ondevice", precision=precision)
+    t = time.perf_counter() - t0
+    return {"value": 2.0 * n ** 3 / t / 1e12, "unit": "TFLOP/s",
+            "cores": int(threads), "kind": "port",
+            "sample": f"oracle matmul_numpy(pipeline='ondevice', precision='{precision}') "
+                      f"{n}x{n}x{n} N(0,1), one run of {t:.1f} s "
+                      f"(NumPy/OpenBLAS, {threads} BLAS threads)"}
+
+
+def accuracy_rows(A, B, C, precision, rows):
+    """Max scaled error of C[rows] vs the oracle (same 2Sum order) and vs
+    FP64, scaled per element by (|A||B|)_ij."""
+    import oracle
+    from oracle import pipeline as OP
+    n_hi, n_lo = OP.resolve_precision(precision)
+    K = A.shape[1]
+    rho = oracle.rho_f32(K)
+    Ar = A[rows]
+    ref = oracle.matmul_ondevice_a4(Ar, B, "raise", n_hi, n_lo)
+    scale = np.abs(Ar) @ np.abs(B)
+    return (float(np.max(np.abs(C - ref) / scale)),
+            float(np.max(np.abs(C - Ar @ B) / scale)), rho)
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; "
+                          "--gpus must be 1"}))
+        sys.exit(2)
+    import torch
+    import ozaki_jax_amd as ozk
+    from ozaki_jax_amd import _lib, lowlevel as ll
+    from ozaki_jax_amd.matmul import _resolve_precision
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    n = args.n
+    n_hi, n_lo = _resolve_precision(args.precision)
+    n_pairs = n_hi * n_hi + 2 * n_hi * n_lo
+    rs = np.random.RandomState(0)
+    A = rs.randn(n, n)
+    B = rs.randn(n, n)
+    At = torch.from_numpy(A).to(dev)
+    Bt = torch.from_numpy(B).to(dev)
+    torch.cuda.synchronize()
+
+    def step():
+        return ozk.matmul(At, Bt, pipeline="ondevice", accumulation="fused",
+                          precision=args.precision)
+
+    log(f"warmup {args.warmup} x matmul ondevice {args.precision} {n}^3")
+    C = None
+    for _ in range(args.warmup):
+        C = step()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        C = step()
+    torch.cuda.synchronize()
+    dt = (time.perf_counter() - t0) / args.steps
+    value = 2.0 * n ** 3 / dt / 1e12
+    log(f"{dt * 1e3:.2f} ms/step, {value:.2f} FP64-eq TFLOP/s")
+
+    # Fused GEMM kernel alone: HIP events on the stream it is launched on.
+    rho = _lib.load().ozk_rho_f32(n)
+    pa = ll.extract(At, 0, rho, n_hi, n_lo)
+    pb = ll.extract(Bt, 1, rho, n_hi, n_lo)
+    ll.gemm(pa, pb, ll.PIPE_ONDEVICE, n_hi, n_lo, ll.ORDER_2SUM)
+    stream = torch.cuda.current_stream()
+    ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = max(3, args.steps)
+    ev0.record(stream)
+    for _ in range(reps):
+        ll.gemm(pa, pb, ll.PIPE_ONDEVICE, n_hi, n_lo, ll.ORDER_2SUM)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    gemm_s = ev0.elapsed_time(ev1) / 1e3 / reps
+    flops = n_pairs * 2.0 * n ** 3
+    achieved = flops / gemm_s / 1e12
+    log(f"gemm kernel {gemm_s * 1e3:.2f} ms, {achieved:.1f} TFLOP/s BF16")
+
+    # Extraction phase (split + A rows + B columns) for reference.
+    ev0.record(stream)
+    for _ in range(reps):
+        ll.extract(At, 0, rho, n_hi, n_lo)
+        ll.extract(Bt, 1, rho, n_hi, n_lo)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    ext_s = ev0.elapsed_time(ev1) / 1e3 / reps
+
+    # rocBLAS DGEMM on the same operands.
+    for _ in range(2):
+        torch.matmul(At, Bt)
+    ev0.record(stream)
+    for _ in range(3):
+        torch.matmul(At, Bt)
+    ev1.record(stream)
+    torch.cuda.synchronize()
+    dgemm_s = ev0.elapsed_time(ev1) / 1e3 / 3
+
+    acc = None
+    if not args.no_check:
+        rows = np.linspace(0, n - 1, 8).astype(int)
+        Cr = C[rows].cpu().numpy()
+        log("accuracy check on 8 rows vs oracle (full B extraction on CPU)")
+        e_ref, e_f64, _ = accuracy_rows(A, B, Cr, args.precision, rows)
+        acc = {"rows_checked": rows.tolist(), "max_scaled_err_vs_ref": e_ref,
+               "max_scaled_err_vs_fp64": e_f64,
+               "scale": "|C - C_ref| / (|A||B|)_ij"}
+
+    cpu = None if args.no_cpu else cpu_baseline(args.precision)
+    traffic = read_traffic()
+    dev_name = torch.cuda.get_device_name(0)
+    out = {
+        "metric": METRIC,
+        "value": value,
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": dt * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic N(0,1), RandomState(0), A drawn before B",
+        "config": {
+            "workload": f"matmul(pipeline='ondevice', accumulation='fused', "
+                        f"precision='{args.precision}') FP64 {n}x{n}x{n}",
+            "M": n, "N": n, "K": n, "n_hi": n_hi, "n_lo": n_lo,
+            "slice_gemms": n_pairs, "rho": rho,
+        },
+        "roofline": {
+            "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+            "traffic": traffic,
+            "kernel": f"gemm_allpairs<ondevice,{n_hi},{n_lo},2SUM>",
+            "kernel_ms": gemm_s * 1e3,
+            "algorithmic_flops_per_launch": flops,
+        },
+        "extraction": {"ms": ext_s * 1e3,
+                       "algorithmic_bytes": 2 * n * n * (8 + 2 * (n_hi + n_lo)),
+                       "GB_per_s": 2 * n * n * (8 + 2 * (n_hi + n_lo)) / ext_s / 1e9,
+                       "peak_GB_per_s": PEAK_HBM_GBS},
+        "rocblas_dgemm": {"ms": dgemm_s * 1e3,
+                          "tflops": 2.0 * n ** 3 / dgemm_s / 1e12},
+        "accuracy": acc,
+        "cpu_baseline": cpu,
+        "device": dev_name,
+    }
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,166 @@
+/*
+ * ozaki_amd.h -- C ABI of the MI355X (gfx950) Ozaki-scheme matmul engine.
+ *
+ * The reference (Efithor/ozaki-jax) has no FFI: its operator API is the Python
+ * functions matmul / matmul_numpy / gram / residual / solve, each lowered by
+ * jax.jit.  This header is the boundary that replaces those jitted programs;
+ * every entry point names the reference code it stands in for.  The Python
+ * host layer (ozaki_jax_amd) binds these symbols with ctypes.
+ *
+ * Conventions
+ *  - All array arguments are DEVICE pointers (hipMalloc'd or equivalent);
+ *    matrices are row-major with an explicit leading dimension in elements.
+ *  - `stream` is a hipStream_t (NULL = default stream).  Calls enqueue work
+ *    and return; they do not synchronise.
+ *  - Returns OZK_OK (0) or a negative status; ozk_last_error() then holds a
+ *    message (thread-local).  No call aborts the process.
+ *  - The library keeps no device memory of its own.  Drivers take a caller
+ *    workspace whose size the matching *_workspace_bytes() query returns.
+ *  - `flags` (device uint32) receives OZK_FLAG_NONFINITE when an input holds
+ *    NaN/Inf; drivers clear it first.  It replaces the host-side
+ *    np.isfinite preflight scan (ozaki_jax/matmul.py:108-109, :623-628).
+ *  - Slice planes: BF16 bit patterns, [plane][line][k] with
+ *    k stride ozk_slice_ld(len) and ozk_slice_lines(lines) lines per plane;
+ *    padding is zero.  Exponents: int32 [plane][ozk_slice_lines(lines)].
+ */
+#ifndef OZAKI_AMD_H
+#define OZAKI_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define OZK_OK 0
+#define OZK_ERR_INVALID (-1)     /* bad argument (shape, mode, size) */
+#define OZK_ERR_HIP (-2)         /* HIP runtime / launch failure */
+#define OZK_ERR_UNSUPPORTED (-3) /* valid request this build cannot serve */
+#define OZK_ERR_WORKSPACE (-4)   /* workspace too small */
+
+#define OZK_FLAG_NONFINITE 1u
+
+/* Accumulation orders (the four orders of the reference). */
+#define OZK_ORDER_2SUM 0     /* A4: pallas_ops.py:178-239 == matmul.py:382-488 */
+#define OZK_ORDER_BLOCK64 1  /* A3: matmul.py:543-597 (accumulation="host")  */
+#define OZK_ORDER_HOST_JAX 2 /* A2: matmul.py:35-64 (matmul, pipeline="host") */
+#define OZK_ORDER_HOST_NP 3  /* A1: matmul.py:879-898 (matmul_numpy, "host")  */
+
+/* Pipelines / pair schedules. */
+#define OZK_PIPE_ONDEVICE 0 /* hh, hl, lh blocks: pallas_gemm_accum.py:26-87 */
+#define OZK_PIPE_HOST 1     /* triangle i+j <= n-1: matmul.py:23-32           */
+
+/* ---- library --------------------------------------------------------- */
+const char* ozk_last_error(void);
+int ozk_abi_version(void);
+/* Writes the device name of the current device into buf (NUL-terminated)
+ * and its compute-unit count into *cu_count. */
+int ozk_device_info(char* buf, size_t len, int* cu_count);
+
+/* ---- parameters ------------------------------------------------------ */
+/* extract.py:12-18 `_compute_rho` (FP64 extraction, m1=53). */
+int ozk_rho_f64(int64_t K);
+/* extract.py:109-113 `_compute_rho_f32` (FP32 extraction, m1=24). */
+int ozk_rho_f32(int64_t K);
+/* Padded K stride / line count of slice planes. */
+int64_t ozk_slice_ld(int64_t len);
+int64_t ozk_slice_lines(int64_t lines);
+
+/* ---- extraction ------------------------------------------------------ */
+/* FP64 -> (FP32 hi, FP32 lo) split (matmul.py:204-213) fused with FP32
+ * sigma-trick extraction: n_hi slices of hi then n_lo slices of lo
+ * (extract.py:197-286; NumPy twin extract.py:116-191).  by_cols = 0 extracts
+ * per row of X (rows x cols), by_cols = 1 per column; in both cases a line
+ * is stored contiguously (columns are transposed through the workspace).
+ * Output planes: n_hi + n_lo. */
+size_t ozk_extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols);
+int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+                    int by_cols, int rho, int n_hi, int n_lo,
+                    uint16_t* slices, int32_t* exps, uint32_t* flags,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* FP64 sigma-trick extraction, n_slices planes (extract.py:21-103); slices
+ * are the FP32 rounding of v * 2^-c (extract.py:57-60), stored as BF16. */
+int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+                    int by_cols, int rho, int n_slices,
+                    uint16_t* slices, int32_t* exps, uint32_t* flags,
+                    void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- slice-pair GEMM + accumulation ---------------------------------- */
+/* Number of slice pairs of a schedule (matmul.py:636; host: n(n+1)/2). */
+int ozk_pair_count(int pipeline, int n_hi, int n_lo);
+
+/* Fused slice-pair GEMMs (BF16 MFMA, FP32 accumulate) with the selected
+ * accumulation order folded in registers; writes C (N x M, FP64).
+ * Replaces `_fully_fused_f64_jit` / `_bf16_interleaved_f64_jit`
+ * (matmul.py:514-540), the Pallas kernel `fused_gemm_accum`
+ * (pallas_gemm_accum.py:191-275), `_ondevice_gemms_jit` + accumulate_2sum
+ * (matmul.py:706-722), `_accumulate_block_products` (matmul.py:543-597),
+ * `_ozaki_gemms_jit` + `_accumulate_products` (matmul.py:23-64) and the
+ * matmul_numpy host loop (matmul.py:879-898).  A planes are rows of A
+ * (N lines), B planes are columns of B (M lines); both of length K. */
+int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
+             const uint16_t* b_slices, const int32_t* b_exps,
+             int64_t N, int64_t M, int64_t K,
+             int pipeline, int n_hi, int n_lo, int order,
+             double* C, int64_t ldc, void* stream);
+
+/* Test hook: the per-pair FP32 products P[p] = S^A_a(p) . S^B_b(p) written
+ * to P[p][N][ldp] in schedule order (matmul.py:216-233, :757-773, :885-887). */
+int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
+                       int64_t N, int64_t M, int64_t K,
+                       int pipeline, int n_hi, int n_lo,
+                       float* P, int64_t ldp, void* stream);
+
+/* ---- drivers --------------------------------------------------------- */
+/* matmul(A, B, pipeline, accumulation, precision) after preflight:
+ * pipeline OZK_PIPE_ONDEVICE: split + FP32 extraction with
+ *   rho = ozk_rho_f32(K), n_hi/n_lo slices, order 2SUM or BLOCK64
+ *   (matmul.py:641-728);
+ * pipeline OZK_PIPE_HOST: FP64 extraction with rho = ozk_rho_f64(K),
+ *   n_hi = n_slices (n_lo ignored), order HOST_JAX or HOST_NP
+ *   (matmul.py:823-851, :866-900). */
+size_t ozk_matmul_workspace_bytes(int64_t N, int64_t K, int64_t M,
+                                  int pipeline, int n_hi, int n_lo);
+int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
+               double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
+               int pipeline, int n_hi, int n_lo, int order,
+               void* workspace, size_t workspace_bytes, uint32_t* flags,
+               void* stream);
+
+/* gram(A, mode="ozaki"): G = Ozaki(A^T, A) in order 2SUM with
+ * rho = ozk_rho_f32(rows), then G = (G + G^T) * 0.5 (gram.py:19-37, :92-95).
+ * A is rows x cols; G is cols x cols.  One column extraction of A serves
+ * both operands. */
+size_t ozk_gram_workspace_bytes(int64_t rows, int64_t cols, int n_hi,
+                                int n_lo);
+int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
+             int n_hi, int n_lo, double* G, int64_t ldg,
+             void* workspace, size_t workspace_bytes, uint32_t* flags,
+             void* stream);
+
+/* residual(A, x, b, mode="ozaki"): r = b - Ozaki(A, x) in order 2SUM with
+ * rho = ozk_rho_f32(K); x is K x ncols, b and r are N x ncols
+ * (solve.py:38-53, :78-82, :91-151). */
+size_t ozk_residual_workspace_bytes(int64_t N, int64_t K, int64_t ncols,
+                                    int n_hi, int n_lo);
+int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
+                 const double* b, int64_t ldb, double* r, int64_t ldr,
+                 int64_t N, int64_t K, int64_t ncols, int n_hi, int n_lo,
+                 void* workspace, size_t workspace_bytes, uint32_t* flags,
+                 void* stream);
+
+/* np.isfinite(X).all() as a flag (matmul.py:108-109, :623-628). */
+int ozk_check_finite(const double* X, int64_t rows, int64_t cols, int64_t ld,
+                     uint32_t* flags, void* stream);
+
+/* Test hook: runs one 32x32x16 BF16 MFMA on a fixed pattern and writes the
+ * 64 lanes x 16 accumulator registers (as int32) to out[64*16]. */
+int ozk_probe_mfma_layout(int32_t* out, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OZAKI_AMD_H */

@@ -1,0 +1,29 @@
+"""ozaki_jax_amd: the Ozaki-scheme FP64 matmul of ozaki-jax, MI355X-native.
+
+Drop-in for the hot path of ozaki_jax (``ozaki_jax/__init__.py:5-25``):
+``matmul``, ``matmul_numpy``, ``gram``, ``residual``, ``solve`` and the
+``*extract_split_*`` helpers, same signatures and defaults.  Every
+computation runs in hand-written HIP kernels for gfx950 (libozaki_amd.so,
+C ABI in include/ozaki_amd.h), bound with ctypes; PyTorch-ROCm provides
+device memory and the current stream.  NumPy in -> NumPy out; torch tensors
+play the role of the reference's JAX arrays.
+"""
+
+__version__ = "0.7.0"
+
+from .matmul import matmul, matmul_numpy  # noqa: F401
+from .gram import gram  # noqa: F401
+from .solve import residual, solve  # noqa: F401
+from .extract import (  # noqa: F401
+    extract_split_rows, extract_split_cols,
+    f32_extract_split_rows, f32_extract_split_cols,
+    jax_extract_split_rows, jax_extract_split_cols,
+    rho_f32, rho_f64,
+)
+
+__all__ = [
+    "gram", "matmul", "matmul_numpy", "residual", "solve",
+    "extract_split_rows", "extract_split_cols",
+    "f32_extract_split_rows", "f32_extract_split_cols",
+    "jax_extract_split_rows", "jax_extract_split_cols",
+]

@@ -1,0 +1,435 @@
+// C ABI of the Ozaki-scheme engine: argument checks, workspace carving and
+// the driver sequences (extract A, extract B, fused GEMM, epilogue kernels).
+
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "common.h"
+
+namespace ozk {
+
+static thread_local std::string g_error;
+
+void set_error(const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_error = buf;
+}
+void clear_error() { g_error.clear(); }
+
+// Implemented in extract.hip / gemm.hip.
+template <typename W>
+int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+            int by_cols, int rho, int n0, int n1, uint16_t* S, int32_t* E,
+            uint32_t* flags, void* ws, size_t wsb, hipStream_t st);
+size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols);
+int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
+int launch_check_finite(const double* X, int64_t rows, int64_t cols,
+                        int64_t ld, uint32_t* flags, hipStream_t st);
+int launch_gemm(const uint16_t* As, const int32_t* Ae, const uint16_t* Bs,
+                const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
+                int nhi, int nlo, int order, double* C, int64_t ldc,
+                hipStream_t st, bool allow_allpairs);
+int launch_products(const uint16_t* As, const uint16_t* Bs, int64_t N,
+                    int64_t M, int64_t K, int pipe, int nhi, int nlo, float* P,
+                    int64_t ldp, hipStream_t st);
+int launch_probe_mfma(int32_t* out, hipStream_t st);
+
+constexpr int kMaxSlices = 32;
+constexpr size_t kAlign = 256;
+
+static int rho_generic(int64_t K, int m1) {
+  // rho = max(ceil(m1 - (24 - ceil(log2 max(K, 2))) / 2), m1 + 1 - 8)
+  const int64_t k = K < 2 ? 2 : K;
+  int clog2 = 0;
+  while (((int64_t)1 << clog2) < k) ++clog2;
+  const int num = 2 * m1 - 24 + clog2;
+  const int gamma = num >= 0 ? (num + 1) / 2 : -((-num) / 2);
+  const int xi = m1 + 1 - 8;
+  return gamma > xi ? gamma : xi;
+}
+
+// Sequential carving of one workspace into aligned regions.
+struct Carver {
+  char* base;
+  size_t off = 0;
+  explicit Carver(void* b) : base((char*)b) {}
+  void* take(size_t bytes) {
+    void* p = base ? base + off : nullptr;
+    off += (bytes + kAlign - 1) / kAlign * kAlign;
+    return p;
+  }
+};
+
+struct SliceSet {
+  uint16_t* s;
+  int32_t* e;
+};
+
+static SliceSet carve_slices(Carver& c, int planes, int64_t lines, int64_t len) {
+  const int64_t lp = round_up(lines, kLinePad), ld = round_up(len, kKPad);
+  SliceSet r;
+  r.s = (uint16_t*)c.take((size_t)planes * lp * ld * sizeof(uint16_t));
+  r.e = (int32_t*)c.take((size_t)planes * lp * sizeof(int32_t));
+  return r;
+}
+
+static int check_counts(int pipe, int nhi, int nlo) {
+  OZK_CHECK_ARG(pipe == OZK_PIPE_ONDEVICE || pipe == OZK_PIPE_HOST,
+                "unknown pipeline %d", pipe);
+  OZK_CHECK_ARG(nhi >= 1 && nhi <= kMaxSlices, "n_hi/n_slices=%d outside [1, %d]",
+                nhi, kMaxSlices);
+  if (pipe == OZK_PIPE_ONDEVICE)
+    OZK_CHECK_ARG(nlo >= 1 && nlo <= kMaxSlices, "n_lo=%d outside [1, %d]", nlo,
+                  kMaxSlices);
+  return OZK_OK;
+}
+
+static int check_order(int order) {
+  OZK_CHECK_ARG(order >= OZK_ORDER_2SUM && order <= OZK_ORDER_HOST_NP,
+                "unknown accumulation order %d", order);
+  return OZK_OK;
+}
+
+// y = b - y (residual epilogue), N x ncols with leading dimensions.
+__global__ void sub_from_kernel(const double* __restrict__ b, int64_t ldb,
+                                double* __restrict__ y, int64_t ldy,
+                                double* __restrict__ r, int64_t ldr, int64_t n,
+                                int64_t ncols) {
+  const int64_t total = n * ncols;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t row = i / ncols, c = i - row * ncols;
+    r[row * ldr + c] = b[row * ldb + c] - y[row * ldy + c];
+  }
+}
+
+// G = (G + G^T) * 0.5 in place (gram.py:37); each unordered pair once.
+__global__ void symmetrize_kernel(double* __restrict__ G, int64_t n,
+                                  int64_t ld) {
+  const int64_t total = n * n;
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+       i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t r = i / n, c = i - r * n;
+    if (c < r) continue;
+    const double a = G[r * ld + c], b = G[c * ld + r];
+    const double s = (a + b) * 0.5;
+    G[r * ld + c] = s;
+    if (c != r) G[c * ld + r] = (b + a) * 0.5;
+  }
+}
+
+static unsigned grid_for(int64_t total) {
+  int64_t b = (total + 255) / 256;
+  if (b < 1) b = 1;
+  if (b > 8192) b = 8192;
+  return (unsigned)b;
+}
+
+}  // namespace ozk
+
+using namespace ozk;
+
+extern "C" {
+
+const char* ozk_last_error(void) { return g_error.c_str(); }
+
+int ozk_abi_version(void) { return 1; }
+
+int ozk_device_info(char* buf, size_t len, int* cu_count) {
+  clear_error();
+  int dev = 0;
+  OZK_HIP(hipGetDevice(&dev));
+  hipDeviceProp_t prop;
+  OZK_HIP(hipGetDeviceProperties(&prop, dev));
+  if (buf && len) {
+    snprintf(buf, len, "%s (%s)", prop.name, prop.gcnArchName);
+  }
+  if (cu_count) *cu_count = prop.multiProcessorCount;
+  return OZK_OK;
+}
+
+int ozk_rho_f64(int64_t K) { return rho_generic(K, 53); }
+int ozk_rho_f32(int64_t K) { return rho_generic(K, 24); }
+int64_t ozk_slice_ld(int64_t len) { return round_up(len, kKPad); }
+int64_t ozk_slice_lines(int64_t lines) { return round_up(lines, kLinePad); }
+
+int ozk_pair_count(int pipeline, int n_hi, int n_lo) {
+  clear_error();
+  int rc = check_counts(pipeline, n_hi, n_lo);
+  if (rc) return rc;
+  return pipeline == OZK_PIPE_ONDEVICE ? n_hi * n_hi + 2 * n_hi * n_lo
+                                       : n_hi * (n_hi + 1) / 2;
+}
+
+size_t ozk_extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols) {
+  return extract_workspace_bytes(rows, cols, by_cols);
+}
+
+int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+                    int by_cols, int rho, int n_hi, int n_lo,
+                    uint16_t* slices, int32_t* exps, uint32_t* flags,
+                    void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  OZK_CHECK_ARG(ldx >= cols || rows <= 1, "ldx=%lld < cols=%lld", (long long)ldx,
+                (long long)cols);
+  // n_lo = 0 extracts the hi part only (the FP32 helpers of the reference
+  // take FP32 input, for which lo is identically zero).
+  OZK_CHECK_ARG(n_hi >= 1 && n_hi <= kMaxSlices && n_lo >= 0 && n_lo <= kMaxSlices,
+                "slice counts (%d, %d) outside [1, %d] x [0, %d]", n_hi, n_lo,
+                kMaxSlices, kMaxSlices);
+  if (rows == 0 || cols == 0) return OZK_OK;
+  OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
+  return extract<float>(X, rows, cols, ldx, by_cols, rho, n_hi, n_lo, slices,
+                        exps, flags, workspace, workspace_bytes,
+                        (hipStream_t)stream);
+}
+
+int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+                    int by_cols, int rho, int n_slices, uint16_t* slices,
+                    int32_t* exps, uint32_t* flags, void* workspace,
+                    size_t workspace_bytes, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  OZK_CHECK_ARG(ldx >= cols || rows <= 1, "ldx < cols");
+  int rc = check_counts(OZK_PIPE_HOST, n_slices, 0);
+  if (rc) return rc;
+  if (rows == 0 || cols == 0) return OZK_OK;
+  OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
+  return extract<double>(X, rows, cols, ldx, by_cols, rho, n_slices, 0, slices,
+                         exps, flags, workspace, workspace_bytes,
+                         (hipStream_t)stream);
+}
+
+int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
+             const uint16_t* b_slices, const int32_t* b_exps, int64_t N,
+             int64_t M, int64_t K, int pipeline, int n_hi, int n_lo, int order,
+             double* C, int64_t ldc, void* stream) {
+  clear_error();
+  int rc = check_counts(pipeline, n_hi, n_lo);
+  if (rc) return rc;
+  if ((rc = check_order(order))) return rc;
+  OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape N=%lld M=%lld K=%lld",
+                (long long)N, (long long)M, (long long)K);
+  OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
+  if (N == 0 || M == 0) return OZK_OK;
+  return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K, pipeline,
+                     n_hi, n_lo, order, C, ldc, (hipStream_t)stream, true);
+}
+
+int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
+                       int64_t N, int64_t M, int64_t K, int pipeline, int n_hi,
+                       int n_lo, float* P, int64_t ldp, void* stream) {
+  clear_error();
+  int rc = check_counts(pipeline, n_hi, n_lo);
+  if (rc) return rc;
+  OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape");
+  OZK_CHECK_ARG(ldp >= M, "ldp < M");
+  if (N == 0 || M == 0) return OZK_OK;
+  return launch_products(a_slices, b_slices, N, M, K, pipeline, n_hi, n_lo, P,
+                         ldp, (hipStream_t)stream);
+}
+
+static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
+                        int nlo, bool carve, void* ws, SliceSet* a,
+                        SliceSet* b, void** tws) {
+  const int planes = pipeline == OZK_PIPE_ONDEVICE ? nhi + nlo : nhi;
+  Carver c(carve ? ws : nullptr);
+  SliceSet sa = carve_slices(c, planes, N, K);
+  SliceSet sb = carve_slices(c, planes, M, K);
+  void* t = c.take(extract_workspace_bytes(K, M, 1));
+  if (a) *a = sa;
+  if (b) *b = sb;
+  if (tws) *tws = t;
+  return c.off;
+}
+
+size_t ozk_matmul_workspace_bytes(int64_t N, int64_t K, int64_t M,
+                                  int pipeline, int n_hi, int n_lo) {
+  return matmul_ws(N, K, M, pipeline, n_hi, n_lo, false, nullptr, nullptr,
+                   nullptr, nullptr);
+}
+
+int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
+               double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
+               int pipeline, int n_hi, int n_lo, int order, void* workspace,
+               size_t workspace_bytes, uint32_t* flags, void* stream) {
+  clear_error();
+  hipStream_t st = (hipStream_t)stream;
+  int rc = check_counts(pipeline, n_hi, n_lo);
+  if (rc) return rc;
+  if ((rc = check_order(order))) return rc;
+  OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape N=%lld K=%lld M=%lld",
+                (long long)N, (long long)K, (long long)M);
+  OZK_CHECK_ARG((lda >= K || N <= 1) && (ldb >= M || K <= 1) &&
+                    (ldc >= M || N <= 1),
+                "leading dimension smaller than the row length");
+  OZK_CHECK_ARG(flags, "null flags pointer");
+  if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
+  if (N == 0 || M == 0) return OZK_OK;
+  const size_t need = ozk_matmul_workspace_bytes(N, K, M, pipeline, n_hi, n_lo);
+  if (!workspace || workspace_bytes < need) {
+    set_error("matmul: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return OZK_ERR_WORKSPACE;
+  }
+  SliceSet sa, sb;
+  void* tws;
+  matmul_ws(N, K, M, pipeline, n_hi, n_lo, true, workspace, &sa, &sb, &tws);
+  const size_t tbytes = extract_workspace_bytes(K, M, 1);
+  if (pipeline == OZK_PIPE_ONDEVICE) {
+    const int rho = rho_generic(K, 24);
+    if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
+                             nullptr, 0, st)))
+      return rc;
+    if ((rc = extract<float>(B, K, M, ldb, 1, rho, n_hi, n_lo, sb.s, sb.e, flags,
+                             tws, tbytes, st)))
+      return rc;
+  } else {
+    const int rho = rho_generic(K, 53);
+    if ((rc = extract<double>(A, N, K, lda, 0, rho, n_hi, 0, sa.s, sa.e, flags,
+                              nullptr, 0, st)))
+      return rc;
+    if ((rc = extract<double>(B, K, M, ldb, 1, rho, n_hi, 0, sb.s, sb.e, flags,
+                              tws, tbytes, st)))
+      return rc;
+  }
+  return launch_gemm(sa.s, sa.e, sb.s, sb.e, N, M, K, pipeline, n_hi, n_lo,
+                     order, C, ldc, st, true);
+}
+
+static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,
+                      SliceSet* s, void** tws) {
+  Carver c(ws);
+  SliceSet ss = carve_slices(c, nhi + nlo, cols, rows);
+  void* t = c.take(extract_workspace_bytes(rows, cols, 1));
+  if (s) *s = ss;
+  if (tws) *tws = t;
+  return c.off;
+}
+
+size_t ozk_gram_workspace_bytes(int64_t rows, int64_t cols, int n_hi,
+                                int n_lo) {
+  return gram_ws(rows, cols, n_hi, n_lo, nullptr, nullptr, nullptr);
+}
+
+int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
+             int n_hi, int n_lo, double* G, int64_t ldg, void* workspace,
+             size_t workspace_bytes, uint32_t* flags, void* stream) {
+  clear_error();
+  hipStream_t st = (hipStream_t)stream;
+  int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
+  if (rc) return rc;
+  OZK_CHECK_ARG(rows >= 1 && cols >= 0, "invalid shape rows=%lld cols=%lld",
+                (long long)rows, (long long)cols);
+  OZK_CHECK_ARG((lda >= cols || rows <= 1) && (ldg >= cols || cols <= 1),
+                "leading dimension too small");
+  OZK_CHECK_ARG(flags, "null flags pointer");
+  if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
+  if (cols == 0) return OZK_OK;
+  const size_t need = ozk_gram_workspace_bytes(rows, cols, n_hi, n_lo);
+  if (!workspace || workspace_bytes < need) {
+    set_error("gram: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return OZK_ERR_WORKSPACE;
+  }
+  SliceSet s;
+  void* tws;
+  gram_ws(rows, cols, n_hi, n_lo, workspace, &s, &tws);
+  // Row extraction of A^T == column extraction of A: one set of slices is
+  // both operands (gram.py:22-35 extracts the same values twice).
+  const int rho = rho_generic(rows, 24);
+  if ((rc = extract<float>(A, rows, cols, lda, 1, rho, n_hi, n_lo, s.s, s.e,
+                           flags, tws, extract_workspace_bytes(rows, cols, 1), st)))
+    return rc;
+  if ((rc = launch_gemm(s.s, s.e, s.s, s.e, cols, cols, rows, OZK_PIPE_ONDEVICE,
+                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, st, true)))
+    return rc;
+  hipLaunchKernelGGL(symmetrize_kernel, dim3(grid_for(cols * cols)), dim3(256),
+                     0, st, G, cols, ldg);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
+                          int nlo, void* ws, SliceSet* a, SliceSet* x,
+                          double** y, void** tws) {
+  Carver c(ws);
+  SliceSet sa = carve_slices(c, nhi + nlo, N, K);
+  SliceSet sx = carve_slices(c, nhi + nlo, ncols, K);
+  double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
+  void* t = c.take(extract_workspace_bytes(K, ncols, 1));
+  if (a) *a = sa;
+  if (x) *x = sx;
+  if (y) *y = yy;
+  if (tws) *tws = t;
+  return c.off;
+}
+
+size_t ozk_residual_workspace_bytes(int64_t N, int64_t K, int64_t ncols,
+                                    int n_hi, int n_lo) {
+  return residual_ws(N, K, ncols, n_hi, n_lo, nullptr, nullptr, nullptr,
+                     nullptr, nullptr);
+}
+
+int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
+                 const double* b, int64_t ldb, double* r, int64_t ldr,
+                 int64_t N, int64_t K, int64_t ncols, int n_hi, int n_lo,
+                 void* workspace, size_t workspace_bytes, uint32_t* flags,
+                 void* stream) {
+  clear_error();
+  hipStream_t st = (hipStream_t)stream;
+  int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
+  if (rc) return rc;
+  OZK_CHECK_ARG(N >= 0 && K >= 1 && ncols >= 0, "invalid shape");
+  OZK_CHECK_ARG((lda >= K || N <= 1) && (ldx >= ncols || K <= 1) &&
+                    (ldb >= ncols || N <= 1) && (ldr >= ncols || N <= 1),
+                "leading dimension too small");
+  OZK_CHECK_ARG(flags, "null flags pointer");
+  if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
+  if (N == 0 || ncols == 0) return OZK_OK;
+  const size_t need = ozk_residual_workspace_bytes(N, K, ncols, n_hi, n_lo);
+  if (!workspace || workspace_bytes < need) {
+    set_error("residual: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return OZK_ERR_WORKSPACE;
+  }
+  SliceSet sa, sx;
+  double* y;
+  void* tws;
+  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws);
+  const int rho = rho_generic(K, 24);
+  if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
+                           nullptr, 0, st)))
+    return rc;
+  if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,
+                           flags, tws, extract_workspace_bytes(K, ncols, 1), st)))
+    return rc;
+  if ((rc = launch_gemm(sa.s, sa.e, sx.s, sx.e, N, ncols, K, OZK_PIPE_ONDEVICE,
+                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, st, true)))
+    return rc;
+  hipLaunchKernelGGL(sub_from_kernel, dim3(grid_for(N * ncols)), dim3(256), 0,
+                     st, b, ldb, y, ncols, r, ldr, N, ncols);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+int ozk_check_finite(const double* X, int64_t rows, int64_t cols, int64_t ld,
+                     uint32_t* flags, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  OZK_CHECK_ARG(flags, "null flags pointer");
+  return launch_check_finite(X, rows, cols, ld, flags, (hipStream_t)stream);
+}
+
+int ozk_probe_mfma_layout(int32_t* out, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(out, "null pointer");
+  return launch_probe_mfma(out, (hipStream_t)stream);
+}
+
+}  // extern "C"

@@ -1,0 +1,71 @@
+// Shared definitions for the Ozaki-scheme kernels (gfx950 / CDNA4).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <string>
+
+#include "../../include/ozaki_amd.h"
+
+namespace ozk {
+
+// ---------------------------------------------------------------- errors
+// Thread-local message behind ozk_last_error(); every entry point clears it
+// on entry and returns a negative status with a message on failure.
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define OZK_CHECK_ARG(cond, ...)            \
+  do {                                      \
+    if (!(cond)) {                          \
+      ::ozk::set_error(__VA_ARGS__);        \
+      return OZK_ERR_INVALID;               \
+    }                                       \
+  } while (0)
+
+#define OZK_HIP(call)                                                     \
+  do {                                                                    \
+    hipError_t e_ = (call);                                               \
+    if (e_ != hipSuccess) {                                               \
+      ::ozk::set_error("%s failed: %s", #call, hipGetErrorString(e_));    \
+      return OZK_ERR_HIP;                                                 \
+    }                                                                     \
+  } while (0)
+
+#define OZK_LAUNCH_CHECK()                                                \
+  do {                                                                    \
+    hipError_t e_ = hipGetLastError();                                    \
+    if (e_ != hipSuccess) {                                               \
+      ::ozk::set_error("kernel launch failed: %s", hipGetErrorString(e_)); \
+      return OZK_ERR_HIP;                                                 \
+    }                                                                     \
+  } while (0)
+
+// ---------------------------------------------------------------- layout
+// Slice planes are BF16, [plane][line][k] with lines padded to kLinePad and
+// k padded to kKPad; padding holds zeros, so the GEMM needs no bounds checks
+// in its K loop or its operand tiles.
+constexpr int64_t kKPad = 64;
+constexpr int64_t kLinePad = 64;
+
+inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+// ---------------------------------------------------------------- device
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float floatx16 __attribute__((ext_vector_type(16)));
+typedef float floatx4 __attribute__((ext_vector_type(4)));
+
+// FP32 -> BF16 bits, round to nearest even.  Slices are BF16-exact by
+// construction (at most 8 significant bits), so this is exact for them.
+__device__ __forceinline__ uint16_t f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+__device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
+  return __uint_as_float(((uint32_t)h) << 16);
+}
+
+}  // namespace ozk

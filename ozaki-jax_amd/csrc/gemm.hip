@@ -1,0 +1,509 @@
+// Slice-pair GEMMs on BF16 MFMA (FP32 accumulate) with the reference's
+// accumulation order folded into registers.
+//
+// Products.  Slices are integers on the grid 2^(rho-p) with at most 8
+// significant bits, so every BF16 x BF16 product is exact in FP32 and, while
+// the partial sums stay below 2^24 grid units (the reference's exactness
+// model, matmul.py:615-621), every FP32 sum is exact as well: the product of
+// a slice pair is the same bit pattern whatever the summation order.  That is
+// why the K loop may use any blocking and any k permutation inside an MFMA
+// fragment, provided A and B fragments use the same one.
+//
+// Tiling (gfx950, 64-wide waves).  A workgroup of 4 waves owns a 64x64 output
+// tile; each wave owns a 32x32 sub-tile and keeps one v_mfma_f32_32x32x16_bf16
+// accumulator (16 VGPRs per lane) per slice pair.  Per 32-wide K stage the
+// workgroup stages every slice plane it needs (A: 64 rows, B: 64 columns)
+// into LDS in fragment order: each 1 KiB block holds exactly the 64 lanes'
+// 16-byte operands of one MFMA, so fragment reads are conflict-free
+// ds_read_b128.  A fragment of A slice a is loaded once per stage and reused
+// by every pair (a, b) -- for precision="high" 10 fragments feed 24 MFMAs.
+//
+// Accumulation.  After the K loop each lane folds its 16 output elements'
+// pair products in schedule order (pallas_gemm_accum.py:26-87):
+//   2SUM     (A4) pallas_ops.py:195-237  double-float FP32 2Sum chain
+//   BLOCK64  (A3) matmul.py:562-597      FP32 col scale, FP64 group sum
+//   HOST_JAX (A2) matmul.py:47-64        FP64 col scale, FP64 group sum
+//   HOST_NP  (A1) matmul.py:879-898      (f64(P) * row) * col, running sum
+// All operations are single IEEE RN ops (-ffp-contract=off), so the result
+// is bit-identical to the NumPy restatement of each order.
+
+#include "common.h"
+
+namespace ozk {
+
+// ---------------------------------------------------------------- schedule
+
+struct PairInfo {
+  int a, b;   // A / B slice (plane) index
+  int blk;    // block id (0 hh, 1 hl, 2 lh; host: 0)
+  bool gs;    // first pair of its group
+  bool ge;    // last pair of its group
+  bool bs;    // first pair of its block
+  bool be;    // last pair of its block
+};
+
+__host__ __device__ constexpr int pair_count(int pipe, int nhi, int nlo) {
+  return pipe == OZK_PIPE_ONDEVICE ? nhi * nhi + 2 * nhi * nlo
+                                   : nhi * (nhi + 1) / 2;
+}
+
+// Pair p of the schedule.  Ondevice: hh (i, j), hl (i, n_hi + j), lh
+// (n_hi + i, j), i-major (pallas_gemm_accum.py:39-53, groups :59-79).
+// Host: (i, j) with i + j <= n - 1, i-major (matmul.py:27-31).
+__host__ __device__ constexpr PairInfo pair_info(int pipe, int nhi, int nlo,
+                                                 int p) {
+  PairInfo r{0, 0, 0, false, false, false, false};
+  if (pipe == OZK_PIPE_ONDEVICE) {
+    const int hh = nhi * nhi, hl = nhi * nlo;
+    if (p < hh) {
+      const int i = p / nhi, j = p % nhi;
+      r = PairInfo{i, j, 0, j == 0, j == nhi - 1, p == 0, p == hh - 1};
+    } else if (p < hh + hl) {
+      const int q = p - hh, i = q / nlo, j = q % nlo;
+      r = PairInfo{i, nhi + j, 1, j == 0, j == nlo - 1, q == 0, q == hl - 1};
+    } else {
+      const int q = p - hh - hl, i = q / nhi, j = q % nhi;
+      r = PairInfo{nhi + i, j, 2, j == 0, j == nhi - 1, q == 0, q == hl - 1};
+    }
+  } else {
+    const int n = nhi;
+    int q = p, i = 0;
+    while (q >= n - i) {
+      q -= n - i;
+      ++i;
+    }
+    const int np = n * (n + 1) / 2;
+    r = PairInfo{i, q, 0, q == 0, q == n - 1 - i, p == 0, p == np - 1};
+  }
+  return r;
+}
+
+// ---------------------------------------------------------------- fold
+
+__device__ __forceinline__ void twosum(float& s, float& l, float x) {
+  const float t = s + x;
+  const float e = (s - t) + x;
+  s = t;
+  l = l + e;
+}
+
+struct Fold2Sum {
+  float it, il, bt, bl, ct, cl, p0, p1, p2;
+  __device__ __forceinline__ void init() {
+    it = il = bt = bl = ct = cl = p0 = p1 = p2 = 0.0f;
+  }
+  __device__ __forceinline__ void pair(const PairInfo& q, float P, float cs32,
+                                       float rs32, double, double) {
+    if (q.bs) { bt = 0.0f; bl = 0.0f; }
+    if (q.gs) { it = 0.0f; il = 0.0f; }
+    twosum(it, il, P * cs32);
+    if (q.ge) {
+      const float ht = it * rs32, hl = il * rs32;
+      twosum(bt, bl, ht);
+      twosum(bt, bl, hl);
+      if (q.be) {
+        twosum(ct, cl, bt);
+        if (q.blk == 0) p0 = bl;
+        else if (q.blk == 1) p1 = bl;
+        else p2 = bl;
+      }
+    }
+  }
+  __device__ __forceinline__ double finish(int nblocks) {
+    twosum(ct, cl, p0);
+    if (nblocks > 1) twosum(ct, cl, p1);
+    if (nblocks > 2) twosum(ct, cl, p2);
+    return (double)ct + (double)cl;
+  }
+};
+
+template <int ORDER>
+struct Fold64 {
+  double c, in;
+  __device__ __forceinline__ void init() { c = 0.0; in = 0.0; }
+  __device__ __forceinline__ void pair(const PairInfo& q, float P, float cs32,
+                                       float, double cs64, double rs64) {
+    if (ORDER == OZK_ORDER_HOST_NP) {
+      double t = (double)P * rs64;
+      t = t * cs64;
+      c = c + t;
+      return;
+    }
+    if (q.gs) in = 0.0;
+    if (ORDER == OZK_ORDER_BLOCK64) {
+      in = in + (double)(P * cs32);
+    } else {  // OZK_ORDER_HOST_JAX
+      in = in + (double)P * cs64;
+    }
+    if (q.ge) {
+      in = in * rs64;
+      c = c + in;
+    }
+  }
+  __device__ __forceinline__ double finish(int) { return c; }
+};
+
+template <int ORDER> struct FoldOf { typedef Fold64<ORDER> type; };
+template <> struct FoldOf<OZK_ORDER_2SUM> { typedef Fold2Sum type; };
+
+// ---------------------------------------------------------------- tiling
+
+constexpr int kBM = 64, kBN = 64, kBK = 32, kThreads = 256;
+
+// Output-tile order: consecutive workgroups go round-robin to the 8 XCDs, so
+// first gather each XCD's share into a contiguous range, then walk that range
+// in groups of kGroupM tile-rows (column-major inside a group) so that the
+// ~32 tiles resident on one XCD share A rows and B columns in its L2.
+constexpr int kXcds = 8, kGroupM = 8;
+
+__device__ __forceinline__ void tile_coords(int bid, int ntm, int ntn, int& tm,
+                                            int& tn) {
+  const int nt = ntm * ntn;
+  const int q = nt / kXcds, rem = nt % kXcds;
+  const int xcd = bid % kXcds, slot = bid / kXcds;
+  const int L = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + slot;
+  const int per_group = kGroupM * ntn;
+  const int g = L / per_group, first_m = g * kGroupM;
+  const int gsz = min(ntm - first_m, kGroupM);
+  const int inner = L - g * per_group;
+  tm = first_m + inner % gsz;
+  tn = inner / gsz;
+}
+
+// LDS offset (in 16-byte units) of the operand of (slot, 32-row group, MFMA
+// k-step, lane) inside one stage buffer.  Tile line r (0..63) and 8-wide k
+// chunk c (0..3) of a stage go to lane (r & 31) + 32 * (c & 1) of block
+// (slot, r >> 5, c >> 1).
+__device__ __forceinline__ int frag_off(int slot, int rg, int ks, int lane) {
+  return ((slot * 2 + rg) * 2 + ks) * 64 + lane;
+}
+
+// One operand side (A or B) of a stage: N slot tiles of 64 lines x 32 k.
+// Thread t moves line t/4, chunk t%4 of every slot: one 16-byte global load
+// and one 16-byte LDS store per slot.
+template <int N>
+struct HalfStage {
+  uint4 v[N];
+  __device__ __forceinline__ void load(const uint16_t* const (&ptr)[N],
+                                       int64_t ld, int64_t k0) {
+    const int t = threadIdx.x;
+    const int64_t off = (int64_t)(t >> 2) * ld + k0 + (t & 3) * 8;
+#pragma unroll
+    for (int s = 0; s < N; ++s) v[s] = *(const uint4*)(ptr[s] + off);
+  }
+  __device__ __forceinline__ void store(uint4* buf, int slot0) const {
+    const int t = threadIdx.x;
+    const int r = t >> 2, c = t & 3;
+    const int lane = (r & 31) + 32 * (c & 1);
+#pragma unroll
+    for (int s = 0; s < N; ++s) buf[frag_off(slot0 + s, r >> 5, c >> 1, lane)] = v[s];
+  }
+};
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) {
+  return __builtin_bit_cast(bf16x8, v);
+}
+
+// Output element of accumulator register r of a 32x32 MFMA in lane `lane`:
+// column lane % 32, row 8 * (r / 4) + 4 * (lane / 32) + r % 4.
+__device__ __forceinline__ int acc_row(int r, int lane) {
+  return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+}
+
+// K sweep shared by both kernels: double-buffered LDS stages; while one
+// buffer feeds the MFMAs the next stage is fetched half by half (A slots
+// during k-step 0, B slots during k-step 1) through NA or NB registers.
+// `mma(buf, ks)` issues the MFMAs of one 16-wide k-step.
+template <int NA, int NB, class MMA>
+__device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
+                                        const uint16_t* const (&b_ptr)[NB],
+                                        int64_t ld, uint4* lds, MMA& mma) {
+  constexpr int kBuf = (NA + NB) * 4 * 64;  // uint4 per stage buffer
+  const int64_t nst = ld / kBK;
+  {
+    HalfStage<NA> ha;
+    ha.load(a_ptr, ld, 0);
+    ha.store(lds, 0);
+    HalfStage<NB> hb;
+    hb.load(b_ptr, ld, 0);
+    hb.store(lds, NA);
+  }
+  __syncthreads();
+  for (int64_t s = 0; s < nst; ++s) {
+    uint4* cur = lds + (s & 1) * kBuf;
+    uint4* nxt = lds + ((s + 1) & 1) * kBuf;
+    const bool more = s + 1 < nst;
+    const int64_t k1 = (s + 1) * kBK;
+    {
+      HalfStage<NA> ha;
+      if (more) ha.load(a_ptr, ld, k1);
+      mma(cur, 0);
+      if (more) ha.store(nxt, 0);
+    }
+    {
+      HalfStage<NB> hb;
+      if (more) hb.load(b_ptr, ld, k1);
+      mma(cur, 1);
+      if (more) hb.store(nxt, NA);
+    }
+    __syncthreads();
+  }
+}
+
+// ---------------------------------------------------------------- kernels
+
+// MFMAs of every pair of a compile-time schedule: the fragment of A slice a
+// is read once per k-step and reused by every pair (a, b).
+template <int PIPE, int NHI, int NLO, int NT, int NP>
+struct AllPairsMMA {
+  floatx16 acc[NP];
+  int lane, wm, wn;
+  __device__ __forceinline__ void operator()(const uint4* buf, int ks) {
+    bf16x8 bf[NT];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) bf[s] = as_bf16x8(buf[frag_off(NT + s, wn, ks, lane)]);
+#pragma unroll
+    for (int sa = 0; sa < NT; ++sa) {
+      const bf16x8 af = as_bf16x8(buf[frag_off(sa, wm, ks, lane)]);
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const PairInfo q = pair_info(PIPE, NHI, NLO, p);
+        if (q.a == sa)
+          acc[p] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[q.b], acc[p], 0, 0, 0);
+      }
+    }
+  }
+};
+
+// All pairs of the schedule in one K sweep (schedules whose accumulators fit
+// in registers).  PIPE/NHI/NLO fix the schedule at compile time.
+template <int PIPE, int NHI, int NLO, int ORDER>
+__global__ __launch_bounds__(kThreads) void gemm_allpairs(
+    const uint16_t* __restrict__ As, const int32_t* __restrict__ Ae,
+    const uint16_t* __restrict__ Bs, const int32_t* __restrict__ Be,
+    int64_t N, int64_t M, int64_t ld, int64_t a_lines, int64_t b_lines,
+    double* __restrict__ C, int64_t ldc) {
+  constexpr int NT = PIPE == OZK_PIPE_ONDEVICE ? NHI + NLO : NHI;
+  constexpr int NP = pair_count(PIPE, NHI, NLO);
+  constexpr int NBLK = PIPE == OZK_PIPE_ONDEVICE ? 3 : 1;
+  __shared__ uint4 lds[2 * (NT + NT) * 4 * 64];
+
+  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
+  int tm, tn;
+  tile_coords(blockIdx.x, ntm, ntn, tm, tn);
+  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  const int64_t aplane = a_lines * ld, bplane = b_lines * ld;
+
+  const uint16_t* a_ptr[NT];
+  const uint16_t* b_ptr[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) {
+    a_ptr[s] = As + s * aplane + row0 * ld;
+    b_ptr[s] = Bs + s * bplane + col0 * ld;
+  }
+
+  AllPairsMMA<PIPE, NHI, NLO, NT, NP> mma;
+  mma.lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  mma.wm = wave >> 1;
+  mma.wn = wave & 1;
+#pragma unroll
+  for (int p = 0; p < NP; ++p) mma.acc[p] = floatx16{};
+  k_sweep<NT, NT>(a_ptr, b_ptr, ld, lds, mma);
+
+  // Fold in schedule order and store.
+  const int lane = mma.lane;
+  const int64_t col = col0 + 32 * mma.wn + (lane & 31);
+  int eb[NT];
+#pragma unroll
+  for (int s = 0; s < NT; ++s) eb[s] = Be[s * b_lines + col];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
+    int ea[NT];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) ea[s] = Ae[s * a_lines + row];
+    typename FoldOf<ORDER>::type f;
+    f.init();
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const PairInfo q = pair_info(PIPE, NHI, NLO, p);
+      f.pair(q, mma.acc[p][r], ldexpf(1.0f, eb[q.b]), ldexpf(1.0f, ea[q.a]),
+             ldexp(1.0, eb[q.b]), ldexp(1.0, ea[q.a]));
+    }
+    const double out = f.finish(NBLK);
+    if (row < N && col < M) C[row * ldc + col] = out;
+  }
+}
+
+struct OnePairMMA {
+  floatx16 acc;
+  int lane, wm, wn;
+  __device__ __forceinline__ void operator()(const uint4* buf, int ks) {
+    const bf16x8 bf = as_bf16x8(buf[frag_off(1, wn, ks, lane)]);
+    const bf16x8 af = as_bf16x8(buf[frag_off(0, wm, ks, lane)]);
+    acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf, acc, 0, 0, 0);
+  }
+};
+
+// Any schedule: one pair per K sweep, the pair's slices chosen at run time.
+// MODE 0: fold with ORDER and write C; MODE 1: write the raw FP32 products
+// P[p][row][col] (test hook).  The fold state of the lane's 16 elements is
+// kept as one register array per field.
+template <int ORDER, int MODE>
+__global__ __launch_bounds__(kThreads) void gemm_pairwise(
+    const uint16_t* __restrict__ As, const int32_t* __restrict__ Ae,
+    const uint16_t* __restrict__ Bs, const int32_t* __restrict__ Be,
+    int64_t N, int64_t M, int64_t ld, int64_t a_lines, int64_t b_lines,
+    int pipe, int nhi, int nlo, double* __restrict__ C, int64_t ldc,
+    float* __restrict__ P, int64_t ldp) {
+  __shared__ uint4 lds[2 * 2 * 4 * 64];
+  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
+  int tm, tn;
+  tile_coords(blockIdx.x, ntm, ntn, tm, tn);
+  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  const int64_t aplane = a_lines * ld, bplane = b_lines * ld;
+  OnePairMMA mma;
+  mma.lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  mma.wm = wave >> 1;
+  mma.wn = wave & 1;
+  const int lane = mma.lane;
+  const int64_t col = col0 + 32 * mma.wn + (lane & 31);
+  const int np = pair_count(pipe, nhi, nlo);
+  const int nblocks = pipe == OZK_PIPE_ONDEVICE ? 3 : 1;
+
+  typename FoldOf<ORDER>::type f[16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) f[r].init();
+
+  for (int p = 0; p < np; ++p) {
+    const PairInfo q = pair_info(pipe, nhi, nlo, p);
+    const uint16_t* a_ptr[1] = {As + q.a * aplane + row0 * ld};
+    const uint16_t* b_ptr[1] = {Bs + q.b * bplane + col0 * ld};
+    mma.acc = floatx16{};
+    k_sweep<1, 1>(a_ptr, b_ptr, ld, lds, mma);
+    if (MODE == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
+        if (row < N && col < M) P[((int64_t)p * N + row) * ldp + col] = mma.acc[r];
+      }
+      continue;
+    }
+    const int eb = Be[q.b * b_lines + col];
+    const float cs32 = ldexpf(1.0f, eb);
+    const double cs64 = ldexp(1.0, eb);
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
+      const int ea = Ae[q.a * a_lines + row];
+      f[r].pair(q, mma.acc[r], cs32, ldexpf(1.0f, ea), cs64, ldexp(1.0, ea));
+    }
+  }
+  if (MODE == 1) return;
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
+    const double out = f[r].finish(nblocks);
+    if (row < N && col < M) C[row * ldc + col] = out;
+  }
+}
+
+// One MFMA on a pattern that encodes (row, col) in the result:
+// A[i][0] = i, A[i][1] = 1, B[0][j] = 1, B[1][j] = 64 j, all other k zero,
+// under the operand layout lane l -> (row l % 32, k 8 * (l / 32) + e).
+// Then C[i][j] = i + 64 j identifies every accumulator register.
+__global__ void probe_mfma_kernel(int32_t* out) {
+  const int l = threadIdx.x;
+  bf16x8 a = bf16x8{}, b = bf16x8{};
+  if (l < 32) {
+    a[0] = (__bf16)(float)l;
+    a[1] = (__bf16)1.0f;
+    b[0] = (__bf16)1.0f;
+    b[1] = (__bf16)(64.0f * (float)l);
+  }
+  floatx16 acc = floatx16{};
+  acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) out[l * 16 + r] = (int32_t)acc[r];
+}
+
+// ---------------------------------------------------------------- launch
+
+// Compile-time instantiations of the all-pairs kernel.
+template <int PIPE, int NHI, int NLO>
+static bool try_allpairs(int pipe, int nhi, int nlo, int order, dim3 grid,
+                         hipStream_t st, const uint16_t* As, const int32_t* Ae,
+                         const uint16_t* Bs, const int32_t* Be, int64_t N,
+                         int64_t M, int64_t ld, int64_t al, int64_t bl,
+                         double* C, int64_t ldc) {
+  if (pipe != PIPE || nhi != NHI || (PIPE == OZK_PIPE_ONDEVICE && nlo != NLO))
+    return false;
+#define OZK_AP(O)                                                         \
+  hipLaunchKernelGGL((gemm_allpairs<PIPE, NHI, NLO, O>), grid,            \
+                     dim3(kThreads), 0, st, As, Ae, Bs, Be, N, M, ld, al, \
+                     bl, C, ldc)
+  switch (order) {
+    case OZK_ORDER_2SUM: OZK_AP(OZK_ORDER_2SUM); break;
+    case OZK_ORDER_BLOCK64: OZK_AP(OZK_ORDER_BLOCK64); break;
+    case OZK_ORDER_HOST_JAX: OZK_AP(OZK_ORDER_HOST_JAX); break;
+    default: OZK_AP(OZK_ORDER_HOST_NP); break;
+  }
+#undef OZK_AP
+  return true;
+}
+
+int launch_gemm(const uint16_t* As, const int32_t* Ae, const uint16_t* Bs,
+                const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
+                int nhi, int nlo, int order, double* C, int64_t ldc,
+                hipStream_t st, bool allow_allpairs) {
+  const int64_t ld = round_up(K, kKPad);
+  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
+  const int64_t ntiles = (al / kBM) * (bl / kBN);
+  OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
+  const dim3 grid((unsigned)ntiles);
+  if (allow_allpairs) {
+    if (try_allpairs<OZK_PIPE_ONDEVICE, 4, 1>(pipe, nhi, nlo, order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, C, ldc) ||
+        try_allpairs<OZK_PIPE_ONDEVICE, 3, 1>(pipe, nhi, nlo, order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, C, ldc)) {
+      OZK_LAUNCH_CHECK();
+      return OZK_OK;
+    }
+  }
+#define OZK_PW(O)                                                              \
+  hipLaunchKernelGGL((gemm_pairwise<O, 0>), grid, dim3(kThreads), 0, st, As,   \
+                     Ae, Bs, Be, N, M, ld, al, bl, pipe, nhi, nlo, C, ldc,     \
+                     (float*)nullptr, (int64_t)0)
+  switch (order) {
+    case OZK_ORDER_2SUM: OZK_PW(OZK_ORDER_2SUM); break;
+    case OZK_ORDER_BLOCK64: OZK_PW(OZK_ORDER_BLOCK64); break;
+    case OZK_ORDER_HOST_JAX: OZK_PW(OZK_ORDER_HOST_JAX); break;
+    default: OZK_PW(OZK_ORDER_HOST_NP); break;
+  }
+#undef OZK_PW
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+int launch_products(const uint16_t* As, const uint16_t* Bs, int64_t N,
+                    int64_t M, int64_t K, int pipe, int nhi, int nlo, float* P,
+                    int64_t ldp, hipStream_t st) {
+  const int64_t ld = round_up(K, kKPad);
+  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
+  const int64_t ntiles = (al / kBM) * (bl / kBN);
+  OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
+  hipLaunchKernelGGL((gemm_pairwise<OZK_ORDER_2SUM, 1>), dim3((unsigned)ntiles),
+                     dim3(kThreads), 0, st, As, (const int32_t*)nullptr, Bs,
+                     (const int32_t*)nullptr, N, M, ld, al, bl, pipe, nhi, nlo,
+                     (double*)nullptr, (int64_t)0, P, ldp);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+int launch_probe_mfma(int32_t* out, hipStream_t st) {
+  hipLaunchKernelGGL(probe_mfma_kernel, dim3(1), dim3(64), 0, st, out);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+}  // namespace ozk

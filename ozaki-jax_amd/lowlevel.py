@@ -1,0 +1,102 @@
+"""Stage-level access to the C ABI (extraction planes, slice GEMM, per-pair
+products) on device tensors.  Used by the parity tests to check each stage of
+the pipeline separately, and by callers that keep slices resident (e.g. to
+reuse one operand's extraction across several products)."""
+
+from . import _device as D
+from . import _lib
+
+PIPE_ONDEVICE = _lib.PIPE_ONDEVICE
+PIPE_HOST = _lib.PIPE_HOST
+ORDER_2SUM = _lib.ORDER_2SUM
+ORDER_BLOCK64 = _lib.ORDER_BLOCK64
+ORDER_HOST_JAX = _lib.ORDER_HOST_JAX
+ORDER_HOST_NP = _lib.ORDER_HOST_NP
+
+
+class Planes:
+    """Slice planes of one operand on the device.
+
+    s: int16 (planes, lines_pad, ld) BF16 bit patterns; e: int32
+    (planes, lines_pad) exponents; lines / length: logical sizes.
+    """
+
+    def __init__(self, s, e, lines, length, flags):
+        self.s, self.e, self.lines, self.length, self.flags = s, e, lines, length, flags
+
+    def values(self):
+        """float32 (planes, lines, length) slice values (device)."""
+        v = (self.s.to(D.torch.int32) << 16).view(D.torch.float32)
+        return v[:, :self.lines, :self.length]
+
+    def exponents(self):
+        return self.e[:, :self.lines]
+
+    def nonfinite(self):
+        return D.read_flags(self.flags) & _lib.OZK_FLAG_NONFINITE
+
+
+def extract(X, by_cols, rho, n0, n1=0, f64=False):
+    """Run ozk_extract_f32 (n0 hi slices, n1 lo slices) or ozk_extract_f64
+    (n0 slices) on X (any 2-D array; copied to the device as float64)."""
+    lib = _lib.load()
+    dev = D.require_gpu()
+    Xt = D.to_device_f64(X, dev)
+    rows, cols = Xt.shape
+    lines, length = (cols, rows) if by_cols else (rows, cols)
+    planes = n0 if f64 else n0 + n1
+    s = D.torch.zeros((planes, lib.ozk_slice_lines(max(lines, 1)),
+                       lib.ozk_slice_ld(max(length, 1))),
+                      dtype=D.torch.int16, device=dev)
+    e = D.torch.zeros((planes, lib.ozk_slice_lines(max(lines, 1))),
+                      dtype=D.torch.int32, device=dev)
+    flags = D.new_flags(dev)
+    wsb = lib.ozk_extract_workspace_bytes(rows, cols, int(by_cols))
+    ws = D.workspace(wsb, dev)
+    if f64:
+        rc = lib.ozk_extract_f64(Xt.data_ptr(), rows, cols, D.ld_of(Xt),
+                                 int(by_cols), rho, n0, s.data_ptr(),
+                                 e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
+                                 wsb, D.stream_handle())
+    else:
+        rc = lib.ozk_extract_f32(Xt.data_ptr(), rows, cols, D.ld_of(Xt),
+                                 int(by_cols), rho, n0, n1, s.data_ptr(),
+                                 e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
+                                 wsb, D.stream_handle())
+    _lib.check(rc)
+    return Planes(s, e, lines, length, flags)
+
+
+def gemm(a, b, pipeline, n_hi, n_lo, order):
+    """ozk_gemm on two Planes (a: rows of A, b: columns of B) -> C (N, M)."""
+    lib = _lib.load()
+    dev = a.s.device
+    N, M, K = a.lines, b.lines, a.length
+    C = D.torch.empty((N, M), dtype=D.torch.float64, device=dev)
+    _lib.check(lib.ozk_gemm(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
+                            b.e.data_ptr(), N, M, K, pipeline, n_hi, n_lo,
+                            order, C.data_ptr(), max(M, 1), D.stream_handle()))
+    return C
+
+
+def slice_products(a, b, pipeline, n_hi, n_lo):
+    """ozk_slice_products -> float32 (n_pairs, N, M) device tensor."""
+    lib = _lib.load()
+    dev = a.s.device
+    N, M, K = a.lines, b.lines, a.length
+    npairs = _lib.check(lib.ozk_pair_count(pipeline, n_hi, n_lo))
+    P = D.torch.zeros((npairs, N, M), dtype=D.torch.float32, device=dev)
+    _lib.check(lib.ozk_slice_products(a.s.data_ptr(), b.s.data_ptr(), N, M, K,
+                                      pipeline, n_hi, n_lo, P.data_ptr(),
+                                      max(M, 1), D.stream_handle()))
+    return P
+
+
+def probe_mfma_layout():
+    """(64, 16) int32: accumulator register r of lane l after the layout
+    probe MFMA; the value encodes row + 64 * col of the output element."""
+    lib = _lib.load()
+    dev = D.require_gpu()
+    out = D.torch.zeros((64, 16), dtype=D.torch.int32, device=dev)
+    _lib.check(lib.ozk_probe_mfma_layout(out.data_ptr(), D.stream_handle()))
+    return out.cpu().numpy()

@@ -1,0 +1,242 @@
+"""FP64-accurate matrix multiplication via the Ozaki scheme on MI355X.
+
+Host-side mirror of ``ozaki_jax/matmul.py``: the same functions, arguments,
+defaults, validation order and error messages, with every computation done by
+the HIP kernels of libozaki_amd.so.
+
+Array families.  The reference accepts NumPy or JAX arrays; here the second
+family is PyTorch tensors.  NumPy in -> NumPy out; torch in -> torch (on the
+GPU) out for pipeline='ondevice'; the host pipeline always returns NumPy
+(matmul.py:826-851); mixed families raise ValueError (matmul.py:803-808).
+"""
+
+import numpy as np
+
+from . import _device as D
+from . import _lib
+from .extract import rho_f32, rho_f64
+
+# matmul.py:168-172
+_PRECISION_PRESETS = {
+    "high": (4, 1),    # 24 GEMMs
+    "medium": (3, 1),  # 15 GEMMs
+    "max": (5, 4),     # 65 GEMMs
+}
+
+_ACCUMULATION_MODES = {"fused", "bf16_interleaved", "ondevice", "host"}
+
+
+def _resolve_precision(precision):
+    """matmul.py:175-194: preset name or a custom (n_hi, n_lo) tuple."""
+    if isinstance(precision, tuple) and len(precision) == 2:
+        n_hi, n_lo = precision
+        if n_hi < 1 or n_lo < 1:
+            raise ValueError(
+                f"Custom precision tuple must have n_hi >= 1 and n_lo >= 1, "
+                f"got ({n_hi}, {n_lo}).")
+        return precision
+    if precision not in _PRECISION_PRESETS:
+        raise ValueError(
+            f"Unknown precision={precision!r}; expected one of "
+            f"{sorted(_PRECISION_PRESETS)} or a (n_hi, n_lo) tuple.")
+    return _PRECISION_PRESETS[precision]
+
+
+def _validate_accumulation_mode(accumulation):
+    """matmul.py:138-144."""
+    if accumulation not in _ACCUMULATION_MODES:
+        raise ValueError(
+            f"Unknown accumulation={accumulation!r}; expected one of "
+            f"{sorted(_ACCUMULATION_MODES)}.")
+
+
+def _validate_shapes(A, B):
+    """matmul.py:67-74."""
+    if A.ndim != 2 or B.ndim != 2:
+        raise ValueError("Inputs must be rank-2 matrices.")
+    if A.shape[1] != B.shape[0]:
+        raise ValueError(
+            f"Incompatible shapes for matmul: {tuple(A.shape)} and "
+            f"{tuple(B.shape)}.")
+
+
+def _kbound_reasons(K, bits, too_large):
+    """Exactness-bound part of the preflight (matmul.py:89-100, :609-621)."""
+    reasons = []
+    if bits <= 0:
+        reasons.append(
+            f"non-positive bits per slice ({bits}); K={K} is too {too_large}")
+    elif K * (2 ** bits - 1) ** 2 >= 2 ** 24:
+        max_K = int(2 ** 24 / (2 ** bits - 1) ** 2)
+        reasons.append(
+            f"K={K} violates BF16->FP32 exact inner-product bound "
+            f"(need K <= {max_K})")
+    return reasons
+
+
+def _check_safe_mode(safe_mode):
+    """matmul.py:121-125."""
+    allowed = {"raise", "fallback"}
+    if safe_mode not in allowed:
+        raise ValueError(
+            f"Invalid safe_mode={safe_mode!r}; expected one of "
+            f"{sorted(allowed)}.")
+
+
+def _nonfinite(tensors, dev):
+    """np.isfinite(...).all() on the device (matmul.py:108-109, :623-628)."""
+    lib = _lib.load()
+    flags = D.new_flags(dev)
+    for t in tensors:
+        if t.numel() == 0:
+            continue
+        _lib.check(lib.ozk_check_finite(t.data_ptr(), t.shape[0], t.shape[1],
+                                        D.ld_of(t), flags.data_ptr(),
+                                        D.stream_handle()))
+    return D.read_flags(flags) & _lib.OZK_FLAG_NONFINITE
+
+
+def _fp64_fallback(At, Bt):
+    """safe_mode='fallback' result (matmul.py:133-134): the plain FP64
+    product, computed on the GPU by rocBLAS DGEMM through torch.matmul."""
+    return D.torch.matmul(At, Bt)
+
+
+def _unsafe(reasons, safe_mode, At, Bt):
+    """matmul.py:127-135 once the reasons are known."""
+    if not reasons:
+        return None
+    if safe_mode == "fallback":
+        return _fp64_fallback(At, Bt)
+    raise ValueError("Ozaki preflight marked this input as unsafe: "
+                     + "; ".join(reasons))
+
+
+def _run_matmul(At, Bt, pipeline, n_hi, n_lo, order, dev):
+    """ozk_matmul on device tensors; returns (C tensor, nonfinite flag)."""
+    lib = _lib.load()
+    N, K = At.shape
+    M = Bt.shape[1]
+    C = D.torch.empty((N, M), dtype=D.torch.float64, device=dev)
+    flags = D.new_flags(dev)
+    if N == 0 or M == 0:
+        return C, 0
+    wsb = lib.ozk_matmul_workspace_bytes(N, K, M, pipeline, n_hi, n_lo)
+    ws = D.workspace(wsb, dev)
+    _lib.check(lib.ozk_matmul(
+        At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
+        D.ld_of(C), N, K, M, pipeline, n_hi, n_lo, order, ws.data_ptr(), wsb,
+        flags.data_ptr(), D.stream_handle()))
+    return C, D.read_flags(flags) & _lib.OZK_FLAG_NONFINITE
+
+
+def _matmul_ondevice(At, Bt, safe_mode, accumulation, n_hi, n_lo, dev):
+    """matmul.py:641-728: preflight, then split + FP32 extraction + fused
+    slice GEMMs with the accumulation order of `accumulation`
+    ('fused' / 'bf16_interleaved' / 'ondevice' -> 2Sum A4; 'host' -> A3)."""
+    _validate_accumulation_mode(accumulation)
+    _validate_shapes(At, Bt)
+    K = At.shape[1]
+    if K == 0:
+        raise ValueError("zero-size array to reduction operation maximum "
+                         "which has no identity")
+    bits = 24 - rho_f32(K)
+    reasons = _kbound_reasons(K, bits, "large for FP32 extraction")
+    _check_safe_mode(safe_mode)
+    if reasons:
+        if _nonfinite((At, Bt), dev):
+            reasons.append("inputs contain NaN or Inf")
+        return _unsafe(reasons, safe_mode, At, Bt)
+    order = _lib.ORDER_BLOCK64 if accumulation == "host" else _lib.ORDER_2SUM
+    C, bad = _run_matmul(At, Bt, _lib.PIPE_ONDEVICE, n_hi, n_lo, order, dev)
+    if bad:
+        return _unsafe(["inputs contain NaN or Inf"], safe_mode, At, Bt)
+    return C
+
+
+def _matmul_host(At, Bt, n_slices, safe_mode, order, dev):
+    """matmul.py:826-851 / :866-900: FP64 extraction (rho from
+    `_compute_rho`), triangular slice pairs i + j <= n_slices - 1, FP64
+    accumulation in order A2 (matmul) or A1 (matmul_numpy)."""
+    if n_slices < 1:
+        raise ValueError("n_slices must be >= 1.")
+    _validate_shapes(At, Bt)
+    K = At.shape[1]
+    if K == 0:
+        raise ValueError("zero-size array to reduction operation maximum "
+                         "which has no identity")
+    bits = 53 - rho_f64(K)
+    reasons = _kbound_reasons(
+        K, bits, "large for this BF16->FP32 exactness model")
+    if n_slices * max(bits, 0) < 53:
+        reasons.append(f"insufficient slice budget: n_slices*bits_per_slice="
+                       f"{n_slices * max(bits, 0)} < 53")
+    _check_safe_mode(safe_mode)
+    if reasons:
+        if _nonfinite((At, Bt), dev):
+            reasons.append("inputs contain NaN or Inf")
+        return _unsafe(reasons, safe_mode, At, Bt)
+    if n_slices > 32:
+        raise NotImplementedError("n_slices > 32 is not supported")
+    C, bad = _run_matmul(At, Bt, _lib.PIPE_HOST, n_slices, 0, order, dev)
+    if bad:
+        return _unsafe(["inputs contain NaN or Inf"], safe_mode, At, Bt)
+    return C
+
+
+def _families(A, B):
+    a_t, b_t = D.is_torch(A), D.is_torch(B)
+    if a_t != b_t:
+        raise ValueError(
+            "A and B must both be numpy arrays or both be torch tensors.")
+    return a_t
+
+
+def matmul(A, B, n_slices=8, safe_mode="raise", pipeline="host",
+           accumulation="fused", precision="high"):
+    """FP64 matmul via Ozaki Extract (matmul.py:781-851).
+
+    pipeline='host': FP64 extraction, n_slices slices per operand, triangular
+    pairs, FP64 accumulation (order of `_accumulate_products`); returns NumPy.
+    pipeline='ondevice': FP64 -> FP32 hi/lo split, FP32 extraction with
+    `precision` ('high' (4,1) 24 GEMMs, 'medium' (3,1) 15, 'max' (5,4) 65, or
+    a custom (n_hi, n_lo)), one fused kernel for the slice GEMMs and the
+    accumulation (`accumulation`: 'fused', 'bf16_interleaved', 'ondevice' ->
+    double-float 2Sum; 'host' -> FP64 block accumulation); output family
+    follows the input family.
+    """
+    want_torch = _families(A, B)
+    dev = D.require_gpu()
+    if pipeline == "ondevice":
+        n_hi, n_lo = _resolve_precision(precision)
+        At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
+        C = _matmul_ondevice(At, Bt, safe_mode, accumulation, n_hi, n_lo, dev)
+        return D.to_family(C, want_torch)
+    if pipeline != "host":
+        raise ValueError(
+            f"Unknown pipeline={pipeline!r}; expected 'host' or 'ondevice'.")
+    At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
+    C = _matmul_host(At, Bt, n_slices, safe_mode, _lib.ORDER_HOST_JAX, dev)
+    return D.to_family(C, False)
+
+
+def matmul_numpy(A_f64, B_f64, n_slices=8, safe_mode="raise", pipeline="host",
+                 precision="high"):
+    """`matmul_numpy` (matmul.py:854-900): the results of the reference's
+    NumPy pipeline -- accumulation order A1 for pipeline='host' and A3
+    (`_accumulate_block_products`) for 'ondevice' -- computed by the same
+    GPU kernels.  Accepts array-likes; returns NumPy."""
+    dev = D.require_gpu()
+    A = np.asarray(A_f64, dtype=np.float64) if not D.is_torch(A_f64) else A_f64
+    B = np.asarray(B_f64, dtype=np.float64) if not D.is_torch(B_f64) else B_f64
+    if pipeline == "ondevice":
+        n_hi, n_lo = _resolve_precision(precision)
+        At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
+        C = _matmul_ondevice(At, Bt, safe_mode, "host", n_hi, n_lo, dev)
+        return D.to_family(C, False)
+    if pipeline != "host":
+        raise ValueError(
+            f"Unknown pipeline={pipeline!r}; expected 'host' or 'ondevice'.")
+    At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
+    C = _matmul_host(At, Bt, n_slices, safe_mode, _lib.ORDER_HOST_NP, dev)
+    return D.to_family(C, False)

@@ -1,0 +1,154 @@
+"""Accurate residual and iterative-refinement solve (mirror of
+``ozaki_jax/solve.py``).
+
+residual(mode='ozaki') is b - Ozaki(A, x) with the 2Sum order, computed by the
+HIP kernels (solve.py:38-53, :78-82).  solve(residual_mode='ozaki') is FP32 LU
+plus max_iterations refinement steps whose residuals come from the same
+kernels (solve.py:154-167).  The FP32 LU (jnp.linalg.solve in the
+reference) is a library dependency here: torch.linalg's GPU LU, factored once
+and reused -- the reference re-solves with the same matrix each iteration,
+which yields the same factors.  mode='f64' paths are plain FP64 products
+(rocBLAS DGEMM through torch).
+"""
+
+from . import _device as D
+from . import _lib
+from .extract import rho_f32  # noqa: F401  (rho is derived inside the library)
+from .matmul import _resolve_precision
+
+
+def _validate_solve_inputs(A, b):
+    """solve.py:22-35."""
+    if A.ndim != 2 or A.shape[0] != A.shape[1]:
+        raise ValueError(f"A must be square, got shape {tuple(A.shape)}.")
+    N = A.shape[0]
+    if b.ndim == 1:
+        if b.shape[0] != N:
+            raise ValueError(f"b length {b.shape[0]} != A size {N}.")
+    elif b.ndim == 2:
+        if b.shape[0] != N:
+            raise ValueError(f"b rows {b.shape[0]} != A size {N}.")
+    else:
+        raise ValueError(f"b must be 1D or 2D, got ndim={b.ndim}.")
+
+
+def _validate_residual_inputs(A, x, b):
+    """solve.py:55-75."""
+    if A.ndim != 2:
+        raise ValueError(f"A must be 2D, got ndim={A.ndim}.")
+    N, K = A.shape
+    if x.ndim == 1:
+        if x.shape[0] != K:
+            raise ValueError(f"x length {x.shape[0]} != A columns {K}.")
+        if b.ndim != 1 or b.shape[0] != N:
+            raise ValueError(
+                f"b shape {tuple(b.shape)} incompatible with A @ x shape "
+                f"({N},).")
+    elif x.ndim == 2:
+        if x.shape[0] != K:
+            raise ValueError(f"x rows {x.shape[0]} != A columns {K}.")
+        if b.ndim != 2 or b.shape[0] != N or b.shape[1] != x.shape[1]:
+            raise ValueError(
+                f"b shape {tuple(b.shape)} incompatible with A @ x shape "
+                f"({N}, {x.shape[1]}).")
+    else:
+        raise ValueError(f"x must be 1D or 2D, got ndim={x.ndim}.")
+
+
+def _check_mode(mode, accumulation, name):
+    allowed = {"f64", "ozaki"}
+    if mode not in allowed:
+        raise ValueError(f"{name}={mode!r}; expected one of {sorted(allowed)}.")
+    if mode == "ozaki":
+        allowed_accum = {"bf16_interleaved", "fused"}
+        if accumulation not in allowed_accum:
+            raise ValueError(
+                f"accumulation={accumulation!r}; expected one of "
+                f"{sorted(allowed_accum)}.")
+
+
+def _asarray(v):
+    if D.is_torch(v):
+        return v
+    import numpy as np
+    return np.asarray(v)
+
+
+def ozaki_residual_device(At, xt, bt, n_hi, n_lo, dev):
+    """r = b - Ozaki(A, x) on device tensors (x, b 2-D)."""
+    lib = _lib.load()
+    N, K = At.shape
+    nc = xt.shape[1]
+    r = D.torch.empty((N, nc), dtype=D.torch.float64, device=dev)
+    if N == 0 or nc == 0:
+        return r
+    if K == 0:
+        raise ValueError("zero-size array to reduction operation maximum "
+                         "which has no identity")
+    flags = D.new_flags(dev)
+    wsb = lib.ozk_residual_workspace_bytes(N, K, nc, n_hi, n_lo)
+    ws = D.workspace(wsb, dev)
+    _lib.check(lib.ozk_residual(
+        At.data_ptr(), D.ld_of(At), xt.data_ptr(), D.ld_of(xt), bt.data_ptr(),
+        D.ld_of(bt), r.data_ptr(), D.ld_of(r), N, K, nc, n_hi, n_lo,
+        ws.data_ptr(), wsb, flags.data_ptr(), D.stream_handle()))
+    return r
+
+
+def residual(A, x, b, precision="high", accumulation="bf16_interleaved",
+             mode="f64"):
+    """solve.py:91-151: b - A @ x; same family and shape as b."""
+    _check_mode(mode, accumulation, "mode")
+    A, x, b = _asarray(A), _asarray(x), _asarray(b)
+    want_torch = D.is_torch(A)
+    _validate_residual_inputs(A, x, b)
+    dev = D.require_gpu()
+    At = D.to_device_f64(A, dev)
+    xt = D.to_device_f64(x, dev)
+    bt = D.to_device_f64(b, dev)
+    vec = xt.dim() == 1
+    if vec:
+        xt = xt[:, None].contiguous()
+        bt = bt[:, None].contiguous()
+    if mode == "f64":
+        r = bt - D.torch.matmul(At, xt)
+    else:
+        n_hi, n_lo = _resolve_precision(precision)
+        r = ozaki_residual_device(At, xt, bt, n_hi, n_lo, dev)
+    if vec:
+        r = r[:, 0]
+    return D.to_family(r, want_torch)
+
+
+def solve(A, b, precision="high", accumulation="bf16_interleaved",
+          max_iterations=3, residual_mode="f64"):
+    """solve.py:189-257: FP32 LU + iterative refinement."""
+    _check_mode(residual_mode, accumulation, "residual_mode")
+    A, b = _asarray(A), _asarray(b)
+    want_torch = D.is_torch(A)
+    _validate_solve_inputs(A, b)
+    dev = D.require_gpu()
+    torch = D.torch
+    At = D.to_device_f64(A, dev)
+    bt = D.to_device_f64(b, dev)
+    vec = bt.dim() == 1
+    if vec:
+        bt = bt[:, None].contiguous()
+    A32 = At.to(torch.float32)
+    LU, piv = torch.linalg.lu_factor(A32)
+
+    def solve32(rhs):
+        return torch.linalg.lu_solve(LU, piv, rhs.to(torch.float32)).to(torch.float64)
+
+    x = solve32(bt)
+    if residual_mode == "ozaki":
+        n_hi, n_lo = _resolve_precision(precision)
+    for _ in range(max_iterations):
+        if residual_mode == "f64":
+            r = bt - torch.matmul(At, x)
+        else:
+            r = ozaki_residual_device(At, x.contiguous(), bt, n_hi, n_lo, dev)
+        x = x + solve32(r)
+    if vec:
+        x = x[:, 0]
+    return D.to_family(x, want_torch)

@@ -1,0 +1,99 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+declared in include/ozaki_amd.h with the bound signature, its host-only
+functions agree with the oracle, and invalid arguments are rejected before
+any device work (no compute calls are made here)."""
+
+import ctypes
+import re
+
+import pytest
+
+import oracle as O
+from conftest import ROOT
+
+HEADER = ROOT / "include" / "ozaki_amd.h"
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from ozaki_jax_amd import _lib
+    return _lib.load()
+
+
+def declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(ozk_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    from ozaki_jax_amd import _lib
+    assert declared_functions() == sorted(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol(lib):
+    raw = ctypes.CDLL(str(ROOT / "ozaki-jax_amd" / "libozaki_amd.so"))
+    for name in declared_functions():
+        assert hasattr(raw, name), name
+
+
+def test_header_compiles_as_c(tmp_path):
+    import subprocess
+    src = tmp_path / "t.c"
+    src.write_text('#include "ozaki_amd.h"\nint main(void){return ozk_abi_version() < 0;}\n')
+    subprocess.run(["gcc", "-std=c99", "-Wall", "-Werror", "-c", str(src),
+                    "-I", str(ROOT / "include"), "-o", str(tmp_path / "t.o")],
+                   check=True)
+
+
+def test_host_functions(lib):
+    assert lib.ozk_abi_version() == 1
+    for K in [1, 2, 3, 64, 1040, 4096, 8192, 32768, 65536, 2 ** 22, 2 ** 22 + 1, 10 ** 9]:
+        assert lib.ozk_rho_f32(K) == O.rho_f32(K)
+        assert lib.ozk_rho_f64(K) == O.rho_f64(K)
+    assert lib.ozk_slice_ld(1) == 64 and lib.ozk_slice_ld(65) == 128
+    assert lib.ozk_slice_lines(8192) == 8192
+    assert lib.ozk_pair_count(0, 4, 1) == 24
+    assert lib.ozk_pair_count(0, 5, 4) == 65
+    assert lib.ozk_pair_count(1, 8, 0) == 36
+    assert lib.ozk_pair_count(0, 0, 1) == -1
+    assert b"outside" in lib.ozk_last_error()
+
+
+def test_workspace_sizes(lib):
+    # A and B slice planes (BF16) + exponents + the FP64 transpose of B
+    N = K = M = 8192
+    ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, 4, 1)
+    planes = 2 * 5 * 8192 * 8192 * 2
+    assert planes + 8 * K * M <= ws <= planes + 8 * K * M + 2 * 5 * 8192 * 4 + 4096
+    assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
+    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == 100 * 50 * 8
+
+
+def test_argument_errors_before_device_work(lib):
+    from ozaki_jax_amd import _lib
+    # bad slice counts / order / shapes are rejected with OZK_ERR_INVALID and
+    # a message; no pointer is dereferenced and no kernel is launched.
+    rc = lib.ozk_gemm(None, None, None, None, 4, 4, 4, 0, 0, 1, 0, None, 4, None)
+    assert rc == _lib.OZK_ERR_INVALID
+    rc = lib.ozk_gemm(None, None, None, None, 4, 4, 4, 0, 4, 1, 9, None, 4, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"order" in lib.ozk_last_error()
+    rc = lib.ozk_matmul(None, 4, None, 4, None, 4, 4, 0, 4, 0, 4, 1, 0, None, 0, None, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"invalid shape" in lib.ozk_last_error()
+    rc = lib.ozk_matmul(None, 2, None, 4, None, 4, 4, 4, 4, 0, 4, 1, 0, None, 0, None, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"leading dimension" in lib.ozk_last_error()
+    rc = lib.ozk_extract_f32(None, 4, 4, 4, 0, 19, 40, 1, None, None, None, None, 0, None)
+    assert rc == _lib.OZK_ERR_INVALID
+    rc = lib.ozk_gram(None, 4, 0, 4, 4, 1, None, 4, None, 0, None, None)
+    assert rc == _lib.OZK_ERR_INVALID
+    with pytest.raises(ValueError):
+        _lib.check(rc)
+
+
+def test_package_fails_loudly_without_gpu():
+    import numpy as np
+    import torch
+    import ozaki_jax_amd as ozk
+    if torch.cuda.is_available():
+        pytest.skip("a GPU is present")
+    with pytest.raises(RuntimeError, match="no CPU implementation"):
+        ozk.matmul(np.eye(4), np.eye(4), pipeline="ondevice")

@@ -1,0 +1,431 @@
+"""Parity of the HIP path (through the C ABI) with the oracle.
+
+Bar: bit-exact slices, exponents, per-pair products and outputs (values
+compared with np.array_equal, so +0 == -0) against the oracle restating the
+same accumulation order; the 2-ulp scaled bound |C - C_ref| <= 2^-51 (|A||B|)
+is asserted as well.  Sizes keep the oracle to seconds.
+"""
+
+import json
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+from oracle import pipeline as OP
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+def rel_err(a, r):
+    d = np.linalg.norm(r)
+    return 0.0 if d == 0 else float(np.linalg.norm(a - r) / d)
+
+
+def gen(kind, shape, seed):
+    rng = np.random.RandomState(seed)
+    if kind == "randn":
+        return rng.randn(*shape)
+    if kind == "wide":      # (U - 0.5) * exp(4 N)
+        return (rng.rand(*shape) - 0.5) * np.exp(4.0 * rng.randn(*shape))
+    if kind == "wide2":
+        return (rng.rand(*shape) - 0.5) * np.exp(2.0 * rng.randn(*shape))
+    if kind == "scaled":
+        return rng.randn(*shape) * 10.0 ** rng.uniform(-10, 30)
+    if kind == "zerorows":
+        X = rng.randn(*shape)
+        X[::3] = 0.0
+        if X.shape[1] > 2:
+            X[:, 1] = 0.0
+        return X
+    raise ValueError(kind)
+
+
+@pytest.fixture(scope="module")
+def ll(ozk):
+    from ozaki_jax_amd import lowlevel
+    return lowlevel
+
+
+def to_np(t):
+    return t.cpu().numpy()
+
+
+# ---------------------------------------------------------------- layout
+
+def test_mfma_output_layout(ll):
+    case("probe_mfma_layout 32x32x16 bf16")
+    out = ll.probe_mfma_layout()
+    for lane in range(64):
+        for r in range(16):
+            row = 8 * (r // 4) + 4 * (lane // 32) + (r % 4)
+            col = lane % 32
+            assert out[lane, r] == row + 64 * col, (lane, r, out[lane, r])
+
+
+# ---------------------------------------------------------------- extraction
+
+EXTRACT_SHAPES = [(1, 1), (3, 5), (64, 64), (130, 257), (77, 1000), (5, 4100), (3, 9000)]
+
+
+@pytest.mark.parametrize("kind", ["randn", "wide", "scaled", "zerorows"])
+@pytest.mark.parametrize("shape", EXTRACT_SHAPES)
+def test_extract_f32_rows_and_cols(ll, kind, shape):
+    X = gen(kind, shape, 100 + shape[0])
+    for by_cols in (0, 1):
+        lines, length = (shape[1], shape[0]) if by_cols else shape
+        rho = O.rho_f32(length)
+        case(f"ozk_extract_f32 {kind} {shape} by_cols={by_cols} rho={rho}")
+        pl = ll.extract(X, by_cols, rho, 4, 1)
+        v, e = to_np(pl.values()), to_np(pl.exponents())
+        hi, lo = O.split_hi_lo(X)
+        if by_cols:
+            sh, eh = O.extract_cols_f32(hi, rho, 4)
+            sl, el = O.extract_cols_f32(lo, rho, 1)
+            sh, sl = sh.transpose(0, 2, 1), sl.transpose(0, 2, 1)
+        else:
+            sh, eh = O.extract_rows_f32(hi, rho, 4)
+            sl, el = O.extract_rows_f32(lo, rho, 1)
+        assert np.array_equal(v, np.concatenate([sh, sl])), "slices"
+        assert np.array_equal(e, np.concatenate([eh, el]).astype(np.int32)), "exponents"
+        assert not pl.nonfinite()
+
+
+@pytest.mark.parametrize("shape", [(1, 1), (40, 30), (130, 257), (9, 5000), (2, 17000)])
+def test_extract_f64_rows_and_cols(ll, shape):
+    X = gen("wide", shape, 7 + shape[1])
+    for by_cols in (0, 1):
+        length = shape[0] if by_cols else shape[1]
+        rho = O.rho_f64(length)
+        case(f"ozk_extract_f64 {shape} by_cols={by_cols} rho={rho}")
+        pl = ll.extract(X, by_cols, rho, 8, f64=True)
+        v, e = to_np(pl.values()), to_np(pl.exponents())
+        if by_cols:
+            s, ee = O.extract_cols_f64(X, rho, 8)
+            s = s.transpose(0, 2, 1)
+        else:
+            s, ee = O.extract_rows_f64(X, rho, 8)
+        assert np.array_equal(v, s) and np.array_equal(e, ee.astype(np.int32))
+
+
+def test_extract_long_lines_streaming(ll):
+    # lines longer than the register-resident kernels hold
+    X = gen("wide2", (3, 40000), 5)
+    rho = O.rho_f32(40000)
+    case(f"ozk_extract_f32 streaming (3, 40000) rho={rho}")
+    pl = ll.extract(X, 0, rho, 4, 1)
+    hi, lo = O.split_hi_lo(X)
+    sh, eh = O.extract_rows_f32(hi, rho, 4)
+    sl, el = O.extract_rows_f32(lo, rho, 1)
+    assert np.array_equal(to_np(pl.values()), np.concatenate([sh, sl]))
+    assert np.array_equal(to_np(pl.exponents()), np.concatenate([eh, el]).astype(np.int32))
+
+
+def test_extract_log2_edge_fixture(ll, golden_dir):
+    d = np.load(golden_dir / "log2_edges.npz")
+    case("log2 edge fixture: f32 rows / cols, f64 rows")
+    pl = ll.extract(d["X32"], 0, int(d["rho32"]), 4, 1)
+    v, e = to_np(pl.values()), to_np(pl.exponents())
+    assert np.array_equal(v[:4], d["rows32_s"]) and np.array_equal(e[:4], d["rows32_e"])
+    assert np.array_equal(v[4:], d["rows32_lo_s"]) and np.array_equal(e[4:], d["rows32_lo_e"])
+    pl = ll.extract(d["X32"].T.copy(), 1, int(d["rho32c"]), 4, 1)
+    v, e = to_np(pl.values()), to_np(pl.exponents())
+    assert np.array_equal(v[:4], d["cols32_s"].transpose(0, 2, 1))
+    assert np.array_equal(e[:4], d["cols32_e"])
+    pl = ll.extract(d["X64"], 0, int(d["rho64"]), 8, f64=True)
+    assert np.array_equal(to_np(pl.values()), d["rows64_s"])
+    assert np.array_equal(to_np(pl.exponents()), d["rows64_e"].astype(np.int32))
+
+
+def test_extract_nonfinite_flag(ll):
+    X = np.ones((5, 7))
+    X[2, 3] = np.inf
+    case("nonfinite flag (inf)")
+    assert ll.extract(X, 0, 17, 4, 1).nonfinite()
+    X[2, 3] = np.nan
+    case("nonfinite flag (nan) by cols")
+    assert ll.extract(X, 1, 17, 4, 1).nonfinite()
+
+
+# ---------------------------------------------------------------- products
+
+SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
+             ("ondevice", 2, 3), ("host", 8, 0)]
+
+
+def _slices(ll, A, B, pipe, nh, nl):
+    K = A.shape[1]
+    if pipe == "host":
+        rho = O.rho_f64(K)
+        a = ll.extract(A, 0, rho, nh, f64=True)
+        b = ll.extract(B, 1, rho, nh, f64=True)
+        oa, oae, ob, obe = O.host_slices(A, B, rho, nh)
+        sched = O.host_schedule(nh)
+        code = ll.PIPE_HOST
+    else:
+        rho = O.rho_f32(K)
+        a = ll.extract(A, 0, rho, nh, nl)
+        b = ll.extract(B, 1, rho, nh, nl)
+        oa, oae, ob, obe = O.ondevice_slices(A, B, rho, nh, nl)
+        sched = O.ondevice_schedule(nh, nl)
+        code = ll.PIPE_ONDEVICE
+    return a, b, (oa, oae, ob, obe), sched, code
+
+
+@pytest.mark.parametrize("pipe,nh,nl", SCHEDULES)
+@pytest.mark.parametrize("shape", [(96, 70, 160), (64, 64, 64), (1, 33, 1), (130, 257, 67)])
+def test_slice_products_bit_exact(ll, pipe, nh, nl, shape):
+    N, K, M = shape
+    if pipe == "host" and K > 1024:
+        pytest.skip("host schedule needs K <= 1024")
+    A, B = gen("randn", (N, K), 1), gen("wide2", (K, M), 2)
+    a, b, (oa, oae, ob, obe), sched, code = _slices(ll, A, B, pipe, nh, nl)
+    case(f"ozk_slice_products {pipe} ({nh},{nl}) N,K,M={shape}")
+    P = to_np(ll.slice_products(a, b, code, nh, nl))
+    Pref = O.slice_products(oa, ob, sched)
+    assert OP.products_exact_certificate(
+        oa, ob, sched, 2.0 ** (O.rho_f32(K) - 24 if pipe != "host" else O.rho_f64(K) - 53),
+        2.0 ** (O.rho_f32(K) - 24 if pipe != "host" else O.rho_f64(K) - 53))
+    assert np.array_equal(P, Pref)
+
+
+# ---------------------------------------------------------------- orders
+
+ORDERS = {"ondevice": [("A4", 0), ("A3", 1)], "host": [("A2", 2), ("A1", 3)]}
+
+
+@pytest.mark.parametrize("pipe,nh,nl", SCHEDULES)
+@pytest.mark.parametrize("shape", [(96, 70, 160), (130, 257, 67), (2, 5, 3)])
+def test_gemm_orders_bit_exact(ll, pipe, nh, nl, shape):
+    N, K, M = shape
+    A, B = gen("wide2", (N, K), 3), gen("randn", (K, M), 4)
+    a, b, (oa, oae, ob, obe), sched, code = _slices(ll, A, B, pipe, nh, nl)
+    Pref = O.slice_products(oa, ob, sched)
+    refs = {"A4": lambda: OP.combine_f64(*O.accumulate_a4(Pref, sched, oae, obe)),
+            "A3": lambda: O.accumulate_a3(Pref, sched, oae, obe),
+            "A2": lambda: O.accumulate_a2(Pref, sched, oae, obe),
+            "A1": lambda: O.accumulate_a1(Pref, sched, oae, obe)}
+    for name, code_o in ORDERS[pipe]:
+        case(f"ozk_gemm {pipe} ({nh},{nl}) order {name} N,K,M={shape}")
+        C = to_np(ll.gemm(a, b, code, nh, nl, code_o))
+        assert np.array_equal(C, refs[name]()), name
+
+
+# ---------------------------------------------------------------- public API
+
+@pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (2, 2)])
+@pytest.mark.parametrize("accumulation", ["fused", "bf16_interleaved", "ondevice", "host"])
+def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
+    A, B = gen("randn", (150, 300), 21), gen("randn", (300, 90), 22)
+    case(f"matmul ondevice {precision} {accumulation} (150,300,90)")
+    C = ozk.matmul(A, B, pipeline="ondevice", accumulation=accumulation,
+                   precision=precision)
+    nh, nl = OP.resolve_precision(precision)
+    if accumulation == "host":
+        ref = O.matmul_ondevice_a3(A, B, "raise", nh, nl)
+    else:
+        ref = O.matmul_ondevice_a4(A, B, "raise", nh, nl)
+    assert isinstance(C, np.ndarray) and C.dtype == np.float64
+    assert np.array_equal(C, ref)
+    assert np.all(np.abs(C - ref) <= 2.0 ** -51 * (np.abs(A) @ np.abs(B)))
+
+
+def test_matmul_numpy_bit_exact(ozk):
+    A, B = gen("wide2", (70, 200), 31), gen("wide2", (200, 50), 32)
+    case("matmul_numpy host / ondevice (70,200,50)")
+    assert np.array_equal(ozk.matmul_numpy(A, B), O.matmul_numpy(A, B))
+    assert np.array_equal(ozk.matmul_numpy(A, B, pipeline="ondevice"),
+                          O.matmul_numpy(A, B, pipeline="ondevice"))
+    assert np.array_equal(ozk.matmul_numpy(A, B, pipeline="ondevice", precision="max"),
+                          O.matmul_numpy(A, B, pipeline="ondevice", precision="max"))
+    case("matmul host (70,200,50)")
+    assert np.array_equal(ozk.matmul(A, B), OP.matmul_host_a2(A, B))
+    assert np.array_equal(ozk.matmul(A, B, n_slices=9), OP.matmul_host_a2(A, B, n_slices=9))
+
+
+def _digest(a):
+    import hashlib
+    a = np.ascontiguousarray(a)
+    return hashlib.sha256(a.tobytes()).hexdigest() + f":{a.dtype}:{a.shape}"
+
+
+def test_config1_host_256(ozk, ll, golden_dir):
+    """256x256 RandomState(0), n_slices=8, host pipeline: slices, exponents,
+    each per-pair product and C bit-exact against the committed digests."""
+    doc = json.loads((golden_dir / "config1.json").read_text())
+    rs = np.random.RandomState(0)
+    A, B = rs.randn(256, 256), rs.randn(256, 256)
+    case("config1 host 256: extraction + products + matmul_numpy")
+    a = ll.extract(A, 0, doc["rho64"], 8, f64=True)
+    b = ll.extract(B, 1, doc["rho64"], 8, f64=True)
+    assert _digest(to_np(a.values())) == doc["a_slices"]
+    assert _digest(to_np(a.exponents())) == doc["a_exps"]
+    assert _digest(to_np(b.values()).transpose(0, 2, 1)) == doc["b_slices_cols"]
+    assert _digest(to_np(b.exponents())) == doc["b_exps"]
+    assert _digest(to_np(ll.slice_products(a, b, ll.PIPE_HOST, 8, 0))) == doc["products"]
+    C = ozk.matmul_numpy(A, B)
+    assert _digest(C) == doc["C_numpy_order"]
+    assert _digest(ozk.matmul(A, B)) == doc["C_jax_order"]
+
+
+def _exact(A, B):
+    from fractions import Fraction
+    Af = [[Fraction(float(v)) for v in r] for r in A]
+    Bf = [[Fraction(float(v)) for v in r] for r in B]
+    return np.array([[float(sum(Af[i][t] * Bf[t][j] for t in range(A.shape[1])))
+                      for j in range(B.shape[1])] for i in range(A.shape[0])])
+
+
+def test_error_vs_exact_no_worse_than_reference(ozk):
+    A, B = gen("wide2", (7, 48), 41), gen("wide2", (48, 6), 42)
+    ex = _exact(A, B)
+    case("exact-rational comparison (7,48,6)")
+    for kw, ref in [({"pipeline": "ondevice"}, O.matmul_ondevice_a4(A, B)),
+                    ({"pipeline": "ondevice", "precision": "max"},
+                     O.matmul_ondevice_a4(A, B, "raise", 5, 4)),
+                    ({}, OP.matmul_host_a2(A, B))]:
+        C = ozk.matmul(A, B, **kw)
+        assert np.all(np.abs(C - ex) <= np.abs(ref - ex)), kw
+
+
+def test_ragged_and_degenerate_shapes(ozk):
+    for N, K, M in [(1, 1, 1), (1, 700, 1), (65, 1, 63), (3, 64, 200), (0, 5, 4), (4, 5, 0)]:
+        A, B = gen("randn", (N, K), N + K), gen("randn", (K, M), K + M)
+        case(f"matmul ondevice ragged {N},{K},{M}")
+        C = ozk.matmul(A, B, pipeline="ondevice")
+        assert C.shape == (N, M)
+        if N and M:
+            assert np.array_equal(C, O.matmul_ondevice_a4(A, B))
+    with pytest.raises(ValueError):
+        ozk.matmul(np.ones((2, 0)), np.ones((0, 2)), pipeline="ondevice")
+
+
+def test_preflight_and_families(ozk):
+    import torch
+    A = gen("randn", (8, 16), 1)
+    B = gen("randn", (16, 4), 2)
+    case("preflight errors")
+    bad = A.copy()
+    bad[1, 1] = np.nan
+    with pytest.raises(ValueError, match="NaN or Inf"):
+        ozk.matmul(bad, B, pipeline="ondevice")
+    fb = ozk.matmul(bad, B, pipeline="ondevice", safe_mode="fallback")
+    assert np.isnan(fb[1]).all() and np.allclose(fb[0], (bad @ B)[0], rtol=1e-14)
+    with pytest.raises(ValueError, match="Unknown accumulation"):
+        ozk.matmul(A, B, pipeline="ondevice", accumulation="x")
+    with pytest.raises(ValueError, match="Unknown precision"):
+        ozk.matmul(A, B, pipeline="ondevice", precision="x")
+    with pytest.raises(ValueError, match="Unknown pipeline"):
+        ozk.matmul(A, B, pipeline="x")
+    with pytest.raises(ValueError, match="Invalid safe_mode"):
+        ozk.matmul(A, B, pipeline="ondevice", safe_mode="x")
+    with pytest.raises(ValueError, match="both be numpy"):
+        ozk.matmul(torch.tensor(A), B, pipeline="ondevice")
+    case("safe_mode fallback (2,10000)@(10000,2)")
+    rng = np.random.RandomState(0)
+    Ab, Bb = rng.randn(2, 10000), rng.randn(10000, 2)
+    with pytest.raises(ValueError, match="insufficient slice budget"):
+        ozk.matmul(Ab, Bb)
+    Cf = ozk.matmul(Ab, Bb, safe_mode="fallback")
+    assert rel_err(Cf, Ab @ Bb) <= 1e-14
+    case("torch family on device")
+    At = torch.tensor(A, device="cuda")
+    Bt = torch.tensor(B, device="cuda")
+    Ct = ozk.matmul(At, Bt, pipeline="ondevice")
+    assert isinstance(Ct, torch.Tensor) and Ct.is_cuda
+    assert np.array_equal(Ct.cpu().numpy(), O.matmul_ondevice_a4(A, B))
+    Ch = ozk.matmul(At, Bt)   # host pipeline always returns NumPy
+    assert isinstance(Ch, np.ndarray)
+    # non-contiguous views are accepted
+    Av = torch.tensor(gen("randn", (16, 8), 3), device="cuda").T
+    Cv = ozk.matmul(Av, Bt, pipeline="ondevice")
+    assert np.array_equal(Cv.cpu().numpy(), O.matmul_ondevice_a4(Av.cpu().numpy(), B))
+
+
+# ---------------------------------------------------------------- gram / residual / solve
+
+@pytest.mark.parametrize("shape", [(64, 64), (300, 40), (33, 130)])
+@pytest.mark.parametrize("precision", ["high", "medium"])
+def test_gram_bit_exact(ozk, shape, precision):
+    A = gen("randn", shape, 51)
+    case(f"gram ozaki {shape} {precision}")
+    for acc in ("bf16_interleaved", "fused"):
+        G = ozk.gram(A, mode="ozaki", precision=precision, accumulation=acc)
+        assert np.array_equal(G, O.gram_ozaki(A, precision))
+        assert np.array_equal(G, G.T)
+
+
+@pytest.mark.parametrize("shape", [(64, 64), (200, 50), (37, 300)])
+def test_residual_bit_exact(ozk, shape):
+    N, K = shape
+    rng = np.random.RandomState(61)
+    A, x, b = rng.randn(N, K), rng.randn(K), rng.randn(N)
+    case(f"residual ozaki {shape}")
+    r = ozk.residual(A, x, b, mode="ozaki")
+    assert r.shape == (N,) and np.array_equal(r, O.residual_ozaki(A, x, b))
+    X, Bm = rng.randn(K, 3), rng.randn(N, 3)
+    R = ozk.residual(A, X, Bm, mode="ozaki", accumulation="fused")
+    assert np.array_equal(R, O.residual_ozaki(A, X, Bm))
+
+
+def test_known_answers_on_gpu(ozk, golden_dir):
+    """gram / residual errors recorded by the reference (tpu_full_results.json
+    :77,93,109,157,173,189) from the same RandomState(42) draws."""
+    known = json.loads((golden_dir / "reference_known_answers.json").read_text())["tpu_full_results"]
+    rng = np.random.RandomState(42)
+    for n in [64, 128, 256]:
+        rng.randn(n, n), rng.randn(n, n)
+    rng.randn(128, 128), rng.randn(128, 128), rng.randn(64, 256), rng.randn(256, 32)
+    for n in [64, 128, 256]:
+        A = rng.randn(n, n)
+        case(f"known answer gram n={n}")
+        e = rel_err(ozk.gram(A, mode="ozaki"), A.T @ A)
+        assert e == pytest.approx(known[f"gram ozaki n={n}"]["error"], rel=1e-6)
+    rng.randn(256, 64), rng.randn(128, 128)
+    for n in [64, 128, 256]:
+        A, x, b = rng.randn(n, n), rng.randn(n), rng.randn(n)
+        case(f"known answer residual n={n}")
+        e = rel_err(ozk.residual(A, x, b, mode="ozaki"), b - A @ x)
+        assert e == pytest.approx(known[f"residual ozaki n={n}"]["error"], rel=1e-6)
+
+
+def test_solve_ozaki(ozk):
+    """ci_solve_validate.py:49-71 thresholds; FP32 LU comes from a different
+    LAPACK than the oracle's, so the comparison is by tolerance."""
+    rng = np.random.RandomState(42)
+    n = 128
+    A, b = rng.randn(n, n), rng.randn(n)
+    xr = np.linalg.solve(A, b)
+    case("solve ozaki n=128")
+    assert rel_err(ozk.solve(A, b, residual_mode="ozaki"), xr) <= 1e-7
+    assert rel_err(ozk.solve(A, b, residual_mode="ozaki", precision="medium"), xr) <= 1e-5
+    assert rel_err(ozk.solve(A, b, residual_mode="ozaki", accumulation="fused"), xr) <= 1e-7
+    assert rel_err(ozk.solve(A, b), xr) <= 1e-12
+    e0 = rel_err(ozk.solve(A, b, max_iterations=0), xr)
+    e1 = rel_err(ozk.solve(A, b, max_iterations=1), xr)
+    e3 = rel_err(ozk.solve(A, b, max_iterations=3), xr)
+    assert e1 < e0 * 1e-4 and e3 < e1
+    X = ozk.solve(A, rng.randn(n, 4), residual_mode="ozaki")
+    assert X.shape == (n, 4)
+    with pytest.raises(ValueError, match="square"):
+        ozk.solve(rng.randn(3, 4), rng.randn(3))
+
+
+def test_extract_api_helpers(ozk):
+    X = gen("wide2", (20, 33), 71)
+    case("extract_split_* API helpers")
+    s, e = ozk.extract_split_rows(X, O.rho_f64(33), 8)
+    rs, re_ = O.extract_rows_f64(X, O.rho_f64(33), 8)
+    assert np.array_equal(np.stack(s), rs) and np.array_equal(np.stack(e), re_)
+    s, e = ozk.f32_extract_split_cols(X.astype(np.float32), O.rho_f32(20), 5)
+    rs, re_ = O.extract_cols_f32(X.astype(np.float32), O.rho_f32(20), 5)
+    assert np.array_equal(np.stack(s), rs) and np.array_equal(np.stack(e), re_)
+    st, et = ozk.jax_extract_split_rows(X.astype(np.float32), 17, 4)
+    rs, re_ = O.extract_rows_f32(X.astype(np.float32), 17, 4)
+    assert np.array_equal(st, rs) and np.array_equal(et, re_)
