@@ -155,8 +155,10 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
 int ozk_check_finite(const double* X, int64_t rows, int64_t cols, int64_t ld,
                      uint32_t* flags, void* stream);
 
-/* Test hook: runs one 32x32x16 BF16 MFMA on a fixed pattern and writes the
- * 64 lanes x 16 accumulator registers (as int32) to out[64*16]. */
+/* Test hook: runs one 32x32x16 and one 16x16x32 BF16 MFMA on a fixed
+ * pattern and writes their accumulator registers as int32: out[0..1023] =
+ * 64 lanes x 16 registers (32x32x16), out[1024..1279] = 64 lanes x 4
+ * registers (16x16x32).  out must hold 1280 int32. */
 int ozk_probe_mfma_layout(int32_t* out, void* stream);
 
 #ifdef __cplusplus

@@ -252,33 +252,81 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 
 // ---------------------------------------------------------------- kernels
 
-// MFMAs of every pair of a compile-time schedule: the fragment of A slice a
-// is read once per k-step and reused by every pair (a, b).
+// ---------------------------------------------------------------- all pairs
+//
+// The all-pairs kernel uses 8 waves (2 per SIMD).  Wave w owns rows
+// 32 * (w >> 2) .. +31 and columns 16 * (w & 3) .. +15 of the 64x64 tile as
+// two v_mfma_f32_16x16x32_bf16 blocks, so a pair costs 8 accumulator VGPRs
+// and the 24 pairs of precision="high" fit in the 256 AGPRs with the
+// operand registers in the remaining VGPRs.
+//
+// LDS stage: one 1 KiB fragment per (slot, 16-line group): lane l of the
+// fragment holds line l % 16, k chunk l / 16 (8 BF16).  Wave w moves
+// fragments w, w + 8, ...: lane l loads its 16 bytes from global memory and
+// stores them at fragment * 1 KiB + l * 16, so LDS writes and the MFMA
+// operand reads are both linear in the lane index.
+
+constexpr int kThreads16 = 512;
+
+__device__ __forceinline__ int frag16(int slot, int lg, int lane) {
+  return (slot * 4 + lg) * 64 + lane;
+}
+
+typedef __attribute__((address_space(3))) void lds_void_t;
+
+// One K stage straight from global memory into LDS (global_load_lds_dwordx4:
+// lane l's 16 bytes land at the wave-uniform LDS base + 16 l), so staging
+// takes no VGPRs.  Every address is inside the zero-padded slice planes.
+template <int NA, int NB>
+__device__ __forceinline__ void stage16_dma(const uint16_t* As, int64_t aplane,
+                                            const uint16_t* Bs, int64_t bplane,
+                                            int64_t ld, int64_t k0, uint4* buf,
+                                            int wave, int lane) {
+  constexpr int kFrags = (NA + NB) * 4;
+  constexpr int kPer = (kFrags + 7) / 8;
+  const int64_t lane_off = (int64_t)(lane & 15) * ld + k0 + 8 * (lane >> 4);
+#pragma unroll
+  for (int i = 0; i < kPer; ++i) {
+    const int F = wave + 8 * i;
+    if (kFrags % 8 == 0 || F < kFrags) {
+      const int slot = F >> 2, lg = F & 3;
+      const uint16_t* base = slot < NA ? As + slot * aplane
+                                       : Bs + (slot - NA) * bplane;
+      __builtin_amdgcn_global_load_lds(
+          (const void*)(base + (int64_t)(lg * 16) * ld + lane_off),
+          (lds_void_t*)(buf + F * 64), 16, 0, 0);
+    }
+  }
+}
+
 template <int PIPE, int NHI, int NLO, int NT, int NP>
-struct AllPairsMMA {
-  floatx16 acc[NP];
-  int lane, wm, wn;
-  __device__ __forceinline__ void operator()(const uint4* buf, int ks) {
+struct AllPairsMMA16 {
+  floatx4 acc[NP][2];
+  int lane, wr, wc;
+  __device__ __forceinline__ void operator()(const uint4* buf) {
     bf16x8 bf[NT];
 #pragma unroll
-    for (int s = 0; s < NT; ++s) bf[s] = as_bf16x8(buf[frag_off(NT + s, wn, ks, lane)]);
+    for (int s = 0; s < NT; ++s) bf[s] = as_bf16x8(buf[frag16(NT + s, wc, lane)]);
 #pragma unroll
     for (int sa = 0; sa < NT; ++sa) {
-      const bf16x8 af = as_bf16x8(buf[frag_off(sa, wm, ks, lane)]);
 #pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-        if (q.a == sa)
-          acc[p] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af, bf[q.b], acc[p], 0, 0, 0);
+      for (int h = 0; h < 2; ++h) {
+        const bf16x8 af = as_bf16x8(buf[frag16(sa, 2 * wr + h, lane)]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const PairInfo q = pair_info(PIPE, NHI, NLO, p);
+          if (q.a == sa)
+            acc[p][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[q.b], acc[p][h], 0, 0, 0);
+        }
       }
     }
   }
 };
 
 // All pairs of the schedule in one K sweep (schedules whose accumulators fit
-// in registers).  PIPE/NHI/NLO fix the schedule at compile time.
+// in the AGPRs).  PIPE/NHI/NLO fix the schedule at compile time.
 template <int PIPE, int NHI, int NLO, int ORDER>
-__global__ __launch_bounds__(kThreads) void gemm_allpairs(
+__global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     const uint16_t* __restrict__ As, const int32_t* __restrict__ Ae,
     const uint16_t* __restrict__ Bs, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t ld, int64_t a_lines, int64_t b_lines,
@@ -286,53 +334,75 @@ __global__ __launch_bounds__(kThreads) void gemm_allpairs(
   constexpr int NT = PIPE == OZK_PIPE_ONDEVICE ? NHI + NLO : NHI;
   constexpr int NP = pair_count(PIPE, NHI, NLO);
   constexpr int NBLK = PIPE == OZK_PIPE_ONDEVICE ? 3 : 1;
-  __shared__ uint4 lds[2 * (NT + NT) * 4 * 64];
+  constexpr int kBuf = (NT + NT) * 4 * 64;  // uint4 per stage buffer
+  // Two separate LDS objects so the compiler can tell the buffer being
+  // filled by DMA from the one being read.
+  __shared__ uint4 lds0[kBuf];
+  __shared__ uint4 lds1[kBuf];
 
   const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
   int tm, tn;
   tile_coords(blockIdx.x, ntm, ntn, tm, tn);
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
   const int64_t aplane = a_lines * ld, bplane = b_lines * ld;
+  const uint16_t* At = As + row0 * ld;
+  const uint16_t* Bt = Bs + col0 * ld;
 
-  const uint16_t* a_ptr[NT];
-  const uint16_t* b_ptr[NT];
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  AllPairsMMA16<PIPE, NHI, NLO, NT, NP> mma;
+  mma.lane = lane;
+  mma.wr = wave >> 2;
+  mma.wc = wave & 3;
 #pragma unroll
-  for (int s = 0; s < NT; ++s) {
-    a_ptr[s] = As + s * aplane + row0 * ld;
-    b_ptr[s] = Bs + s * bplane + col0 * ld;
+  for (int p = 0; p < NP; ++p) {
+    mma.acc[p][0] = floatx4{};
+    mma.acc[p][1] = floatx4{};
   }
 
-  AllPairsMMA<PIPE, NHI, NLO, NT, NP> mma;
-  mma.lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  mma.wm = wave >> 1;
-  mma.wn = wave & 1;
-#pragma unroll
-  for (int p = 0; p < NP; ++p) mma.acc[p] = floatx16{};
-  k_sweep<NT, NT>(a_ptr, b_ptr, ld, lds, mma);
+  // Barrier, then fetch stage s + 1 into the other buffer (its readers
+  // finished before the barrier), then run the MFMAs of stage s; the
+  // barrier of the next step waits for the fetch.  Unrolled by two so that
+  // each step names its buffers statically.
+  const int64_t nst = ld / kBK;  // even: ld is a multiple of 64
+  stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, 0, lds0, wave, lane);
+  for (int64_t s = 0; s < nst; s += 2) {
+    __syncthreads();
+    stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, (s + 1) * kBK, lds1, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);  // keep the fetch ahead of the MFMAs
+    mma(lds0);
+    __syncthreads();
+    if (s + 2 < nst)
+      stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, (s + 2) * kBK, lds0, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+    mma(lds1);
+  }
 
-  // Fold in schedule order and store.
-  const int lane = mma.lane;
-  const int64_t col = col0 + 32 * mma.wn + (lane & 31);
+  // Fold in schedule order and store.  Accumulator register r of lane l of a
+  // 16x16 block holds row 4 * (l / 16) + r, column l % 16.
+  const int64_t col = col0 + 16 * mma.wc + (lane & 15);
   int eb[NT];
 #pragma unroll
   for (int s = 0; s < NT; ++s) eb[s] = Be[s * b_lines + col];
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
-    int ea[NT];
+  for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int s = 0; s < NT; ++s) ea[s] = Ae[s * a_lines + row];
-    typename FoldOf<ORDER>::type f;
-    f.init();
+    for (int r = 0; r < 4; ++r) {
+      const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
+      int ea[NT];
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-      f.pair(q, mma.acc[p][r], ldexpf(1.0f, eb[q.b]), ldexpf(1.0f, ea[q.a]),
-             ldexp(1.0, eb[q.b]), ldexp(1.0, ea[q.a]));
+      for (int s = 0; s < NT; ++s) ea[s] = Ae[s * a_lines + row];
+      typename FoldOf<ORDER>::type f;
+      f.init();
+#pragma unroll
+      for (int p = 0; p < NP; ++p) {
+        const PairInfo q = pair_info(PIPE, NHI, NLO, p);
+        f.pair(q, mma.acc[p][h][r], ldexpf(1.0f, eb[q.b]), ldexpf(1.0f, ea[q.a]),
+               ldexp(1.0, eb[q.b]), ldexp(1.0, ea[q.a]));
+      }
+      const double out = f.finish(NBLK);
+      if (row < N && col < M) C[row * ldc + col] = out;
     }
-    const double out = f.finish(NBLK);
-    if (row < N && col < M) C[row * ldc + col] = out;
   }
 }
 
@@ -429,6 +499,23 @@ __global__ void probe_mfma_kernel(int32_t* out) {
   for (int r = 0; r < 16; ++r) out[l * 16 + r] = (int32_t)acc[r];
 }
 
+// Same probe for v_mfma_f32_16x16x32_bf16: lane l -> (row l % 16, k 8 * (l / 16)
+// + e); C[i][j] = i + 64 j.  Writes 64 lanes x 4 registers to out[1024..1279].
+__global__ void probe_mfma16_kernel(int32_t* out) {
+  const int l = threadIdx.x;
+  bf16x8 a = bf16x8{}, b = bf16x8{};
+  if (l < 16) {
+    a[0] = (__bf16)(float)l;
+    a[1] = (__bf16)1.0f;
+    b[0] = (__bf16)1.0f;
+    b[1] = (__bf16)(64.0f * (float)l);
+  }
+  floatx4 acc = floatx4{};
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[1024 + l * 4 + r] = (int32_t)acc[r];
+}
+
 // ---------------------------------------------------------------- launch
 
 // Compile-time instantiations of the all-pairs kernel.
@@ -442,8 +529,8 @@ static bool try_allpairs(int pipe, int nhi, int nlo, int order, dim3 grid,
     return false;
 #define OZK_AP(O)                                                         \
   hipLaunchKernelGGL((gemm_allpairs<PIPE, NHI, NLO, O>), grid,            \
-                     dim3(kThreads), 0, st, As, Ae, Bs, Be, N, M, ld, al, \
-                     bl, C, ldc)
+                     dim3(kThreads16), 0, st, As, Ae, Bs, Be, N, M, ld,   \
+                     al, bl, C, ldc)
   switch (order) {
     case OZK_ORDER_2SUM: OZK_AP(OZK_ORDER_2SUM); break;
     case OZK_ORDER_BLOCK64: OZK_AP(OZK_ORDER_BLOCK64); break;
@@ -502,6 +589,8 @@ int launch_products(const uint16_t* As, const uint16_t* Bs, int64_t N,
 
 int launch_probe_mfma(int32_t* out, hipStream_t st) {
   hipLaunchKernelGGL(probe_mfma_kernel, dim3(1), dim3(64), 0, st, out);
+  OZK_LAUNCH_CHECK();
+  hipLaunchKernelGGL(probe_mfma16_kernel, dim3(1), dim3(64), 0, st, out);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }

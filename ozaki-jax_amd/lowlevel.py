@@ -93,10 +93,12 @@ def slice_products(a, b, pipeline, n_hi, n_lo):
 
 
 def probe_mfma_layout():
-    """(64, 16) int32: accumulator register r of lane l after the layout
-    probe MFMA; the value encodes row + 64 * col of the output element."""
+    """Accumulator registers after the layout-probe MFMAs, as int32 arrays
+    (32x32x16: (64 lanes, 16 regs); 16x16x32: (64 lanes, 4 regs)); each value
+    encodes row + 64 * col of the output element it holds."""
     lib = _lib.load()
     dev = D.require_gpu()
-    out = D.torch.zeros((64, 16), dtype=D.torch.int32, device=dev)
+    out = D.torch.zeros(64 * 16 + 64 * 4, dtype=D.torch.int32, device=dev)
     _lib.check(lib.ozk_probe_mfma_layout(out.data_ptr(), D.stream_handle()))
-    return out.cpu().numpy()
+    o = out.cpu().numpy()
+    return o[:1024].reshape(64, 16), o[1024:].reshape(64, 4)

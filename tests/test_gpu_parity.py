@@ -60,13 +60,17 @@ def to_np(t):
 # ---------------------------------------------------------------- layout
 
 def test_mfma_output_layout(ll):
-    case("probe_mfma_layout 32x32x16 bf16")
-    out = ll.probe_mfma_layout()
+    case("probe_mfma_layout 32x32x16 and 16x16x32 bf16")
+    out, out16 = ll.probe_mfma_layout()
     for lane in range(64):
         for r in range(16):
             row = 8 * (r // 4) + 4 * (lane // 32) + (r % 4)
             col = lane % 32
             assert out[lane, r] == row + 64 * col, (lane, r, out[lane, r])
+        for r in range(4):
+            row = 4 * (lane // 16) + r
+            col = lane % 16
+            assert out16[lane, r] == row + 64 * col, (lane, r, out16[lane, r])
 
 
 # ---------------------------------------------------------------- extraction
