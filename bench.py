@@ -49,6 +49,9 @@ def parse_args():
     ap.add_argument("--precision", default="high")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-check", action="store_true")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="also run a plain 1 GiB device copy (elementwise "
+                         "kernel) to calibrate HBM byte counters")
     return ap.parse_args()
 
 
@@ -174,6 +177,14 @@ def main():
     ev1.record(stream)
     torch.cuda.synchronize()
     dgemm_s = ev0.elapsed_time(ev1) / 1e3 / 3
+
+    if args.copy_calibration:
+        log("copy calibration: 2 x 1 GiB float64 elementwise copy")
+        src = torch.ones(1 << 27, dtype=torch.float64, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(2):
+            torch.mul(src, 1.0, out=dst)
+        torch.cuda.synchronize()
 
     acc = None
     if not args.no_check:

@@ -260,42 +260,65 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 // and the 24 pairs of precision="high" fit in the 256 AGPRs with the
 // operand registers in the remaining VGPRs.
 //
-// LDS stage: one 1 KiB fragment per (slot, 16-line group): lane l of the
-// fragment holds line l % 16, k chunk l / 16 (8 BF16).  Wave w moves
-// fragments w, w + 8, ...: lane l loads its 16 bytes from global memory and
-// stores them at fragment * 1 KiB + l * 16, so LDS writes and the MFMA
-// operand reads are both linear in the lane index.
+// LDS stage (64 k): one 1 KiB fragment per (slot, 32-wide k half, 16-line
+// group): lane l of the fragment holds line l % 16, k chunk l / 16 (8 BF16).
+// Wave w moves fragments w, w + 8, ...: lane l's 16 bytes go from global
+// memory straight to fragment * 1 KiB + l * 16, so the LDS writes and the
+// MFMA operand reads are both linear in the lane index.
 
 constexpr int kThreads16 = 512;
 
-__device__ __forceinline__ int frag16(int slot, int lg, int lane) {
-  return (slot * 4 + lg) * 64 + lane;
+// Stages of kBK16 = 64 k: fragment (slot, k-half kh, 16-line group lg).
+constexpr int kBK16 = 64;
+
+__device__ __forceinline__ int frag16(int slot, int kh, int lg, int lane) {
+  return ((slot * 2 + kh) * 4 + lg) * 64 + lane;
 }
 
-typedef __attribute__((address_space(3))) void lds_void_t;
+// One 16-byte-per-lane direct load from global memory into LDS
+// (global_load_lds_dwordx4): lane l's 16 bytes land at LDS offset
+// `lds_addr` + 16 l.  `lds_addr` and `gbase` are wave-uniform; `voff` is the
+// lane's byte offset from `gbase`.  Written as inline assembly so that the
+// compiler does not order the K loop's LDS reads behind these loads: the
+// kernel waits for them itself (wait_dma) before the barrier that publishes
+// the stage.  M0 carries the LDS address; nothing else in these kernels
+// uses M0.
+__device__ __forceinline__ void dma16(uint32_t lds_addr, const void* gbase,
+                                      uint32_t voff) {
+  asm volatile(
+      "s_mov_b32 m0, %0\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, %2"
+      :
+      : "s"(lds_addr), "v"(voff), "s"(gbase)
+      : "memory");
+}
 
-// One K stage straight from global memory into LDS (global_load_lds_dwordx4:
-// lane l's 16 bytes land at the wave-uniform LDS base + 16 l), so staging
-// takes no VGPRs.  Every address is inside the zero-padded slice planes.
+__device__ __forceinline__ void wait_dma() {
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+}
+
+__device__ __forceinline__ uint32_t lds_offset(const void* p) {
+  return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
+}
+
+// One K stage straight from global memory into LDS: wave w moves fragment
+// (slot i, k-half (w >> 2) & 1, line group w & 3) of every slot i.  All
+// addresses are inside the zero-padded slice planes.
 template <int NA, int NB>
 __device__ __forceinline__ void stage16_dma(const uint16_t* As, int64_t aplane,
                                             const uint16_t* Bs, int64_t bplane,
-                                            int64_t ld, int64_t k0, uint4* buf,
-                                            int wave, int lane) {
-  constexpr int kFrags = (NA + NB) * 4;
-  constexpr int kPer = (kFrags + 7) / 8;
-  const int64_t lane_off = (int64_t)(lane & 15) * ld + k0 + 8 * (lane >> 4);
+                                            int64_t ld, int64_t k0,
+                                            uint32_t buf_lds, int wave,
+                                            uint32_t lane_bytes) {
+  const int kh = (wave >> 2) & 1, lg = wave & 3;
+  const int64_t wave_off = (int64_t)(lg * 16) * ld + 32 * kh + k0;
 #pragma unroll
-  for (int i = 0; i < kPer; ++i) {
-    const int F = wave + 8 * i;
-    if (kFrags % 8 == 0 || F < kFrags) {
-      const int slot = F >> 2, lg = F & 3;
-      const uint16_t* base = slot < NA ? As + slot * aplane
-                                       : Bs + (slot - NA) * bplane;
-      __builtin_amdgcn_global_load_lds(
-          (const void*)(base + (int64_t)(lg * 16) * ld + lane_off),
-          (lds_void_t*)(buf + F * 64), 16, 0, 0);
-    }
+  for (int i = 0; i < NA + NB; ++i) {
+    const uint16_t* base = i < NA ? As + i * aplane : Bs + (i - NA) * bplane;
+    const int F = i * 8 + wave;
+    dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024),
+          (const void*)(base + wave_off), lane_bytes);
   }
 }
 
@@ -303,22 +326,51 @@ template <int PIPE, int NHI, int NLO, int NT, int NP>
 struct AllPairsMMA16 {
   floatx4 acc[NP][2];
   int lane, wr, wc;
+
+  // MFMAs of one (A slot, row block) for every pair of that A slot.
+  template <int SA, int H>
+  __device__ __forceinline__ void block(const bf16x8& af, const bf16x8 (&bf)[NT]) {
+#pragma unroll
+    for (int p = 0; p < NP; ++p) {
+      const PairInfo q = pair_info(PIPE, NHI, NLO, p);
+      if (q.a == SA)
+        acc[p][H] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[q.b], acc[p][H], 0, 0, 0);
+    }
+  }
+
+  // The NT * 2 blocks of one 32-wide k half, A fragments software-pipelined
+  // through kDepth + 1 registers: the read of block j + kDepth is issued
+  // before the MFMAs of block j, so each read has kDepth blocks of MFMAs to
+  // land.  Scheduling barriers keep the compiler from moving reads back.
+  static constexpr int kBlocks = NT * 2, kDepth = 3;
+
+  __device__ __forceinline__ bf16x8 read_a(const uint4* buf, int kh, int j) const {
+    return as_bf16x8(buf[frag16(j >> 1, kh, 2 * wr + (j & 1), lane)]);
+  }
+
+  template <int J>
+  __device__ __forceinline__ void pipe_step(const uint4* buf, int kh,
+                                            bf16x8 (&af)[kDepth + 1],
+                                            const bf16x8 (&bf)[NT]) {
+    if constexpr (J < kBlocks) {
+      if constexpr (J + kDepth < kBlocks) af[(J + kDepth) % (kDepth + 1)] = read_a(buf, kh, J + kDepth);
+      block<J / 2, J % 2>(af[J % (kDepth + 1)], bf);
+      __builtin_amdgcn_sched_barrier(0);
+      pipe_step<J + 1>(buf, kh, af, bf);
+    }
+  }
+
   __device__ __forceinline__ void operator()(const uint4* buf) {
-    bf16x8 bf[NT];
 #pragma unroll
-    for (int s = 0; s < NT; ++s) bf[s] = as_bf16x8(buf[frag16(NT + s, wc, lane)]);
+    for (int kh = 0; kh < 2; ++kh) {
+      bf16x8 bf[NT];
 #pragma unroll
-    for (int sa = 0; sa < NT; ++sa) {
+      for (int s = 0; s < NT; ++s) bf[s] = as_bf16x8(buf[frag16(NT + s, kh, wc, lane)]);
+      bf16x8 af[kDepth + 1];
 #pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        const bf16x8 af = as_bf16x8(buf[frag16(sa, 2 * wr + h, lane)]);
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-          if (q.a == sa)
-            acc[p][h] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[q.b], acc[p][h], 0, 0, 0);
-        }
-      }
+      for (int j = 0; j < kDepth; ++j) af[j] = read_a(buf, kh, j);
+      __builtin_amdgcn_sched_barrier(0);
+      pipe_step<0>(buf, kh, af, bf);
     }
   }
 };
@@ -334,11 +386,9 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   constexpr int NT = PIPE == OZK_PIPE_ONDEVICE ? NHI + NLO : NHI;
   constexpr int NP = pair_count(PIPE, NHI, NLO);
   constexpr int NBLK = PIPE == OZK_PIPE_ONDEVICE ? 3 : 1;
-  constexpr int kBuf = (NT + NT) * 4 * 64;  // uint4 per stage buffer
-  // Two separate LDS objects so the compiler can tell the buffer being
-  // filled by DMA from the one being read.
-  __shared__ uint4 lds0[kBuf];
-  __shared__ uint4 lds1[kBuf];
+  constexpr int kBuf = (NT + NT) * 8 * 64;  // uint4 per stage buffer
+  // Two stage buffers (NT = 5: 2 x 80 KiB, the whole LDS of a gfx950 CU).
+  __shared__ uint4 lds[2 * kBuf];
 
   const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
   int tm, tn;
@@ -360,22 +410,21 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     mma.acc[p][1] = floatx4{};
   }
 
-  // Barrier, then fetch stage s + 1 into the other buffer (its readers
-  // finished before the barrier), then run the MFMAs of stage s; the
-  // barrier of the next step waits for the fetch.  Unrolled by two so that
-  // each step names its buffers statically.
-  const int64_t nst = ld / kBK;  // even: ld is a multiple of 64
-  stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, 0, lds0, wave, lane);
-  for (int64_t s = 0; s < nst; s += 2) {
+  // Per stage: wait for this wave's loads of stage s, barrier (stage s is
+  // complete in LDS and every wave is done with the other buffer), fetch
+  // stage s + 1 into the other buffer, run the MFMAs of stage s.
+  const int64_t nst = ld / kBK16;
+  const uint32_t lane_bytes = (uint32_t)(((lane & 15) * ld + 8 * (lane >> 4)) * 2);
+  const uint32_t lds0 = lds_offset(lds);
+  stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, 0, lds0, wave, lane_bytes);
+  for (int64_t s = 0; s < nst; ++s) {
+    wait_dma();
     __syncthreads();
-    stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, (s + 1) * kBK, lds1, wave, lane);
-    __builtin_amdgcn_sched_barrier(0);  // keep the fetch ahead of the MFMAs
-    mma(lds0);
-    __syncthreads();
-    if (s + 2 < nst)
-      stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, (s + 2) * kBK, lds0, wave, lane);
-    __builtin_amdgcn_sched_barrier(0);
-    mma(lds1);
+    if (s + 1 < nst)
+      stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, (s + 1) * kBK16,
+                          lds0 + (uint32_t)(((s + 1) & 1) * kBuf * 16), wave,
+                          lane_bytes);
+    mma(lds + (s & 1) * kBuf);
   }
 
   // Fold in schedule order and store.  Accumulator register r of lane l of a
