@@ -7,8 +7,10 @@ A step is one full call: split + extraction of A and B, the fused 24-pair
 slice GEMM with the 2Sum accumulation, FP64 output and the non-finite check.
 
 Prints one JSON line with value = 2 M N K / t (TFLOP/s), plus
-  roofline      the fused GEMM kernel's BF16 MFMA rate (HIP events on the
-                stream it runs on) against the 2.5 PFLOP/s dense peak;
+  roofline      the fused GEMM kernel's MFMA rate (HIP events on the stream it
+                runs on) against the dense peak of the matrix-core type it
+                runs on: INT8 (5.0 POP/s) when K > 4096 makes rho >= 19 and
+                the slices fit in int8, else BF16 (2.5 PFLOP/s);
   cpu_baseline  the oracle (NumPy restatement of matmul_numpy(pipeline=
                 "ondevice")) timed on this host at 4096^3;
   rocblas_dgemm FP64 DGEMM of the same matrices (torch.matmul -> rocBLAS);
@@ -32,6 +34,7 @@ sys.path.insert(0, str(ROOT))
 METRIC = ("FP64-equiv TFLOP/s (2MNK/t) 8192³ precision=high; "
           "max scaled err vs ref")
 PEAK_BF16_TFLOPS = 2500.0
+PEAK_INT8_TOPS = 5000.0
 PEAK_HBM_GBS = 8000.0
 PROFILE_TRAFFIC = ROOT / "profiles" / "gemm_allpairs_high_8192_traffic.md"
 
@@ -143,8 +146,9 @@ def main():
 
     # Fused GEMM kernel alone: HIP events on the stream it is launched on.
     rho = _lib.load().ozk_rho_f32(n)
-    pa = ll.extract(At, 0, rho, n_hi, n_lo)
-    pb = ll.extract(Bt, 1, rho, n_hi, n_lo)
+    i8 = rho >= 19 and (n_hi, n_lo) in ((4, 1), (3, 1))
+    pa = ll.extract(At, 0, rho, n_hi, n_lo, i8=i8)
+    pb = ll.extract(Bt, 1, rho, n_hi, n_lo, i8=i8)
     ll.gemm(pa, pb, ll.PIPE_ONDEVICE, n_hi, n_lo, ll.ORDER_2SUM)
     stream = torch.cuda.current_stream()
     ev0, ev1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -157,13 +161,15 @@ def main():
     gemm_s = ev0.elapsed_time(ev1) / 1e3 / reps
     flops = n_pairs * 2.0 * n ** 3
     achieved = flops / gemm_s / 1e12
-    log(f"gemm kernel {gemm_s * 1e3:.2f} ms, {achieved:.1f} TFLOP/s BF16")
+    peak = PEAK_INT8_TOPS if i8 else PEAK_BF16_TFLOPS
+    log(f"gemm kernel {gemm_s * 1e3:.2f} ms, {achieved:.1f} T(FL)OP/s "
+        f"{'INT8' if i8 else 'BF16'} of {peak}")
 
     # Extraction phase (split + A rows + B columns) for reference.
     ev0.record(stream)
     for _ in range(reps):
-        ll.extract(At, 0, rho, n_hi, n_lo)
-        ll.extract(Bt, 1, rho, n_hi, n_lo)
+        ll.extract(At, 0, rho, n_hi, n_lo, i8=i8)
+        ll.extract(Bt, 1, rho, n_hi, n_lo, i8=i8)
     ev1.record(stream)
     torch.cuda.synchronize()
     ext_s = ev0.elapsed_time(ev1) / 1e3 / reps
@@ -196,6 +202,7 @@ def main():
                "max_scaled_err_vs_fp64": e_f64,
                "scale": "|C - C_ref| / (|A||B|)_ij"}
 
+    ext_bytes = 2 * n * n * (8 + (1 if i8 else 2) * (n_hi + n_lo))
     cpu = None if args.no_cpu else cpu_baseline(args.precision)
     traffic = read_traffic()
     dev_name = torch.cuda.get_device_name(0)
@@ -210,25 +217,27 @@ def main():
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": "int8" if i8 else "bf16",
         "data": "synthetic N(0,1), RandomState(0), A drawn before B",
         "config": {
             "workload": f"matmul(pipeline='ondevice', accumulation='fused', "
                         f"precision='{args.precision}') FP64 {n}x{n}x{n}",
             "M": n, "N": n, "K": n, "n_hi": n_hi, "n_lo": n_lo,
             "slice_gemms": n_pairs, "rho": rho,
+            "slice_format": "int8 (q = slice * 2^(24-rho), INT32 sums)" if i8
+                            else "bf16 (FP32 sums)",
         },
         "roofline": {
-            "bound": "mfma", "achieved": achieved, "peak": PEAK_BF16_TFLOPS,
-            "unit": "TFLOP/s", "frac": achieved / PEAK_BF16_TFLOPS,
+            "bound": "mfma", "achieved": achieved, "peak": peak,
+            "unit": "TFLOP/s", "frac": achieved / peak,
             "traffic": traffic,
-            "kernel": f"gemm_allpairs<ondevice,{n_hi},{n_lo},2SUM>",
+            "kernel": f"gemm_allpairs<{'OpI8' if i8 else 'OpBf16'},{n_hi},{n_lo},2SUM>",
             "kernel_ms": gemm_s * 1e3,
             "algorithmic_flops_per_launch": flops,
         },
         "extraction": {"ms": ext_s * 1e3,
-                       "algorithmic_bytes": 2 * n * n * (8 + 2 * (n_hi + n_lo)),
-                       "GB_per_s": 2 * n * n * (8 + 2 * (n_hi + n_lo)) / ext_s / 1e9,
+                       "algorithmic_bytes": ext_bytes,
+                       "GB_per_s": ext_bytes / ext_s / 1e9,
                        "peak_GB_per_s": PEAK_HBM_GBS},
         "rocblas_dgemm": {"ms": dgemm_s * 1e3,
                           "tflops": 2.0 * n ** 3 / dgemm_s / 1e12},

@@ -80,6 +80,17 @@ int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
                     uint16_t* slices, int32_t* exps, uint32_t* flags,
                     void* workspace, size_t workspace_bytes, void* stream);
 
+/* As ozk_extract_f32, with INT8 planes: each slice is stored as its integer
+ * count of grid steps, q = slice * 2^(24 - rho), which needs rho >= 19
+ * (|q| <= 2^(25 - rho) <= 64; returns OZK_ERR_UNSUPPORTED otherwise).  Same
+ * plane layout with 1-byte elements.  No counterpart in the reference: an
+ * exact re-encoding of its BF16-exact slices (extract.py:145-151) for the
+ * INT8 matrix cores. */
+int ozk_extract_f32_i8(const double* X, int64_t rows, int64_t cols,
+                       int64_t ldx, int by_cols, int rho, int n_hi, int n_lo,
+                       int8_t* slices, int32_t* exps, uint32_t* flags,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* FP64 sigma-trick extraction, n_slices planes (extract.py:21-103); slices
  * are the FP32 rounding of v * 2^-c (extract.py:57-60), stored as BF16. */
 int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
@@ -99,12 +110,24 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * (matmul.py:706-722), `_accumulate_block_products` (matmul.py:543-597),
  * `_ozaki_gemms_jit` + `_accumulate_products` (matmul.py:23-64) and the
  * matmul_numpy host loop (matmul.py:879-898).  A planes are rows of A
- * (N lines), B planes are columns of B (M lines); both of length K. */
+ * (N lines), B planes are columns of B (M lines); both of length K.
+ * The drivers below use INT8 planes (ozk_gemm_i8) instead when the
+ * contraction length gives rho >= 19 and the schedule is a preset. */
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
              const uint16_t* b_slices, const int32_t* b_exps,
              int64_t N, int64_t M, int64_t K,
              int pipeline, int n_hi, int n_lo, int order,
              double* C, int64_t ldc, void* stream);
+
+/* ozk_gemm on INT8 planes (ozk_extract_f32_i8 with the same rho): INT8 MFMA
+ * with exact INT32 sums; each pair product is the integer sum times
+ * 2^(2 rho - 48), the FP32 product of the BF16 path whenever that one is
+ * exact.  On-device preset schedules (4,1) and (3,1). */
+int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
+                const int8_t* b_slices, const int32_t* b_exps,
+                int64_t N, int64_t M, int64_t K, int rho,
+                int n_hi, int n_lo, int order,
+                double* C, int64_t ldc, void* stream);
 
 /* Test hook: the per-pair FP32 products P[p] = S^A_a(p) . S^B_b(p) written
  * to P[p][N][ldp] in schedule order (matmul.py:216-233, :757-773, :885-887). */
@@ -112,6 +135,12 @@ int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
                        int64_t N, int64_t M, int64_t K,
                        int pipeline, int n_hi, int n_lo,
                        float* P, int64_t ldp, void* stream);
+
+/* Test hook: ozk_slice_products on INT8 planes. */
+int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
+                          int64_t N, int64_t M, int64_t K, int rho,
+                          int n_hi, int n_lo, float* P, int64_t ldp,
+                          void* stream);
 
 /* ---- drivers --------------------------------------------------------- */
 /* matmul(A, B, pipeline, accumulation, precision) after preflight:
@@ -155,10 +184,11 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
 int ozk_check_finite(const double* X, int64_t rows, int64_t cols, int64_t ld,
                      uint32_t* flags, void* stream);
 
-/* Test hook: runs one 32x32x16 and one 16x16x32 BF16 MFMA on a fixed
- * pattern and writes their accumulator registers as int32: out[0..1023] =
- * 64 lanes x 16 registers (32x32x16), out[1024..1279] = 64 lanes x 4
- * registers (16x16x32).  out must hold 1280 int32. */
+/* Test hook: runs one 32x32x16 and one 16x16x32 BF16 MFMA and one
+ * 16x16x64 INT8 MFMA on fixed patterns and writes their accumulator
+ * registers as int32: out[0..1023] = 64 lanes x 16 registers (32x32x16),
+ * out[1024..1279] and out[1280..1535] = 64 lanes x 4 registers (16x16x32,
+ * 16x16x64).  out must hold 1536 int32. */
 int ozk_probe_mfma_layout(int32_t* out, void* stream);
 
 #ifdef __cplusplus

@@ -45,12 +45,19 @@ SIGNATURES = {
     "ozk_extract_f32": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                  _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
                                  _c_size, _c_vp]),
+    "ozk_extract_f32_i8": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                    _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                    _c_size, _c_vp]),
     "ozk_extract_f64": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                  _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_size,
                                  _c_vp]),
     "ozk_pair_count": (_c_int, [_c_int, _c_int, _c_int]),
     "ozk_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                           _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
+    "ozk_gemm_i8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                             _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
+    "ozk_slice_products_i8": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
+                                       _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_slice_products": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                     _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_matmul_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int,

@@ -23,19 +23,20 @@ void clear_error() { g_error.clear(); }
 // Implemented in extract.hip / gemm.hip.
 template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
-            int by_cols, int rho, int n0, int n1, uint16_t* S, int32_t* E,
-            uint32_t* flags, void* ws, size_t wsb, hipStream_t st);
+            int by_cols, int rho, int n0, int n1, void* S, int32_t* E,
+            uint32_t* flags, void* ws, size_t wsb, hipStream_t st, bool i8);
 size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols);
 int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
 int launch_check_finite(const double* X, int64_t rows, int64_t cols,
                         int64_t ld, uint32_t* flags, hipStream_t st);
-int launch_gemm(const uint16_t* As, const int32_t* Ae, const uint16_t* Bs,
+bool allpairs_supported(int pipe, int nhi, int nlo);
+int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
-                hipStream_t st, bool allow_allpairs);
-int launch_products(const uint16_t* As, const uint16_t* Bs, int64_t N,
-                    int64_t M, int64_t K, int pipe, int nhi, int nlo, float* P,
-                    int64_t ldp, hipStream_t st);
+                hipStream_t st, bool i8, int rho);
+int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
+                    int64_t K, int pipe, int nhi, int nlo, float* P,
+                    int64_t ldp, hipStream_t st, bool i8, int rho);
 int launch_probe_mfma(int32_t* out, hipStream_t st);
 
 constexpr int kMaxSlices = 32;
@@ -65,16 +66,24 @@ struct Carver {
 };
 
 struct SliceSet {
-  uint16_t* s;
+  void* s;
   int32_t* e;
 };
 
-static SliceSet carve_slices(Carver& c, int planes, int64_t lines, int64_t len) {
+static SliceSet carve_slices(Carver& c, int planes, int64_t lines, int64_t len,
+                             size_t elem_bytes) {
   const int64_t lp = round_up(lines, kLinePad), ld = round_up(len, kKPad);
   SliceSet r;
-  r.s = (uint16_t*)c.take((size_t)planes * lp * ld * sizeof(uint16_t));
+  r.s = c.take((size_t)planes * lp * ld * elem_bytes);
   r.e = (int32_t*)c.take((size_t)planes * lp * sizeof(int32_t));
   return r;
+}
+
+// The drivers use INT8 slice planes (exact for rho >= 19, i.e. K > 4096)
+// whenever the schedule has an all-pairs kernel, BF16 planes otherwise.
+static bool use_i8(int pipe, int64_t contraction, int nhi, int nlo) {
+  return pipe == OZK_PIPE_ONDEVICE && rho_generic(contraction, 24) >= 19 &&
+         allpairs_supported(pipe, nhi, nlo);
 }
 
 static int check_counts(int pipe, int nhi, int nlo) {
@@ -186,7 +195,29 @@ int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
   OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
   return extract<float>(X, rows, cols, ldx, by_cols, rho, n_hi, n_lo, slices,
                         exps, flags, workspace, workspace_bytes,
-                        (hipStream_t)stream);
+                        (hipStream_t)stream, false);
+}
+
+int ozk_extract_f32_i8(const double* X, int64_t rows, int64_t cols,
+                       int64_t ldx, int by_cols, int rho, int n_hi, int n_lo,
+                       int8_t* slices, int32_t* exps, uint32_t* flags,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
+  OZK_CHECK_ARG(ldx >= cols || rows <= 1, "ldx=%lld < cols=%lld", (long long)ldx,
+                (long long)cols);
+  OZK_CHECK_ARG(n_hi >= 1 && n_hi <= kMaxSlices && n_lo >= 0 && n_lo <= kMaxSlices,
+                "slice counts (%d, %d) outside [1, %d] x [0, %d]", n_hi, n_lo,
+                kMaxSlices, kMaxSlices);
+  if (rho < 19) {
+    set_error("int8 slice planes need rho >= 19 (got %d)", rho);
+    return OZK_ERR_UNSUPPORTED;
+  }
+  if (rows == 0 || cols == 0) return OZK_OK;
+  OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
+  return extract<float>(X, rows, cols, ldx, by_cols, rho, n_hi, n_lo, slices,
+                        exps, flags, workspace, workspace_bytes,
+                        (hipStream_t)stream, true);
 }
 
 int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
@@ -202,7 +233,7 @@ int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
   OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
   return extract<double>(X, rows, cols, ldx, by_cols, rho, n_slices, 0, slices,
                          exps, flags, workspace, workspace_bytes,
-                         (hipStream_t)stream);
+                         (hipStream_t)stream, false);
 }
 
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
@@ -218,7 +249,29 @@ int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
   OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
   if (N == 0 || M == 0) return OZK_OK;
   return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K, pipeline,
-                     n_hi, n_lo, order, C, ldc, (hipStream_t)stream, true);
+                     n_hi, n_lo, order, C, ldc, (hipStream_t)stream, false, 0);
+}
+
+int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
+                const int8_t* b_slices, const int32_t* b_exps, int64_t N,
+                int64_t M, int64_t K, int rho, int n_hi, int n_lo, int order,
+                double* C, int64_t ldc, void* stream) {
+  clear_error();
+  int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
+  if (rc) return rc;
+  if ((rc = check_order(order))) return rc;
+  OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape N=%lld M=%lld K=%lld",
+                (long long)N, (long long)M, (long long)K);
+  OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
+  if (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
+    set_error("int8 planes need rho >= 19 and a preset schedule (rho=%d, (%d, %d))",
+              rho, n_hi, n_lo);
+    return OZK_ERR_UNSUPPORTED;
+  }
+  if (N == 0 || M == 0) return OZK_OK;
+  return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K,
+                     OZK_PIPE_ONDEVICE, n_hi, n_lo, order, C, ldc,
+                     (hipStream_t)stream, true, rho);
 }
 
 int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
@@ -231,16 +284,34 @@ int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
   OZK_CHECK_ARG(ldp >= M, "ldp < M");
   if (N == 0 || M == 0) return OZK_OK;
   return launch_products(a_slices, b_slices, N, M, K, pipeline, n_hi, n_lo, P,
-                         ldp, (hipStream_t)stream);
+                         ldp, (hipStream_t)stream, false, 0);
+}
+
+int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
+                          int64_t N, int64_t M, int64_t K, int rho, int n_hi,
+                          int n_lo, float* P, int64_t ldp, void* stream) {
+  clear_error();
+  int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
+  if (rc) return rc;
+  OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape");
+  OZK_CHECK_ARG(ldp >= M, "ldp < M");
+  if (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
+    set_error("int8 planes need rho >= 19 and a preset schedule");
+    return OZK_ERR_UNSUPPORTED;
+  }
+  if (N == 0 || M == 0) return OZK_OK;
+  return launch_products(a_slices, b_slices, N, M, K, OZK_PIPE_ONDEVICE, n_hi,
+                         n_lo, P, ldp, (hipStream_t)stream, true, rho);
 }
 
 static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
                         int nlo, bool carve, void* ws, SliceSet* a,
                         SliceSet* b, void** tws) {
   const int planes = pipeline == OZK_PIPE_ONDEVICE ? nhi + nlo : nhi;
+  const size_t eb = use_i8(pipeline, K, nhi, nlo) ? 1 : 2;
   Carver c(carve ? ws : nullptr);
-  SliceSet sa = carve_slices(c, planes, N, K);
-  SliceSet sb = carve_slices(c, planes, M, K);
+  SliceSet sa = carve_slices(c, planes, N, K, eb);
+  SliceSet sb = carve_slices(c, planes, M, K, eb);
   void* t = c.take(extract_workspace_bytes(K, M, 1));
   if (a) *a = sa;
   if (b) *b = sb;
@@ -281,31 +352,34 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   void* tws;
   matmul_ws(N, K, M, pipeline, n_hi, n_lo, true, workspace, &sa, &sb, &tws);
   const size_t tbytes = extract_workspace_bytes(K, M, 1);
+  const bool i8 = use_i8(pipeline, K, n_hi, n_lo);
+  int rho;
   if (pipeline == OZK_PIPE_ONDEVICE) {
-    const int rho = rho_generic(K, 24);
+    rho = rho_generic(K, 24);
     if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                             nullptr, 0, st)))
+                             nullptr, 0, st, i8)))
       return rc;
     if ((rc = extract<float>(B, K, M, ldb, 1, rho, n_hi, n_lo, sb.s, sb.e, flags,
-                             tws, tbytes, st)))
+                             tws, tbytes, st, i8)))
       return rc;
   } else {
-    const int rho = rho_generic(K, 53);
+    rho = rho_generic(K, 53);
     if ((rc = extract<double>(A, N, K, lda, 0, rho, n_hi, 0, sa.s, sa.e, flags,
-                              nullptr, 0, st)))
+                              nullptr, 0, st, false)))
       return rc;
     if ((rc = extract<double>(B, K, M, ldb, 1, rho, n_hi, 0, sb.s, sb.e, flags,
-                              tws, tbytes, st)))
+                              tws, tbytes, st, false)))
       return rc;
   }
   return launch_gemm(sa.s, sa.e, sb.s, sb.e, N, M, K, pipeline, n_hi, n_lo,
-                     order, C, ldc, st, true);
+                     order, C, ldc, st, i8, rho);
 }
 
 static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,
                       SliceSet* s, void** tws) {
   Carver c(ws);
-  SliceSet ss = carve_slices(c, nhi + nlo, cols, rows);
+  SliceSet ss = carve_slices(c, nhi + nlo, cols, rows,
+                             use_i8(OZK_PIPE_ONDEVICE, rows, nhi, nlo) ? 1 : 2);
   void* t = c.take(extract_workspace_bytes(rows, cols, 1));
   if (s) *s = ss;
   if (tws) *tws = t;
@@ -343,11 +417,13 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
   // Row extraction of A^T == column extraction of A: one set of slices is
   // both operands (gram.py:22-35 extracts the same values twice).
   const int rho = rho_generic(rows, 24);
+  const bool i8 = use_i8(OZK_PIPE_ONDEVICE, rows, n_hi, n_lo);
   if ((rc = extract<float>(A, rows, cols, lda, 1, rho, n_hi, n_lo, s.s, s.e,
-                           flags, tws, extract_workspace_bytes(rows, cols, 1), st)))
+                           flags, tws, extract_workspace_bytes(rows, cols, 1), st,
+                           i8)))
     return rc;
   if ((rc = launch_gemm(s.s, s.e, s.s, s.e, cols, cols, rows, OZK_PIPE_ONDEVICE,
-                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, st, true)))
+                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, st, i8, rho)))
     return rc;
   hipLaunchKernelGGL(symmetrize_kernel, dim3(grid_for(cols * cols)), dim3(256),
                      0, st, G, cols, ldg);
@@ -359,8 +435,9 @@ static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
                           int nlo, void* ws, SliceSet* a, SliceSet* x,
                           double** y, void** tws) {
   Carver c(ws);
-  SliceSet sa = carve_slices(c, nhi + nlo, N, K);
-  SliceSet sx = carve_slices(c, nhi + nlo, ncols, K);
+  const size_t eb = use_i8(OZK_PIPE_ONDEVICE, K, nhi, nlo) ? 1 : 2;
+  SliceSet sa = carve_slices(c, nhi + nlo, N, K, eb);
+  SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
   double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
   void* t = c.take(extract_workspace_bytes(K, ncols, 1));
   if (a) *a = sa;
@@ -403,14 +480,16 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   void* tws;
   residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws);
   const int rho = rho_generic(K, 24);
+  const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
   if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                           nullptr, 0, st)))
+                           nullptr, 0, st, i8)))
     return rc;
   if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,
-                           flags, tws, extract_workspace_bytes(K, ncols, 1), st)))
+                           flags, tws, extract_workspace_bytes(K, ncols, 1), st,
+                           i8)))
     return rc;
   if ((rc = launch_gemm(sa.s, sa.e, sx.s, sx.e, N, ncols, K, OZK_PIPE_ONDEVICE,
-                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, st, true)))
+                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, st, i8, rho)))
     return rc;
   hipLaunchKernelGGL(sub_from_kernel, dim3(grid_for(N * ncols)), dim3(256), 0,
                      st, b, ldb, y, ncols, r, ldr, N, ncols);

@@ -256,33 +256,60 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 //
 // The all-pairs kernel uses 8 waves (2 per SIMD).  Wave w owns rows
 // 32 * (w >> 2) .. +31 and columns 16 * (w & 3) .. +15 of the 64x64 tile as
-// two v_mfma_f32_16x16x32_bf16 blocks, so a pair costs 8 accumulator VGPRs
-// and the 24 pairs of precision="high" fit in the 256 AGPRs with the
-// operand registers in the remaining VGPRs.
+// two 16x16 MFMA blocks, so a pair costs 8 accumulator registers and the 24
+// pairs of precision="high" fit with the operand registers in 256.
 //
-// LDS stage (64 k): one 1 KiB fragment per (slot, 32-wide k half, 16-line
-// group): lane l of the fragment holds line l % 16, k chunk l / 16 (8 BF16).
-// Wave w moves fragments w, w + 8, ...: lane l's 16 bytes go from global
-// memory straight to fragment * 1 KiB + l * 16, so the LDS writes and the
-// MFMA operand reads are both linear in the lane index.
+// Operands come in one of two plane formats, each 64 bytes of a line per
+// MFMA k-step:
+//   BF16  v_mfma_f32_16x16x32_bf16, FP32 accumulators.
+//   I8    v_mfma_i32_16x16x64_i8 on q = slice * 2^(24 - rho) (rho >= 19:
+//         |q| <= 64), INT32 accumulators; the product is the integer sum
+//         scaled by 2^(2 rho - 48), i.e. the same FP32 value as the BF16
+//         product whenever that one is exact (partial sums < 2^24 units).
+//
+// LDS: a ring of kRing stage buffers, one 64-byte k-step each; fragment
+// (slot, 16-line group lg) holds line lg * 16 + l % 16, bytes 16 (l / 16) ..
+// +15 in lane l's 16 bytes.  Wave w fetches the fragments w, w + 8, ... of a
+// stage with direct global->LDS loads (lane l's bytes land at fragment * 1 KiB
+// + 16 l), kRing - 1 stages ahead of the MFMAs; LDS writes and MFMA operand
+// reads are both linear in the lane index.
 
 constexpr int kThreads16 = 512;
+constexpr int kRing = 4;       // stage buffers (kRing - 1 stages in flight)
+constexpr int kStageB = 64;    // bytes of a line per stage
 
-// Stages of kBK16 = 64 k: fragment (slot, k-half kh, 16-line group lg).
-constexpr int kBK16 = 64;
+typedef int int32x4 __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ int frag16(int slot, int kh, int lg, int lane) {
-  return ((slot * 2 + kh) * 4 + lg) * 64 + lane;
-}
+struct OpBf16 {
+  typedef floatx4 acc_t;
+  static constexpr int kElemBytes = 2;
+  static __device__ __forceinline__ acc_t mma(uint4 a, uint4 b, acc_t c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(
+        __builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float product(float x, float) { return x; }
+};
+
+struct OpI8 {
+  typedef int32x4 acc_t;
+  static constexpr int kElemBytes = 1;
+  static __device__ __forceinline__ acc_t mma(uint4 a, uint4 b, acc_t c) {
+    return __builtin_amdgcn_mfma_i32_16x16x64_i8(
+        __builtin_bit_cast(int32x4, a), __builtin_bit_cast(int32x4, b), c, 0, 0, 0);
+  }
+  static __device__ __forceinline__ float product(int x, float unit2) {
+    return (float)x * unit2;
+  }
+};
 
 // One 16-byte-per-lane direct load from global memory into LDS
 // (global_load_lds_dwordx4): lane l's 16 bytes land at LDS offset
 // `lds_addr` + 16 l.  `lds_addr` and `gbase` are wave-uniform; `voff` is the
 // lane's byte offset from `gbase`.  Written as inline assembly so that the
 // compiler does not order the K loop's LDS reads behind these loads: the
-// kernel waits for them itself (wait_dma) before the barrier that publishes
-// the stage.  M0 carries the LDS address; nothing else in these kernels
-// uses M0.
+// kernel waits for them itself (wait_vm) before the barrier that publishes
+// a stage.  M0 carries the LDS address; nothing else in these kernels uses
+// M0.
 __device__ __forceinline__ void dma16(uint32_t lds_addr, const void* gbase,
                                       uint32_t voff) {
   asm volatile(
@@ -294,163 +321,197 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, const void* gbase,
       : "memory");
 }
 
-__device__ __forceinline__ void wait_dma() {
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+// Wait until at most N of this wave's vector-memory loads are outstanding.
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
 }
 
-// One K stage straight from global memory into LDS: wave w moves fragment
-// (slot i, k-half (w >> 2) & 1, line group w & 3) of every slot i.  All
-// addresses are inside the zero-padded slice planes.
-template <int NA, int NB>
-__device__ __forceinline__ void stage16_dma(const uint16_t* As, int64_t aplane,
-                                            const uint16_t* Bs, int64_t bplane,
-                                            int64_t ld, int64_t k0,
-                                            uint32_t buf_lds, int wave,
-                                            uint32_t lane_bytes) {
-  const int kh = (wave >> 2) & 1, lg = wave & 3;
-  const int64_t wave_off = (int64_t)(lg * 16) * ld + 32 * kh + k0;
+// Fetch stage `st` (bytes st * 64 .. +63 of every line of the tile) into the
+// LDS buffer at byte offset `buf_lds`: wave w moves fragments F = w + 8 i,
+// i.e. slot 2 i + (w >> 2), line group w & 3.  All addresses lie inside the
+// zero-padded slice planes.
+template <int NT>
+__device__ __forceinline__ void stage_dma(const char* At, int64_t aplane,
+                                          const char* Bt, int64_t bplane,
+                                          int64_t ldb, int64_t st,
+                                          uint32_t buf_lds, int wave,
+                                          uint32_t lane_bytes) {
+  const int64_t wave_off = (int64_t)((wave & 3) * 16) * ldb + st * kStageB;
 #pragma unroll
-  for (int i = 0; i < NA + NB; ++i) {
-    const uint16_t* base = i < NA ? As + i * aplane : Bs + (i - NA) * bplane;
-    const int F = i * 8 + wave;
+  for (int i = 0; i < NT; ++i) {
+    const int slot = 2 * i + (wave >> 2);
+    const char* base = slot < NT ? At + slot * aplane : Bt + (slot - NT) * bplane;
+    const int F = 8 * i + wave;
     dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024),
           (const void*)(base + wave_off), lane_bytes);
   }
 }
 
-template <int PIPE, int NHI, int NLO, int NT, int NP>
-struct AllPairsMMA16 {
-  floatx4 acc[NP][2];
+template <class Op, int PIPE, int NHI, int NLO, int NT, int NP>
+struct AllPairsMMA {
+  typename Op::acc_t acc[NP][2];
   int lane, wr, wc;
 
   // MFMAs of one (A slot, row block) for every pair of that A slot.
   template <int SA, int H>
-  __device__ __forceinline__ void block(const bf16x8& af, const bf16x8 (&bf)[NT]) {
+  __device__ __forceinline__ void block(uint4 af, const uint4 (&bf)[NT]) {
 #pragma unroll
     for (int p = 0; p < NP; ++p) {
       const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-      if (q.a == SA)
-        acc[p][H] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(af, bf[q.b], acc[p][H], 0, 0, 0);
+      if (q.a == SA) acc[p][H] = Op::mma(af, bf[q.b], acc[p][H]);
     }
   }
 
-  // The NT * 2 blocks of one 32-wide k half, A fragments software-pipelined
-  // through kDepth + 1 registers: the read of block j + kDepth is issued
-  // before the MFMAs of block j, so each read has kDepth blocks of MFMAs to
-  // land.  Scheduling barriers keep the compiler from moving reads back.
+  // The NT * 2 blocks of a stage, A fragments software-pipelined through
+  // kDepth + 1 registers: the read of block j + kDepth is issued before the
+  // MFMAs of block j.  Scheduling barriers keep the reads where they are.
   static constexpr int kBlocks = NT * 2, kDepth = 3;
 
-  __device__ __forceinline__ bf16x8 read_a(const uint4* buf, int kh, int j) const {
-    return as_bf16x8(buf[frag16(j >> 1, kh, 2 * wr + (j & 1), lane)]);
+  __device__ __forceinline__ uint4 read_a(const uint4* buf, int j) const {
+    return buf[((j >> 1) * 4 + 2 * wr + (j & 1)) * 64 + lane];
   }
 
   template <int J>
-  __device__ __forceinline__ void pipe_step(const uint4* buf, int kh,
-                                            bf16x8 (&af)[kDepth + 1],
-                                            const bf16x8 (&bf)[NT]) {
+  __device__ __forceinline__ void pipe_step(const uint4* buf,
+                                            uint4 (&af)[kDepth + 1],
+                                            const uint4 (&bf)[NT]) {
     if constexpr (J < kBlocks) {
-      if constexpr (J + kDepth < kBlocks) af[(J + kDepth) % (kDepth + 1)] = read_a(buf, kh, J + kDepth);
+      if constexpr (J + kDepth < kBlocks)
+        af[(J + kDepth) % (kDepth + 1)] = read_a(buf, J + kDepth);
       block<J / 2, J % 2>(af[J % (kDepth + 1)], bf);
       __builtin_amdgcn_sched_barrier(0);
-      pipe_step<J + 1>(buf, kh, af, bf);
+      pipe_step<J + 1>(buf, af, bf);
     }
   }
 
   __device__ __forceinline__ void operator()(const uint4* buf) {
+    uint4 bf[NT];
 #pragma unroll
-    for (int kh = 0; kh < 2; ++kh) {
-      bf16x8 bf[NT];
+    for (int s = 0; s < NT; ++s) bf[s] = buf[((NT + s) * 4 + wc) * 64 + lane];
+    uint4 af[kDepth + 1];
 #pragma unroll
-      for (int s = 0; s < NT; ++s) bf[s] = as_bf16x8(buf[frag16(NT + s, kh, wc, lane)]);
-      bf16x8 af[kDepth + 1];
-#pragma unroll
-      for (int j = 0; j < kDepth; ++j) af[j] = read_a(buf, kh, j);
-      __builtin_amdgcn_sched_barrier(0);
-      pipe_step<0>(buf, kh, af, bf);
-    }
+    for (int j = 0; j < kDepth; ++j) af[j] = read_a(buf, j);
+    __builtin_amdgcn_sched_barrier(0);
+    pipe_step<0>(buf, af, bf);
   }
 };
 
+// vmcnt wait before consuming stage s: the loads of the `later` stages
+// already issued after it (each NT instructions per wave) may stay in flight.
+template <int NT>
+__device__ __forceinline__ void wait_stage(int64_t later) {
+  if (later >= 2) wait_vm<2 * NT>();
+  else if (later == 1) wait_vm<NT>();
+  else wait_vm<0>();
+}
+
 // All pairs of the schedule in one K sweep (schedules whose accumulators fit
-// in the AGPRs).  PIPE/NHI/NLO fix the schedule at compile time.
-template <int PIPE, int NHI, int NLO, int ORDER>
+// in registers).  PIPE/NHI/NLO fix the schedule at compile time.  ORDER < 0
+// writes the per-pair FP32 products P[p][row][col] instead of C (test hook).
+// `unit2` is the product scale 2^(2 rho - 48) of the I8 format.
+constexpr int kOrderProducts = -1;
+
+template <class Op, int PIPE, int NHI, int NLO, int ORDER>
 __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
-    const uint16_t* __restrict__ As, const int32_t* __restrict__ Ae,
-    const uint16_t* __restrict__ Bs, const int32_t* __restrict__ Be,
+    const char* __restrict__ As, const int32_t* __restrict__ Ae,
+    const char* __restrict__ Bs, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t ld, int64_t a_lines, int64_t b_lines,
-    double* __restrict__ C, int64_t ldc) {
+    float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
+    int64_t ldp) {
   constexpr int NT = PIPE == OZK_PIPE_ONDEVICE ? NHI + NLO : NHI;
   constexpr int NP = pair_count(PIPE, NHI, NLO);
   constexpr int NBLK = PIPE == OZK_PIPE_ONDEVICE ? 3 : 1;
-  constexpr int kBuf = (NT + NT) * 8 * 64;  // uint4 per stage buffer
-  // Two stage buffers (NT = 5: 2 x 80 KiB, the whole LDS of a gfx950 CU).
-  __shared__ uint4 lds[2 * kBuf];
+  constexpr int kBuf = (NT + NT) * 4 * 64;  // uint4 per stage buffer
+  static_assert(kRing == 4, "wait_stage assumes 4 stage buffers");
+  // NT = 5: 4 x 40 KiB, the whole 160 KiB LDS of a gfx950 CU.
+  __shared__ uint4 lds[kRing * kBuf];
 
   const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
   int tm, tn;
   tile_coords(blockIdx.x, ntm, ntn, tm, tn);
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
-  const int64_t aplane = a_lines * ld, bplane = b_lines * ld;
-  const uint16_t* At = As + row0 * ld;
-  const uint16_t* Bt = Bs + col0 * ld;
+  const int64_t ldb = ld * Op::kElemBytes;  // bytes per line
+  const int64_t aplane = a_lines * ldb, bplane = b_lines * ldb;
+  const char* At = As + row0 * ldb;
+  const char* Bt = Bs + col0 * ldb;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  AllPairsMMA16<PIPE, NHI, NLO, NT, NP> mma;
+  AllPairsMMA<Op, PIPE, NHI, NLO, NT, NP> mma;
   mma.lane = lane;
   mma.wr = wave >> 2;
   mma.wc = wave & 3;
 #pragma unroll
   for (int p = 0; p < NP; ++p) {
-    mma.acc[p][0] = floatx4{};
-    mma.acc[p][1] = floatx4{};
+    mma.acc[p][0] = typename Op::acc_t{};
+    mma.acc[p][1] = typename Op::acc_t{};
   }
 
-  // Per stage: wait for this wave's loads of stage s, barrier (stage s is
-  // complete in LDS and every wave is done with the other buffer), fetch
-  // stage s + 1 into the other buffer, run the MFMAs of stage s.
-  const int64_t nst = ld / kBK16;
-  const uint32_t lane_bytes = (uint32_t)(((lane & 15) * ld + 8 * (lane >> 4)) * 2);
+  // Per stage s: wait for this wave's loads of stage s, barrier (stage s is
+  // complete in LDS and every wave has finished stage s - 1, whose buffer is
+  // refilled next), fetch stage s + kRing - 1, run the MFMAs of stage s.
+  const int64_t nst = ldb / kStageB;
+  const uint32_t lane_bytes = (uint32_t)((lane & 15) * ldb + 16 * (lane >> 4));
   const uint32_t lds0 = lds_offset(lds);
-  stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, 0, lds0, wave, lane_bytes);
+  for (int i = 0; i < kRing - 1; ++i)
+    if (i < nst)
+      stage_dma<NT>(At, aplane, Bt, bplane, ldb, i, lds0 + i * kBuf * 16, wave, lane_bytes);
   for (int64_t s = 0; s < nst; ++s) {
-    wait_dma();
+    const int64_t later = nst - 1 - s;
+    wait_stage<NT>(later < kRing - 2 ? later : kRing - 2);
     __syncthreads();
-    if (s + 1 < nst)
-      stage16_dma<NT, NT>(At, aplane, Bt, bplane, ld, (s + 1) * kBK16,
-                          lds0 + (uint32_t)(((s + 1) & 1) * kBuf * 16), wave,
-                          lane_bytes);
-    mma(lds + (s & 1) * kBuf);
+    const int64_t fetch = s + kRing - 1;
+    if (fetch < nst)
+      stage_dma<NT>(At, aplane, Bt, bplane, ldb, fetch,
+                    lds0 + (uint32_t)((fetch % kRing) * kBuf * 16), wave, lane_bytes);
+    mma(lds + (s % kRing) * kBuf);
   }
 
-  // Fold in schedule order and store.  Accumulator register r of lane l of a
-  // 16x16 block holds row 4 * (l / 16) + r, column l % 16.
+  // Accumulator register r of lane l of a 16x16 block holds row
+  // 4 * (l / 16) + r, column l % 16.
   const int64_t col = col0 + 16 * mma.wc + (lane & 15);
-  int eb[NT];
+  if constexpr (ORDER == kOrderProducts) {
 #pragma unroll
-  for (int s = 0; s < NT; ++s) eb[s] = Be[s * b_lines + col];
+    for (int h = 0; h < 2; ++h) {
 #pragma unroll
-  for (int h = 0; h < 2; ++h) {
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
+        if (row < N && col < M) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
-      int ea[NT];
-#pragma unroll
-      for (int s = 0; s < NT; ++s) ea[s] = Ae[s * a_lines + row];
-      typename FoldOf<ORDER>::type f;
-      f.init();
-#pragma unroll
-      for (int p = 0; p < NP; ++p) {
-        const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-        f.pair(q, mma.acc[p][h][r], ldexpf(1.0f, eb[q.b]), ldexpf(1.0f, ea[q.a]),
-               ldexp(1.0, eb[q.b]), ldexp(1.0, ea[q.a]));
+          for (int p = 0; p < NP; ++p)
+            P[((int64_t)p * N + row) * ldp + col] = Op::product(mma.acc[p][h][r], unit2);
+        }
       }
-      const double out = f.finish(NBLK);
-      if (row < N && col < M) C[row * ldc + col] = out;
+    }
+  } else {
+    // Fold in schedule order and store.
+    int eb[NT];
+#pragma unroll
+    for (int s = 0; s < NT; ++s) eb[s] = Be[s * b_lines + col];
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
+        int ea[NT];
+#pragma unroll
+        for (int s = 0; s < NT; ++s) ea[s] = Ae[s * a_lines + row];
+        typename FoldOf<ORDER>::type f;
+        f.init();
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const PairInfo q = pair_info(PIPE, NHI, NLO, p);
+          f.pair(q, Op::product(mma.acc[p][h][r], unit2), ldexpf(1.0f, eb[q.b]),
+                 ldexpf(1.0f, ea[q.a]), ldexp(1.0, eb[q.b]), ldexp(1.0, ea[q.a]));
+        }
+        const double out = f.finish(NBLK);
+        if (row < N && col < M) C[row * ldc + col] = out;
+      }
     }
   }
 }
@@ -567,48 +628,102 @@ __global__ void probe_mfma16_kernel(int32_t* out) {
 
 // ---------------------------------------------------------------- launch
 
-// Compile-time instantiations of the all-pairs kernel.
-template <int PIPE, int NHI, int NLO>
-static bool try_allpairs(int pipe, int nhi, int nlo, int order, dim3 grid,
-                         hipStream_t st, const uint16_t* As, const int32_t* Ae,
-                         const uint16_t* Bs, const int32_t* Be, int64_t N,
-                         int64_t M, int64_t ld, int64_t al, int64_t bl,
-                         double* C, int64_t ldc) {
-  if (pipe != PIPE || nhi != NHI || (PIPE == OZK_PIPE_ONDEVICE && nlo != NLO))
-    return false;
-#define OZK_AP(O)                                                         \
-  hipLaunchKernelGGL((gemm_allpairs<PIPE, NHI, NLO, O>), grid,            \
-                     dim3(kThreads16), 0, st, As, Ae, Bs, Be, N, M, ld,   \
-                     al, bl, C, ldc)
-  switch (order) {
-    case OZK_ORDER_2SUM: OZK_AP(OZK_ORDER_2SUM); break;
-    case OZK_ORDER_BLOCK64: OZK_AP(OZK_ORDER_BLOCK64); break;
-    case OZK_ORDER_HOST_JAX: OZK_AP(OZK_ORDER_HOST_JAX); break;
-    default: OZK_AP(OZK_ORDER_HOST_NP); break;
-  }
-#undef OZK_AP
-  return true;
+// Schedules with an all-pairs instantiation (accumulators fit in registers).
+static bool allpairs_schedule(int pipe, int nhi, int nlo) {
+  return pipe == OZK_PIPE_ONDEVICE && ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1));
 }
 
-int launch_gemm(const uint16_t* As, const int32_t* Ae, const uint16_t* Bs,
-                const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
-                int nhi, int nlo, int order, double* C, int64_t ldc,
-                hipStream_t st, bool allow_allpairs) {
+bool allpairs_supported(int pipe, int nhi, int nlo) {
+  return allpairs_schedule(pipe, nhi, nlo);
+}
+
+template <class Op, int NHI, int NLO, int ORDER>
+static void launch_ap(dim3 grid, hipStream_t st, const void* As,
+                      const int32_t* Ae, const void* Bs, const int32_t* Be,
+                      int64_t N, int64_t M, int64_t ld, int64_t al, int64_t bl,
+                      float unit2, double* C, int64_t ldc, float* P,
+                      int64_t ldp) {
+  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER>),
+                     grid, dim3(kThreads16), 0, st, (const char*)As, Ae,
+                     (const char*)Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P,
+                     ldp);
+}
+
+template <class Op, int NHI, int NLO>
+static void launch_ap_order(int order, dim3 grid, hipStream_t st,
+                            const void* As, const int32_t* Ae, const void* Bs,
+                            const int32_t* Be, int64_t N, int64_t M,
+                            int64_t ld, int64_t al, int64_t bl, float unit2,
+                            double* C, int64_t ldc, float* P, int64_t ldp) {
+  switch (order) {
+    case OZK_ORDER_2SUM:
+      launch_ap<Op, NHI, NLO, OZK_ORDER_2SUM>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      break;
+    case OZK_ORDER_BLOCK64:
+      launch_ap<Op, NHI, NLO, OZK_ORDER_BLOCK64>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      break;
+    case OZK_ORDER_HOST_JAX:
+      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      break;
+    case OZK_ORDER_HOST_NP:
+      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_NP>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      break;
+    default:
+      launch_ap<Op, NHI, NLO, kOrderProducts>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      break;
+  }
+}
+
+// All-pairs launch for a preset schedule; `i8` selects the INT8 plane
+// format (rho >= 19).  order = kOrderProducts writes P.
+static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
+                           const void* Bs, const int32_t* Be, int64_t N,
+                           int64_t M, int64_t K, int rho, int nhi, int nlo,
+                           int order, double* C, int64_t ldc, float* P,
+                           int64_t ldp, hipStream_t st) {
   const int64_t ld = round_up(K, kKPad);
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
   const int64_t ntiles = (al / kBM) * (bl / kBN);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
   const dim3 grid((unsigned)ntiles);
-  if (allow_allpairs) {
-    if (try_allpairs<OZK_PIPE_ONDEVICE, 4, 1>(pipe, nhi, nlo, order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, C, ldc) ||
-        try_allpairs<OZK_PIPE_ONDEVICE, 3, 1>(pipe, nhi, nlo, order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, C, ldc)) {
-      OZK_LAUNCH_CHECK();
-      return OZK_OK;
-    }
+  const float unit2 = ldexpf(1.0f, 2 * rho - 48);
+#define OZK_AP_ALL(Op)                                                              \
+  do {                                                                              \
+    if (nhi == 4)                                                                   \
+      launch_ap_order<Op, 4, 1>(order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, \
+                                unit2, C, ldc, P, ldp);                             \
+    else                                                                            \
+      launch_ap_order<Op, 3, 1>(order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, \
+                                unit2, C, ldc, P, ldp);                             \
+  } while (0)
+  if (i8) OZK_AP_ALL(OpI8);
+  else OZK_AP_ALL(OpBf16);
+#undef OZK_AP_ALL
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
+                const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
+                int nhi, int nlo, int order, double* C, int64_t ldc,
+                hipStream_t st, bool i8, int rho) {
+  if (allpairs_schedule(pipe, nhi, nlo))
+    return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, order,
+                           C, ldc, nullptr, 0, st);
+  if (i8) {
+    set_error("int8 slice planes need a preset on-device schedule");
+    return OZK_ERR_UNSUPPORTED;
   }
+  const int64_t ld = round_up(K, kKPad);
+  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
+  const int64_t ntiles = (al / kBM) * (bl / kBN);
+  OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
+  const dim3 grid((unsigned)ntiles);
+  const uint16_t* A16 = (const uint16_t*)As;
+  const uint16_t* B16 = (const uint16_t*)Bs;
 #define OZK_PW(O)                                                              \
-  hipLaunchKernelGGL((gemm_pairwise<O, 0>), grid, dim3(kThreads), 0, st, As,   \
-                     Ae, Bs, Be, N, M, ld, al, bl, pipe, nhi, nlo, C, ldc,     \
+  hipLaunchKernelGGL((gemm_pairwise<O, 0>), grid, dim3(kThreads), 0, st, A16,  \
+                     Ae, B16, Be, N, M, ld, al, bl, pipe, nhi, nlo, C, ldc,    \
                      (float*)nullptr, (int64_t)0)
   switch (order) {
     case OZK_ORDER_2SUM: OZK_PW(OZK_ORDER_2SUM); break;
@@ -621,25 +736,53 @@ int launch_gemm(const uint16_t* As, const int32_t* Ae, const uint16_t* Bs,
   return OZK_OK;
 }
 
-int launch_products(const uint16_t* As, const uint16_t* Bs, int64_t N,
-                    int64_t M, int64_t K, int pipe, int nhi, int nlo, float* P,
-                    int64_t ldp, hipStream_t st) {
+// Per-pair products.  Preset schedules run the all-pairs kernel (the one the
+// drivers use); other schedules (BF16 only) the pairwise kernel.
+int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
+                    int64_t K, int pipe, int nhi, int nlo, float* P,
+                    int64_t ldp, hipStream_t st, bool i8, int rho) {
+  if (allpairs_schedule(pipe, nhi, nlo))
+    return launch_allpairs(i8, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
+                           kOrderProducts, nullptr, 0, P, ldp, st);
+  if (i8) {
+    set_error("int8 slice planes need a preset on-device schedule");
+    return OZK_ERR_UNSUPPORTED;
+  }
   const int64_t ld = round_up(K, kKPad);
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
   const int64_t ntiles = (al / kBM) * (bl / kBN);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
   hipLaunchKernelGGL((gemm_pairwise<OZK_ORDER_2SUM, 1>), dim3((unsigned)ntiles),
-                     dim3(kThreads), 0, st, As, (const int32_t*)nullptr, Bs,
+                     dim3(kThreads), 0, st, (const uint16_t*)As,
+                     (const int32_t*)nullptr, (const uint16_t*)Bs,
                      (const int32_t*)nullptr, N, M, ld, al, bl, pipe, nhi, nlo,
                      (double*)nullptr, (int64_t)0, P, ldp);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }
 
+// Probe for v_mfma_i32_16x16x64_i8: bytes 0 and 1 of lane l < 16 hold
+// A[l][k0] = l, A[l][k1] = 16 and B[k0][l] = 1, B[k1][l] = l, so that
+// C[i][j] = i + 16 j.  Writes 64 lanes x 4 registers to out[1280..1535].
+__global__ void probe_mfma_i8_kernel(int32_t* out) {
+  const int l = threadIdx.x;
+  int32x4 a = int32x4{}, b = int32x4{};
+  if (l < 16) {
+    a[0] = l | (16 << 8);
+    b[0] = 1 | (l << 8);
+  }
+  int32x4 acc = int32x4{};
+  acc = __builtin_amdgcn_mfma_i32_16x16x64_i8(a, b, acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) out[1280 + l * 4 + r] = acc[r];
+}
+
 int launch_probe_mfma(int32_t* out, hipStream_t st) {
   hipLaunchKernelGGL(probe_mfma_kernel, dim3(1), dim3(64), 0, st, out);
   OZK_LAUNCH_CHECK();
   hipLaunchKernelGGL(probe_mfma16_kernel, dim3(1), dim3(64), 0, st, out);
+  OZK_LAUNCH_CHECK();
+  hipLaunchKernelGGL(probe_mfma_i8_kernel, dim3(1), dim3(64), 0, st, out);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }

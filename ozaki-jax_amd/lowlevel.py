@@ -17,16 +17,25 @@ ORDER_HOST_NP = _lib.ORDER_HOST_NP
 class Planes:
     """Slice planes of one operand on the device.
 
-    s: int16 (planes, lines_pad, ld) BF16 bit patterns; e: int32
-    (planes, lines_pad) exponents; lines / length: logical sizes.
+    s: (planes, lines_pad, ld) -- int16 BF16 bit patterns, or int8 grid
+    counts q = slice * 2^(24 - rho) when `rho` is set (INT8 format);
+    e: int32 (planes, lines_pad) exponents; lines / length: logical sizes.
     """
 
-    def __init__(self, s, e, lines, length, flags):
+    def __init__(self, s, e, lines, length, flags, rho=None):
         self.s, self.e, self.lines, self.length, self.flags = s, e, lines, length, flags
+        self.rho = rho
+
+    @property
+    def i8(self):
+        return self.rho is not None
 
     def values(self):
         """float32 (planes, lines, length) slice values (device)."""
-        v = (self.s.to(D.torch.int32) << 16).view(D.torch.float32)
+        if self.i8:
+            v = self.s.to(D.torch.float32) * 2.0 ** (self.rho - 24)
+        else:
+            v = (self.s.to(D.torch.int32) << 16).view(D.torch.float32)
         return v[:, :self.lines, :self.length]
 
     def exponents(self):
@@ -36,9 +45,10 @@ class Planes:
         return D.read_flags(self.flags) & _lib.OZK_FLAG_NONFINITE
 
 
-def extract(X, by_cols, rho, n0, n1=0, f64=False):
-    """Run ozk_extract_f32 (n0 hi slices, n1 lo slices) or ozk_extract_f64
-    (n0 slices) on X (any 2-D array; copied to the device as float64)."""
+def extract(X, by_cols, rho, n0, n1=0, f64=False, i8=False):
+    """Run ozk_extract_f32 (n0 hi slices, n1 lo slices), ozk_extract_f32_i8
+    (the same with INT8 planes) or ozk_extract_f64 (n0 slices) on X (any 2-D
+    array; copied to the device as float64)."""
     lib = _lib.load()
     dev = D.require_gpu()
     Xt = D.to_device_f64(X, dev)
@@ -47,7 +57,7 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False):
     planes = n0 if f64 else n0 + n1
     s = D.torch.zeros((planes, lib.ozk_slice_lines(max(lines, 1)),
                        lib.ozk_slice_ld(max(length, 1))),
-                      dtype=D.torch.int16, device=dev)
+                      dtype=D.torch.int8 if i8 else D.torch.int16, device=dev)
     e = D.torch.zeros((planes, lib.ozk_slice_lines(max(lines, 1))),
                       dtype=D.torch.int32, device=dev)
     flags = D.new_flags(dev)
@@ -59,12 +69,12 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False):
                                  e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
                                  wsb, D.stream_handle())
     else:
-        rc = lib.ozk_extract_f32(Xt.data_ptr(), rows, cols, D.ld_of(Xt),
-                                 int(by_cols), rho, n0, n1, s.data_ptr(),
-                                 e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
-                                 wsb, D.stream_handle())
+        fn = lib.ozk_extract_f32_i8 if i8 else lib.ozk_extract_f32
+        rc = fn(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols), rho, n0,
+                n1, s.data_ptr(), e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
+                wsb, D.stream_handle())
     _lib.check(rc)
-    return Planes(s, e, lines, length, flags)
+    return Planes(s, e, lines, length, flags, rho if i8 else None)
 
 
 def gemm(a, b, pipeline, n_hi, n_lo, order):
@@ -73,9 +83,15 @@ def gemm(a, b, pipeline, n_hi, n_lo, order):
     dev = a.s.device
     N, M, K = a.lines, b.lines, a.length
     C = D.torch.empty((N, M), dtype=D.torch.float64, device=dev)
-    _lib.check(lib.ozk_gemm(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
-                            b.e.data_ptr(), N, M, K, pipeline, n_hi, n_lo,
-                            order, C.data_ptr(), max(M, 1), D.stream_handle()))
+    if a.i8:
+        rc = lib.ozk_gemm_i8(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
+                             b.e.data_ptr(), N, M, K, a.rho, n_hi, n_lo, order,
+                             C.data_ptr(), max(M, 1), D.stream_handle())
+    else:
+        rc = lib.ozk_gemm(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
+                          b.e.data_ptr(), N, M, K, pipeline, n_hi, n_lo, order,
+                          C.data_ptr(), max(M, 1), D.stream_handle())
+    _lib.check(rc)
     return C
 
 
@@ -86,19 +102,26 @@ def slice_products(a, b, pipeline, n_hi, n_lo):
     N, M, K = a.lines, b.lines, a.length
     npairs = _lib.check(lib.ozk_pair_count(pipeline, n_hi, n_lo))
     P = D.torch.zeros((npairs, N, M), dtype=D.torch.float32, device=dev)
-    _lib.check(lib.ozk_slice_products(a.s.data_ptr(), b.s.data_ptr(), N, M, K,
-                                      pipeline, n_hi, n_lo, P.data_ptr(),
-                                      max(M, 1), D.stream_handle()))
+    if a.i8:
+        rc = lib.ozk_slice_products_i8(a.s.data_ptr(), b.s.data_ptr(), N, M, K,
+                                       a.rho, n_hi, n_lo, P.data_ptr(),
+                                       max(M, 1), D.stream_handle())
+    else:
+        rc = lib.ozk_slice_products(a.s.data_ptr(), b.s.data_ptr(), N, M, K,
+                                    pipeline, n_hi, n_lo, P.data_ptr(),
+                                    max(M, 1), D.stream_handle())
+    _lib.check(rc)
     return P
 
 
 def probe_mfma_layout():
     """Accumulator registers after the layout-probe MFMAs, as int32 arrays
-    (32x32x16: (64 lanes, 16 regs); 16x16x32: (64 lanes, 4 regs)); each value
-    encodes row + 64 * col of the output element it holds."""
+    (32x32x16 BF16: (64 lanes, 16 regs), values row + 64 col; 16x16x32 BF16:
+    (64, 4), row + 64 col; 16x16x64 INT8: (64, 4), row + 16 col)."""
     lib = _lib.load()
     dev = D.require_gpu()
-    out = D.torch.zeros(64 * 16 + 64 * 4, dtype=D.torch.int32, device=dev)
+    out = D.torch.zeros(64 * 16 + 2 * 64 * 4, dtype=D.torch.int32, device=dev)
     _lib.check(lib.ozk_probe_mfma_layout(out.data_ptr(), D.stream_handle()))
     o = out.cpu().numpy()
-    return o[:1024].reshape(64, 16), o[1024:].reshape(64, 4)
+    return (o[:1024].reshape(64, 16), o[1024:1280].reshape(64, 4),
+            o[1280:].reshape(64, 4))

@@ -60,13 +60,34 @@ def test_host_functions(lib):
 
 
 def test_workspace_sizes(lib):
-    # A and B slice planes (BF16) + exponents + the FP64 transpose of B
-    N = K = M = 8192
-    ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, 4, 1)
-    planes = 2 * 5 * 8192 * 8192 * 2
-    assert planes + 8 * K * M <= ws <= planes + 8 * K * M + 2 * 5 * 8192 * 4 + 4096
+    # A and B slice planes + exponents + the FP64 transpose of B; planes are
+    # INT8 when K > 4096 (rho >= 19) and the schedule is a preset, else BF16
+    for K, eb in [(8192, 1), (4096, 2)]:
+        N = M = 8192
+        for nh, nl in [(4, 1), (3, 1)]:
+            ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, nh, nl)
+            planes = 2 * (nh + nl) * 8192 * K * eb
+            extra = 2 * (nh + nl) * 8192 * 4 + 4096
+            assert planes + 8 * K * M <= ws <= planes + 8 * K * M + extra, (K, nh, nl)
+    ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
+    assert ws >= 2 * 9 * 8192 * 8192 * 2
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
     assert lib.ozk_extract_workspace_bytes(100, 50, 1) == 100 * 50 * 8
+
+
+def test_int8_entry_points_reject_before_device_work(lib):
+    from ozaki_jax_amd import _lib
+    # INT8 planes need rho >= 19 (|q| <= 64) and a preset schedule
+    rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, 18, 4, 1, None, None, None, None, 0, None)
+    assert rc == _lib.OZK_ERR_UNSUPPORTED and b"rho >= 19" in lib.ozk_last_error()
+    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 18, 4, 1, 0, None, 4, None)
+    assert rc == _lib.OZK_ERR_UNSUPPORTED
+    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 5, 4, 0, None, 4, None)
+    assert rc == _lib.OZK_ERR_UNSUPPORTED
+    rc = lib.ozk_slice_products_i8(None, None, 4, 4, 8192, 19, 2, 3, None, 4, None)
+    assert rc == _lib.OZK_ERR_UNSUPPORTED
+    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4, None)
+    assert rc == _lib.OZK_ERR_INVALID
 
 
 def test_argument_errors_before_device_work(lib):

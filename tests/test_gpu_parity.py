@@ -60,8 +60,8 @@ def to_np(t):
 # ---------------------------------------------------------------- layout
 
 def test_mfma_output_layout(ll):
-    case("probe_mfma_layout 32x32x16 and 16x16x32 bf16")
-    out, out16 = ll.probe_mfma_layout()
+    case("probe_mfma_layout 32x32x16 / 16x16x32 bf16, 16x16x64 i8")
+    out, out16, out8 = ll.probe_mfma_layout()
     for lane in range(64):
         for r in range(16):
             row = 8 * (r // 4) + 4 * (lane // 32) + (r % 4)
@@ -71,6 +71,7 @@ def test_mfma_output_layout(ll):
             row = 4 * (lane // 16) + r
             col = lane % 16
             assert out16[lane, r] == row + 64 * col, (lane, r, out16[lane, r])
+            assert out8[lane, r] == row + 16 * col, (lane, r, out8[lane, r])
 
 
 # ---------------------------------------------------------------- extraction
@@ -157,6 +158,41 @@ def test_extract_nonfinite_flag(ll):
     assert ll.extract(X, 1, 17, 4, 1).nonfinite()
 
 
+# INT8 planes: q = slice * 2^(24 - rho), exact for rho >= 19.  Lines of
+# length > 4096 give rho >= 19 by themselves; shorter ones are run with an
+# explicit rho in [19, 24] (any rho is a valid extraction grid).
+I8_CASES = [((3, 5000), None), ((130, 4200), None), ((2, 9000), None),
+            ((64, 64), 19), ((77, 300), 21), ((5, 33), 24), ((1, 1), 19)]
+
+
+@pytest.mark.parametrize("kind", ["randn", "wide", "zerorows"])
+@pytest.mark.parametrize("shape,rho_fixed", I8_CASES)
+def test_extract_f32_i8_rows_and_cols(ll, kind, shape, rho_fixed):
+    X = gen(kind, shape, 200 + shape[1])
+    hi, lo = O.split_hi_lo(X)
+    for by_cols in (0, 1):
+        Xi = X.T.copy() if by_cols else X
+        rho = rho_fixed or O.rho_f32(shape[1])
+        case(f"ozk_extract_f32_i8 {kind} {shape} by_cols={by_cols} rho={rho}")
+        pl = ll.extract(Xi, by_cols, rho, 4, 1, i8=True)
+        sh, eh = O.extract_rows_f32(hi, rho, 4)
+        sl, el = O.extract_rows_f32(lo, rho, 1)
+        ref = np.concatenate([sh, sl]).astype(np.float64) * 2.0 ** (24 - rho)
+        assert np.all(np.abs(ref) <= 64) and np.array_equal(ref, np.round(ref))
+        q = to_np(pl.s)[:, :shape[0], :shape[1]]
+        assert np.array_equal(q, ref.astype(np.int8)), "int8 slices"
+        assert np.array_equal(to_np(pl.exponents()),
+                              np.concatenate([eh, el]).astype(np.int32)), "exponents"
+        # padding stays zero (the GEMM reads it)
+        assert not to_np(pl.s)[:, :, shape[1]:].any()
+
+
+def test_extract_i8_rejects_coarse_grid(ll):
+    case("ozk_extract_f32_i8 rho=18 -> unsupported")
+    with pytest.raises(NotImplementedError, match="rho >= 19"):
+        ll.extract(np.ones((4, 4)), 0, 18, 4, 1, i8=True)
+
+
 # ---------------------------------------------------------------- products
 
 SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
@@ -199,6 +235,45 @@ def test_slice_products_bit_exact(ll, pipe, nh, nl, shape):
     assert np.array_equal(P, Pref)
 
 
+I8_SHAPES = [((96, 5000, 160), None), ((2, 8192, 3), None), ((130, 4100, 67), None),
+             ((64, 64, 64), 19), ((96, 70, 160), 20), ((1, 33, 1), 24)]
+
+
+def _slices_i8(ll, A, B, nh, nl, rho_fixed):
+    rho = rho_fixed or O.rho_f32(A.shape[1])
+    a = ll.extract(A, 0, rho, nh, nl, i8=True)
+    b = ll.extract(B, 1, rho, nh, nl, i8=True)
+    return a, b, O.ondevice_slices(A, B, rho, nh, nl), O.ondevice_schedule(nh, nl), rho
+
+
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1)])
+@pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
+def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
+    N, K, M = shape
+    A, B = gen("randn", (N, K), 5), gen("wide2", (K, M), 6)
+    a, b, (oa, oae, ob, obe), sched, rho = _slices_i8(ll, A, B, nh, nl, rho_fixed)
+    case(f"ozk_slice_products_i8 ({nh},{nl}) N,K,M={shape} rho={rho}")
+    P = to_np(ll.slice_products(a, b, ll.PIPE_ONDEVICE, nh, nl))
+    unit = 2.0 ** (rho - 24)
+    assert OP.products_exact_certificate(oa, ob, sched, unit, unit)
+    assert np.array_equal(P, O.slice_products(oa, ob, sched))
+
+
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1)])
+@pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
+def test_gemm_i8_orders_bit_exact(ll, nh, nl, shape, rho_fixed):
+    N, K, M = shape
+    A, B = gen("wide2", (N, K), 7), gen("randn", (K, M), 8)
+    a, b, (oa, oae, ob, obe), sched, rho = _slices_i8(ll, A, B, nh, nl, rho_fixed)
+    Pref = O.slice_products(oa, ob, sched)
+    case(f"ozk_gemm_i8 ({nh},{nl}) order A4 N,K,M={shape} rho={rho}")
+    C = to_np(ll.gemm(a, b, ll.PIPE_ONDEVICE, nh, nl, ll.ORDER_2SUM))
+    assert np.array_equal(C, OP.combine_f64(*O.accumulate_a4(Pref, sched, oae, obe)))
+    case(f"ozk_gemm_i8 ({nh},{nl}) order A3 N,K,M={shape} rho={rho}")
+    C = to_np(ll.gemm(a, b, ll.PIPE_ONDEVICE, nh, nl, ll.ORDER_BLOCK64))
+    assert np.array_equal(C, O.accumulate_a3(Pref, sched, oae, obe))
+
+
 # ---------------------------------------------------------------- orders
 
 ORDERS = {"ondevice": [("A4", 0), ("A3", 1)], "host": [("A2", 2), ("A1", 3)]}
@@ -238,6 +313,18 @@ def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
     assert isinstance(C, np.ndarray) and C.dtype == np.float64
     assert np.array_equal(C, ref)
     assert np.all(np.abs(C - ref) <= 2.0 ** -51 * (np.abs(A) @ np.abs(B)))
+
+
+@pytest.mark.parametrize("precision", ["high", "medium", "max"])
+def test_matmul_long_contraction_bit_exact(ozk, precision):
+    # K > 4096: rho >= 19, the presets run on INT8 planes
+    A, B = gen("randn", (40, 6000), 23), gen("wide2", (6000, 70), 24)
+    nh, nl = OP.resolve_precision(precision)
+    for acc, ref in [("fused", lambda: O.matmul_ondevice_a4(A, B, "raise", nh, nl)),
+                     ("host", lambda: O.matmul_ondevice_a3(A, B, "raise", nh, nl))]:
+        case(f"matmul ondevice {precision} {acc} (40,6000,70)")
+        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=precision)
+        assert np.array_equal(C, ref())
 
 
 def test_matmul_numpy_bit_exact(ozk):
@@ -354,7 +441,7 @@ def test_preflight_and_families(ozk):
 
 # ---------------------------------------------------------------- gram / residual / solve
 
-@pytest.mark.parametrize("shape", [(64, 64), (300, 40), (33, 130)])
+@pytest.mark.parametrize("shape", [(64, 64), (300, 40), (33, 130), (5000, 24)])
 @pytest.mark.parametrize("precision", ["high", "medium"])
 def test_gram_bit_exact(ozk, shape, precision):
     A = gen("randn", shape, 51)
@@ -365,7 +452,7 @@ def test_gram_bit_exact(ozk, shape, precision):
         assert np.array_equal(G, G.T)
 
 
-@pytest.mark.parametrize("shape", [(64, 64), (200, 50), (37, 300)])
+@pytest.mark.parametrize("shape", [(64, 64), (200, 50), (37, 300), (20, 5000)])
 def test_residual_bit_exact(ozk, shape):
     N, K = shape
     rng = np.random.RandomState(61)
