@@ -12,7 +12,8 @@ Prints one JSON line with value = 2 M N K / t (TFLOP/s), plus
                 runs on: INT8 (5.0 POP/s) when K > 4096 makes rho >= 19 and
                 the slices fit in int8, else BF16 (2.5 PFLOP/s);
   cpu_baseline  the oracle (NumPy restatement of matmul_numpy(pipeline=
-                "ondevice")) timed on this host at 4096^3;
+                "ondevice")) timed on this host on a 2048-row block of the
+                same A against the same B;
   rocblas_dgemm FP64 DGEMM of the same matrices (torch.matmul -> rocBLAS);
   accuracy      max scaled error vs the oracle (same order, must be 0) and vs
                 FP64, on a subset of rows of the full-size product.
@@ -66,7 +67,10 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(precision):
+def cpu_baseline(A, B, precision, rows=2048):
+    """The oracle's matmul_numpy(pipeline="ondevice") on the first `rows` rows
+    of the same A against the full B (same K, rho and slices as the timed
+    workload), rated as 2 * rows * K * M / t."""
     import oracle
     try:
         from threadpoolctl import threadpool_info
@@ -74,17 +78,17 @@ def cpu_baseline(precision):
                        if p.get("user_api") == "blas"), default=1)
     except Exception:
         threads = os.cpu_count() or 1
-    n = 4096
-    rs = np.random.RandomState(0)
-    A, B = rs.randn(n, n), rs.randn(n, n)
-    log(f"cpu baseline: oracle matmul_numpy ondevice {precision} {n}^3")
+    K, M = B.shape
+    Ar = A[:rows]
+    log(f"cpu baseline: oracle matmul_numpy ondevice {precision} {rows}x{K}x{M}")
     t0 = time.perf_counter()
-    oracle.matmul_numpy(A, B, pipeline="ondevice", precision=precision)
+    oracle.matmul_numpy(Ar, B, pipeline="ondevice", precision=precision)
     t = time.perf_counter() - t0
-    return {"value": 2.0 * n ** 3 / t / 1e12, "unit": "TFLOP/s",
+    return {"value": 2.0 * rows * K * M / t / 1e12, "unit": "TFLOP/s",
             "cores": int(threads), "kind": "port",
             "sample": f"oracle matmul_numpy(pipeline='ondevice', precision='{precision}') "
-                      f"{n}x{n}x{n} N(0,1), one run of {t:.1f} s "
+                      f"on rows 0..{rows - 1} of the timed A ({rows}x{K}) times the full "
+                      f"B ({K}x{M}), one run of {t:.1f} s including B's extraction "
                       f"(NumPy/OpenBLAS, {threads} BLAS threads)"}
 
 
@@ -203,7 +207,7 @@ def main():
                "scale": "|C - C_ref| / (|A||B|)_ij"}
 
     ext_bytes = 2 * n * n * (8 + (1 if i8 else 2) * (n_hi + n_lo))
-    cpu = None if args.no_cpu else cpu_baseline(args.precision)
+    cpu = None if args.no_cpu else cpu_baseline(A, B, args.precision, min(2048, n))
     traffic = read_traffic()
     dev_name = torch.cuda.get_device_name(0)
     out = {
