@@ -19,9 +19,14 @@
  *  - `flags` (device uint32) receives OZK_FLAG_NONFINITE when an input holds
  *    NaN/Inf; drivers clear it first.  It replaces the host-side
  *    np.isfinite preflight scan (ozaki_jax/matmul.py:108-109, :623-628).
- *  - Slice planes: BF16 bit patterns, [plane][line][k] with
- *    k stride ozk_slice_ld(len) and ozk_slice_lines(lines) lines per plane;
- *    padding is zero.  Exponents: int32 [plane][ozk_slice_lines(lines)].
+ *  - Slice planes: BF16 bit patterns (2 bytes) or INT8 grid counts (1 byte),
+ *    L = ozk_slice_lines(lines) lines of ld = ozk_slice_ld(len) elements per
+ *    plane, planes back to back; padding is zero.  Inside a plane the bytes
+ *    are chunk-major: byte b of line r lies at
+ *        ((b / 64) * L + r) * 64 + 16 * (((b % 64) / 16) ^ s(r)) + b % 16,
+ *    s(r) = (((r & 15) >> 1) ^ ((r & 15) >> 2)) & 3, so the 64 lines of an
+ *    output tile form one contiguous 4 KiB block per 64-byte chunk.
+ *    Exponents: int32 [plane][L].
  */
 #ifndef OZAKI_AMD_H
 #define OZAKI_AMD_H
@@ -185,10 +190,11 @@ int ozk_check_finite(const double* X, int64_t rows, int64_t cols, int64_t ld,
                      uint32_t* flags, void* stream);
 
 /* Test hook: runs one 32x32x16 and one 16x16x32 BF16 MFMA and one
- * 16x16x64 INT8 MFMA on fixed patterns and writes their accumulator
- * registers as int32: out[0..1023] = 64 lanes x 16 registers (32x32x16),
- * out[1024..1279] and out[1280..1535] = 64 lanes x 4 registers (16x16x32,
- * 16x16x64).  out must hold 1536 int32. */
+ * 16x16x64 and one 32x32x32 INT8 MFMA on fixed patterns and writes their
+ * accumulator registers as int32: out[0..1023] = 64 lanes x 16 registers
+ * (32x32x16), out[1024..1279] and out[1280..1535] = 64 lanes x 4 registers
+ * (16x16x32, 16x16x64), out[1536..2559] = 64 lanes x 16 registers
+ * (32x32x32).  out must hold 2560 int32. */
 int ozk_probe_mfma_layout(int32_t* out, void* stream);
 
 #ifdef __cplusplus

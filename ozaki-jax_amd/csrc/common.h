@@ -43,13 +43,39 @@ void clear_error();
   } while (0)
 
 // ---------------------------------------------------------------- layout
-// Slice planes are BF16, [plane][line][k] with lines padded to kLinePad and
-// k padded to kKPad; padding holds zeros, so the GEMM needs no bounds checks
-// in its K loop or its operand tiles.
+// Slice planes hold BF16 bit patterns or INT8 grid counts with lines padded
+// to kLinePad and k padded to kKPad elements; padding holds zeros, so the
+// GEMM needs no bounds checks in its K loop or its operand tiles.
+//
+// Inside a plane the bytes are chunk-major: k is cut into 64-byte chunks
+// (32 BF16 or 64 INT8 values) and chunk c of every line is stored together,
+// [c][line][64 bytes].  The 64 lines of an output tile therefore occupy one
+// contiguous 4 KiB block per chunk, which the GEMM moves into LDS with
+// fully contiguous 1 KiB loads.  Within a line's 64 bytes the four 16-byte
+// units are stored in the order u ^ unit_swizzle(line), which spreads the
+// MFMA fragment reads of 16 or 32 consecutive lines over all LDS banks.
 constexpr int64_t kKPad = 64;
 constexpr int64_t kLinePad = 64;
+constexpr int kChunkBytes = 64;
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
+
+__host__ __device__ __forceinline__ int unit_swizzle(int64_t line) {
+  const int r = (int)(line & 15);
+  return ((r >> 1) ^ (r >> 2)) & 3;
+}
+
+// Element offset of (line, k) inside one plane of `lpad` lines, for
+// elements of `EB` bytes.
+template <int EB>
+__host__ __device__ __forceinline__ int64_t plane_offset(int64_t line, int64_t k,
+                                                         int64_t lpad) {
+  constexpr int kPer = kChunkBytes / EB;
+  const int64_t c = k / kPer;
+  const int b = (int)(k - c * kPer) * EB;
+  const int u = b >> 4;
+  return ((c * lpad + line) * kChunkBytes + 16 * (u ^ unit_swizzle(line)) + (b & 15)) / EB;
+}
 
 // ---------------------------------------------------------------- device
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

@@ -178,25 +178,27 @@ __device__ __forceinline__ int frag_off(int slot, int rg, int ks, int lane) {
   return ((slot * 2 + rg) * 2 + ks) * 64 + lane;
 }
 
-// One operand side (A or B) of a stage: N slot tiles of 64 lines x 32 k.
-// Thread t moves line t/4, chunk t%4 of every slot: one 16-byte global load
-// and one 16-byte LDS store per slot.
+// One operand side (A or B) of a stage: N slot tiles of 64 lines x 32 k,
+// i.e. one 64-byte chunk of each of the tile's lines, which is a contiguous
+// 4 KiB block of the plane.  Thread t moves the block's 16-byte unit t
+// (line t / 4, stored unit t % 4, which holds logical unit
+// (t % 4) ^ unit_swizzle(line)): one 16-byte global load and one 16-byte LDS
+// store per slot.
 template <int N>
 struct HalfStage {
   uint4 v[N];
   __device__ __forceinline__ void load(const uint16_t* const (&ptr)[N],
-                                       int64_t ld, int64_t k0) {
-    const int t = threadIdx.x;
-    const int64_t off = (int64_t)(t >> 2) * ld + k0 + (t & 3) * 8;
+                                       int64_t stage_stride, int64_t s) {
+    const int64_t off = s * stage_stride + (int64_t)threadIdx.x * 8;
 #pragma unroll
-    for (int s = 0; s < N; ++s) v[s] = *(const uint4*)(ptr[s] + off);
+    for (int i = 0; i < N; ++i) v[i] = *(const uint4*)(ptr[i] + off);
   }
   __device__ __forceinline__ void store(uint4* buf, int slot0) const {
     const int t = threadIdx.x;
-    const int r = t >> 2, c = t & 3;
+    const int r = t >> 2, c = (t & 3) ^ unit_swizzle(r);
     const int lane = (r & 31) + 32 * (c & 1);
 #pragma unroll
-    for (int s = 0; s < N; ++s) buf[frag_off(slot0 + s, r >> 5, c >> 1, lane)] = v[s];
+    for (int i = 0; i < N; ++i) buf[frag_off(slot0 + i, r >> 5, c >> 1, lane)] = v[i];
   }
 };
 
@@ -210,22 +212,24 @@ __device__ __forceinline__ int acc_row(int r, int lane) {
   return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
 }
 
-// K sweep shared by both kernels: double-buffered LDS stages; while one
+// K sweep of the pairwise kernel: double-buffered LDS stages; while one
 // buffer feeds the MFMAs the next stage is fetched half by half (A slots
 // during k-step 0, B slots during k-step 1) through NA or NB registers.
-// `mma(buf, ks)` issues the MFMAs of one 16-wide k-step.
+// `mma(buf, ks)` issues the MFMAs of one 16-wide k-step.  a_ptr / b_ptr
+// point at the tile's first line in chunk 0; chunk s lies s * a_stride /
+// s * b_stride elements further.
 template <int NA, int NB, class MMA>
 __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
                                         const uint16_t* const (&b_ptr)[NB],
-                                        int64_t ld, uint4* lds, MMA& mma) {
+                                        int64_t a_stride, int64_t b_stride,
+                                        int64_t nst, uint4* lds, MMA& mma) {
   constexpr int kBuf = (NA + NB) * 4 * 64;  // uint4 per stage buffer
-  const int64_t nst = ld / kBK;
   {
     HalfStage<NA> ha;
-    ha.load(a_ptr, ld, 0);
+    ha.load(a_ptr, a_stride, 0);
     ha.store(lds, 0);
     HalfStage<NB> hb;
-    hb.load(b_ptr, ld, 0);
+    hb.load(b_ptr, b_stride, 0);
     hb.store(lds, NA);
   }
   __syncthreads();
@@ -233,16 +237,15 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
     uint4* cur = lds + (s & 1) * kBuf;
     uint4* nxt = lds + ((s + 1) & 1) * kBuf;
     const bool more = s + 1 < nst;
-    const int64_t k1 = (s + 1) * kBK;
     {
       HalfStage<NA> ha;
-      if (more) ha.load(a_ptr, ld, k1);
+      if (more) ha.load(a_ptr, a_stride, s + 1);
       mma(cur, 0);
       if (more) ha.store(nxt, 0);
     }
     {
       HalfStage<NB> hb;
-      if (more) hb.load(b_ptr, ld, k1);
+      if (more) hb.load(b_ptr, b_stride, s + 1);
       mma(cur, 1);
       if (more) hb.store(nxt, NA);
     }
@@ -267,18 +270,20 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 //         scaled by 2^(2 rho - 48), i.e. the same FP32 value as the BF16
 //         product whenever that one is exact (partial sums < 2^24 units).
 //
-// LDS: a ring of kRing stage buffers, one 64-byte k-step each; fragment
-// (slot, 16-line group lg) holds line lg * 16 + l % 16, bytes 16 (l / 16) ..
-// +15 in lane l's 16 bytes.  Wave w fetches the fragments w, w + 8, ... of a
-// stage with direct global->LDS loads (lane l's bytes land at fragment * 1 KiB
-// + 16 l), kRing - 1 stages ahead of the MFMAs; LDS writes and MFMA operand
-// reads are both linear in the lane index.
+// LDS: a ring of kRing stage buffers, one 64-byte chunk of every line each.
+// Fragment (slot, 16-line group lg) is the 1 KiB block of lines
+// 16 lg .. 16 lg + 15 of that chunk exactly as it lies in the plane (line r
+// at byte 64 (r % 16), units swizzled).  Wave w fetches the fragments w,
+// w + 8, ... of a stage with contiguous direct global->LDS loads, kRing - 1
+// stages ahead of the MFMAs.  MFMA lane l reads line l % 16, logical unit
+// l / 16 of a fragment (frag_lane); the swizzle spreads those 64 reads over
+// all LDS banks.
 
 constexpr int kThreads16 = 512;
 constexpr int kRing = 4;       // stage buffers (kRing - 1 stages in flight)
-constexpr int kStageB = 64;    // bytes of a line per stage
 
 typedef int int32x4 __attribute__((ext_vector_type(4)));
+typedef int int32x16 __attribute__((ext_vector_type(16)));
 
 struct OpBf16 {
   typedef floatx4 acc_t;
@@ -331,31 +336,40 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
 }
 
-// Fetch stage `st` (bytes st * 64 .. +63 of every line of the tile) into the
-// LDS buffer at byte offset `buf_lds`: wave w moves fragments F = w + 8 i,
-// i.e. slot 2 i + (w >> 2), line group w & 3.  All addresses lie inside the
+// Fetch stage `st` (chunk st of every line of the tile) into the LDS buffer
+// at byte offset `buf_lds`: wave w moves fragments F = w + 8 i, i.e. slot
+// 2 i + (w >> 2), line group w & 3, each a contiguous 1 KiB of the plane.
+// At, Bt point at the tile's first line in chunk 0; chunk st lies
+// st * a_stage / st * b_stage bytes further.  All addresses lie inside the
 // zero-padded slice planes.
 template <int NT>
 __device__ __forceinline__ void stage_dma(const char* At, int64_t aplane,
-                                          const char* Bt, int64_t bplane,
-                                          int64_t ldb, int64_t st,
-                                          uint32_t buf_lds, int wave,
-                                          uint32_t lane_bytes) {
-  const int64_t wave_off = (int64_t)((wave & 3) * 16) * ldb + st * kStageB;
+                                          int64_t a_stage, const char* Bt,
+                                          int64_t bplane, int64_t b_stage,
+                                          int64_t st, uint32_t buf_lds,
+                                          int wave, uint32_t lane_bytes) {
+  const int64_t g = (int64_t)(wave & 3) * 1024;
+  const int64_t qa = st * a_stage + g, qb = st * b_stage + g;
 #pragma unroll
   for (int i = 0; i < NT; ++i) {
     const int slot = 2 * i + (wave >> 2);
-    const char* base = slot < NT ? At + slot * aplane : Bt + (slot - NT) * bplane;
+    const char* base = slot < NT ? At + slot * aplane + qa : Bt + (slot - NT) * bplane + qb;
     const int F = 8 * i + wave;
-    dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024),
-          (const void*)(base + wave_off), lane_bytes);
+    dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024), (const void*)base,
+          lane_bytes);
   }
+}
+
+// uint4 index inside a 1 KiB fragment of the 16x16x64 operand of lane l:
+// line l % 16, logical unit l / 16.
+__device__ __forceinline__ int frag_lane(int lane) {
+  return (lane & 15) * 4 + ((lane >> 4) ^ unit_swizzle(lane & 15));
 }
 
 template <class Op, int PIPE, int NHI, int NLO, int NT, int NP>
 struct AllPairsMMA {
   typename Op::acc_t acc[NP][2];
-  int lane, wr, wc;
+  int fl, wr, wc;  // fl = frag_lane(lane)
 
   // MFMAs of one (A slot, row block) for every pair of that A slot.
   template <int SA, int H>
@@ -373,7 +387,7 @@ struct AllPairsMMA {
   static constexpr int kBlocks = NT * 2, kDepth = 3;
 
   __device__ __forceinline__ uint4 read_a(const uint4* buf, int j) const {
-    return buf[((j >> 1) * 4 + 2 * wr + (j & 1)) * 64 + lane];
+    return buf[((j >> 1) * 4 + 2 * wr + (j & 1)) * 64 + fl];
   }
 
   template <int J>
@@ -392,7 +406,7 @@ struct AllPairsMMA {
   __device__ __forceinline__ void operator()(const uint4* buf) {
     uint4 bf[NT];
 #pragma unroll
-    for (int s = 0; s < NT; ++s) bf[s] = buf[((NT + s) * 4 + wc) * 64 + lane];
+    for (int s = 0; s < NT; ++s) bf[s] = buf[((NT + s) * 4 + wc) * 64 + fl];
     uint4 af[kDepth + 1];
 #pragma unroll
     for (int j = 0; j < kDepth; ++j) af[j] = read_a(buf, j);
@@ -420,7 +434,7 @@ template <class Op, int PIPE, int NHI, int NLO, int ORDER>
 __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     const char* __restrict__ As, const int32_t* __restrict__ Ae,
     const char* __restrict__ Bs, const int32_t* __restrict__ Be,
-    int64_t N, int64_t M, int64_t ld, int64_t a_lines, int64_t b_lines,
+    int64_t N, int64_t M, int64_t nst, int64_t a_lines, int64_t b_lines,
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
     int64_t ldp) {
   constexpr int NT = PIPE == OZK_PIPE_ONDEVICE ? NHI + NLO : NHI;
@@ -435,15 +449,15 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   int tm, tn;
   tile_coords(blockIdx.x, ntm, ntn, tm, tn);
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
-  const int64_t ldb = ld * Op::kElemBytes;  // bytes per line
-  const int64_t aplane = a_lines * ldb, bplane = b_lines * ldb;
-  const char* At = As + row0 * ldb;
-  const char* Bt = Bs + col0 * ldb;
+  const int64_t a_stage = a_lines * kChunkBytes, b_stage = b_lines * kChunkBytes;
+  const int64_t aplane = a_stage * nst, bplane = b_stage * nst;
+  const char* At = As + row0 * kChunkBytes;
+  const char* Bt = Bs + col0 * kChunkBytes;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   AllPairsMMA<Op, PIPE, NHI, NLO, NT, NP> mma;
-  mma.lane = lane;
+  mma.fl = frag_lane(lane);
   mma.wr = wave >> 2;
   mma.wc = wave & 3;
 #pragma unroll
@@ -455,19 +469,19 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   // Per stage s: wait for this wave's loads of stage s, barrier (stage s is
   // complete in LDS and every wave has finished stage s - 1, whose buffer is
   // refilled next), fetch stage s + kRing - 1, run the MFMAs of stage s.
-  const int64_t nst = ldb / kStageB;
-  const uint32_t lane_bytes = (uint32_t)((lane & 15) * ldb + 16 * (lane >> 4));
+  const uint32_t lane_bytes = 16u * (uint32_t)lane;
   const uint32_t lds0 = lds_offset(lds);
   for (int i = 0; i < kRing - 1; ++i)
     if (i < nst)
-      stage_dma<NT>(At, aplane, Bt, bplane, ldb, i, lds0 + i * kBuf * 16, wave, lane_bytes);
+      stage_dma<NT>(At, aplane, a_stage, Bt, bplane, b_stage, i,
+                    lds0 + i * kBuf * 16, wave, lane_bytes);
   for (int64_t s = 0; s < nst; ++s) {
     const int64_t later = nst - 1 - s;
     wait_stage<NT>(later < kRing - 2 ? later : kRing - 2);
     __syncthreads();
     const int64_t fetch = s + kRing - 1;
     if (fetch < nst)
-      stage_dma<NT>(At, aplane, Bt, bplane, ldb, fetch,
+      stage_dma<NT>(At, aplane, a_stage, Bt, bplane, b_stage, fetch,
                     lds0 + (uint32_t)((fetch % kRing) * kBuf * 16), wave, lane_bytes);
     mma(lds + (s % kRing) * kBuf);
   }
@@ -543,6 +557,7 @@ __global__ __launch_bounds__(kThreads) void gemm_pairwise(
   tile_coords(blockIdx.x, ntm, ntn, tm, tn);
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
   const int64_t aplane = a_lines * ld, bplane = b_lines * ld;
+  constexpr int64_t kPer = kChunkBytes / 2;  // BF16 values per chunk
   OnePairMMA mma;
   mma.lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -559,10 +574,10 @@ __global__ __launch_bounds__(kThreads) void gemm_pairwise(
 
   for (int p = 0; p < np; ++p) {
     const PairInfo q = pair_info(pipe, nhi, nlo, p);
-    const uint16_t* a_ptr[1] = {As + q.a * aplane + row0 * ld};
-    const uint16_t* b_ptr[1] = {Bs + q.b * bplane + col0 * ld};
+    const uint16_t* a_ptr[1] = {As + q.a * aplane + row0 * kPer};
+    const uint16_t* b_ptr[1] = {Bs + q.b * bplane + col0 * kPer};
     mma.acc = floatx16{};
-    k_sweep<1, 1>(a_ptr, b_ptr, ld, lds, mma);
+    k_sweep<1, 1>(a_ptr, b_ptr, a_lines * kPer, b_lines * kPer, ld / kPer, lds, mma);
     if (MODE == 1) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
@@ -640,12 +655,12 @@ bool allpairs_supported(int pipe, int nhi, int nlo) {
 template <class Op, int NHI, int NLO, int ORDER>
 static void launch_ap(dim3 grid, hipStream_t st, const void* As,
                       const int32_t* Ae, const void* Bs, const int32_t* Be,
-                      int64_t N, int64_t M, int64_t ld, int64_t al, int64_t bl,
+                      int64_t N, int64_t M, int64_t nst, int64_t al, int64_t bl,
                       float unit2, double* C, int64_t ldc, float* P,
                       int64_t ldp) {
   hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER>),
                      grid, dim3(kThreads16), 0, st, (const char*)As, Ae,
-                     (const char*)Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P,
+                     (const char*)Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P,
                      ldp);
 }
 
@@ -653,23 +668,23 @@ template <class Op, int NHI, int NLO>
 static void launch_ap_order(int order, dim3 grid, hipStream_t st,
                             const void* As, const int32_t* Ae, const void* Bs,
                             const int32_t* Be, int64_t N, int64_t M,
-                            int64_t ld, int64_t al, int64_t bl, float unit2,
+                            int64_t nst, int64_t al, int64_t bl, float unit2,
                             double* C, int64_t ldc, float* P, int64_t ldp) {
   switch (order) {
     case OZK_ORDER_2SUM:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_2SUM>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      launch_ap<Op, NHI, NLO, OZK_ORDER_2SUM>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
       break;
     case OZK_ORDER_BLOCK64:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_BLOCK64>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      launch_ap<Op, NHI, NLO, OZK_ORDER_BLOCK64>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
       break;
     case OZK_ORDER_HOST_JAX:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
       break;
     case OZK_ORDER_HOST_NP:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_NP>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_NP>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
       break;
     default:
-      launch_ap<Op, NHI, NLO, kOrderProducts>(grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, unit2, C, ldc, P, ldp);
+      launch_ap<Op, NHI, NLO, kOrderProducts>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
       break;
   }
 }
@@ -681,7 +696,8 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
                            int order, double* C, int64_t ldc, float* P,
                            int64_t ldp, hipStream_t st) {
-  const int64_t ld = round_up(K, kKPad);
+  // chunks per line: round_up(K, kKPad) elements of 1 or 2 bytes
+  const int64_t nst = round_up(K, kKPad) * (i8 ? 1 : 2) / kChunkBytes;
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
   const int64_t ntiles = (al / kBM) * (bl / kBN);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
@@ -690,10 +706,10 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
 #define OZK_AP_ALL(Op)                                                              \
   do {                                                                              \
     if (nhi == 4)                                                                   \
-      launch_ap_order<Op, 4, 1>(order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, \
+      launch_ap_order<Op, 4, 1>(order, grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, \
                                 unit2, C, ldc, P, ldp);                             \
     else                                                                            \
-      launch_ap_order<Op, 3, 1>(order, grid, st, As, Ae, Bs, Be, N, M, ld, al, bl, \
+      launch_ap_order<Op, 3, 1>(order, grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, \
                                 unit2, C, ldc, P, ldp);                             \
   } while (0)
   if (i8) OZK_AP_ALL(OpI8);
@@ -777,12 +793,30 @@ __global__ void probe_mfma_i8_kernel(int32_t* out) {
   for (int r = 0; r < 4; ++r) out[1280 + l * 4 + r] = acc[r];
 }
 
+// Probe for v_mfma_i32_32x32x32_i8: bytes 0 and 1 of lane l < 32 hold
+// A[l][k0] = l, A[l][k1] = 64 and B[k0][l] = 1, B[k1][l] = l, so that
+// C[i][j] = i + 64 j.  Writes 64 lanes x 16 registers to out[1536..2559].
+__global__ void probe_mfma_i8_32_kernel(int32_t* out) {
+  const int l = threadIdx.x;
+  int32x4 a = int32x4{}, b = int32x4{};
+  if (l < 32) {
+    a[0] = l | (64 << 8);
+    b[0] = 1 | (l << 8);
+  }
+  int32x16 acc = int32x16{};
+  acc = __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, acc, 0, 0, 0);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) out[1536 + l * 16 + r] = acc[r];
+}
+
 int launch_probe_mfma(int32_t* out, hipStream_t st) {
   hipLaunchKernelGGL(probe_mfma_kernel, dim3(1), dim3(64), 0, st, out);
   OZK_LAUNCH_CHECK();
   hipLaunchKernelGGL(probe_mfma16_kernel, dim3(1), dim3(64), 0, st, out);
   OZK_LAUNCH_CHECK();
   hipLaunchKernelGGL(probe_mfma_i8_kernel, dim3(1), dim3(64), 0, st, out);
+  OZK_LAUNCH_CHECK();
+  hipLaunchKernelGGL(probe_mfma_i8_32_kernel, dim3(1), dim3(64), 0, st, out);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }

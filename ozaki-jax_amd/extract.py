@@ -17,6 +17,7 @@ import numpy as np
 
 from . import _device as D
 from . import _lib
+from .lowlevel import Planes
 
 
 def _rho(K, m1):
@@ -83,9 +84,8 @@ def _extract(X, rho, n_slices, by_cols, f64):
                                      flags.data_ptr(), ws.data_ptr(), wsb,
                                      D.stream_handle())
         _lib.check(rc)
-    # BF16 bits -> float32 values; back to the input orientation.
-    vals = (S.to(D.torch.int32) << 16).view(D.torch.float32)
-    vals = vals[:, :lines, :length]
+    # chunk-major BF16 planes -> float32 values; back to the input orientation.
+    vals = Planes(S, E, lines, length, flags).values()
     if by_cols:
         vals = vals.transpose(1, 2)
     return vals.contiguous(), E[:, :lines], want_torch

@@ -14,11 +14,24 @@ ORDER_HOST_JAX = _lib.ORDER_HOST_JAX
 ORDER_HOST_NP = _lib.ORDER_HOST_NP
 
 
+CHUNK_BYTES = 64
+
+
+def unit_swizzle(line):
+    """Stored position of logical 16-byte unit 0 of `line` (XOR key)."""
+    r = line & 15
+    return ((r >> 1) ^ (r >> 2)) & 3
+
+
 class Planes:
     """Slice planes of one operand on the device.
 
-    s: (planes, lines_pad, ld) -- int16 BF16 bit patterns, or int8 grid
-    counts q = slice * 2^(24 - rho) when `rho` is set (INT8 format);
+    s: (planes, lines_pad, ld) storage of int16 BF16 bit patterns, or of int8
+    grid counts q = slice * 2^(24 - rho) when `rho` is set (INT8 format).
+    The bytes of a plane are chunk-major (64-byte chunks of k, chunk c of
+    every line together, the four 16-byte units of a line's chunk stored in
+    the order u ^ unit_swizzle(line)); grid() returns the plain
+    (planes, lines_pad, ld) arrangement.
     e: int32 (planes, lines_pad) exponents; lines / length: logical sizes.
     """
 
@@ -30,12 +43,26 @@ class Planes:
     def i8(self):
         return self.rho is not None
 
+    def grid(self):
+        """Plane elements as (planes, lines_pad, ld), line-major (device)."""
+        torch = D.torch
+        P, L, ld = self.s.shape
+        eb = self.s.element_size()
+        nch = ld * eb // CHUNK_BYTES
+        raw = self.s.contiguous().view(-1).view(torch.uint8).reshape(P, nch, L, 4, 16)
+        r = torch.arange(L, device=raw.device)
+        stored = torch.arange(4, device=raw.device)[None, :] ^ unit_swizzle(r)[:, None]
+        raw = raw[:, :, r[:, None], stored, :]
+        raw = raw.permute(0, 2, 1, 3, 4).contiguous().reshape(P, L, nch * CHUNK_BYTES)
+        return raw.view(self.s.dtype).reshape(P, L, ld)
+
     def values(self):
         """float32 (planes, lines, length) slice values (device)."""
+        g = self.grid()
         if self.i8:
-            v = self.s.to(D.torch.float32) * 2.0 ** (self.rho - 24)
+            v = g.to(D.torch.float32) * 2.0 ** (self.rho - 24)
         else:
-            v = (self.s.to(D.torch.int32) << 16).view(D.torch.float32)
+            v = (g.to(D.torch.int32) << 16).view(D.torch.float32)
         return v[:, :self.lines, :self.length]
 
     def exponents(self):
@@ -117,11 +144,12 @@ def slice_products(a, b, pipeline, n_hi, n_lo):
 def probe_mfma_layout():
     """Accumulator registers after the layout-probe MFMAs, as int32 arrays
     (32x32x16 BF16: (64 lanes, 16 regs), values row + 64 col; 16x16x32 BF16:
-    (64, 4), row + 64 col; 16x16x64 INT8: (64, 4), row + 16 col)."""
+    (64, 4), row + 64 col; 16x16x64 INT8: (64, 4), row + 16 col; 32x32x32
+    INT8: (64 lanes, 16 regs), row + 64 col)."""
     lib = _lib.load()
     dev = D.require_gpu()
-    out = D.torch.zeros(64 * 16 + 2 * 64 * 4, dtype=D.torch.int32, device=dev)
+    out = D.torch.zeros(2 * 64 * 16 + 2 * 64 * 4, dtype=D.torch.int32, device=dev)
     _lib.check(lib.ozk_probe_mfma_layout(out.data_ptr(), D.stream_handle()))
     o = out.cpu().numpy()
     return (o[:1024].reshape(64, 16), o[1024:1280].reshape(64, 4),
-            o[1280:].reshape(64, 4))
+            o[1280:1536].reshape(64, 4), o[1536:].reshape(64, 16))

@@ -6,6 +6,7 @@ any device work (no compute calls are made here)."""
 import ctypes
 import re
 
+import numpy as np
 import pytest
 
 import oracle as O
@@ -118,3 +119,26 @@ def test_package_fails_loudly_without_gpu():
         pytest.skip("a GPU is present")
     with pytest.raises(RuntimeError, match="no CPU implementation"):
         ozk.matmul(np.eye(4), np.eye(4), pipeline="ondevice")
+
+
+@pytest.mark.parametrize("eb,lines,ld", [(1, 64, 64), (1, 128, 192), (2, 64, 64), (2, 192, 128)])
+def test_plane_layout_decode_matches_header_formula(eb, lines, ld):
+    """Planes.grid() inverts the chunk-major byte layout documented in
+    include/ozaki_amd.h: byte b of line r at ((b/64) L + r) 64 +
+    16 (((b%64)/16) ^ s(r)) + b%16."""
+    import torch
+    from ozaki_jax_amd.lowlevel import Planes
+    rng = np.random.RandomState(eb * 1000 + lines)
+    P = 2
+    dt = np.int8 if eb == 1 else np.int16
+    grid = rng.randint(-100, 100, size=(P, lines, ld)).astype(dt)
+    gb = grid.view(np.uint8).reshape(P, lines, ld * eb)
+    store = np.zeros((P, lines * ld * eb), np.uint8)
+    for r in range(lines):
+        s = (((r & 15) >> 1) ^ ((r & 15) >> 2)) & 3
+        for b in range(ld * eb):
+            off = ((b // 64) * lines + r) * 64 + 16 * (((b % 64) // 16) ^ s) + b % 16
+            store[:, off] = gb[:, r, b]
+    st = torch.from_numpy(store.view(dt).reshape(P, lines, ld).copy())
+    pl = Planes(st, None, lines, ld, None, rho=19 if eb == 1 else None)
+    assert np.array_equal(pl.grid().numpy(), grid)

@@ -61,12 +61,13 @@ def to_np(t):
 
 def test_mfma_output_layout(ll):
     case("probe_mfma_layout 32x32x16 / 16x16x32 bf16, 16x16x64 i8")
-    out, out16, out8 = ll.probe_mfma_layout()
+    out, out16, out8, out8_32 = ll.probe_mfma_layout()
     for lane in range(64):
         for r in range(16):
             row = 8 * (r // 4) + 4 * (lane // 32) + (r % 4)
             col = lane % 32
             assert out[lane, r] == row + 64 * col, (lane, r, out[lane, r])
+            assert out8_32[lane, r] == row + 64 * col, (lane, r, out8_32[lane, r])
         for r in range(4):
             row = 4 * (lane // 16) + r
             col = lane % 16
@@ -179,12 +180,13 @@ def test_extract_f32_i8_rows_and_cols(ll, kind, shape, rho_fixed):
         sl, el = O.extract_rows_f32(lo, rho, 1)
         ref = np.concatenate([sh, sl]).astype(np.float64) * 2.0 ** (24 - rho)
         assert np.all(np.abs(ref) <= 64) and np.array_equal(ref, np.round(ref))
-        q = to_np(pl.s)[:, :shape[0], :shape[1]]
+        q = to_np(pl.grid())[:, :shape[0], :shape[1]]
         assert np.array_equal(q, ref.astype(np.int8)), "int8 slices"
         assert np.array_equal(to_np(pl.exponents()),
                               np.concatenate([eh, el]).astype(np.int32)), "exponents"
         # padding stays zero (the GEMM reads it)
-        assert not to_np(pl.s)[:, :, shape[1]:].any()
+        g = to_np(pl.grid())
+        assert not g[:, :, shape[1]:].any() and not g[:, shape[0]:, :].any()
 
 
 def test_extract_i8_rejects_coarse_grid(ll):
