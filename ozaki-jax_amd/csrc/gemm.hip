@@ -403,15 +403,59 @@ struct AllPairsMMA {
     }
   }
 
+  // Opening of a stage: the pairs of A slot 0 walk the B slots (both row
+  // blocks per B slot), so the first MFMA needs only B0 and A0's two
+  // fragments; later B fragments are read two pairs ahead and the A ring for
+  // blocks 2.. is filled on the way.
+  static constexpr int count_a0() {
+    int n = 0;
+    for (int p = 0; p < NP; ++p) n += pair_info(PIPE, NHI, NLO, p).a == 0;
+    return n;
+  }
+  static constexpr int a0_pair(int k) {  // k-th pair of A slot 0
+    for (int p = 0; p < NP; ++p)
+      if (pair_info(PIPE, NHI, NLO, p).a == 0 && k-- == 0) return p;
+    return -1;
+  }
+  static constexpr int kA0 = count_a0();
+
+  __device__ __forceinline__ uint4 read_b(const uint4* buf, int s) const {
+    return buf[((NT + s) * 4 + wc) * 64 + fl];
+  }
+
+  template <int K>
+  __device__ __forceinline__ void opening(const uint4* buf, uint4 (&af)[kDepth + 1],
+                                          uint4 (&bf)[NT]) {
+    if constexpr (K < kA0) {
+      constexpr int p = a0_pair(K);
+      constexpr int b = pair_info(PIPE, NHI, NLO, p).b;
+      if constexpr (K + 2 < kA0) {
+        constexpr int b2 = pair_info(PIPE, NHI, NLO, a0_pair(K + 2)).b;
+        bf[b2] = read_b(buf, b2);
+      }
+      if constexpr (K == kA0 - 2) af[2] = read_a(buf, 2);
+      if constexpr (K == kA0 - 1) af[3] = read_a(buf, 3);
+      acc[p][0] = Op::mma(af[0], bf[b], acc[p][0]);
+      if constexpr (K == kA0 - 1) af[0] = read_a(buf, 4);
+      acc[p][1] = Op::mma(af[1], bf[b], acc[p][1]);
+      __builtin_amdgcn_sched_barrier(0);
+      opening<K + 1>(buf, af, bf);
+    }
+  }
+
   __device__ __forceinline__ void operator()(const uint4* buf) {
+    static_assert(kDepth == 3, "the opening fills ring slots 2, 3, 0");
     uint4 bf[NT];
-#pragma unroll
-    for (int s = 0; s < NT; ++s) bf[s] = buf[((NT + s) * 4 + wc) * 64 + fl];
     uint4 af[kDepth + 1];
-#pragma unroll
-    for (int j = 0; j < kDepth; ++j) af[j] = read_a(buf, j);
+    constexpr int b0 = pair_info(PIPE, NHI, NLO, a0_pair(0)).b;
+    constexpr int b1 = pair_info(PIPE, NHI, NLO, a0_pair(1)).b;
+    bf[b0] = read_b(buf, b0);
+    af[0] = read_a(buf, 0);
+    af[1] = read_a(buf, 1);
+    bf[b1] = read_b(buf, b1);
     __builtin_amdgcn_sched_barrier(0);
-    pipe_step<0>(buf, af, bf);
+    opening<0>(buf, af, bf);
+    pipe_step<2>(buf, af, bf);
   }
 };
 
