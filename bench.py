@@ -56,6 +56,13 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="also run a plain 1 GiB device copy (elementwise "
                          "kernel) to calibrate HBM byte counters")
+    ap.add_argument("--suite", action="store_true",
+                    help="instead of the metric line, time every workload "
+                         "configuration (host 256, 4096 high, 8192 medium/max "
+                         "wide range, gram / residual 32768x2048, long K, "
+                         "solve) and print one JSON line each")
+    ap.add_argument("--suite-out", default=None,
+                    help="also write the suite's JSON lines to this file")
     return ap.parse_args()
 
 
@@ -107,8 +114,147 @@ def accuracy_rows(A, B, C, precision, rows):
             float(np.max(np.abs(C - Ar @ B) / scale)), rho)
 
 
+def _timeit(fn, reps, sync):
+    fn()
+    sync()
+    t0 = time.perf_counter()
+    for _ in range(reps):
+        fn()
+    sync()
+    return (time.perf_counter() - t0) / reps
+
+
+def _wide(rs, shape, phi):
+    return (rs.rand(*shape) - 0.5) * np.exp(phi * rs.randn(*shape))
+
+
+def suite(args):
+    """Times each workload configuration on HBM-resident inputs (NumPy-in
+    configurations also with their transfers) and checks sampled rows against
+    the oracle in the same accumulation order."""
+    import torch
+    import oracle
+    from oracle import pipeline as OP
+    import ozaki_jax_amd as ozk
+
+    torch.cuda.set_device(0)
+    dev = torch.device("cuda", 0)
+    sync = torch.cuda.synchronize
+    out = []
+
+    def emit(d):
+        line = json.dumps(d)
+        print(line, flush=True)
+        out.append(line)
+
+    def scaled_err(C, ref, A, B):
+        return float(np.max(np.abs(C - ref) / (np.abs(A) @ np.abs(B))))
+
+    # 0: matmul_numpy host pipeline, n_slices=8, 256^3, RandomState(0)
+    rs = np.random.RandomState(0)
+    A, B = rs.randn(256, 256), rs.randn(256, 256)
+    log("suite: host 256")
+    t = _timeit(lambda: ozk.matmul_numpy(A, B), 10, sync)
+    C = ozk.matmul_numpy(A, B)
+    t0 = time.perf_counter()
+    ref = oracle.matmul_numpy(A, B)
+    t_cpu = time.perf_counter() - t0
+    emit({"config": "matmul_numpy host n_slices=8 256^3 N(0,1) seed 0",
+          "ms": t * 1e3, "bit_exact_vs_oracle": bool(np.array_equal(C, ref)),
+          "oracle_cpu_ms": t_cpu * 1e3, "note": "NumPy in/out, transfers included"})
+
+    def ondevice(name, A, B, precision, rows, phi=None):
+        At = torch.from_numpy(A).to(dev)
+        Bt = torch.from_numpy(B).to(dev)
+        n, k = A.shape
+        m = B.shape[1]
+        reps = 5 if n * k * m <= 4096 ** 3 else 3
+        log(f"suite: {name}")
+        t = _timeit(lambda: ozk.matmul(At, Bt, pipeline="ondevice", precision=precision),
+                    reps, sync)
+        C = ozk.matmul(At, Bt, pipeline="ondevice", precision=precision)
+        Cr = C[rows].cpu().numpy()
+        nh, nl = OP.resolve_precision(precision)
+        ref = oracle.matmul_ondevice_a4(A[rows], B, "raise", nh, nl)
+        t_dg = _timeit(lambda: torch.matmul(At, Bt), 3, sync)
+        d = {"config": name, "ms": t * 1e3, "fp64_eq_tflops": 2.0 * n * k * m / t / 1e12,
+             "rocblas_dgemm_ms": t_dg * 1e3,
+             "max_scaled_err_vs_oracle": scaled_err(Cr, ref, A[rows], B),
+             "max_scaled_err_vs_fp64": scaled_err(Cr, A[rows] @ B, A[rows], B),
+             "rows_checked": len(rows)}
+        del At, Bt, C
+        return d
+
+    # 1: 4096^3 high, N(0,1)
+    rs = np.random.RandomState(0)
+    A, B = rs.randn(4096, 4096), rs.randn(4096, 4096)
+    emit(ondevice("matmul ondevice fused high 4096^3 N(0,1)", A, B, "high",
+                  np.linspace(0, 4095, 4).astype(int)))
+    # 2: 8192^3 medium / max, (U - 0.5) exp(phi N), phi in {0.5, 4} for A and B
+    n = 8192
+    rows = np.array([0, 4095, 8191])
+    for pa in (0.5, 4.0):
+        for pb in (0.5, 4.0):
+            rs = np.random.RandomState(1)
+            A = _wide(rs, (n, n), pa)
+            B = _wide(rs, (n, n), pb)
+            for prec in ("medium", "max"):
+                d = ondevice(f"matmul ondevice fused {prec} 8192^3 wide phi_A={pa} phi_B={pb}",
+                             A, B, prec, rows)
+                emit(d)
+    del A, B
+    # 3: gram 32768 x 2048 and residual, N(0,1)
+    rs = np.random.RandomState(0)
+    A = rs.randn(32768, 2048)
+    x, b = rs.randn(2048), rs.randn(32768)
+    At = torch.from_numpy(A).to(dev)
+    xt, bt = torch.from_numpy(x).to(dev), torch.from_numpy(b).to(dev)
+    log("suite: gram / residual 32768x2048")
+    t = _timeit(lambda: ozk.gram(At, mode="ozaki"), 3, sync)
+    G = ozk.gram(At, mode="ozaki").cpu().numpy()
+    cols = np.array([0, 1023, 2047])
+    Gref = oracle.gram_ozaki(A, "high")
+    emit({"config": "gram ozaki high 32768x2048 N(0,1)", "ms": t * 1e3,
+          "fp64_eq_tflops": 2.0 * 2048 * 2048 * 32768 / t / 1e12,
+          "bit_exact_vs_oracle": bool(np.array_equal(G[cols], Gref[cols]))})
+    t = _timeit(lambda: ozk.residual(At, xt, bt, mode="ozaki"), 5, sync)
+    r = ozk.residual(At, xt, bt, mode="ozaki").cpu().numpy()
+    emit({"config": "residual ozaki high 32768x2048 N(0,1)", "ms": t * 1e3,
+          "GB_per_s_of_A": A.nbytes / t / 1e9,
+          "bit_exact_vs_oracle": bool(np.array_equal(r, oracle.residual_ozaki(A, x, b)))})
+    del At, G, Gref
+    # 4: long K 1024 x 65536 x 1024 high, (U - 0.5) exp(2 N); solve n=4096 cond 1e6
+    rs = np.random.RandomState(2)
+    A = _wide(rs, (1024, 65536), 2.0)
+    B = _wide(rs, (65536, 1024), 2.0)
+    emit(ondevice("matmul ondevice fused high long-K 1024x65536x1024 wide phi=2", A, B,
+                  "high", np.array([0, 511, 1023])))
+    rs = np.random.RandomState(3)
+    nn = 4096
+    Q1, _ = np.linalg.qr(rs.randn(nn, nn))
+    Q2, _ = np.linalg.qr(rs.randn(nn, nn))
+    As = (Q1 * np.logspace(0, 6, nn)) @ Q2.T
+    bs = rs.randn(nn)
+    Ast, bst = torch.from_numpy(As).to(dev), torch.from_numpy(bs).to(dev)
+    log("suite: solve 4096 cond 1e6")
+    t = _timeit(lambda: ozk.solve(Ast, bst, residual_mode="ozaki"), 3, sync)
+    xs = ozk.solve(Ast, bst, residual_mode="ozaki").cpu().numpy()
+    xr = np.linalg.solve(As, bs)
+    emit({"config": "solve residual_mode=ozaki n=4096 cond 1e6", "ms": t * 1e3,
+          "rel_err_vs_lapack_fp64": float(np.linalg.norm(xs - xr) / np.linalg.norm(xr))})
+    if args.suite_out:
+        Path(args.suite_out).write_text("\n".join(out) + "\n")
+
+
 def main():
     args = parse_args()
+    if args.suite:
+        if args.gpus != 1:
+            print(json.dumps({"error": "this build runs on one GPU only; "
+                              "--gpus must be 1"}))
+            sys.exit(2)
+        suite(args)
+        return
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; "
                           "--gpus must be 1"}))
