@@ -117,22 +117,31 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * matmul_numpy host loop (matmul.py:879-898).  A planes are rows of A
  * (N lines), B planes are columns of B (M lines); both of length K.
  * The drivers below use INT8 planes (ozk_gemm_i8) instead when the
- * contraction length gives rho >= 19 and the schedule is a preset. */
+ * contraction length gives rho >= 19 and the schedule is a preset.
+ *
+ * The on-device presets high (4,1) and medium (3,1) run in one K sweep;
+ * max (5,4) runs its hh, hl and lh blocks (matmul.py:670-674) as three
+ * sweeps and keeps the fold state between them in the workspace
+ * (ozk_gemm_workspace_bytes; 0 bytes for the other schedules). */
+size_t ozk_gemm_workspace_bytes(int64_t N, int64_t M, int pipeline, int n_hi,
+                                int n_lo, int order);
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
              const uint16_t* b_slices, const int32_t* b_exps,
              int64_t N, int64_t M, int64_t K,
              int pipeline, int n_hi, int n_lo, int order,
-             double* C, int64_t ldc, void* stream);
+             double* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+             void* stream);
 
 /* ozk_gemm on INT8 planes (ozk_extract_f32_i8 with the same rho): INT8 MFMA
  * with exact INT32 sums; each pair product is the integer sum times
  * 2^(2 rho - 48), the FP32 product of the BF16 path whenever that one is
- * exact.  On-device preset schedules (4,1) and (3,1). */
+ * exact.  On-device preset schedules (4,1), (3,1) and (5,4). */
 int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
                 const int8_t* b_slices, const int32_t* b_exps,
                 int64_t N, int64_t M, int64_t K, int rho,
                 int n_hi, int n_lo, int order,
-                double* C, int64_t ldc, void* stream);
+                double* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+                void* stream);
 
 /* Test hook: the per-pair FP32 products P[p] = S^A_a(p) . S^B_b(p) written
  * to P[p][N][ldp] in schedule order (matmul.py:216-233, :757-773, :885-887). */

@@ -52,10 +52,14 @@ SIGNATURES = {
                                  _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_size,
                                  _c_vp]),
     "ozk_pair_count": (_c_int, [_c_int, _c_int, _c_int]),
+    "ozk_gemm_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_int, _c_int,
+                                           _c_int]),
     "ozk_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
-                          _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
+                          _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp,
+                          _c_size, _c_vp]),
     "ozk_gemm_i8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
-                             _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
+                             _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp,
+                             _c_size, _c_vp]),
     "ozk_slice_products_i8": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                        _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_slice_products": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,

@@ -33,7 +33,9 @@ bool allpairs_supported(int pipe, int nhi, int nlo);
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
-                hipStream_t st, bool i8, int rho);
+                void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho);
+size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
+                            int order);
 int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho);
@@ -146,7 +148,7 @@ extern "C" {
 
 const char* ozk_last_error(void) { return g_error.c_str(); }
 
-int ozk_abi_version(void) { return 1; }
+int ozk_abi_version(void) { return 2; }
 
 int ozk_device_info(char* buf, size_t len, int* cu_count) {
   clear_error();
@@ -236,10 +238,17 @@ int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
                          (hipStream_t)stream, false);
 }
 
+size_t ozk_gemm_workspace_bytes(int64_t N, int64_t M, int pipeline, int n_hi,
+                                int n_lo, int order) {
+  if (N < 0 || M < 0) return 0;
+  return gemm_workspace_bytes(N, M, pipeline, n_hi, n_lo, order);
+}
+
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
              const uint16_t* b_slices, const int32_t* b_exps, int64_t N,
              int64_t M, int64_t K, int pipeline, int n_hi, int n_lo, int order,
-             double* C, int64_t ldc, void* stream) {
+             double* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+             void* stream) {
   clear_error();
   int rc = check_counts(pipeline, n_hi, n_lo);
   if (rc) return rc;
@@ -249,13 +258,15 @@ int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
   OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
   if (N == 0 || M == 0) return OZK_OK;
   return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K, pipeline,
-                     n_hi, n_lo, order, C, ldc, (hipStream_t)stream, false, 0);
+                     n_hi, n_lo, order, C, ldc, workspace, workspace_bytes,
+                     (hipStream_t)stream, false, 0);
 }
 
 int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
                 const int8_t* b_slices, const int32_t* b_exps, int64_t N,
                 int64_t M, int64_t K, int rho, int n_hi, int n_lo, int order,
-                double* C, int64_t ldc, void* stream) {
+                double* C, int64_t ldc, void* workspace, size_t workspace_bytes,
+                void* stream) {
   clear_error();
   int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
   if (rc) return rc;
@@ -270,8 +281,8 @@ int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
   }
   if (N == 0 || M == 0) return OZK_OK;
   return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K,
-                     OZK_PIPE_ONDEVICE, n_hi, n_lo, order, C, ldc,
-                     (hipStream_t)stream, true, rho);
+                     OZK_PIPE_ONDEVICE, n_hi, n_lo, order, C, ldc, workspace,
+                     workspace_bytes, (hipStream_t)stream, true, rho);
 }
 
 int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
@@ -306,16 +317,22 @@ int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
 
 static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
                         int nlo, bool carve, void* ws, SliceSet* a,
-                        SliceSet* b, void** tws) {
+                        SliceSet* b, void** tws, void** gws = nullptr,
+                        size_t* gwsb = nullptr) {
   const int planes = pipeline == OZK_PIPE_ONDEVICE ? nhi + nlo : nhi;
   const size_t eb = use_i8(pipeline, K, nhi, nlo) ? 1 : 2;
   Carver c(carve ? ws : nullptr);
   SliceSet sa = carve_slices(c, planes, N, K, eb);
   SliceSet sb = carve_slices(c, planes, M, K, eb);
   void* t = c.take(extract_workspace_bytes(K, M, 1));
+  // fold state between sweeps; the 2Sum state bounds every order's
+  const size_t gb = gemm_workspace_bytes(N, M, pipeline, nhi, nlo, OZK_ORDER_2SUM);
+  void* g = c.take(gb);
   if (a) *a = sa;
   if (b) *b = sb;
   if (tws) *tws = t;
+  if (gws) *gws = g;
+  if (gwsb) *gwsb = gb;
   return c.off;
 }
 
@@ -349,8 +366,10 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
     return OZK_ERR_WORKSPACE;
   }
   SliceSet sa, sb;
-  void* tws;
-  matmul_ws(N, K, M, pipeline, n_hi, n_lo, true, workspace, &sa, &sb, &tws);
+  void *tws, *gws;
+  size_t gwsb;
+  matmul_ws(N, K, M, pipeline, n_hi, n_lo, true, workspace, &sa, &sb, &tws, &gws,
+            &gwsb);
   const size_t tbytes = extract_workspace_bytes(K, M, 1);
   const bool i8 = use_i8(pipeline, K, n_hi, n_lo);
   int rho;
@@ -372,17 +391,23 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
       return rc;
   }
   return launch_gemm(sa.s, sa.e, sb.s, sb.e, N, M, K, pipeline, n_hi, n_lo,
-                     order, C, ldc, st, i8, rho);
+                     order, C, ldc, gws, gwsb, st, i8, rho);
 }
 
 static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,
-                      SliceSet* s, void** tws) {
+                      SliceSet* s, void** tws, void** gws = nullptr,
+                      size_t* gwsb = nullptr) {
   Carver c(ws);
   SliceSet ss = carve_slices(c, nhi + nlo, cols, rows,
                              use_i8(OZK_PIPE_ONDEVICE, rows, nhi, nlo) ? 1 : 2);
   void* t = c.take(extract_workspace_bytes(rows, cols, 1));
+  const size_t gb = gemm_workspace_bytes(cols, cols, OZK_PIPE_ONDEVICE, nhi, nlo,
+                                         OZK_ORDER_2SUM);
+  void* g = c.take(gb);
   if (s) *s = ss;
   if (tws) *tws = t;
+  if (gws) *gws = g;
+  if (gwsb) *gwsb = gb;
   return c.off;
 }
 
@@ -412,8 +437,9 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
     return OZK_ERR_WORKSPACE;
   }
   SliceSet s;
-  void* tws;
-  gram_ws(rows, cols, n_hi, n_lo, workspace, &s, &tws);
+  void *tws, *gws;
+  size_t gwsb;
+  gram_ws(rows, cols, n_hi, n_lo, workspace, &s, &tws, &gws, &gwsb);
   // Row extraction of A^T == column extraction of A: one set of slices is
   // both operands (gram.py:22-35 extracts the same values twice).
   const int rho = rho_generic(rows, 24);
@@ -423,7 +449,7 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
                            i8)))
     return rc;
   if ((rc = launch_gemm(s.s, s.e, s.s, s.e, cols, cols, rows, OZK_PIPE_ONDEVICE,
-                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, st, i8, rho)))
+                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, gws, gwsb, st, i8, rho)))
     return rc;
   hipLaunchKernelGGL(symmetrize_kernel, dim3(grid_for(cols * cols)), dim3(256),
                      0, st, G, cols, ldg);
@@ -433,17 +459,23 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
 
 static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
                           int nlo, void* ws, SliceSet* a, SliceSet* x,
-                          double** y, void** tws) {
+                          double** y, void** tws, void** gws = nullptr,
+                          size_t* gwsb = nullptr) {
   Carver c(ws);
   const size_t eb = use_i8(OZK_PIPE_ONDEVICE, K, nhi, nlo) ? 1 : 2;
   SliceSet sa = carve_slices(c, nhi + nlo, N, K, eb);
   SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
   double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
   void* t = c.take(extract_workspace_bytes(K, ncols, 1));
+  const size_t gb = gemm_workspace_bytes(N, ncols, OZK_PIPE_ONDEVICE, nhi, nlo,
+                                         OZK_ORDER_2SUM);
+  void* g = c.take(gb);
   if (a) *a = sa;
   if (x) *x = sx;
   if (y) *y = yy;
   if (tws) *tws = t;
+  if (gws) *gws = g;
+  if (gwsb) *gwsb = gb;
   return c.off;
 }
 
@@ -477,8 +509,9 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   }
   SliceSet sa, sx;
   double* y;
-  void* tws;
-  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws);
+  void *tws, *gws;
+  size_t gwsb;
+  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws, &gws, &gwsb);
   const int rho = rho_generic(K, 24);
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
   if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
@@ -489,7 +522,7 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
                            i8)))
     return rc;
   if ((rc = launch_gemm(sa.s, sa.e, sx.s, sx.e, N, ncols, K, OZK_PIPE_ONDEVICE,
-                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, st, i8, rho)))
+                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, gws, gwsb, st, i8, rho)))
     return rc;
   hipLaunchKernelGGL(sub_from_kernel, dim3(grid_for(N * ncols)), dim3(256), 0,
                      st, b, ldb, y, ncols, r, ldr, N, ncols);

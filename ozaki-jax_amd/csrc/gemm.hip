@@ -336,64 +336,67 @@ __device__ __forceinline__ uint32_t lds_offset(const void* p) {
   return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
 }
 
-// Fetch stage `st` (chunk st of every line of the tile) into the LDS buffer
-// at byte offset `buf_lds`: wave w moves fragments F = w + 8 i, i.e. slot
-// 2 i + (w >> 2), line group w & 3, each a contiguous 1 KiB of the plane.
-// At, Bt point at the tile's first line in chunk 0; chunk st lies
-// st * a_stage / st * b_stage bytes further.  All addresses lie inside the
-// zero-padded slice planes.
-template <int NT>
-__device__ __forceinline__ void stage_dma(const char* At, int64_t aplane,
-                                          int64_t a_stage, const char* Bt,
-                                          int64_t bplane, int64_t b_stage,
-                                          int64_t st, uint32_t buf_lds,
-                                          int wave, uint32_t lane_bytes) {
-  const int64_t g = (int64_t)(wave & 3) * 1024;
-  const int64_t qa = st * a_stage + g, qb = st * b_stage + g;
-#pragma unroll
-  for (int i = 0; i < NT; ++i) {
-    const int slot = 2 * i + (wave >> 2);
-    const char* base = slot < NT ? At + slot * aplane + qa : Bt + (slot - NT) * bplane + qb;
-    const int F = 8 * i + wave;
-    dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024), (const void*)base,
-          lane_bytes);
-  }
-}
-
 // uint4 index inside a 1 KiB fragment of the 16x16x64 operand of lane l:
 // line l % 16, logical unit l / 16.
 __device__ __forceinline__ int frag_lane(int lane) {
   return (lane & 15) * 4 + ((lane >> 4) ^ unit_swizzle(lane & 15));
 }
 
-template <class Op, int PIPE, int NHI, int NLO, int NT, int NP>
+// Pairs and planes of one K sweep over the blocks B0..B1 of the on-device
+// schedule (0 hh, 1 hl, 2 lh; each block is a contiguous pair range).  Block
+// hh uses the hi planes of A and B, hl the hi planes of A and the lo planes
+// of B, lh the lo planes of A and the hi planes of B; a sweep stages exactly
+// the planes its blocks use.
+template <int PIPE, int NHI, int NLO, int B0, int B1>
+struct Sweep {
+  static_assert(PIPE == OZK_PIPE_ONDEVICE, "sweeps cover the on-device schedule");
+  static constexpr int A0 = B0 == 2 ? NHI : 0;                    // first A plane
+  static constexpr int NA = (B1 == 2 ? NHI + NLO : NHI) - A0;     // A planes
+  static constexpr int BB = (B0 == 1 && B1 == 1) ? NHI : 0;       // first B plane
+  static constexpr int NB = ((B0 <= 1 && B1 >= 1) ? NHI + NLO : NHI) - BB;
+  static constexpr int P0 = B0 == 0 ? 0 : (B0 == 1 ? NHI * NHI : NHI * NHI + NHI * NLO);
+  static constexpr int P1 = B1 == 0 ? NHI * NHI
+                                    : (B1 == 1 ? NHI * NHI + NHI * NLO
+                                               : NHI * NHI + 2 * NHI * NLO);
+  static constexpr int NP = P1 - P0;  // pairs of the sweep
+  static constexpr int S = NA + NB;   // LDS slots per stage
+  static constexpr PairInfo pair(int k) { return pair_info(PIPE, NHI, NLO, P0 + k); }
+  static constexpr int la(int k) { return pair(k).a - A0; }  // local A slot
+  static constexpr int lb(int k) { return pair(k).b - BB; }  // local B slot
+};
+
+template <class Op, class SW>
 struct AllPairsMMA {
+  static constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
   typename Op::acc_t acc[NP][2];
   int fl, wr, wc;  // fl = frag_lane(lane)
 
   // MFMAs of one (A slot, row block) for every pair of that A slot.
   template <int SA, int H>
-  __device__ __forceinline__ void block(uint4 af, const uint4 (&bf)[NT]) {
+  __device__ __forceinline__ void block(uint4 af, const uint4 (&bf)[NB]) {
 #pragma unroll
-    for (int p = 0; p < NP; ++p) {
-      const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-      if (q.a == SA) acc[p][H] = Op::mma(af, bf[q.b], acc[p][H]);
-    }
+    for (int k = 0; k < NP; ++k)
+      if (SW::la(k) == SA) acc[k][H] = Op::mma(af, bf[SW::lb(k)], acc[k][H]);
   }
 
-  // The NT * 2 blocks of a stage, A fragments software-pipelined through
-  // kDepth + 1 registers: the read of block j + kDepth is issued before the
-  // MFMAs of block j.  Scheduling barriers keep the reads where they are.
-  static constexpr int kBlocks = NT * 2, kDepth = 3;
+  // The 2 NA blocks of a stage (A slot j >> 1, row block j & 1), A fragments
+  // software-pipelined through kDepth + 1 registers: the read of block
+  // j + kDepth is issued before the MFMAs of block j.  Scheduling barriers
+  // keep the reads where they are.
+  static constexpr int kBlocks = NA * 2, kDepth = 3;
+  static_assert(kBlocks >= kDepth + 2, "the opening fills blocks 2 .. 4");
 
   __device__ __forceinline__ uint4 read_a(const uint4* buf, int j) const {
     return buf[((j >> 1) * 4 + 2 * wr + (j & 1)) * 64 + fl];
+  }
+  __device__ __forceinline__ uint4 read_b(const uint4* buf, int s) const {
+    return buf[((NA + s) * 4 + wc) * 64 + fl];
   }
 
   template <int J>
   __device__ __forceinline__ void pipe_step(const uint4* buf,
                                             uint4 (&af)[kDepth + 1],
-                                            const uint4 (&bf)[NT]) {
+                                            const uint4 (&bf)[NB]) {
     if constexpr (J < kBlocks) {
       if constexpr (J + kDepth < kBlocks)
         af[(J + kDepth) % (kDepth + 1)] = read_a(buf, J + kDepth);
@@ -404,40 +407,37 @@ struct AllPairsMMA {
   }
 
   // Opening of a stage: the pairs of A slot 0 walk the B slots (both row
-  // blocks per B slot), so the first MFMA needs only B0 and A0's two
+  // blocks per B slot), so the first MFMA needs only one B and A slot 0's two
   // fragments; later B fragments are read two pairs ahead and the A ring for
   // blocks 2.. is filled on the way.
   static constexpr int count_a0() {
     int n = 0;
-    for (int p = 0; p < NP; ++p) n += pair_info(PIPE, NHI, NLO, p).a == 0;
+    for (int k = 0; k < NP; ++k) n += SW::la(k) == 0;
     return n;
   }
-  static constexpr int a0_pair(int k) {  // k-th pair of A slot 0
-    for (int p = 0; p < NP; ++p)
-      if (pair_info(PIPE, NHI, NLO, p).a == 0 && k-- == 0) return p;
+  static constexpr int a0_pair(int i) {  // i-th pair of A slot 0
+    for (int k = 0; k < NP; ++k)
+      if (SW::la(k) == 0 && i-- == 0) return k;
     return -1;
   }
   static constexpr int kA0 = count_a0();
-
-  __device__ __forceinline__ uint4 read_b(const uint4* buf, int s) const {
-    return buf[((NT + s) * 4 + wc) * 64 + fl];
-  }
+  static_assert(kA0 >= 2, "A slot 0 pairs with at least two B slots");
 
   template <int K>
   __device__ __forceinline__ void opening(const uint4* buf, uint4 (&af)[kDepth + 1],
-                                          uint4 (&bf)[NT]) {
+                                          uint4 (&bf)[NB]) {
     if constexpr (K < kA0) {
-      constexpr int p = a0_pair(K);
-      constexpr int b = pair_info(PIPE, NHI, NLO, p).b;
+      constexpr int k = a0_pair(K);
+      constexpr int b = SW::lb(k);
       if constexpr (K + 2 < kA0) {
-        constexpr int b2 = pair_info(PIPE, NHI, NLO, a0_pair(K + 2)).b;
+        constexpr int b2 = SW::lb(a0_pair(K + 2));
         bf[b2] = read_b(buf, b2);
       }
       if constexpr (K == kA0 - 2) af[2] = read_a(buf, 2);
       if constexpr (K == kA0 - 1) af[3] = read_a(buf, 3);
-      acc[p][0] = Op::mma(af[0], bf[b], acc[p][0]);
+      acc[k][0] = Op::mma(af[0], bf[b], acc[k][0]);
       if constexpr (K == kA0 - 1) af[0] = read_a(buf, 4);
-      acc[p][1] = Op::mma(af[1], bf[b], acc[p][1]);
+      acc[k][1] = Op::mma(af[1], bf[b], acc[k][1]);
       __builtin_amdgcn_sched_barrier(0);
       opening<K + 1>(buf, af, bf);
     }
@@ -445,10 +445,10 @@ struct AllPairsMMA {
 
   __device__ __forceinline__ void operator()(const uint4* buf) {
     static_assert(kDepth == 3, "the opening fills ring slots 2, 3, 0");
-    uint4 bf[NT];
+    uint4 bf[NB];
     uint4 af[kDepth + 1];
-    constexpr int b0 = pair_info(PIPE, NHI, NLO, a0_pair(0)).b;
-    constexpr int b1 = pair_info(PIPE, NHI, NLO, a0_pair(1)).b;
+    constexpr int b0 = SW::lb(a0_pair(0));
+    constexpr int b1 = SW::lb(a0_pair(1));
     bf[b0] = read_b(buf, b0);
     af[0] = read_a(buf, 0);
     af[1] = read_a(buf, 1);
@@ -459,34 +459,105 @@ struct AllPairsMMA {
   }
 };
 
-// vmcnt wait before consuming stage s: the loads of the `later` stages
-// already issued after it (each NT instructions per wave) may stay in flight.
-template <int NT>
+// Fetch stage `st` (chunk st of every line of the tile) into the LDS buffer
+// at byte offset `buf_lds`.  Fragment F (slot F / 4, line group F % 4) is a
+// contiguous 1 KiB of its plane; wave w moves F = w + 8 i for F < 4 S, i.e.
+// slot 2 i + (w >> 2), line group w & 3.  At, Bt point at the tile's first
+// line of the sweep's first A / B plane in chunk 0; chunk st lies
+// st * a_stage / st * b_stage bytes further.  All addresses lie inside the
+// zero-padded slice planes.
+template <int NA, int NB>
+__device__ __forceinline__ void stage_dma(const char* At, int64_t aplane,
+                                          int64_t a_stage, const char* Bt,
+                                          int64_t bplane, int64_t b_stage,
+                                          int64_t st, uint32_t buf_lds,
+                                          int wave, uint32_t lane_bytes) {
+  constexpr int kFrags = 4 * (NA + NB);
+  const int64_t g = (int64_t)(wave & 3) * 1024;
+  const int64_t qa = st * a_stage + g, qb = st * b_stage + g;
+#pragma unroll
+  for (int i = 0; i < (kFrags + 7) / 8; ++i) {
+    const int slot = 2 * i + (wave >> 2);
+    const int F = 8 * i + wave;
+    if (8 * i + 8 <= kFrags || F < kFrags) {
+      const char* base = slot < NA ? At + slot * aplane + qa : Bt + (slot - NA) * bplane + qb;
+      dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024), (const void*)base,
+            lane_bytes);
+    }
+  }
+}
+
+// vmcnt wait before consuming a stage: the loads of the `later` stages
+// already issued after it (PER instructions per wave each) may stay in
+// flight.
+template <int PER>
 __device__ __forceinline__ void wait_stage(int64_t later) {
-  if (later >= 2) wait_vm<2 * NT>();
-  else if (later == 1) wait_vm<NT>();
+  if (later >= 2) wait_vm<2 * PER>();
+  else if (later == 1) wait_vm<PER>();
   else wait_vm<0>();
 }
 
-// All pairs of the schedule in one K sweep (schedules whose accumulators fit
-// in registers).  PIPE/NHI/NLO fix the schedule at compile time.  ORDER < 0
-// writes the per-pair FP32 products P[p][row][col] instead of C (test hook).
+// Fold state at a block boundary, kept in a workspace between the sweeps of
+// one product: 2Sum order (ct, cl, p0, p1, p2) as FP32 fields, the FP64
+// block order the running sum c.  Field f of element (row, col) lies at
+// state[f * N * M + row * M + col].
+template <int ORDER> struct FoldState {  // the FP64 orders: the running sum
+  static constexpr int kBytes = 8;
+  static __device__ __forceinline__ void load(Fold64<ORDER>& f, const char* st, int64_t e,
+                                              int64_t) {
+    f.c = ((const double*)st)[e];
+  }
+  static __device__ __forceinline__ void store(const Fold64<ORDER>& f, char* st, int64_t e,
+                                               int64_t) {
+    ((double*)st)[e] = f.c;
+  }
+};
+
+template <> struct FoldState<OZK_ORDER_2SUM> {
+  static constexpr int kBytes = 5 * 4;
+  static __device__ __forceinline__ void load(Fold2Sum& f, const char* st, int64_t e,
+                                              int64_t nm) {
+    const float* s = (const float*)st;
+    f.ct = s[e];
+    f.cl = s[nm + e];
+    f.p0 = s[2 * nm + e];
+    f.p1 = s[3 * nm + e];
+    f.p2 = s[4 * nm + e];
+  }
+  static __device__ __forceinline__ void store(const Fold2Sum& f, char* st, int64_t e,
+                                               int64_t nm) {
+    float* s = (float*)st;
+    s[e] = f.ct;
+    s[nm + e] = f.cl;
+    s[2 * nm + e] = f.p0;
+    s[3 * nm + e] = f.p1;
+    s[4 * nm + e] = f.p2;
+  }
+};
+// One K sweep over blocks B0..B1 of the on-device schedule, every pair of
+// those blocks accumulated in registers.  ORDER < 0 writes the per-pair FP32
+// products P[p][row][col] instead (test hook).  A sweep that does not start
+// the schedule reloads the fold state from `state`; one that does not end it
+// stores the state there instead of writing C.  `nst` = chunks per line;
 // `unit2` is the product scale 2^(2 rho - 48) of the I8 format.
 constexpr int kOrderProducts = -1;
 
-template <class Op, int PIPE, int NHI, int NLO, int ORDER>
+template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1>
 __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     const char* __restrict__ As, const int32_t* __restrict__ Ae,
     const char* __restrict__ Bs, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t nst, int64_t a_lines, int64_t b_lines,
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
-    int64_t ldp) {
-  constexpr int NT = PIPE == OZK_PIPE_ONDEVICE ? NHI + NLO : NHI;
-  constexpr int NP = pair_count(PIPE, NHI, NLO);
-  constexpr int NBLK = PIPE == OZK_PIPE_ONDEVICE ? 3 : 1;
-  constexpr int kBuf = (NT + NT) * 4 * 64;  // uint4 per stage buffer
+    int64_t ldp, char* __restrict__ state) {
+  typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
+  constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
+  constexpr int NBLK = 3;
+  constexpr int kFrags = 4 * SW::S;
+  constexpr int kPerHi = (kFrags + 7) / 8, kPerLo = kFrags / 8;  // DMA per wave
+  constexpr int kBuf = SW::S * 4 * 64;  // uint4 per stage buffer
   static_assert(kRing == 4, "wait_stage assumes 4 stage buffers");
-  // NT = 5: 4 x 40 KiB, the whole 160 KiB LDS of a gfx950 CU.
+  static_assert(SW::S <= 10, "a stage holds at most 10 planes (160 KiB ring)");
+  // S = 10: 4 x 40 KiB, the whole 160 KiB LDS of a gfx950 CU.
   __shared__ uint4 lds[kRing * kBuf];
 
   const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
@@ -495,19 +566,21 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
   const int64_t a_stage = a_lines * kChunkBytes, b_stage = b_lines * kChunkBytes;
   const int64_t aplane = a_stage * nst, bplane = b_stage * nst;
-  const char* At = As + row0 * kChunkBytes;
-  const char* Bt = Bs + col0 * kChunkBytes;
+  const char* At = As + SW::A0 * aplane + row0 * kChunkBytes;
+  const char* Bt = Bs + SW::BB * bplane + col0 * kChunkBytes;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  AllPairsMMA<Op, PIPE, NHI, NLO, NT, NP> mma;
+  // waves 0 .. (kFrags % 8) - 1 issue one more load per stage
+  const bool extra = kPerHi != kPerLo && (8 * kPerLo + wave) < kFrags;
+  AllPairsMMA<Op, SW> mma;
   mma.fl = frag_lane(lane);
   mma.wr = wave >> 2;
   mma.wc = wave & 3;
 #pragma unroll
-  for (int p = 0; p < NP; ++p) {
-    mma.acc[p][0] = typename Op::acc_t{};
-    mma.acc[p][1] = typename Op::acc_t{};
+  for (int k = 0; k < NP; ++k) {
+    mma.acc[k][0] = typename Op::acc_t{};
+    mma.acc[k][1] = typename Op::acc_t{};
   }
 
   // Per stage s: wait for this wave's loads of stage s, barrier (stage s is
@@ -517,16 +590,17 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   const uint32_t lds0 = lds_offset(lds);
   for (int i = 0; i < kRing - 1; ++i)
     if (i < nst)
-      stage_dma<NT>(At, aplane, a_stage, Bt, bplane, b_stage, i,
-                    lds0 + i * kBuf * 16, wave, lane_bytes);
+      stage_dma<NA, NB>(At, aplane, a_stage, Bt, bplane, b_stage, i,
+                        lds0 + i * kBuf * 16, wave, lane_bytes);
   for (int64_t s = 0; s < nst; ++s) {
-    const int64_t later = nst - 1 - s;
-    wait_stage<NT>(later < kRing - 2 ? later : kRing - 2);
+    const int64_t later = nst - 1 - s < kRing - 2 ? nst - 1 - s : kRing - 2;
+    if (extra) wait_stage<kPerHi>(later);
+    else wait_stage<kPerLo>(later);
     __syncthreads();
     const int64_t fetch = s + kRing - 1;
     if (fetch < nst)
-      stage_dma<NT>(At, aplane, a_stage, Bt, bplane, b_stage, fetch,
-                    lds0 + (uint32_t)((fetch % kRing) * kBuf * 16), wave, lane_bytes);
+      stage_dma<NA, NB>(At, aplane, a_stage, Bt, bplane, b_stage, fetch,
+                        lds0 + (uint32_t)((fetch % kRing) * kBuf * 16), wave, lane_bytes);
     mma(lds + (s % kRing) * kBuf);
   }
 
@@ -541,34 +615,45 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
         const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
         if (row < N && col < M) {
 #pragma unroll
-          for (int p = 0; p < NP; ++p)
-            P[((int64_t)p * N + row) * ldp + col] = Op::product(mma.acc[p][h][r], unit2);
+          for (int k = 0; k < NP; ++k)
+            P[((int64_t)(SW::P0 + k) * N + row) * ldp + col] =
+                Op::product(mma.acc[k][h][r], unit2);
         }
       }
     }
   } else {
-    // Fold in schedule order and store.
-    int eb[NT];
+    // Fold in schedule order; carry the state to the next sweep or store C.
+    int eb[NB];
 #pragma unroll
-    for (int s = 0; s < NT; ++s) eb[s] = Be[s * b_lines + col];
+    for (int s = 0; s < NB; ++s) eb[s] = Be[(SW::BB + s) * b_lines + col];
+    const int64_t nm = N * M;
 #pragma unroll
     for (int h = 0; h < 2; ++h) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
-        int ea[NT];
+        const bool live = row < N && col < M;
+        int ea[NA];
 #pragma unroll
-        for (int s = 0; s < NT; ++s) ea[s] = Ae[s * a_lines + row];
+        for (int s = 0; s < NA; ++s) ea[s] = Ae[(SW::A0 + s) * a_lines + row];
         typename FoldOf<ORDER>::type f;
         f.init();
-#pragma unroll
-        for (int p = 0; p < NP; ++p) {
-          const PairInfo q = pair_info(PIPE, NHI, NLO, p);
-          f.pair(q, Op::product(mma.acc[p][h][r], unit2), ldexpf(1.0f, eb[q.b]),
-                 ldexpf(1.0f, ea[q.a]), ldexp(1.0, eb[q.b]), ldexp(1.0, ea[q.a]));
+        if constexpr (B0 > 0) {
+          if (live) FoldState<ORDER>::load(f, state, row * M + col, nm);
         }
-        const double out = f.finish(NBLK);
-        if (row < N && col < M) C[row * ldc + col] = out;
+#pragma unroll
+        for (int k = 0; k < NP; ++k) {
+          const PairInfo q = SW::pair(k);
+          const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
+          f.pair(q, Op::product(mma.acc[k][h][r], unit2), ldexpf(1.0f, ib),
+                 ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+        }
+        if constexpr (B1 < NBLK - 1) {
+          if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
+        } else {
+          const double out = f.finish(NBLK);
+          if (live) C[row * ldc + col] = out;
+        }
       }
     }
   }
@@ -687,74 +772,117 @@ __global__ void probe_mfma16_kernel(int32_t* out) {
 
 // ---------------------------------------------------------------- launch
 
-// Schedules with an all-pairs instantiation (accumulators fit in registers).
+// Schedules with an all-pairs instantiation: high (4,1) and medium (3,1)
+// in one sweep, max (5,4) in three (hh, hl, lh; at most 25 pairs and 10
+// planes each).
 static bool allpairs_schedule(int pipe, int nhi, int nlo) {
-  return pipe == OZK_PIPE_ONDEVICE && ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1));
+  return pipe == OZK_PIPE_ONDEVICE &&
+         ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1) || (nhi == 5 && nlo == 4));
 }
 
 bool allpairs_supported(int pipe, int nhi, int nlo) {
   return allpairs_schedule(pipe, nhi, nlo);
 }
 
+static int allpairs_sweeps(int nhi, int nlo) { return nhi == 5 && nlo == 4 ? 3 : 1; }
+
+static int fold_state_bytes(int order) {
+  return order == OZK_ORDER_2SUM ? FoldState<OZK_ORDER_2SUM>::kBytes
+                                 : FoldState<OZK_ORDER_BLOCK64>::kBytes;
+}
+
+size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
+                            int order) {
+  if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(nhi, nlo) == 1 ||
+      order < 0)
+    return 0;
+  return (size_t)N * (size_t)M * (size_t)fold_state_bytes(order);
+}
+
+struct ApArgs {
+  dim3 grid;
+  hipStream_t st;
+  const char *As, *Bs;
+  const int32_t *Ae, *Be;
+  int64_t N, M, nst, al, bl;
+  float unit2;
+  double* C;
+  int64_t ldc;
+  float* P;
+  int64_t ldp;
+  char* state;
+};
+
+template <class Op, int NHI, int NLO, int ORDER, int B0, int B1>
+static void launch_sweep(const ApArgs& a) {
+  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1>),
+                     a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
+                     a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state);
+}
+
 template <class Op, int NHI, int NLO, int ORDER>
-static void launch_ap(dim3 grid, hipStream_t st, const void* As,
-                      const int32_t* Ae, const void* Bs, const int32_t* Be,
-                      int64_t N, int64_t M, int64_t nst, int64_t al, int64_t bl,
-                      float unit2, double* C, int64_t ldc, float* P,
-                      int64_t ldp) {
-  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER>),
-                     grid, dim3(kThreads16), 0, st, (const char*)As, Ae,
-                     (const char*)Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P,
-                     ldp);
+static void launch_schedule(const ApArgs& a) {
+  if constexpr (NHI == 5 && NLO == 4) {
+    launch_sweep<Op, NHI, NLO, ORDER, 0, 0>(a);
+    launch_sweep<Op, NHI, NLO, ORDER, 1, 1>(a);
+    launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
+  } else {
+    launch_sweep<Op, NHI, NLO, ORDER, 0, 2>(a);
+  }
 }
 
 template <class Op, int NHI, int NLO>
-static void launch_ap_order(int order, dim3 grid, hipStream_t st,
-                            const void* As, const int32_t* Ae, const void* Bs,
-                            const int32_t* Be, int64_t N, int64_t M,
-                            int64_t nst, int64_t al, int64_t bl, float unit2,
-                            double* C, int64_t ldc, float* P, int64_t ldp) {
+static void launch_ap_order(int order, const ApArgs& a) {
   switch (order) {
-    case OZK_ORDER_2SUM:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_2SUM>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
-      break;
-    case OZK_ORDER_BLOCK64:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_BLOCK64>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
-      break;
-    case OZK_ORDER_HOST_JAX:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
-      break;
-    case OZK_ORDER_HOST_NP:
-      launch_ap<Op, NHI, NLO, OZK_ORDER_HOST_NP>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
-      break;
-    default:
-      launch_ap<Op, NHI, NLO, kOrderProducts>(grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, unit2, C, ldc, P, ldp);
-      break;
+    case OZK_ORDER_2SUM: launch_schedule<Op, NHI, NLO, OZK_ORDER_2SUM>(a); break;
+    case OZK_ORDER_BLOCK64: launch_schedule<Op, NHI, NLO, OZK_ORDER_BLOCK64>(a); break;
+    case OZK_ORDER_HOST_JAX: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a); break;
+    case OZK_ORDER_HOST_NP: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a); break;
+    default: launch_schedule<Op, NHI, NLO, kOrderProducts>(a); break;
   }
 }
 
 // All-pairs launch for a preset schedule; `i8` selects the INT8 plane
-// format (rho >= 19).  order = kOrderProducts writes P.
+// format (rho >= 19).  order = kOrderProducts writes P.  `state` holds
+// gemm_workspace_bytes() for multi-sweep schedules.
 static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
                            const void* Bs, const int32_t* Be, int64_t N,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
                            int order, double* C, int64_t ldc, float* P,
-                           int64_t ldp, hipStream_t st) {
-  // chunks per line: round_up(K, kKPad) elements of 1 or 2 bytes
-  const int64_t nst = round_up(K, kKPad) * (i8 ? 1 : 2) / kChunkBytes;
+                           int64_t ldp, void* state, size_t state_bytes,
+                           hipStream_t st) {
+  const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, nhi, nlo, order);
+  if (state_bytes < need || (need && !state)) {
+    set_error("gemm workspace of %zu bytes < %zu needed", state_bytes, need);
+    return OZK_ERR_WORKSPACE;
+  }
+  ApArgs a;
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
   const int64_t ntiles = (al / kBM) * (bl / kBN);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
-  const dim3 grid((unsigned)ntiles);
-  const float unit2 = ldexpf(1.0f, 2 * rho - 48);
-#define OZK_AP_ALL(Op)                                                              \
-  do {                                                                              \
-    if (nhi == 4)                                                                   \
-      launch_ap_order<Op, 4, 1>(order, grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, \
-                                unit2, C, ldc, P, ldp);                             \
-    else                                                                            \
-      launch_ap_order<Op, 3, 1>(order, grid, st, As, Ae, Bs, Be, N, M, nst, al, bl, \
-                                unit2, C, ldc, P, ldp);                             \
+  a.grid = dim3((unsigned)ntiles);
+  a.st = st;
+  a.As = (const char*)As;
+  a.Bs = (const char*)Bs;
+  a.Ae = Ae;
+  a.Be = Be;
+  a.N = N;
+  a.M = M;
+  // chunks per line: round_up(K, kKPad) elements of 1 or 2 bytes
+  a.nst = round_up(K, kKPad) * (i8 ? 1 : 2) / kChunkBytes;
+  a.al = al;
+  a.bl = bl;
+  a.unit2 = ldexpf(1.0f, 2 * rho - 48);
+  a.C = C;
+  a.ldc = ldc;
+  a.P = P;
+  a.ldp = ldp;
+  a.state = (char*)state;
+#define OZK_AP_ALL(Op)                                       \
+  do {                                                       \
+    if (nhi == 4) launch_ap_order<Op, 4, 1>(order, a);       \
+    else if (nhi == 3) launch_ap_order<Op, 3, 1>(order, a);  \
+    else launch_ap_order<Op, 5, 4>(order, a);                \
   } while (0)
   if (i8) OZK_AP_ALL(OpI8);
   else OZK_AP_ALL(OpBf16);
@@ -766,10 +894,10 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
-                hipStream_t st, bool i8, int rho) {
+                void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho) {
   if (allpairs_schedule(pipe, nhi, nlo))
     return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, order,
-                           C, ldc, nullptr, 0, st);
+                           C, ldc, nullptr, 0, ws, ws_bytes, st);
   if (i8) {
     set_error("int8 slice planes need a preset on-device schedule");
     return OZK_ERR_UNSUPPORTED;
@@ -803,7 +931,7 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t ldp, hipStream_t st, bool i8, int rho) {
   if (allpairs_schedule(pipe, nhi, nlo))
     return launch_allpairs(i8, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
-                           kOrderProducts, nullptr, 0, P, ldp, st);
+                           kOrderProducts, nullptr, 0, P, ldp, nullptr, 0, st);
   if (i8) {
     set_error("int8 slice planes need a preset on-device schedule");
     return OZK_ERR_UNSUPPORTED;

@@ -110,14 +110,18 @@ def gemm(a, b, pipeline, n_hi, n_lo, order):
     dev = a.s.device
     N, M, K = a.lines, b.lines, a.length
     C = D.torch.empty((N, M), dtype=D.torch.float64, device=dev)
+    wsb = lib.ozk_gemm_workspace_bytes(N, M, pipeline, n_hi, n_lo, order)
+    ws = D.workspace(wsb, dev)
     if a.i8:
         rc = lib.ozk_gemm_i8(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
                              b.e.data_ptr(), N, M, K, a.rho, n_hi, n_lo, order,
-                             C.data_ptr(), max(M, 1), D.stream_handle())
+                             C.data_ptr(), max(M, 1), ws.data_ptr(), wsb,
+                             D.stream_handle())
     else:
         rc = lib.ozk_gemm(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
                           b.e.data_ptr(), N, M, K, pipeline, n_hi, n_lo, order,
-                          C.data_ptr(), max(M, 1), D.stream_handle())
+                          C.data_ptr(), max(M, 1), ws.data_ptr(), wsb,
+                          D.stream_handle())
     _lib.check(rc)
     return C
 

@@ -47,7 +47,7 @@ def test_header_compiles_as_c(tmp_path):
 
 
 def test_host_functions(lib):
-    assert lib.ozk_abi_version() == 1
+    assert lib.ozk_abi_version() == 2
     for K in [1, 2, 3, 64, 1040, 4096, 8192, 32768, 65536, 2 ** 22, 2 ** 22 + 1, 10 ** 9]:
         assert lib.ozk_rho_f32(K) == O.rho_f32(K)
         assert lib.ozk_rho_f64(K) == O.rho_f64(K)
@@ -70,8 +70,21 @@ def test_workspace_sizes(lib):
             planes = 2 * (nh + nl) * 8192 * K * eb
             extra = 2 * (nh + nl) * 8192 * 4 + 4096
             assert planes + 8 * K * M <= ws <= planes + 8 * K * M + extra, (K, nh, nl)
+    # max (5, 4): INT8 planes + transpose + the 2Sum fold state between its
+    # three sweeps (5 FP32 fields per output element)
     ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
-    assert ws >= 2 * 9 * 8192 * 8192 * 2
+    base = 2 * 9 * 8192 * 8192 + 8 * 8192 * 8192 + 20 * 8192 * 8192
+    assert base <= ws <= base + 2 * 9 * 8192 * 4 + 8192
+
+
+def test_gemm_workspace_bytes(lib):
+    # only the three-sweep max schedule keeps state between launches
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 4, 1, 0) == 0
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 3, 1, 1) == 0
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 8, 0, 3) == 0
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 0) == 100 * 70 * 20
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == 100 * 70 * 8
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == 0
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
     assert lib.ozk_extract_workspace_bytes(100, 50, 1) == 100 * 50 * 8
 
@@ -81,13 +94,16 @@ def test_int8_entry_points_reject_before_device_work(lib):
     # INT8 planes need rho >= 19 (|q| <= 64) and a preset schedule
     rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, 18, 4, 1, None, None, None, None, 0, None)
     assert rc == _lib.OZK_ERR_UNSUPPORTED and b"rho >= 19" in lib.ozk_last_error()
-    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 18, 4, 1, 0, None, 4, None)
+    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 18, 4, 1, 0, None, 4,
+                         None, 0, None)
     assert rc == _lib.OZK_ERR_UNSUPPORTED
-    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 5, 4, 0, None, 4, None)
+    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 2, 3, 0, None, 4,
+                         None, 0, None)
     assert rc == _lib.OZK_ERR_UNSUPPORTED
     rc = lib.ozk_slice_products_i8(None, None, 4, 4, 8192, 19, 2, 3, None, 4, None)
     assert rc == _lib.OZK_ERR_UNSUPPORTED
-    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4, None)
+    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4,
+                         None, 0, None)
     assert rc == _lib.OZK_ERR_INVALID
 
 
@@ -95,9 +111,9 @@ def test_argument_errors_before_device_work(lib):
     from ozaki_jax_amd import _lib
     # bad slice counts / order / shapes are rejected with OZK_ERR_INVALID and
     # a message; no pointer is dereferenced and no kernel is launched.
-    rc = lib.ozk_gemm(None, None, None, None, 4, 4, 4, 0, 0, 1, 0, None, 4, None)
+    rc = lib.ozk_gemm(None, None, None, None, 4, 4, 4, 0, 0, 1, 0, None, 4, None, 0, None)
     assert rc == _lib.OZK_ERR_INVALID
-    rc = lib.ozk_gemm(None, None, None, None, 4, 4, 4, 0, 4, 1, 9, None, 4, None)
+    rc = lib.ozk_gemm(None, None, None, None, 4, 4, 4, 0, 4, 1, 9, None, 4, None, 0, None)
     assert rc == _lib.OZK_ERR_INVALID and b"order" in lib.ozk_last_error()
     rc = lib.ozk_matmul(None, 4, None, 4, None, 4, 4, 0, 4, 0, 4, 1, 0, None, 0, None, None)
     assert rc == _lib.OZK_ERR_INVALID and b"invalid shape" in lib.ozk_last_error()

@@ -248,7 +248,7 @@ def _slices_i8(ll, A, B, nh, nl, rho_fixed):
     return a, b, O.ondevice_slices(A, B, rho, nh, nl), O.ondevice_schedule(nh, nl), rho
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
@@ -261,7 +261,7 @@ def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
     assert np.array_equal(P, O.slice_products(oa, ob, sched))
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_gemm_i8_orders_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
