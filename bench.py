@@ -63,6 +63,9 @@ def parse_args():
                          "solve) and print one JSON line each")
     ap.add_argument("--suite-out", default=None,
                     help="also write the suite's JSON lines to this file")
+    ap.add_argument("--suite-filter", default="",
+                    help="run only the suite groups whose name contains this "
+                         "text: host, 4096, 8192, gram, long, solve")
     return ap.parse_args()
 
 
@@ -150,18 +153,22 @@ def suite(args):
     def scaled_err(C, ref, A, B):
         return float(np.max(np.abs(C - ref) / (np.abs(A) @ np.abs(B))))
 
+    def want(group):
+        return args.suite_filter in group
+
     # 0: matmul_numpy host pipeline, n_slices=8, 256^3, RandomState(0)
-    rs = np.random.RandomState(0)
-    A, B = rs.randn(256, 256), rs.randn(256, 256)
-    log("suite: host 256")
-    t = _timeit(lambda: ozk.matmul_numpy(A, B), 10, sync)
-    C = ozk.matmul_numpy(A, B)
-    t0 = time.perf_counter()
-    ref = oracle.matmul_numpy(A, B)
-    t_cpu = time.perf_counter() - t0
-    emit({"config": "matmul_numpy host n_slices=8 256^3 N(0,1) seed 0",
-          "ms": t * 1e3, "bit_exact_vs_oracle": bool(np.array_equal(C, ref)),
-          "oracle_cpu_ms": t_cpu * 1e3, "note": "NumPy in/out, transfers included"})
+    if want("host"):
+        rs = np.random.RandomState(0)
+        A, B = rs.randn(256, 256), rs.randn(256, 256)
+        log("suite: host 256")
+        t = _timeit(lambda: ozk.matmul_numpy(A, B), 10, sync)
+        C = ozk.matmul_numpy(A, B)
+        t0 = time.perf_counter()
+        ref = oracle.matmul_numpy(A, B)
+        t_cpu = time.perf_counter() - t0
+        emit({"config": "matmul_numpy host n_slices=8 256^3 N(0,1) seed 0",
+              "ms": t * 1e3, "bit_exact_vs_oracle": bool(np.array_equal(C, ref)),
+              "oracle_cpu_ms": t_cpu * 1e3, "note": "NumPy in/out, transfers included"})
 
     def ondevice(name, A, B, precision, rows, phi=None):
         At = torch.from_numpy(A).to(dev)
@@ -186,14 +193,15 @@ def suite(args):
         return d
 
     # 1: 4096^3 high, N(0,1)
-    rs = np.random.RandomState(0)
-    A, B = rs.randn(4096, 4096), rs.randn(4096, 4096)
-    emit(ondevice("matmul ondevice fused high 4096^3 N(0,1)", A, B, "high",
-                  np.linspace(0, 4095, 4).astype(int)))
+    if want("4096"):
+        rs = np.random.RandomState(0)
+        A, B = rs.randn(4096, 4096), rs.randn(4096, 4096)
+        emit(ondevice("matmul ondevice fused high 4096^3 N(0,1)", A, B, "high",
+                      np.linspace(0, 4095, 4).astype(int)))
     # 2: 8192^3 medium / max, (U - 0.5) exp(phi N), phi in {0.5, 4} for A and B
     n = 8192
     rows = np.array([0, 4095, 8191])
-    for pa in (0.5, 4.0):
+    for pa in (0.5, 4.0) if want("8192") else ():
         for pb in (0.5, 4.0):
             rs = np.random.RandomState(1)
             A = _wide(rs, (n, n), pa)
@@ -202,7 +210,19 @@ def suite(args):
                 d = ondevice(f"matmul ondevice fused {prec} 8192^3 wide phi_A={pa} phi_B={pb}",
                              A, B, prec, rows)
                 emit(d)
-    del A, B
+    A = B = None
+    if want("gram"):
+        suite_gram(emit, ozk, oracle, dev, sync)
+    if want("long"):
+        suite_long(emit, ondevice)
+    if want("solve"):
+        suite_solve(emit, ozk, dev, sync)
+    if args.suite_out:
+        Path(args.suite_out).write_text("\n".join(out) + "\n")
+
+
+def suite_gram(emit, ozk, oracle, dev, sync):
+    import torch
     # 3: gram 32768 x 2048 and residual, N(0,1)
     rs = np.random.RandomState(0)
     A = rs.randn(32768, 2048)
@@ -222,13 +242,20 @@ def suite(args):
     emit({"config": "residual ozaki high 32768x2048 N(0,1)", "ms": t * 1e3,
           "GB_per_s_of_A": A.nbytes / t / 1e9,
           "bit_exact_vs_oracle": bool(np.array_equal(r, oracle.residual_ozaki(A, x, b)))})
-    del At, G, Gref
-    # 4: long K 1024 x 65536 x 1024 high, (U - 0.5) exp(2 N); solve n=4096 cond 1e6
+
+
+def suite_long(emit, ondevice):
+    # 4: long K 1024 x 65536 x 1024 high, (U - 0.5) exp(2 N)
     rs = np.random.RandomState(2)
     A = _wide(rs, (1024, 65536), 2.0)
     B = _wide(rs, (65536, 1024), 2.0)
     emit(ondevice("matmul ondevice fused high long-K 1024x65536x1024 wide phi=2", A, B,
                   "high", np.array([0, 511, 1023])))
+
+
+def suite_solve(emit, ozk, dev, sync):
+    import torch
+    # 4 (cont.): solve n=4096, A = Q1 diag(logspace(0, 6, n)) Q2^T
     rs = np.random.RandomState(3)
     nn = 4096
     Q1, _ = np.linalg.qr(rs.randn(nn, nn))
@@ -242,8 +269,6 @@ def suite(args):
     xr = np.linalg.solve(As, bs)
     emit({"config": "solve residual_mode=ozaki n=4096 cond 1e6", "ms": t * 1e3,
           "rel_err_vs_lapack_fp64": float(np.linalg.norm(xs - xr) / np.linalg.norm(xr))})
-    if args.suite_out:
-        Path(args.suite_out).write_text("\n".join(out) + "\n")
 
 
 def main():

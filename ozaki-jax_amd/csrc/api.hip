@@ -40,6 +40,13 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho);
 int launch_probe_mfma(int32_t* out, hipStream_t st);
+bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo);
+size_t residual_rows_xs_bytes(int64_t K, int nhi, int nlo);
+int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
+                         const void* xplanes, bool i8, int64_t ld, int64_t lpad,
+                         const int32_t* xe, int64_t xe_stride, const double* b,
+                         int64_t ldb, double* r, int64_t ldr, int rho, int nhi,
+                         int nlo, float* xs, uint32_t* flags, hipStream_t st);
 
 constexpr int kMaxSlices = 32;
 constexpr size_t kAlign = 256;
@@ -457,12 +464,25 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
   return OZK_OK;
 }
 
+// Residual workspace.  One right-hand side with K <= 4096 takes the fused
+// row kernel (x's planes + x's slices in FP64); otherwise A and x are
+// extracted to planes for the slice GEMM, whose FP64 product y is subtracted
+// from b afterwards.
 static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
                           int nlo, void* ws, SliceSet* a, SliceSet* x,
                           double** y, void** tws, void** gws = nullptr,
-                          size_t* gwsb = nullptr) {
+                          size_t* gwsb = nullptr, float** xs = nullptr) {
   Carver c(ws);
   const size_t eb = use_i8(OZK_PIPE_ONDEVICE, K, nhi, nlo) ? 1 : 2;
+  if (residual_rows_supported(K, ncols, nhi, nlo)) {
+    SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
+    float* xx = (float*)c.take(residual_rows_xs_bytes(K, nhi, nlo));
+    void* t = c.take(extract_workspace_bytes(K, ncols, 1));
+    if (x) *x = sx;
+    if (xs) *xs = xx;
+    if (tws) *tws = t;
+    return c.off;
+  }
   SliceSet sa = carve_slices(c, nhi + nlo, N, K, eb);
   SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
   double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
@@ -509,17 +529,24 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   }
   SliceSet sa, sx;
   double* y;
+  float* xs;
   void *tws, *gws;
   size_t gwsb;
-  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws, &gws, &gwsb);
+  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws, &gws, &gwsb,
+              &xs);
   const int rho = rho_generic(K, 24);
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
-  if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                           nullptr, 0, st, i8)))
-    return rc;
   if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,
                            flags, tws, extract_workspace_bytes(K, ncols, 1), st,
                            i8)))
+    return rc;
+  if (residual_rows_supported(K, ncols, n_hi, n_lo))
+    return launch_residual_rows(A, N, K, lda, sx.s, i8, round_up(K, kKPad),
+                                round_up(ncols, kLinePad), sx.e,
+                                round_up(ncols, kLinePad), b, ldb, r, ldr, rho,
+                                n_hi, n_lo, xs, flags, st);
+  if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
+                           nullptr, 0, st, i8)))
     return rc;
   if ((rc = launch_gemm(sa.s, sa.e, sx.s, sx.e, N, ncols, K, OZK_PIPE_ONDEVICE,
                         n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, gws, gwsb, st, i8, rho)))

@@ -12,64 +12,9 @@
 // All floating-point operations are single IEEE round-to-nearest operations
 // (built with -ffp-contract=off, denormals kept).
 
-#include "common.h"
-#include "log2_thresholds.inc"
+#include "sigma.h"
 
 namespace ozk {
-
-// ---------------------------------------------------------------- exponent
-
-// floor(RN32(log2 m)) for m > 0: binade e plus one when m reaches the
-// binade's rounding threshold (tables generated by gen_log2_thresholds.py).
-__device__ __forceinline__ int floor_log2_rn(float m) {
-  uint32_t u = __float_as_uint(m);
-  int ex = (int)((u >> 23) & 0xffu);
-  int e = ex ? ex - 127 : (-149 + 31 - (int)__clz(u & 0x7fffffu));
-  int idx = e - OZK_THR32_EMIN;
-  idx = idx < 0 ? 0 : (idx >= OZK_THR32_COUNT ? OZK_THR32_COUNT - 1 : idx);
-  return e + (m >= __uint_as_float(ozk_thr32_bits[idx]) ? 1 : 0);
-}
-
-__device__ __forceinline__ int floor_log2_rn(double m) {
-  uint64_t u = (uint64_t)__double_as_longlong(m);
-  int ex = (int)((u >> 52) & 0x7ffu);
-  int e = ex ? ex - 1023
-             : (-1074 + 63 - (int)__clzll((long long)(u & 0xfffffffffffffull)));
-  int idx = e - OZK_THR64_EMIN;
-  idx = idx < 0 ? 0 : (idx >= OZK_THR64_COUNT ? OZK_THR64_COUNT - 1 : idx);
-  return e + (m >= __longlong_as_double((long long)ozk_thr64_bits[idx]) ? 1 : 0);
-}
-
-__device__ __forceinline__ float ldexp_w(float x, int n) { return ldexpf(x, n); }
-__device__ __forceinline__ double ldexp_w(double x, int n) { return ldexp(x, n); }
-__device__ __forceinline__ float max_w(float a, float b) { return fmaxf(a, b); }
-__device__ __forceinline__ double max_w(double a, double b) { return fmax(a, b); }
-
-// Working-precision traits.  FP32: the line is split into (hi, lo) parts,
-// each extracted separately.  FP64: one part, the line itself.
-template <typename W> struct Parts;
-template <> struct Parts<float> { static constexpr int N = 2; };
-template <> struct Parts<double> { static constexpr int N = 1; };
-
-template <typename W>
-__device__ __forceinline__ void split(double x, W (&out)[Parts<W>::N]);
-template <>
-__device__ __forceinline__ void split<float>(double x, float (&out)[2]) {
-  float hi = (float)x;
-  out[0] = hi;
-  out[1] = (float)(x - (double)hi);
-}
-template <>
-__device__ __forceinline__ void split<double>(double x, double (&out)[1]) {
-  out[0] = x;
-}
-
-__device__ __forceinline__ float slice_value_f32(float v, float inv) {
-  return v * inv;
-}
-__device__ __forceinline__ float slice_value_f32(double v, double inv) {
-  return (float)(v * inv);  // extract.py:57-60: FP64 product, then FP32
-}
 
 // Slice plane formats.  BF16: the FP32 slice value's BF16 bits.  I8: the
 // slice as an integer count of its grid step, q = slice * 2^(24 - rho)
@@ -124,24 +69,6 @@ __device__ __forceinline__ void block_max2(W (&m)[NP], W* red) {
 // plane layout, are written from the same XCD.
 __device__ __forceinline__ int64_t xcd_line(int64_t bid, int64_t n) {
   return (bid & 7) * (n >> 3) + (bid >> 3);
-}
-
-// Per-slice constants shared by the line (uniform across the workgroup).
-template <typename W>
-struct SliceConst {
-  W sigma, inv;
-  int c;
-  bool zero;
-};
-
-template <typename W>
-__device__ __forceinline__ SliceConst<W> slice_const(W m, int rho) {
-  SliceConst<W> k;
-  k.zero = (m == W(0));
-  k.c = k.zero ? 0 : floor_log2_rn(m);
-  k.sigma = W(0.75) * ldexp_w(W(1), rho + k.c);
-  k.inv = ldexp_w(W(1), -k.c);
-  return k;
 }
 
 // Register-resident extraction.  A workgroup owns LPB consecutive lines

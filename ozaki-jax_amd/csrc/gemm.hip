@@ -27,124 +27,9 @@
 // All operations are single IEEE RN ops (-ffp-contract=off), so the result
 // is bit-identical to the NumPy restatement of each order.
 
-#include "common.h"
+#include "fold.h"
 
 namespace ozk {
-
-// ---------------------------------------------------------------- schedule
-
-struct PairInfo {
-  int a, b;   // A / B slice (plane) index
-  int blk;    // block id (0 hh, 1 hl, 2 lh; host: 0)
-  bool gs;    // first pair of its group
-  bool ge;    // last pair of its group
-  bool bs;    // first pair of its block
-  bool be;    // last pair of its block
-};
-
-__host__ __device__ constexpr int pair_count(int pipe, int nhi, int nlo) {
-  return pipe == OZK_PIPE_ONDEVICE ? nhi * nhi + 2 * nhi * nlo
-                                   : nhi * (nhi + 1) / 2;
-}
-
-// Pair p of the schedule.  Ondevice: hh (i, j), hl (i, n_hi + j), lh
-// (n_hi + i, j), i-major (pallas_gemm_accum.py:39-53, groups :59-79).
-// Host: (i, j) with i + j <= n - 1, i-major (matmul.py:27-31).
-__host__ __device__ constexpr PairInfo pair_info(int pipe, int nhi, int nlo,
-                                                 int p) {
-  PairInfo r{0, 0, 0, false, false, false, false};
-  if (pipe == OZK_PIPE_ONDEVICE) {
-    const int hh = nhi * nhi, hl = nhi * nlo;
-    if (p < hh) {
-      const int i = p / nhi, j = p % nhi;
-      r = PairInfo{i, j, 0, j == 0, j == nhi - 1, p == 0, p == hh - 1};
-    } else if (p < hh + hl) {
-      const int q = p - hh, i = q / nlo, j = q % nlo;
-      r = PairInfo{i, nhi + j, 1, j == 0, j == nlo - 1, q == 0, q == hl - 1};
-    } else {
-      const int q = p - hh - hl, i = q / nhi, j = q % nhi;
-      r = PairInfo{nhi + i, j, 2, j == 0, j == nhi - 1, q == 0, q == hl - 1};
-    }
-  } else {
-    const int n = nhi;
-    int q = p, i = 0;
-    while (q >= n - i) {
-      q -= n - i;
-      ++i;
-    }
-    const int np = n * (n + 1) / 2;
-    r = PairInfo{i, q, 0, q == 0, q == n - 1 - i, p == 0, p == np - 1};
-  }
-  return r;
-}
-
-// ---------------------------------------------------------------- fold
-
-__device__ __forceinline__ void twosum(float& s, float& l, float x) {
-  const float t = s + x;
-  const float e = (s - t) + x;
-  s = t;
-  l = l + e;
-}
-
-struct Fold2Sum {
-  float it, il, bt, bl, ct, cl, p0, p1, p2;
-  __device__ __forceinline__ void init() {
-    it = il = bt = bl = ct = cl = p0 = p1 = p2 = 0.0f;
-  }
-  __device__ __forceinline__ void pair(const PairInfo& q, float P, float cs32,
-                                       float rs32, double, double) {
-    if (q.bs) { bt = 0.0f; bl = 0.0f; }
-    if (q.gs) { it = 0.0f; il = 0.0f; }
-    twosum(it, il, P * cs32);
-    if (q.ge) {
-      const float ht = it * rs32, hl = il * rs32;
-      twosum(bt, bl, ht);
-      twosum(bt, bl, hl);
-      if (q.be) {
-        twosum(ct, cl, bt);
-        if (q.blk == 0) p0 = bl;
-        else if (q.blk == 1) p1 = bl;
-        else p2 = bl;
-      }
-    }
-  }
-  __device__ __forceinline__ double finish(int nblocks) {
-    twosum(ct, cl, p0);
-    if (nblocks > 1) twosum(ct, cl, p1);
-    if (nblocks > 2) twosum(ct, cl, p2);
-    return (double)ct + (double)cl;
-  }
-};
-
-template <int ORDER>
-struct Fold64 {
-  double c, in;
-  __device__ __forceinline__ void init() { c = 0.0; in = 0.0; }
-  __device__ __forceinline__ void pair(const PairInfo& q, float P, float cs32,
-                                       float, double cs64, double rs64) {
-    if (ORDER == OZK_ORDER_HOST_NP) {
-      double t = (double)P * rs64;
-      t = t * cs64;
-      c = c + t;
-      return;
-    }
-    if (q.gs) in = 0.0;
-    if (ORDER == OZK_ORDER_BLOCK64) {
-      in = in + (double)(P * cs32);
-    } else {  // OZK_ORDER_HOST_JAX
-      in = in + (double)P * cs64;
-    }
-    if (q.ge) {
-      in = in * rs64;
-      c = c + in;
-    }
-  }
-  __device__ __forceinline__ double finish(int) { return c; }
-};
-
-template <int ORDER> struct FoldOf { typedef Fold64<ORDER> type; };
-template <> struct FoldOf<OZK_ORDER_2SUM> { typedef Fold2Sum type; };
 
 // ---------------------------------------------------------------- tiling
 

@@ -467,6 +467,18 @@ def test_residual_bit_exact(ozk, shape):
     assert np.array_equal(R, O.residual_ozaki(A, X, Bm))
 
 
+@pytest.mark.parametrize("N,K", [(37, 1), (37, 1100), (129, 4096), (5, 513)])
+@pytest.mark.parametrize("precision", ["high", "medium", "max"])
+def test_residual_fused_rows_bit_exact(ozk, N, K, precision):
+    # one right-hand side with K <= 4096 runs the fused row kernel
+    rng = np.random.RandomState(N + K)
+    A = (rng.rand(N, K) - 0.5) * np.exp(2.0 * rng.randn(N, K))
+    x, b = rng.randn(K), rng.randn(N)
+    case(f"residual fused rows {precision} N={N} K={K}")
+    r = ozk.residual(A, x, b, mode="ozaki", precision=precision)
+    assert np.array_equal(r, O.residual_ozaki(A, x, b, precision))
+
+
 def test_known_answers_on_gpu(ozk, golden_dir):
     """gram / residual errors recorded by the reference (tpu_full_results.json
     :77,93,109,157,173,189) from the same RandomState(42) draws."""
