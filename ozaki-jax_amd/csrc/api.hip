@@ -20,6 +20,19 @@ void set_error(const char* fmt, ...) {
 }
 void clear_error() { g_error.clear(); }
 
+int cu_count() {
+  static int cache[64];  // 0 = not queried yet; racing writers store the same value
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 256;
+  if (dev >= 0 && dev < 64 && cache[dev] > 0) return cache[dev];
+  int cus = 0;
+  if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+      cus <= 0)
+    cus = 256;
+  if (dev >= 0 && dev < 64) cache[dev] = cus;
+  return cus;
+}
+
 // Implemented in extract.hip / gemm.hip.
 template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,

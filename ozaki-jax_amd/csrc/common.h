@@ -42,6 +42,10 @@ void clear_error();
     }                                                                     \
   } while (0)
 
+// Compute units of the current device (cached per device; 256 if the
+// query fails).  Persistent kernels size their grids with it.
+int cu_count();
+
 // ---------------------------------------------------------------- layout
 // Slice planes hold BF16 bit patterns or INT8 grid counts with lines padded
 // to kLinePad and k padded to kKPad elements; padding holds zeros, so the

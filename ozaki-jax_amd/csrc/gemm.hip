@@ -158,9 +158,9 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 // LDS: a ring of kRing stage buffers, one 64-byte chunk of every line each.
 // Fragment (slot, 16-line group lg) is the 1 KiB block of lines
 // 16 lg .. 16 lg + 15 of that chunk exactly as it lies in the plane (line r
-// at byte 64 (r % 16), units swizzled).  Wave w fetches the fragments w,
-// w + 8, ... of a stage with contiguous direct global->LDS loads, kRing - 1
-// stages ahead of the MFMAs.  MFMA lane l reads line l % 16, logical unit
+// at byte 64 (r % 16), units swizzled).  Waves 0..3 fetch every fragment of
+// a stage with contiguous direct global->LDS loads, kRing - 1 stages ahead of
+// the MFMAs, while waves 4..7 (one on each SIMD) already run theirs.  MFMA lane l reads line l % 16, logical unit
 // l / 16 of a fragment (frag_lane); the swizzle spreads those 64 reads over
 // all LDS banks.
 
@@ -345,30 +345,27 @@ struct AllPairsMMA {
 };
 
 // Fetch stage `st` (chunk st of every line of the tile) into the LDS buffer
-// at byte offset `buf_lds`.  Fragment F (slot F / 4, line group F % 4) is a
-// contiguous 1 KiB of its plane; wave w moves F = w + 8 i for F < 4 S, i.e.
-// slot 2 i + (w >> 2), line group w & 3.  At, Bt point at the tile's first
-// line of the sweep's first A / B plane in chunk 0; chunk st lies
-// st * a_stage / st * b_stage bytes further.  All addresses lie inside the
-// zero-padded slice planes.
+// at byte offset `buf_lds`.  Waves 0..3 move the whole stage: wave w moves
+// line group w of every slot, a contiguous 1 KiB of the slot's plane, into
+// fragment 4 slot + w of the buffer.  Waves 4..7 move nothing, so on every
+// SIMD one wave issues MFMAs while the other waits on the texture
+// addresser, which takes a stage's 40 loads one by one.  At, Bt point at the
+// tile's first line of the sweep's first A / B plane in chunk 0; chunk st
+// lies st * a_stage / st * b_stage bytes further.  All addresses lie inside
+// the zero-padded slice planes.
 template <int NA, int NB>
 __device__ __forceinline__ void stage_dma(const char* At, int64_t aplane,
                                           int64_t a_stage, const char* Bt,
                                           int64_t bplane, int64_t b_stage,
                                           int64_t st, uint32_t buf_lds,
                                           int wave, uint32_t lane_bytes) {
-  constexpr int kFrags = 4 * (NA + NB);
-  const int64_t g = (int64_t)(wave & 3) * 1024;
+  const int64_t g = (int64_t)wave * 1024;
   const int64_t qa = st * a_stage + g, qb = st * b_stage + g;
 #pragma unroll
-  for (int i = 0; i < (kFrags + 7) / 8; ++i) {
-    const int slot = 2 * i + (wave >> 2);
-    const int F = 8 * i + wave;
-    if (8 * i + 8 <= kFrags || F < kFrags) {
-      const char* base = slot < NA ? At + slot * aplane + qa : Bt + (slot - NA) * bplane + qb;
-      dma16(__builtin_amdgcn_readfirstlane(buf_lds + F * 1024), (const void*)base,
-            lane_bytes);
-    }
+  for (int slot = 0; slot < NA + NB; ++slot) {
+    const char* base = slot < NA ? At + slot * aplane + qa : Bt + (slot - NA) * bplane + qb;
+    dma16(__builtin_amdgcn_readfirstlane(buf_lds + (4 * slot + wave) * 1024),
+          (const void*)base, lane_bytes);
   }
 }
 
@@ -425,6 +422,11 @@ template <> struct FoldState<OZK_ORDER_2SUM> {
 // the schedule reloads the fold state from `state`; one that does not end it
 // stores the state there instead of writing C.  `nst` = chunks per line;
 // `unit2` is the product scale 2^(2 rho - 48) of the I8 format.
+//
+// The grid is persistent (one workgroup per CU, gridDim.x <= tiles):
+// workgroup b owns tiles b, b + gridDim.x, ... and runs their stages as one
+// sequence through the LDS ring, so the loads of a tile's first stages are
+// issued during the previous tile's last stages and epilogue.
 constexpr int kOrderProducts = -1;
 
 template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1>
@@ -437,8 +439,6 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
   constexpr int NBLK = 3;
-  constexpr int kFrags = 4 * SW::S;
-  constexpr int kPerHi = (kFrags + 7) / 8, kPerLo = kFrags / 8;  // DMA per wave
   constexpr int kBuf = SW::S * 4 * 64;  // uint4 per stage buffer
   static_assert(kRing == 4, "wait_stage assumes 4 stage buffers");
   static_assert(SW::S <= 10, "a stage holds at most 10 planes (160 KiB ring)");
@@ -446,18 +446,17 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   __shared__ uint4 lds[kRing * kBuf];
 
   const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
-  int tm, tn;
-  tile_coords(blockIdx.x, ntm, ntn, tm, tn);
-  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  const int bid = (int)blockIdx.x, nwg = (int)gridDim.x;
+  const int my_tiles = (ntm * ntn - 1 - bid) / nwg + 1;
+  const int64_t total = (int64_t)my_tiles * nst;  // stages of this workgroup
   const int64_t a_stage = a_lines * kChunkBytes, b_stage = b_lines * kChunkBytes;
   const int64_t aplane = a_stage * nst, bplane = b_stage * nst;
-  const char* At = As + SW::A0 * aplane + row0 * kChunkBytes;
-  const char* Bt = Bs + SW::BB * bplane + col0 * kChunkBytes;
+  const char* Ab = As + SW::A0 * aplane;
+  const char* Bb = Bs + SW::BB * bplane;
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  // waves 0 .. (kFrags % 8) - 1 issue one more load per stage
-  const bool extra = kPerHi != kPerLo && (8 * kPerLo + wave) < kFrags;
+  const bool dma_wave = wave < 4;
   AllPairsMMA<Op, SW> mma;
   mma.fl = frag_lane(lane);
   mma.wr = wave >> 2;
@@ -468,78 +467,122 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     mma.acc[k][1] = typename Op::acc_t{};
   }
 
-  // Per stage s: wait for this wave's loads of stage s, barrier (stage s is
-  // complete in LDS and every wave has finished stage s - 1, whose buffer is
-  // refilled next), fetch stage s + kRing - 1, run the MFMAs of stage s.
+  // Load cursor: chunk fs of this workgroup's tile fj, whose first lines
+  // are fA / fB.
   const uint32_t lane_bytes = 16u * (uint32_t)lane;
   const uint32_t lds0 = lds_offset(lds);
-  for (int i = 0; i < kRing - 1; ++i)
-    if (i < nst)
-      stage_dma<NA, NB>(At, aplane, a_stage, Bt, bplane, b_stage, i,
-                        lds0 + i * kBuf * 16, wave, lane_bytes);
-  for (int64_t s = 0; s < nst; ++s) {
-    const int64_t later = nst - 1 - s < kRing - 2 ? nst - 1 - s : kRing - 2;
-    if (extra) wait_stage<kPerHi>(later);
-    else wait_stage<kPerLo>(later);
-    __syncthreads();
-    const int64_t fetch = s + kRing - 1;
-    if (fetch < nst)
-      stage_dma<NA, NB>(At, aplane, a_stage, Bt, bplane, b_stage, fetch,
-                        lds0 + (uint32_t)((fetch % kRing) * kBuf * 16), wave, lane_bytes);
-    mma(lds + (s % kRing) * kBuf);
-  }
+  int fj = 0;
+  int64_t fs = 0;
+  const char *fA, *fB;
+  auto load_tile = [&](int j) {
+    int tm, tn;
+    tile_coords(bid + j * nwg, ntm, ntn, tm, tn);
+    fA = Ab + (int64_t)tm * kBM * kChunkBytes;
+    fB = Bb + (int64_t)tn * kBN * kChunkBytes;
+  };
+  // issue stage g of the sequence into ring buffer g % kRing
+  auto fetch = [&](int64_t g) {
+    if (dma_wave)
+      stage_dma<NA, NB>(fA, aplane, a_stage, fB, bplane, b_stage, fs,
+                        lds0 + (uint32_t)((g & (kRing - 1)) * kBuf * 16), wave,
+                        lane_bytes);
+    if (++fs == nst) {
+      fs = 0;
+      if (++fj < my_tiles) load_tile(fj);
+    }
+  };
+  load_tile(0);
+  for (int64_t g = 0; g < kRing - 1 && g < total; ++g) fetch(g);
 
-  // Accumulator register r of lane l of a 16x16 block holds row
-  // 4 * (l / 16) + r, column l % 16.
-  const int64_t col = col0 + 16 * mma.wc + (lane & 15);
-  if constexpr (ORDER == kOrderProducts) {
+  // Per stage g: wait for this wave's loads of stage g, barrier (stage g is
+  // complete in LDS and every wave has finished stage g - 1, whose buffer is
+  // refilled next), fetch stage g + kRing - 1, run the MFMAs of stage g;
+  // after a tile's last stage fold and store it.
+  int j = 0;  // tile of the MFMA cursor
+  int64_t s = 0;
+  for (int64_t g = 0; g < total; ++g) {
+    const int64_t later = total - 1 - g < kRing - 2 ? total - 1 - g : kRing - 2;
+    if (dma_wave) wait_stage<SW::S>(later);
+    __syncthreads();
+    if (g + kRing - 1 < total) fetch(g + kRing - 1);
+    mma(lds + (g & (kRing - 1)) * kBuf);
+    if (++s < nst) continue;
+    s = 0;
+    int tm, tn;
+    tile_coords(bid + j * nwg, ntm, ntn, tm, tn);
+    ++j;
+    const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+
+    // Accumulator register r of lane l of a 16x16 block holds row
+    // 4 * (l / 16) + r, column l % 16.
+    const int64_t col = col0 + 16 * mma.wc + (lane & 15);
+    if constexpr (ORDER == kOrderProducts) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+      for (int h = 0; h < 2; ++h) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
-        if (row < N && col < M) {
+        for (int r = 0; r < 4; ++r) {
+          const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
+          if (row < N && col < M) {
 #pragma unroll
-          for (int k = 0; k < NP; ++k)
-            P[((int64_t)(SW::P0 + k) * N + row) * ldp + col] =
-                Op::product(mma.acc[k][h][r], unit2);
+            for (int k = 0; k < NP; ++k)
+              P[((int64_t)(SW::P0 + k) * N + row) * ldp + col] =
+                  Op::product(mma.acc[k][h][r], unit2);
+          }
+        }
+      }
+    } else {
+      // Fold in schedule order; carry the state to the next sweep or store C.
+      // The exponents of the lane's column, and per 16-row block those of its
+      // 4 consecutive rows (one 16-byte load per A plane), are loaded
+      // together, so the epilogue waits for memory twice.  Rows and columns
+      // up to the padded line counts lie inside Ae / Be.
+      const int64_t rbase = row0 + 32 * mma.wr + 4 * (lane >> 4);
+      int eb[NB];
+#pragma unroll
+      for (int q = 0; q < NB; ++q) eb[q] = Be[(SW::BB + q) * b_lines + col];
+      const int64_t nm = N * M;
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        int32x4 ea4[NA];
+#pragma unroll
+        for (int q = 0; q < NA; ++q)
+          ea4[q] = *(const int32x4*)(Ae + (SW::A0 + q) * a_lines + rbase + 16 * h);
+        // One wait for all of them here: the folds below sit in branches on
+        // `live`, and a wait placed inside them would also wait for the
+        // previous row's store.  (s_waitcnt vmcnt(0), other counters free.)
+        __builtin_amdgcn_s_waitcnt(0x0f70);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int64_t row = rbase + 16 * h + r;
+          const bool live = row < N && col < M;
+          int ea[NA];
+#pragma unroll
+          for (int q = 0; q < NA; ++q) ea[q] = ea4[q][r];
+          typename FoldOf<ORDER>::type f;
+          f.init();
+          if constexpr (B0 > 0) {
+            if (live) FoldState<ORDER>::load(f, state, row * M + col, nm);
+          }
+#pragma unroll
+          for (int k = 0; k < NP; ++k) {
+            const PairInfo q = SW::pair(k);
+            const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
+            f.pair(q, Op::product(mma.acc[k][h][r], unit2), ldexpf(1.0f, ib),
+                   ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+          }
+          if constexpr (B1 < NBLK - 1) {
+            if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
+          } else {
+            const double out = f.finish(NBLK);
+            if (live) C[row * ldc + col] = out;
+          }
         }
       }
     }
-  } else {
-    // Fold in schedule order; carry the state to the next sweep or store C.
-    int eb[NB];
 #pragma unroll
-    for (int s = 0; s < NB; ++s) eb[s] = Be[(SW::BB + s) * b_lines + col];
-    const int64_t nm = N * M;
-#pragma unroll
-    for (int h = 0; h < 2; ++h) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
-        const bool live = row < N && col < M;
-        int ea[NA];
-#pragma unroll
-        for (int s = 0; s < NA; ++s) ea[s] = Ae[(SW::A0 + s) * a_lines + row];
-        typename FoldOf<ORDER>::type f;
-        f.init();
-        if constexpr (B0 > 0) {
-          if (live) FoldState<ORDER>::load(f, state, row * M + col, nm);
-        }
-#pragma unroll
-        for (int k = 0; k < NP; ++k) {
-          const PairInfo q = SW::pair(k);
-          const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
-          f.pair(q, Op::product(mma.acc[k][h][r], unit2), ldexpf(1.0f, ib),
-                 ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
-        }
-        if constexpr (B1 < NBLK - 1) {
-          if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
-        } else {
-          const double out = f.finish(NBLK);
-          if (live) C[row * ldc + col] = out;
-        }
-      }
+    for (int k = 0; k < NP; ++k) {
+      mma.acc[k][0] = typename Op::acc_t{};
+      mma.acc[k][1] = typename Op::acc_t{};
     }
   }
 }
@@ -745,7 +788,9 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
   const int64_t ntiles = (al / kBM) * (bl / kBN);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
-  a.grid = dim3((unsigned)ntiles);
+  // persistent: one workgroup per CU (the 160 KiB ring fills its LDS)
+  const int cus = cu_count();
+  a.grid = dim3((unsigned)(ntiles < cus ? ntiles : cus));
   a.st = st;
   a.As = (const char*)As;
   a.Bs = (const char*)Bs;

@@ -193,9 +193,7 @@ int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
                      dim3(256), 0, st, xplanes, i8 ? 1 : 0, K, kp, ld, lpad, rho, xs);
   OZK_LAUNCH_CHECK();
   // persistent grid: two workgroups per CU, each holding x's slices in LDS
-  int dev = 0, cus = 256;
-  if (hipGetDevice(&dev) == hipSuccess)
-    (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+  const int cus = cu_count();
   const int64_t need = (N + kResRows - 1) / kResRows;
   const dim3 grid((unsigned)(need < 2 * cus ? need : 2 * cus));
   const size_t lds = (size_t)(nhi + nlo) * kp * sizeof(float);
