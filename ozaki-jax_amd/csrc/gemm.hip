@@ -547,6 +547,17 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
 #pragma unroll
         for (int q = 0; q < NA; ++q)
           ea4[q] = *(const int32x4*)(Ae + (SW::A0 + q) * a_lines + rbase + 16 * h);
+        // A sweep that continues the schedule loads the fold state of the
+        // block's 4 rows here too.
+        typename FoldOf<ORDER>::type fr[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          fr[r].init();
+          if constexpr (B0 > 0) {
+            const int64_t row = rbase + 16 * h + r;
+            if (row < N && col < M) FoldState<ORDER>::load(fr[r], state, row * M + col, nm);
+          }
+        }
         // One wait for all of them here: the folds below sit in branches on
         // `live`, and a wait placed inside them would also wait for the
         // previous row's store.  (s_waitcnt vmcnt(0), other counters free.)
@@ -558,11 +569,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
           int ea[NA];
 #pragma unroll
           for (int q = 0; q < NA; ++q) ea[q] = ea4[q][r];
-          typename FoldOf<ORDER>::type f;
-          f.init();
-          if constexpr (B0 > 0) {
-            if (live) FoldState<ORDER>::load(f, state, row * M + col, nm);
-          }
+          typename FoldOf<ORDER>::type& f = fr[r];
 #pragma unroll
           for (int k = 0; k < NP; ++k) {
             const PairInfo q = SW::pair(k);
