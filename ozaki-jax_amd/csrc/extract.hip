@@ -71,18 +71,26 @@ __device__ __forceinline__ int64_t xcd_line(int64_t bid, int64_t n) {
   return (bid & 7) * (n >> 3) + (bid >> 3);
 }
 
-// Register-resident extraction.  A workgroup owns LPB consecutive lines
-// (the 64-byte chunk pieces of neighbouring lines are adjacent in the plane,
-// so their writes meet in one CU's L2 traffic), BLOCK threads each; thread t
-// of a line owns elements k = j*BLOCK + t, j < EPT, which must cover the
-// padded line (EPT * BLOCK >= ld).
+// Register-resident extraction.  A workgroup owns LPB consecutive lines,
+// BLOCK threads each; thread t of a line owns the VEC consecutive elements
+// k = (j * BLOCK + t) * VEC + v, j < EPT, v < VEC, which must cover the
+// padded line (EPT * BLOCK * VEC >= ld).  With `vec_ok` (line starts 16-byte
+// aligned) a thread reads its VEC doubles with 16-byte loads; it writes its
+// VEC plane elements, which are adjacent in the plane, with one store.
 // Planes: part 0 -> [0, n0), part 1 -> [n0, n0 + n1).
-template <typename W, int BLOCK, int EPT, int LPB, int FMT>
+template <int FMT, int VEC> struct PlaneVec;
+template <> struct PlaneVec<kFmtI8, 2> { typedef uint16_t type; };
+template <> struct PlaneVec<kFmtI8, 4> { typedef uint32_t type; };
+template <> struct PlaneVec<kFmtBf16, 2> { typedef uint32_t type; };
+template <> struct PlaneVec<kFmtBf16, 4> { typedef uint2 type; };
+
+template <typename W, int BLOCK, int EPT, int LPB, int FMT, int VEC>
 __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
     const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx,
-    int rho, int n0, int n1, typename PlaneElem<FMT>::type* __restrict__ S,
+    int vec_ok, int rho, int n0, int n1, typename PlaneElem<FMT>::type* __restrict__ S,
     int64_t ld, int64_t plane, int32_t* __restrict__ E, int64_t eplane,
     uint32_t* __restrict__ flags) {
+  static_assert(VEC == 2 || VEC == 4, "VEC doubles are read as 16-byte pairs");
   const float qscale = ldexpf(1.0f, 24 - rho);
   constexpr int NP = Parts<W>::N;
   __shared__ W red[NP * (BLOCK / 64) * LPB];
@@ -90,25 +98,40 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
   const int64_t line = xcd_line(blockIdx.x, gridDim.x) * LPB + threadIdx.x / BLOCK;
   const bool live = line < lines;
   const double* x = X + line * ldx;
-  // Plane offset of element j * BLOCK + t: BLOCK is a multiple of the
-  // elements per chunk, so the in-chunk position (and its swizzle) is fixed
-  // per thread and j only advances the chunk by BLOCK / kPer.
+  // Plane offset of the thread's first element: BLOCK * VEC is a multiple of
+  // the elements per chunk, so the in-chunk position (and its swizzle) is
+  // fixed per thread and j only advances the chunk by BLOCK * VEC / kPer.
   typedef typename PlaneElem<FMT>::type T;
+  typedef typename PlaneVec<FMT, VEC>::type TV;
   constexpr int kPer = kChunkBytes / (int)sizeof(T);
-  static_assert(BLOCK % kPer == 0, "BLOCK must hold whole chunks");
-  const int64_t off0 = plane_offset<sizeof(T)>(line, t, eplane);
-  const int64_t step = (int64_t)(BLOCK / kPer) * eplane * kPer;
-  W R[NP][EPT];
+  static_assert((BLOCK * VEC) % kPer == 0, "BLOCK * VEC must hold whole chunks");
+  const int64_t off0 = plane_offset<sizeof(T)>(line, (int64_t)t * VEC, eplane);
+  const int64_t step = (int64_t)(BLOCK * VEC / kPer) * eplane * kPer;
+  W R[NP][EPT * VEC];
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
-    const int64_t k = (int64_t)j * BLOCK + t;
-    double v = (live && k < len) ? x[k] : 0.0;
-    bad |= !isfinite(v);
-    W p[NP];
-    split<W>(v, p);
+    const int64_t k0 = ((int64_t)j * BLOCK + t) * VEC;
+    double v[VEC];
+    if (vec_ok && live && k0 + VEC <= len) {
 #pragma unroll
-    for (int q = 0; q < NP; ++q) R[q][j] = p[q];
+      for (int u = 0; u < VEC; u += 2) {
+        const double2 d = *(const double2*)(x + k0 + u);
+        v[u] = d.x;
+        v[u + 1] = d.y;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) v[u] = (live && k0 + u < len) ? x[k0 + u] : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) {
+      bad |= !isfinite(v[u]);
+      W p[NP];
+      split<W>(v[u], p);
+#pragma unroll
+      for (int q = 0; q < NP; ++q) R[q][j * VEC + u] = p[q];
+    }
   }
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 
@@ -119,7 +142,7 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
     for (int q = 0; q < NP; ++q) {
       m[q] = W(0);
 #pragma unroll
-      for (int j = 0; j < EPT; ++j) m[q] = max_w(m[q], fabs(R[q][j]));
+      for (int j = 0; j < EPT * VEC; ++j) m[q] = max_w(m[q], fabs(R[q][j]));
     }
     block_max2<W, BLOCK, LPB, NP>(m, red);
 #pragma unroll
@@ -128,15 +151,22 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
       if (s >= nq) continue;  // uniform
       const SliceConst<W> kc = slice_const<W>(m[q], rho);
       const int pl = (q == 0 ? 0 : n0) + s;
-      typename PlaneElem<FMT>::type* out = S + pl * plane + off0;
+      T* out = S + pl * plane + off0;
 #pragma unroll
       for (int j = 0; j < EPT; ++j) {
-        W r = R[q][j];
-        W v = (r + kc.sigma) - kc.sigma;
-        if (kc.zero) v = W(0);
-        R[q][j] = r - v;
-        if ((int64_t)j * BLOCK + t < ld)
-          out[j * step] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+        union {
+          TV w;
+          T e[VEC];
+        } pk;
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+          W r = R[q][j * VEC + u];
+          W v = (r + kc.sigma) - kc.sigma;
+          if (kc.zero) v = W(0);
+          R[q][j * VEC + u] = r - v;
+          pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+        }
+        if (((int64_t)j * BLOCK + t) * VEC < ld) *(TV*)(out + j * step) = pk.w;
       }
       if (t == 0) E[pl * eplane + line] = kc.c;
     }
@@ -262,26 +292,38 @@ static int launch_lines(const double* X, int64_t lines, int64_t len,
   const int64_t lp = round_up(lines, kLinePad);
   const int64_t plane = lp * ld;
   const dim3 grid((unsigned)lp);
-#define OZK_REG(B, EPT, LPB)                                                     \
-  hipLaunchKernelGGL((extract_lines_reg<W, B, EPT, LPB, FMT>), dim3((unsigned)(lp / LPB)), \
-                     dim3(B * LPB), 0, st, X, lines, len, ldx, rho, n0, n1, S, ld,  \
-                     plane, E, lp, flags)
-  if (ld <= 64 * 4) {
-    OZK_REG(64, 4, 4);
-  } else if (ld <= 256 * 4) {
-    OZK_REG(256, 4, 4);
-  } else if (ld <= 256 * 16) {
-    OZK_REG(256, 16, 4);
-  } else if (ld <= 512 * 16) {
-    OZK_REG(512, 16, 2);
-  } else if (ld <= 1024 * 16) {
-    OZK_REG(1024, 16, 1);
-  } else if (sizeof(W) == 4 && ld <= 1024 * 32) {
-    OZK_REG(1024, 32, 1);
+  // 16-byte loads need 16-byte aligned line starts
+  const int vec_ok = ((uintptr_t)X % 16 == 0) && (ldx % 2 == 0);
+#define OZK_REG(B, EPT, LPB, V)                                                        \
+  hipLaunchKernelGGL((extract_lines_reg<W, B, EPT, LPB, FMT, V>),                      \
+                     dim3((unsigned)(lp / LPB)), dim3(B * LPB), 0, st, X, lines, len, ldx, \
+                     vec_ok, rho, n0, n1, S, ld, plane, E, lp, flags)
+  // Shapes measured per line-length bucket (one or two lines per workgroup
+  // so that several workgroups share a CU and overlap loads with stores).
+  if (ld <= 256) {
+    OZK_REG(64, 2, 4, 2);
+  } else if (ld <= 1024) {
+    OZK_REG(128, 4, 1, 2);
+  } else if (ld <= 2048) {
+    OZK_REG(128, 8, 1, 2);
+  } else if (ld <= 4096) {
+    OZK_REG(256, 8, 2, 2);
+  } else if (ld <= 8192) {
+    OZK_REG(256, 8, 1, 4);
+  } else if (ld <= 16384) {
+    OZK_REG(512, 16, 1, 2);
   } else {
-    hipLaunchKernelGGL((extract_lines_stream<W, 1024, FMT>), grid, dim3(1024),
-                       0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E,
-                       lp, flags);
+    bool done = false;
+    if constexpr (sizeof(W) == 4) {  // FP32 parts: 32768 elements still fit
+      if (ld <= 32768) {
+        OZK_REG(512, 16, 1, 4);
+        done = true;
+      }
+    }
+    if (!done)
+      hipLaunchKernelGGL((extract_lines_stream<W, 1024, FMT>), grid, dim3(1024),
+                         0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E,
+                         lp, flags);
   }
 #undef OZK_REG
   OZK_LAUNCH_CHECK();
