@@ -243,25 +243,30 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 }
 
-// X (rows x cols, ldx) -> XT (cols x rows, contiguous), 64x64 tiles via LDS.
-__global__ __launch_bounds__(256) void transpose_f64(
+// X (rows x cols, ldx) -> XT (cols x rows, contiguous) through LDS tiles of
+// 128 rows x 64 columns: each wave reads 512 contiguous bytes of a row of X
+// and writes 512 contiguous bytes of a row of XT.
+__global__ __launch_bounds__(512) void transpose_f64(
     const double* __restrict__ X, int64_t rows, int64_t cols, int64_t ldx,
     double* __restrict__ XT) {
-  __shared__ double tile[64][65];
-  const int64_t r0 = (int64_t)blockIdx.y * 64, c0 = (int64_t)blockIdx.x * 64;
-  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // ty in [0, 4)
+  __shared__ double tile[128][65];
+  const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 64;
+  const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // ty in [0, 8)
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
-    const int rr = ty + 4 * i;
+    const int rr = ty + 8 * i;
     const int64_t r = r0 + rr, c = c0 + tx;
     tile[rr][tx] = (r < rows && c < cols) ? X[r * ldx + c] : 0.0;
   }
   __syncthreads();
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int cc = ty + 4 * i;
-    const int64_t c = c0 + cc, r = r0 + tx;
-    if (c < cols && r < rows) XT[c * rows + r] = tile[tx][cc];
+  for (int i = 0; i < 8; ++i) {
+    const int cc = ty + 8 * i;
+    const int64_t c = c0 + cc;
+    if (c < cols) {
+      if (r0 + tx < rows) XT[c * rows + r0 + tx] = tile[tx][cc];
+      if (r0 + 64 + tx < rows) XT[c * rows + r0 + 64 + tx] = tile[64 + tx][cc];
+    }
   }
 }
 
@@ -360,8 +365,8 @@ int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
       return OZK_ERR_WORKSPACE;
     }
     double* XT = (double*)ws;
-    const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 63) / 64));
-    hipLaunchKernelGGL(transpose_f64, grid, dim3(256), 0, st, X, rows, cols, ldx, XT);
+    const dim3 grid((unsigned)((cols + 63) / 64), (unsigned)((rows + 127) / 128));
+    hipLaunchKernelGGL(transpose_f64, grid, dim3(512), 0, st, X, rows, cols, ldx, XT);
     OZK_LAUNCH_CHECK();
     src = XT;
     lines = cols;
