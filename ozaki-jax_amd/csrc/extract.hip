@@ -252,20 +252,41 @@ __global__ __launch_bounds__(512) void transpose_f64(
   __shared__ double tile[128][65];
   const int64_t r0 = (int64_t)blockIdx.y * 128, c0 = (int64_t)blockIdx.x * 64;
   const int tx = threadIdx.x & 63, ty = threadIdx.x >> 6;  // ty in [0, 8)
+  // Interior tiles skip the bounds checks: with them the compiler no longer
+  // issues the 16 loads back to back (18% slower at 8192^2).
+  const bool full = r0 + 128 <= rows && c0 + 64 <= cols;
+  if (full) {
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const int rr = ty + 8 * i;
-    const int64_t r = r0 + rr, c = c0 + tx;
-    tile[rr][tx] = (r < rows && c < cols) ? X[r * ldx + c] : 0.0;
+    for (int i = 0; i < 16; ++i) {
+      const int rr = ty + 8 * i;
+      tile[rr][tx] = X[(r0 + rr) * ldx + c0 + tx];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int rr = ty + 8 * i;
+      const int64_t r = r0 + rr, c = c0 + tx;
+      tile[rr][tx] = (r < rows && c < cols) ? X[r * ldx + c] : 0.0;
+    }
   }
   __syncthreads();
+  if (full) {
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int cc = ty + 8 * i;
-    const int64_t c = c0 + cc;
-    if (c < cols) {
-      if (r0 + tx < rows) XT[c * rows + r0 + tx] = tile[tx][cc];
-      if (r0 + 64 + tx < rows) XT[c * rows + r0 + 64 + tx] = tile[64 + tx][cc];
+    for (int i = 0; i < 8; ++i) {
+      const int cc = ty + 8 * i;
+      double* o = XT + (c0 + cc) * rows + r0;
+      o[tx] = tile[tx][cc];
+      o[64 + tx] = tile[64 + tx][cc];
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int cc = ty + 8 * i;
+      const int64_t c = c0 + cc;
+      if (c < cols) {
+        if (r0 + tx < rows) XT[c * rows + r0 + tx] = tile[tx][cc];
+        if (r0 + 64 + tx < rows) XT[c * rows + r0 + 64 + tx] = tile[64 + tx][cc];
+      }
     }
   }
 }
