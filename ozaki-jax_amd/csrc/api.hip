@@ -53,6 +53,9 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho);
 int launch_probe_mfma(int32_t* out, hipStream_t st);
+bool gram_sym_supported(int nhi, int nlo);
+int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
+                    int nlo, double* G, int64_t ldg, hipStream_t st, bool i8, int rho);
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo);
 size_t residual_rows_xs_bytes(int64_t K, int nhi, int nlo);
 int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
@@ -468,6 +471,10 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
                            flags, tws, extract_workspace_bytes(rows, cols, 1), st,
                            i8)))
     return rc;
+  // high / medium: upper tiles only, the symmetrisation folded into the
+  // epilogue.  max (three K sweeps): full product, then symmetrise.
+  if (gram_sym_supported(n_hi, n_lo))
+    return launch_gram_sym(s.s, s.e, cols, rows, n_hi, n_lo, G, ldg, st, i8, rho);
   if ((rc = launch_gemm(s.s, s.e, s.s, s.e, cols, cols, rows, OZK_PIPE_ONDEVICE,
                         n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, gws, gwsb, st, i8, rho)))
     return rc;

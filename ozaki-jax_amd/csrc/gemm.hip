@@ -55,6 +55,38 @@ __device__ __forceinline__ void tile_coords(int bid, int ntm, int ntn, int& tm,
   tn = inner / gsz;
 }
 
+// Upper-triangle tile order for a symmetric product (tm <= tn, T x T tiles).
+// As in tile_coords, each XCD gets a contiguous range of the order.  The
+// order walks groups of kGroupM tile-rows; inside a group, tile-columns
+// ascend, and each column's tiles of the group (tm <= tn) are adjacent.
+__device__ __forceinline__ void tile_coords_sym(int bid, int T, int& tm, int& tn) {
+  const int nt = T * (T + 1) / 2;
+  const int q = nt / kXcds, rem = nt % kXcds;
+  const int xcd = bid % kXcds, slot = bid / kXcds;
+  int L = (xcd < rem ? xcd * (q + 1) : rem * (q + 1) + (xcd - rem) * q) + slot;
+  int g0 = 0;
+  for (;;) {
+    const int gsz = min(kGroupM, T - g0);
+    const int cnt = gsz * (gsz + 1) / 2 + gsz * (T - g0 - gsz);
+    if (L < cnt || g0 + gsz >= T) {
+      const int tri = gsz * (gsz + 1) / 2;
+      if (L < tri) {  // columns g0 .. g0 + gsz - 1: 1, 2, .., gsz tiles
+        int c = 0;
+        while ((c + 1) * (c + 2) / 2 <= L) ++c;
+        tn = g0 + c;
+        tm = g0 + (L - c * (c + 1) / 2);
+      } else {  // later columns: gsz tiles each
+        const int o = L - tri;
+        tn = g0 + gsz + o / gsz;
+        tm = g0 + o % gsz;
+      }
+      return;
+    }
+    L -= cnt;
+    g0 += gsz;
+  }
+}
+
 // LDS offset (in 16-byte units) of the operand of (slot, 32-row group, MFMA
 // k-step, lane) inside one stage buffer.  Tile line r (0..63) and 8-wide k
 // chunk c (0..3) of a stage go to lane (r & 31) + 32 * (c & 1) of block
@@ -248,6 +280,12 @@ struct Sweep {
   static constexpr PairInfo pair(int k) { return pair_info(PIPE, NHI, NLO, P0 + k); }
   static constexpr int la(int k) { return pair(k).a - A0; }  // local A slot
   static constexpr int lb(int k) { return pair(k).b - BB; }  // local B slot
+  // Index of pair (b, a) for pair k = (a, b), -1 if the sweep lacks it.
+  static constexpr int tpair(int k) {
+    for (int i = 0; i < NP; ++i)
+      if (pair(i).a == pair(k).b && pair(i).b == pair(k).a) return i;
+    return -1;
+  }
 };
 
 template <class Op, class SW>
@@ -429,7 +467,7 @@ template <> struct FoldState<OZK_ORDER_2SUM> {
 // issued during the previous tile's last stages and epilogue.
 constexpr int kOrderProducts = -1;
 
-template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1>
+template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM>
 __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     const char* __restrict__ As, const int32_t* __restrict__ Ae,
     const char* __restrict__ Bs, const int32_t* __restrict__ Be,
@@ -447,7 +485,16 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
 
   const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
   const int bid = (int)blockIdx.x, nwg = (int)gridDim.x;
-  const int my_tiles = (ntm * ntn - 1 - bid) / nwg + 1;
+  // SYM: B's planes are A's (a gram matrix); only tiles tm <= tn are run
+  // and each element folds both C[i][j] and C[j][i] (see the epilogue).
+  static_assert(!SYM || (B0 == 0 && B1 == 2 && ORDER == OZK_ORDER_2SUM),
+                "symmetric products need the single-sweep schedule");
+  const int ntiles = SYM ? ntm * (ntm + 1) / 2 : ntm * ntn;
+  const int my_tiles = (ntiles - 1 - bid) / nwg + 1;
+  auto coords = [&](int t, int& tm, int& tn) {
+    if constexpr (SYM) tile_coords_sym(t, ntm, tm, tn);
+    else tile_coords(t, ntm, ntn, tm, tn);
+  };
   const int64_t total = (int64_t)my_tiles * nst;  // stages of this workgroup
   const int64_t a_stage = a_lines * kChunkBytes, b_stage = b_lines * kChunkBytes;
   const int64_t aplane = a_stage * nst, bplane = b_stage * nst;
@@ -476,7 +523,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   const char *fA, *fB;
   auto load_tile = [&](int j) {
     int tm, tn;
-    tile_coords(bid + j * nwg, ntm, ntn, tm, tn);
+    coords(bid + j * nwg, tm, tn);
     fA = Ab + (int64_t)tm * kBM * kChunkBytes;
     fB = Bb + (int64_t)tn * kBN * kChunkBytes;
   };
@@ -509,7 +556,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     if (++s < nst) continue;
     s = 0;
     int tm, tn;
-    tile_coords(bid + j * nwg, ntm, ntn, tm, tn);
+    coords(bid + j * nwg, tm, tn);
     ++j;
     const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
 
@@ -577,7 +624,27 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
             f.pair(q, Op::product(mma.acc[k][h][r], unit2), ldexpf(1.0f, ib),
                    ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
           }
-          if constexpr (B1 < NBLK - 1) {
+          if constexpr (SYM) {
+            // Element (col, row) of a gram matrix: its pair (a, b) product is
+            // this lane's pair (b, a) product, its row-side exponents are the
+            // column's and vice versa.  Fold it in schedule order too, then
+            // store (C[i][j] + C[j][i]) * 0.5 at both places (gram.py:37).
+            typename FoldOf<ORDER>::type f2;
+            f2.init();
+#pragma unroll
+            for (int k = 0; k < NP; ++k) {
+              const PairInfo q = SW::pair(k);
+              const int ia = eb[SW::la(k)], ib = ea[SW::lb(k)];
+              f2.pair(q, Op::product(mma.acc[SW::tpair(k)][h][r], unit2), ldexpf(1.0f, ib),
+                      ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+            }
+            const double c1 = f.finish(NBLK), c2 = f2.finish(NBLK);
+            const double out = (c1 + c2) * 0.5;
+            if (live) {
+              C[row * ldc + col] = out;
+              if (tm != tn) C[col * ldc + row] = out;
+            }
+          } else if constexpr (B1 < NBLK - 1) {
             if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
           } else {
             const double out = f.finish(NBLK);
@@ -736,6 +803,7 @@ size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
 
 struct ApArgs {
   dim3 grid;
+  bool sym;
   hipStream_t st;
   const char *As, *Bs;
   const int32_t *Ae, *Be;
@@ -748,9 +816,9 @@ struct ApArgs {
   char* state;
 };
 
-template <class Op, int NHI, int NLO, int ORDER, int B0, int B1>
+template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
 static void launch_sweep(const ApArgs& a) {
-  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1>),
+  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
                      a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
                      a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state);
 }
@@ -769,7 +837,15 @@ static void launch_schedule(const ApArgs& a) {
 template <class Op, int NHI, int NLO>
 static void launch_ap_order(int order, const ApArgs& a) {
   switch (order) {
-    case OZK_ORDER_2SUM: launch_schedule<Op, NHI, NLO, OZK_ORDER_2SUM>(a); break;
+    case OZK_ORDER_2SUM:
+      if constexpr (NLO == 1) {  // single-sweep presets: symmetric form available
+        if (a.sym) {
+          launch_sweep<Op, NHI, NLO, OZK_ORDER_2SUM, 0, 2, true>(a);
+          break;
+        }
+      }
+      launch_schedule<Op, NHI, NLO, OZK_ORDER_2SUM>(a);
+      break;
     case OZK_ORDER_BLOCK64: launch_schedule<Op, NHI, NLO, OZK_ORDER_BLOCK64>(a); break;
     case OZK_ORDER_HOST_JAX: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a); break;
     case OZK_ORDER_HOST_NP: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a); break;
@@ -785,7 +861,7 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
                            int order, double* C, int64_t ldc, float* P,
                            int64_t ldp, void* state, size_t state_bytes,
-                           hipStream_t st) {
+                           hipStream_t st, bool sym = false) {
   const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, nhi, nlo, order);
   if (state_bytes < need || (need && !state)) {
     set_error("gemm workspace of %zu bytes < %zu needed", state_bytes, need);
@@ -793,11 +869,12 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   }
   ApArgs a;
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
-  const int64_t ntiles = (al / kBM) * (bl / kBN);
+  const int64_t ntiles = sym ? (al / kBM) * (al / kBM + 1) / 2 : (al / kBM) * (bl / kBN);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
   // persistent: one workgroup per CU (the 160 KiB ring fills its LDS)
   const int cus = cu_count();
   a.grid = dim3((unsigned)(ntiles < cus ? ntiles : cus));
+  a.sym = sym;
   a.st = st;
   a.As = (const char*)As;
   a.Bs = (const char*)Bs;
@@ -826,6 +903,21 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
 #undef OZK_AP_ALL
   OZK_LAUNCH_CHECK();
   return OZK_OK;
+}
+
+// Gram matrix of one plane set (A's columns) with itself: only the tiles on
+// and above the diagonal are computed, and the epilogue writes
+// (C + C^T) * 0.5 to both halves (2Sum order; presets (4,1) and (3,1)).
+bool gram_sym_supported(int nhi, int nlo) { return nlo == 1 && (nhi == 4 || nhi == 3); }
+
+int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
+                    int nlo, double* G, int64_t ldg, hipStream_t st, bool i8, int rho) {
+  if (!gram_sym_supported(nhi, nlo)) {
+    set_error("symmetric gram needs the high or medium preset");
+    return OZK_ERR_UNSUPPORTED;
+  }
+  return launch_allpairs(i8, S, E, S, E, n, n, K, rho, nhi, nlo, OZK_ORDER_2SUM, G, ldg,
+                         nullptr, 0, nullptr, 0, st, true);
 }
 
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,

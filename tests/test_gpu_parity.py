@@ -443,8 +443,11 @@ def test_preflight_and_families(ozk):
 
 # ---------------------------------------------------------------- gram / residual / solve
 
-@pytest.mark.parametrize("shape", [(64, 64), (300, 40), (33, 130), (5000, 24)])
-@pytest.mark.parametrize("precision", ["high", "medium"])
+# (4500, 600): 10 x 10 tiles of 64 (two tile-row groups of the upper-triangle
+# order, a ragged last tile), INT8 planes; max takes the full product and a
+# separate symmetrisation.
+@pytest.mark.parametrize("shape", [(64, 64), (300, 40), (33, 130), (5000, 24), (4500, 600)])
+@pytest.mark.parametrize("precision", ["high", "medium", "max"])
 def test_gram_bit_exact(ozk, shape, precision):
     A = gen("randn", shape, 51)
     case(f"gram ozaki {shape} {precision}")
