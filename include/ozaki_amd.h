@@ -156,6 +156,23 @@ int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
                           int n_hi, int n_lo, float* P, int64_t ldp,
                           void* stream);
 
+/* accumulate_2sum(products, col_scales, row_scales, block_group_sizes)
+ * (pallas_ops.py:178-239, dispatched by :372-396), the A4 order on products
+ * the caller holds.  products: n_products x N x M FP32, contiguous;
+ * col_scales: n_products x M; row_scales: n_groups x N.  Block b has
+ * block_ngroups[b] groups (n_blocks <= 8) and group g has group_sizes[g]
+ * products (n_groups <= 256; the sizes add up to n_products).  Per output
+ * element: per group, 2Sum of product * column scale from zero, times the
+ * group's row scale, hi then lo 2Sum-added into the block; then every
+ * block's hi, then every block's lo, 2Sum-added into (C_hi, C_lo), N x M
+ * FP32 each.  block_ngroups and group_sizes are host arrays. */
+int ozk_accumulate_2sum(const float* products, int64_t n_products,
+                        int64_t N, int64_t M, const float* col_scales,
+                        const float* row_scales,
+                        const int32_t* block_ngroups, int n_blocks,
+                        const int32_t* group_sizes, int n_groups,
+                        float* C_hi, float* C_lo, void* stream);
+
 /* ---- drivers --------------------------------------------------------- */
 /* matmul(A, B, pipeline, accumulation, precision) after preflight:
  * pipeline OZK_PIPE_ONDEVICE: split + FP32 extraction with

@@ -19,6 +19,8 @@ How each part is pinned (a check that a plausible mistake would fail):
     slices BF16-exact, |slice| <= 2, grid 2^(rho-p); exponent rule checked
     exhaustively over all positive float32 against np.log2.
   * slice products: exact integer sums (Python ints) on small shapes.
+  * accumulate_2sum (A4 on explicit arrays): equal to accumulate_a4 for the
+    schedules' own block/group sizes and scales.
   * orders A1..A4: brute-force scalar re-evaluation with Python floats /
     struct-rounded float32 on small shapes, and the reference's recorded
     known answers (tpu_full_results.json:77,93,109,157,173,189,
@@ -39,6 +41,7 @@ from .pipeline import (  # noqa: F401
     host_safety_report, ondevice_safety_report, handle_unsafe,
     slice_products, ondevice_slices, host_slices, scales_f32,
     accumulate_a1, accumulate_a2, accumulate_a3, accumulate_a4,
+    accumulate_2sum, precompute_accumulation_scales, combine_f64,
     matmul_numpy, matmul_host_a2, matmul_ondevice_a4, matmul_ondevice_a3,
     gram_ozaki, residual_ozaki, solve_ozaki,
 )

@@ -274,6 +274,54 @@ def accumulate_a4(P, sched, A_e, B_e):
     return ch, cl
 
 
+def precompute_accumulation_scales(A_hi_e, A_lo_e, B_hi_e, B_lo_e, N, M, n_hi, n_lo):
+    """pallas_ops.py:105-175: FP32 column scales per product (schedule order
+    hh, hl, lh), row scales per group, and the block/group sizes."""
+    def s32(e, n):
+        return np.ldexp(np.ones(n, np.float32), np.asarray(e).astype(np.int32))
+    cols = ([s32(B_hi_e[j], M) for i in range(n_hi) for j in range(n_hi)]
+            + [s32(B_lo_e[j], M) for i in range(n_hi) for j in range(n_lo)]
+            + [s32(B_hi_e[j], M) for i in range(n_lo) for j in range(n_hi)])
+    rows = ([s32(A_hi_e[i], N) for i in range(n_hi)]
+            + [s32(A_hi_e[i], N) for i in range(n_hi)]
+            + [s32(A_lo_e[i], N) for i in range(n_lo)])
+    bgs = (tuple([n_hi] * n_hi), tuple([n_lo] * n_hi), tuple([n_hi] * n_lo))
+    return np.stack(cols), np.stack(rows), bgs
+
+
+def accumulate_2sum(products, col_scales, row_scales, block_group_sizes):
+    """pallas_ops.py:178-239 on explicit arrays: products (P, N, M),
+    col_scales (P, M), row_scales (G, N), block_group_sizes a tuple of
+    per-block group sizes.  Returns (C_hi, C_lo) FP32."""
+    P = np.asarray(products, np.float32)
+    cs = np.asarray(col_scales, np.float32)
+    rs = np.asarray(row_scales, np.float32)
+    N, M = P.shape[1], P.shape[2]
+    z = np.zeros((N, M), np.float32)
+    blk_res = []
+    p = g = 0
+    for sizes in block_group_sizes:
+        bh, bl = z.copy(), z.copy()
+        for size in sizes:
+            ih, il = z.copy(), z.copy()
+            for _ in range(size):
+                ih, il = _twosum(ih, il, (P[p] * cs[p][None, :]).astype(np.float32))
+                p += 1
+            r = rs[g][:, None]
+            ih = (ih * r).astype(np.float32)
+            il = (il * r).astype(np.float32)
+            bh, bl = _twosum(bh, bl, ih)
+            bh, bl = _twosum(bh, bl, il)
+            g += 1
+        blk_res.append((bh, bl))
+    ch, cl = z.copy(), z.copy()
+    for bh, _ in blk_res:
+        ch, cl = _twosum(ch, cl, bh)
+    for _, bl in blk_res:
+        ch, cl = _twosum(ch, cl, bl)
+    return ch, cl
+
+
 def combine_f64(ch, cl):
     """matmul.py:526, :540: f64(C_hi) + f64(C_lo)."""
     return ch.astype(np.float64) + cl.astype(np.float64)

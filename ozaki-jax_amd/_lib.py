@@ -78,6 +78,9 @@ SIGNATURES = {
                               _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                               _c_vp, _c_size, _c_vp, _c_vp]),
     "ozk_check_finite": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "ozk_accumulate_2sum": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_vp, _c_vp,
+                                     _c_vp, _c_int, _c_vp, _c_int, _c_vp, _c_vp,
+                                     _c_vp]),
     "ozk_probe_mfma_layout": (_c_int, [_c_vp, _c_vp]),
 }
 

@@ -33,7 +33,7 @@ namespace ozk {
 
 // ---------------------------------------------------------------- tiling
 
-constexpr int kBM = 64, kBN = 64, kBK = 32, kThreads = 256;
+constexpr int kBM = 64, kBN = 64, kThreads = 256;
 
 // Output-tile order: consecutive workgroups go round-robin to the 8 XCDs, so
 // first gather each XCD's share into a contiguous range, then walk that range

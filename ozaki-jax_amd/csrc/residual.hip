@@ -17,8 +17,6 @@
 
 namespace ozk {
 
-constexpr int kResMaxPairs = 128;
-constexpr int kResMaxPlanes = 32;
 constexpr int kResRows = 4;  // rows (waves) per workgroup
 
 // Slice values of line 0 of `planes` chunk-major planes (BF16 bits or INT8

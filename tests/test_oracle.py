@@ -357,6 +357,29 @@ def test_orders_match_scalar_evaluation():
             assert c2[i, j] == _scalar_a2(Ph, hs, hae, hbe, i, j)
 
 
+@pytest.mark.parametrize("n_hi,n_lo", [(4, 1), (3, 1), (5, 4)])
+def test_accumulate_2sum_equals_schedule_a4(n_hi, n_lo):
+    # the explicit-array form of A4 (pallas_ops.py:178-239) with the scales
+    # of pallas_ops.py:105-175 must equal the schedule form, which the
+    # scalar evaluation and the reference's known answers pin
+    rng = np.random.RandomState(n_hi * 10 + n_lo)
+    A = (rng.rand(9, 70) - 0.5) * np.exp(2 * rng.randn(9, 70))
+    B = (rng.rand(70, 11) - 0.5) * np.exp(2 * rng.randn(70, 11))
+    rho = O.rho_f32(70)
+    a, ae, b, be = O.ondevice_slices(A, B, rho, n_hi, n_lo)
+    s = O.ondevice_schedule(n_hi, n_lo)
+    Pm = O.slice_products(a, b, s)
+    ch, cl = O.accumulate_a4(Pm, s, ae, be)
+    cs, rs, bgs = O.precompute_accumulation_scales(ae[:n_hi], ae[n_hi:], be[:n_hi],
+                                                   be[n_hi:], 9, 11, n_hi, n_lo)
+    assert cs.shape == (Pm.shape[0], 11) and rs.shape == (2 * n_hi + n_lo, 9)
+    gh, gl = O.accumulate_2sum(Pm, cs, rs, bgs)
+    assert np.array_equal(gh, ch) and np.array_equal(gl, cl)
+    # a block order swapped in the final combine changes the result
+    bh2, bl2 = O.accumulate_2sum(Pm, cs, rs, bgs[::-1])
+    assert not (np.array_equal(bh2, ch) and np.array_equal(bl2, cl))
+
+
 # ---------------------------------------------------------------- end to end
 
 def _exact_product(A, B):
