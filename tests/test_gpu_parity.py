@@ -120,17 +120,31 @@ def test_extract_f64_rows_and_cols(ll, shape):
         assert np.array_equal(v, s) and np.array_equal(e, ee.astype(np.int32))
 
 
-def test_extract_long_lines_streaming(ll):
-    # lines longer than the register-resident kernels hold
-    X = gen("wide2", (3, 40000), 5)
-    rho = O.rho_f32(40000)
-    case(f"ozk_extract_f32 streaming (3, 40000) rho={rho}")
-    pl = ll.extract(X, 0, rho, 4, 1)
+# Lines longer than the register-resident kernels hold: up to 64 Ki elements
+# the hi part stays on chip (registers + LDS) and the lo part is streamed;
+# longer lines stream both parts.  (n0, n1) = (2, 3) runs several lo passes.
+LONG_CASES = [("wide2", (3, 40000), 4, 1, False), ("zerorows", (3, 40000), 4, 1, False),
+              ("wide2", (2, 65536), 4, 1, False), ("wide2", (2, 70000), 4, 1, False),
+              ("wide2", (3, 40000), 2, 3, False), ("randn", (3, 40000), 4, 1, True),
+              ("wide2", (2, 65536), 5, 4, True)]
+
+
+@pytest.mark.parametrize("kind,shape,n0,n1,i8", LONG_CASES)
+def test_extract_long_lines(ll, kind, shape, n0, n1, i8):
+    X = gen(kind, shape, 5 + shape[1])
+    rho = O.rho_f32(shape[1])
     hi, lo = O.split_hi_lo(X)
-    sh, eh = O.extract_rows_f32(hi, rho, 4)
-    sl, el = O.extract_rows_f32(lo, rho, 1)
-    assert np.array_equal(to_np(pl.values()), np.concatenate([sh, sl]))
-    assert np.array_equal(to_np(pl.exponents()), np.concatenate([eh, el]).astype(np.int32))
+    sh, eh = O.extract_rows_f32(hi, rho, n0)
+    sl, el = O.extract_rows_f32(lo, rho, n1)
+    ref = np.concatenate([sh, sl])
+    for by_cols in (0, 1):
+        case(f"ozk_extract_f32 long lines {kind} {shape} ({n0},{n1}) i8={i8} by_cols={by_cols}")
+        pl = ll.extract(X.T.copy() if by_cols else X, by_cols, rho, n0, n1, i8=i8)
+        assert np.array_equal(to_np(pl.values()), ref), "slices"
+        assert np.array_equal(to_np(pl.exponents()),
+                              np.concatenate([eh, el]).astype(np.int32)), "exponents"
+        g = to_np(pl.grid())
+        assert not g[:, :, shape[1]:].any() and not g[:, shape[0]:, :].any(), "padding"
 
 
 def test_extract_log2_edge_fixture(ll, golden_dir):
