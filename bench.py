@@ -184,7 +184,14 @@ def suite(args):
         nh, nl = OP.resolve_precision(precision)
         ref = oracle.matmul_ondevice_a4(A[rows], B, "raise", nh, nl)
         t_dg = _timeit(lambda: torch.matmul(At, Bt), 3, sync)
+        # the whole call's slice-pair rate against the MFMA peak of the plane
+        # format it runs on (INT8 for rho_32 >= 19 and a preset, else BF16)
+        i8 = oracle.rho_f32(k) >= 19
+        pairs = nh * nh + 2 * nh * nl
         d = {"config": name, "ms": t * 1e3, "fp64_eq_tflops": 2.0 * n * k * m / t / 1e12,
+             "slice_format": "int8" if i8 else "bf16",
+             "pair_rate_frac_of_mfma_peak":
+                 pairs * 2.0 * n * k * m / t / 1e12 / (PEAK_INT8_TOPS if i8 else PEAK_BF16_TFLOPS),
              "rocblas_dgemm_ms": t_dg * 1e3,
              "max_scaled_err_vs_oracle": scaled_err(Cr, ref, A[rows], B),
              "max_scaled_err_vs_fp64": scaled_err(Cr, A[rows] @ B, A[rows], B),
@@ -234,13 +241,17 @@ def suite_gram(emit, ozk, oracle, dev, sync):
     G = ozk.gram(At, mode="ozaki").cpu().numpy()
     cols = np.array([0, 1023, 2047])
     Gref = oracle.gram_ozaki(A, "high")
+    # symmetric form: 528 of the 1024 output tiles, 24 pairs each (INT8 planes)
     emit({"config": "gram ozaki high 32768x2048 N(0,1)", "ms": t * 1e3,
           "fp64_eq_tflops": 2.0 * 2048 * 2048 * 32768 / t / 1e12,
+          "tile_pair_rate_frac_of_int8_peak":
+              24 * 2.0 * 528 * 64 * 64 * 32768 / t / 1e12 / PEAK_INT8_TOPS,
           "bit_exact_vs_oracle": bool(np.array_equal(G[cols], Gref[cols]))})
     t = _timeit(lambda: ozk.residual(At, xt, bt, mode="ozaki"), 5, sync)
     r = ozk.residual(At, xt, bt, mode="ozaki").cpu().numpy()
     emit({"config": "residual ozaki high 32768x2048 N(0,1)", "ms": t * 1e3,
           "GB_per_s_of_A": A.nbytes / t / 1e9,
+          "frac_of_hbm_peak": A.nbytes / t / 1e9 / PEAK_HBM_GBS,
           "bit_exact_vs_oracle": bool(np.array_equal(r, oracle.residual_ozaki(A, x, b)))})
 
 
