@@ -284,17 +284,13 @@ def suite_solve(emit, ozk, dev, sync):
 
 def main():
     args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "the engine runs on one GPU per process "
+                          "and measures one GPU only; --gpus must be 1"}))
+        sys.exit(2)
     if args.suite:
-        if args.gpus != 1:
-            print(json.dumps({"error": "this build runs on one GPU only; "
-                              "--gpus must be 1"}))
-            sys.exit(2)
         suite(args)
         return
-    if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU only; "
-                          "--gpus must be 1"}))
-        sys.exit(2)
     import torch
     import ozaki_jax_amd as ozk
     from ozaki_jax_amd import _lib, lowlevel as ll

@@ -41,7 +41,7 @@ extern "C" {
 #define OZK_OK 0
 #define OZK_ERR_INVALID (-1)     /* bad argument (shape, mode, size) */
 #define OZK_ERR_HIP (-2)         /* HIP runtime / launch failure */
-#define OZK_ERR_UNSUPPORTED (-3) /* valid request this build cannot serve */
+#define OZK_ERR_UNSUPPORTED (-3) /* valid request the library does not serve */
 #define OZK_ERR_WORKSPACE (-4)   /* workspace too small */
 
 #define OZK_FLAG_NONFINITE 1u

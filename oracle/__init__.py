@@ -7,7 +7,7 @@ four accumulation orders, plus gram / residual / solve on top of them.  Every
 function cites the reference file:line it restates.
 
 Only ``tests/``, ``__graft_entry__.smoke()`` and ``bench.py``'s CPU-baseline leg
-may import it, and only as the checker.  The product (``ozaki_jax_amd``) never
+may import it, and only to check results against.  The product (``ozaki_jax_amd``) never
 imports, links or executes anything under ``oracle/``.
 
 How each part is pinned (a check that a plausible mistake would fail):

@@ -3,8 +3,8 @@ floor(np.log2(m)) in the working precision, as the reference computes it
 (extract.py:37, :82, :130, :171).  FP32: every positive finite value.  FP64:
 a window around every binade's threshold plus random samples.
 
-Runs on whatever host executes it: on the GPU box it re-checks that box's
-NumPy against the same table."""
+Runs on whatever host executes it: on a GPU machine it re-checks that
+machine's NumPy against the same table."""
 
 import importlib.util
 import re

@@ -1,7 +1,7 @@
 """Pins for the CPU oracle (oracle/), against the reference's own data and
 against mathematics, so that a plausible mistake in the restatement fails.
 
-No GPU needed.  The oracle is only ever the checker; these tests check it.
+No GPU needed.  The oracle only ever checks results; these tests check it.
 """
 
 import json
