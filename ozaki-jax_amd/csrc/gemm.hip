@@ -224,35 +224,6 @@ struct OpI8 {
   }
 };
 
-// One 16-byte-per-lane direct load from global memory into LDS
-// (global_load_lds_dwordx4): lane l's 16 bytes land at LDS offset
-// `lds_addr` + 16 l.  `lds_addr` and `gbase` are wave-uniform; `voff` is the
-// lane's byte offset from `gbase`.  Written as inline assembly so that the
-// compiler does not order the K loop's LDS reads behind these loads: the
-// kernel waits for them itself (wait_vm) before the barrier that publishes
-// a stage.  M0 carries the LDS address; nothing else in these kernels uses
-// M0.
-__device__ __forceinline__ void dma16(uint32_t lds_addr, const void* gbase,
-                                      uint32_t voff) {
-  asm volatile(
-      "s_mov_b32 m0, %0\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, %2"
-      :
-      : "s"(lds_addr), "v"(voff), "s"(gbase)
-      : "memory");
-}
-
-// Wait until at most N of this wave's vector-memory loads are outstanding.
-template <int N>
-__device__ __forceinline__ void wait_vm() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
-}
-
-__device__ __forceinline__ uint32_t lds_offset(const void* p) {
-  return (uint32_t)(size_t)((__attribute__((address_space(3))) const char*)p);
-}
-
 // uint4 index inside a 1 KiB fragment of the 16x16x64 operand of lane l:
 // line l % 16, logical unit l / 16.
 __device__ __forceinline__ int frag_lane(int lane) {

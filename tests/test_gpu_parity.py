@@ -487,13 +487,48 @@ def test_residual_bit_exact(ozk, shape):
 @pytest.mark.parametrize("N,K", [(37, 1), (37, 1100), (129, 4096), (5, 513)])
 @pytest.mark.parametrize("precision", ["high", "medium", "max"])
 def test_residual_fused_rows_bit_exact(ozk, N, K, precision):
-    # one right-hand side with K <= 4096 runs the fused row kernel
+    # one right-hand side with K <= 2048 (high, medium) runs the fused row
+    # kernel; K = 4096 and max take the slice-GEMM route
     rng = np.random.RandomState(N + K)
     A = (rng.rand(N, K) - 0.5) * np.exp(2.0 * rng.randn(N, K))
     x, b = rng.randn(K), rng.randn(N)
     case(f"residual fused rows {precision} N={N} K={K}")
     r = ozk.residual(A, x, b, mode="ozaki", precision=precision)
     assert np.array_equal(r, O.residual_ozaki(A, x, b, precision))
+
+
+@pytest.mark.parametrize("K", [2048, 1500, 1024, 700])
+@pytest.mark.parametrize("precision", ["high", "medium"])
+def test_residual_rows_batches_and_edge_rows(ozk, K, precision):
+    """40000 rows: every wave of the row kernel's persistent grid (one
+    workgroup of 8 waves per CU) takes more than one batch of 16 rows, the
+    last one partial.  K = 2048 / 1024 are whole 64 x EPL rows, 1500 / 700
+    take the guarded loads.  Special rows: all zero (no slice), one nonzero,
+    scaled by 2^-103 (slice exponents below -100: normalised dot products,
+    subnormal lo parts), 2^105 (exponents above 100), a wide row, and one
+    scaled by 2^-110, where 2^-c overflows FP32 in the reference's
+    extraction and its result is NaN (extract.py:145-148; at K = 1024 the
+    2^-103 row's last slices do too); the kernel must give NaN there too.  Rows are independent, so three row ranges are
+    checked against the oracle on those rows alone."""
+    N = 40000
+    rng = np.random.RandomState(K + (7 if precision == "high" else 11))
+    A = rng.randn(N, K)
+    A[3] = 0.0
+    A[5] = 0.0
+    A[5, 7] = 1.5
+    A[100] *= 2.0 ** -103
+    A[101] *= 2.0 ** 105
+    A[102] = rng.randn(K) * np.exp(3.0 * rng.randn(K))
+    A[N - 2] *= 2.0 ** -110
+    x, b = rng.randn(K), rng.randn(N)
+    b[[3, 5, 100, 101, 102, N - 2]] = 0.0  # r = -Ozaki(A, x) exactly there
+    case(f"residual rows N={N} K={K} {precision}")
+    r = ozk.residual(A, x, b, mode="ozaki", precision=precision)
+    sel = np.r_[0:300, 16300:16400, N - 300:N]
+    with np.errstate(over="ignore", invalid="ignore"):
+        ref = O.residual_ozaki(A[sel], x, b[sel], precision)
+    assert np.isnan(ref[-2]) and np.isfinite(ref).sum() >= len(sel) - 2
+    assert np.array_equal(r[sel], ref, equal_nan=True)
 
 
 def test_known_answers_on_gpu(ozk, golden_dir):
