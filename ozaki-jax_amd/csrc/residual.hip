@@ -28,29 +28,6 @@ __device__ __forceinline__ void static_for(F&& f) {
   }
 }
 
-// Slice values of line 0 of `planes` chunk-major planes (BF16 bits or INT8
-// grid counts) -> FP32, xs[p * kp + k] for k < K, zero for K <= k < kp.
-__global__ void decode_line0_kernel(const void* __restrict__ S, int i8,
-                                    int64_t K, int64_t kp, int64_t ld,
-                                    int64_t lpad, int rho,
-                                    float* __restrict__ xs) {
-  const int64_t k = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int p = blockIdx.y;
-  if (k >= kp) return;
-  float v = 0.0f;
-  if (k < K) {
-    const int64_t plane = lpad * ld;
-    if (i8) {
-      const int8_t q = ((const int8_t*)S)[p * plane + plane_offset<1>(0, k, lpad)];
-      v = (float)q * ldexpf(1.0f, rho - 24);
-    } else {
-      const uint16_t h = ((const uint16_t*)S)[p * plane + plane_offset<2>(0, k, lpad)];
-      v = bf16_bits_to_f32(h);
-    }
-  }
-  xs[p * kp + k] = v;
-}
-
 constexpr int kResWaves = 8;   // waves per workgroup: two per SIMD
 constexpr int kResBatch = 16;  // rows whose pair products are folded together
 
@@ -137,6 +114,69 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
   return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, a),
                                         __builtin_bit_cast(bf16x2, b), c, false);
+}
+
+// x's slices for the row kernel, by one workgroup of 4 waves: the split and
+// sigma steps of the extraction kernels applied to x as a single line (x is
+// one column, extract.py:157-191; split matmul.py:204-213).  Thread t holds
+// elements k = 256 j + t.  Writes the FP32 slice values xs[t * kp + k] (zero
+// for K <= k < kp, kp <= 2048), the exponents xe[t], and the flag word
+// (OZK_FLAG_NONFINITE if x holds NaN/Inf, else 0).
+constexpr int kResXThreads = 256;
+
+__global__ __launch_bounds__(kResXThreads) void residual_x_kernel(
+    const double* __restrict__ x, int64_t K, int64_t ldx, int rho, int nhi,
+    int nlo, int64_t kp, float* __restrict__ xs, int32_t* __restrict__ xe,
+    uint32_t* __restrict__ flags) {
+  constexpr int E = 2048 / kResXThreads;
+  constexpr int W = kResXThreads / 64;
+  __shared__ uint32_t wmax[2][W];  // per-wave maxima, alternating buffers
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  float R[2][E];
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < E; ++j) {
+    const int64_t k = (int64_t)j * kResXThreads + tid;
+    const double v = k < K ? x[k * ldx] : 0.0;
+    bad |= !isfinite(v);
+    float pr[2];
+    split<float>(v, pr);
+    R[0][j] = pr[0];
+    R[1][j] = pr[1];
+  }
+  if (__syncthreads_or(bad ? 1 : 0)) {
+    if (tid == 0) flags[0] = OZK_FLAG_NONFINITE;
+  } else if (tid == 0) {
+    flags[0] = 0u;
+  }
+  int step = 0;
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int n = q == 0 ? nhi : nlo;
+    for (int s = 0; s < n; ++s, ++step) {
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < E; ++j) m = fmaxf(m, fabsf(R[q][j]));
+      const float mw = wave_max_uniform(m);
+      if (lane == 0) wmax[step & 1][wave] = __float_as_uint(mw);
+      __syncthreads();
+      uint32_t mb = 0;
+#pragma unroll
+      for (int w = 0; w < W; ++w) mb = max(mb, wmax[step & 1][w]);
+      const SliceConst<float> kc = slice_const<float>(__uint_as_float(mb), rho);
+      const int t = q == 0 ? s : nhi + s;
+#pragma unroll
+      for (int j = 0; j < E; ++j) {
+        const float rr = R[q][j];
+        float v = (rr + kc.sigma) - kc.sigma;
+        if (kc.zero) v = 0.0f;
+        R[q][j] = rr - v;
+        const int64_t k = (int64_t)j * kResXThreads + tid;
+        if (k < kp) xs[t * kp + k] = slice_value_f32(v, kc.inv);
+      }
+      if (tid == 0) xe[t] = kc.c;
+    }
+  }
 }
 
 // Per-row values kept for the batched fold, in LDS: the pair sums, then per
@@ -403,21 +443,27 @@ static int residual_rows_epl(int64_t K) {
   return epl;
 }
 
+// Workspace of the row path: x's FP32 slice values, then their exponents.
 size_t residual_rows_xs_bytes(int64_t K, int nhi, int nlo) {
   return (size_t)(nhi + nlo) * (size_t)(64 * residual_rows_epl(K)) * sizeof(float);
 }
+size_t residual_rows_xe_bytes(int nhi, int nlo) {
+  return (size_t)(nhi + nlo) * sizeof(int32_t);
+}
 
-// x's planes (chunk-major, `lpad` lines, `ld` elements per line) and
-// exponents (plane stride xe_stride) -> r for the N rows of A.
+// r = b - Ozaki(A, x) for one right-hand side x (K elements, stride ldx):
+// x's slices into xs / xe (workspace), then the row kernel.  Also clears
+// `flags` and sets it for a non-finite x or A.
 int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
-                         const void* xplanes, bool i8, int64_t ld, int64_t lpad,
-                         const int32_t* xe, int64_t xe_stride, const double* b,
+                         const double* x, int64_t ldx, const double* b,
                          int64_t ldb, double* r, int64_t ldr, int rho, int nhi,
-                         int nlo, float* xs, uint32_t* flags, hipStream_t st) {
+                         int nlo, float* xs, int32_t* xe, uint32_t* flags,
+                         hipStream_t st) {
   const int epl = residual_rows_epl(K);
   const int64_t kp = 64 * epl;  // the kernel reads xs[p * kp + j * 64 + lane], j < epl
-  hipLaunchKernelGGL(decode_line0_kernel, dim3((unsigned)((kp + 255) / 256), nhi + nlo),
-                     dim3(256), 0, st, xplanes, i8 ? 1 : 0, K, kp, ld, lpad, rho, xs);
+  const int64_t xe_stride = 1;
+  hipLaunchKernelGGL(residual_x_kernel, dim3(1), dim3(kResXThreads), 0, st, x, K,
+                     ldx, rho, nhi, nlo, kp, xs, xe, flags);
   OZK_LAUNCH_CHECK();
   // persistent grid: one workgroup of kResWaves waves per CU
   const int cus = cu_count();

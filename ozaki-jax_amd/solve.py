@@ -85,7 +85,8 @@ def ozaki_residual_device(At, xt, bt, n_hi, n_lo, dev):
     if K == 0:
         raise ValueError("zero-size array to reduction operation maximum "
                          "which has no identity")
-    flags = D.new_flags(dev)
+    # ozk_residual clears the flag word itself
+    flags = D.torch.empty(1, dtype=D.torch.int32, device=dev)
     wsb = lib.ozk_residual_workspace_bytes(N, K, nc, n_hi, n_lo)
     ws = D.workspace(wsb, dev)
     _lib.check(lib.ozk_residual(

@@ -531,6 +531,43 @@ def test_residual_rows_batches_and_edge_rows(ozk, K, precision):
     assert np.array_equal(r[sel], ref, equal_nan=True)
 
 
+@pytest.mark.parametrize("K", [2048, 700, 4096])
+def test_residual_flags_through_c_abi(ozk, K):
+    """ozk_residual clears the flag word itself, whatever it held, and sets
+    OZK_FLAG_NONFINITE for a NaN/Inf in x or in A: on the fused row path
+    (K <= 2048), where the x-slice kernel writes the word, and on the
+    slice-GEMM path (K = 4096)."""
+    import torch
+    from ozaki_jax_amd import _lib, _device as D
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    rng = np.random.RandomState(K)
+    N = 300
+    A = torch.from_numpy(rng.randn(N, K)).to(dev)
+    x = torch.from_numpy(rng.randn(K, 1)).to(dev)
+    b = torch.from_numpy(rng.randn(N, 1)).to(dev)
+    r = torch.empty((N, 1), dtype=torch.float64, device=dev)
+    wsb = lib.ozk_residual_workspace_bytes(N, K, 1, 4, 1)
+    ws = D.workspace(wsb, dev)
+
+    def run(A_, x_):
+        flags = torch.full((1,), -559038737, dtype=torch.int32, device=dev)
+        _lib.check(lib.ozk_residual(
+            A_.data_ptr(), D.ld_of(A_), x_.data_ptr(), D.ld_of(x_), b.data_ptr(),
+            D.ld_of(b), r.data_ptr(), D.ld_of(r), N, K, 1, 4, 1, ws.data_ptr(),
+            wsb, flags.data_ptr(), D.stream_handle()))
+        return int(flags.item()) & 0xffffffff
+
+    case(f"residual flags K={K}")
+    assert run(A, x) == 0
+    x2 = x.clone()
+    x2[K // 3, 0] = float("nan")
+    assert run(A, x2) == _lib.OZK_FLAG_NONFINITE
+    A2 = A.clone()
+    A2[N - 1, K - 1] = float("inf")
+    assert run(A2, x) == _lib.OZK_FLAG_NONFINITE
+
+
 def test_known_answers_on_gpu(ozk, golden_dir):
     """gram / residual errors recorded by the reference (tpu_full_results.json
     :77,93,109,157,173,189) from the same RandomState(42) draws."""

@@ -35,6 +35,29 @@ def test_inc_matches_generator():
     assert gen.render(*gen.tables()) == (CSRC / "log2_thresholds.inc").read_text()
 
 
+def test_fp32_fast_path_bound():
+    """floor_log2_rn(float) returns the binade e without a table lookup when
+    m is normal and its mantissa field is below kLog2FastMant32; that is
+    exact iff no threshold inside its binade has a smaller mantissa field."""
+    fast = int(re.search(r"kLog2FastMant32 = (0x[0-9a-fA-F]+)u;",
+                         (CSRC / "sigma.h").read_text()).group(1), 16)
+    t32, _ = _tables_from_inc()
+    emin = int(re.search(r"OZK_THR32_EMIN \((-?\d+)\)",
+                         (CSRC / "log2_thresholds.inc").read_text()).group(1))
+    bits = t32.view(np.uint32).astype(np.int64)
+    inside = 0
+    for i, b in enumerate(bits):
+        e, ex = emin + i, (b >> 23) & 0xFF
+        if ex == 0xFF:
+            assert b == 0x7F800000  # +inf: no threshold in this binade
+        elif ex != 0 and ex - 127 == e:
+            assert (b & 0x7FFFFF) >= fast, (e, hex(b))
+            inside += 1
+        else:
+            assert e < -126  # subnormal binades always take the table
+    assert inside > 200
+
+
 def _binade32(u):
     ex = (u >> 23).astype(np.int64)
     mant = (u & 0x7FFFFF).astype(np.int64)
