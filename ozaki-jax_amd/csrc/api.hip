@@ -57,13 +57,10 @@ bool gram_sym_supported(int nhi, int nlo);
 int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
                     int nlo, double* G, int64_t ldg, hipStream_t st, bool i8, int rho);
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo);
-size_t residual_rows_xs_bytes(int64_t K, int nhi, int nlo);
-size_t residual_rows_xe_bytes(int nhi, int nlo);
 int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
                          const double* x, int64_t ldx, const double* b,
                          int64_t ldb, double* r, int64_t ldr, int rho, int nhi,
-                         int nlo, float* xs, int32_t* xe, uint32_t* flags,
-                         hipStream_t st);
+                         int nlo, uint32_t* flags, hipStream_t st);
 
 constexpr int kMaxSlices = 32;
 constexpr size_t kAlign = 256;
@@ -486,23 +483,16 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
 }
 
 // Residual workspace.  One right-hand side with K <= 2048 (presets high and
-// medium) takes the fused row kernel (x's slices as FP32 values and their
-// exponents); otherwise A and x are extracted to planes for the slice GEMM,
-// whose FP64 product y is subtracted from b afterwards.
+// medium) takes the fused row kernel, which needs none; otherwise A and x are
+// extracted to planes for the slice GEMM, whose FP64 product y is subtracted
+// from b afterwards.
 static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
                           int nlo, void* ws, SliceSet* a, SliceSet* x,
                           double** y, void** tws, void** gws = nullptr,
-                          size_t* gwsb = nullptr, float** xs = nullptr,
-                          int32_t** xe = nullptr) {
+                          size_t* gwsb = nullptr) {
   Carver c(ws);
   const size_t eb = use_i8(OZK_PIPE_ONDEVICE, K, nhi, nlo) ? 1 : 2;
-  if (residual_rows_supported(K, ncols, nhi, nlo)) {
-    float* xx = (float*)c.take(residual_rows_xs_bytes(K, nhi, nlo));
-    int32_t* ee = (int32_t*)c.take(residual_rows_xe_bytes(nhi, nlo));
-    if (xs) *xs = xx;
-    if (xe) *xe = ee;
-    return c.off;
-  }
+  if (residual_rows_supported(K, ncols, nhi, nlo)) return 0;
   SliceSet sa = carve_slices(c, nhi + nlo, N, K, eb);
   SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
   double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
@@ -541,23 +531,20 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   OZK_CHECK_ARG(flags, "null flags pointer");
   if (N == 0 || ncols == 0) return launch_fill_u32(flags, 0u, st);
   const size_t need = ozk_residual_workspace_bytes(N, K, ncols, n_hi, n_lo);
-  if (!workspace || workspace_bytes < need) {
+  if (need && (!workspace || workspace_bytes < need)) {
     set_error("residual: workspace of %zu bytes needed, %zu given", need,
               workspace_bytes);
     return OZK_ERR_WORKSPACE;
   }
-  SliceSet sa, sx;
-  double* y;
-  float* xs;
-  int32_t* xe;
-  void *tws, *gws;
-  size_t gwsb;
-  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws, &gws, &gwsb,
-              &xs, &xe);
   const int rho = rho_generic(K, 24);
   if (residual_rows_supported(K, ncols, n_hi, n_lo))  // clears and sets flags
     return launch_residual_rows(A, N, K, lda, x, ldx, b, ldb, r, ldr, rho, n_hi,
-                                n_lo, xs, xe, flags, st);
+                                n_lo, flags, st);
+  SliceSet sa, sx;
+  double* y;
+  void *tws, *gws;
+  size_t gwsb;
+  residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws, &gws, &gwsb);
   if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
   if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,

@@ -116,83 +116,23 @@ __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
                                         __builtin_bit_cast(bf16x2, b), c, false);
 }
 
-// x's slices for the row kernel, by one workgroup of 4 waves: the split and
-// sigma steps of the extraction kernels applied to x as a single line (x is
-// one column, extract.py:157-191; split matmul.py:204-213).  Thread t holds
-// elements k = 256 j + t.  Writes the FP32 slice values xs[t * kp + k] (zero
-// for K <= k < kp, kp <= 2048), the exponents xe[t], and the flag word
-// (OZK_FLAG_NONFINITE if x holds NaN/Inf, else 0).
-constexpr int kResXThreads = 256;
-
-__global__ __launch_bounds__(kResXThreads) void residual_x_kernel(
-    const double* __restrict__ x, int64_t K, int64_t ldx, int rho, int nhi,
-    int nlo, int64_t kp, float* __restrict__ xs, int32_t* __restrict__ xe,
-    uint32_t* __restrict__ flags) {
-  constexpr int E = 2048 / kResXThreads;
-  constexpr int W = kResXThreads / 64;
-  __shared__ uint32_t wmax[2][W];  // per-wave maxima, alternating buffers
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  float R[2][E];
-  bool bad = false;
-#pragma unroll
-  for (int j = 0; j < E; ++j) {
-    const int64_t k = (int64_t)j * kResXThreads + tid;
-    const double v = k < K ? x[k * ldx] : 0.0;
-    bad |= !isfinite(v);
-    float pr[2];
-    split<float>(v, pr);
-    R[0][j] = pr[0];
-    R[1][j] = pr[1];
-  }
-  if (__syncthreads_or(bad ? 1 : 0)) {
-    if (tid == 0) flags[0] = OZK_FLAG_NONFINITE;
-  } else if (tid == 0) {
-    flags[0] = 0u;
-  }
-  int step = 0;
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int n = q == 0 ? nhi : nlo;
-    for (int s = 0; s < n; ++s, ++step) {
-      float m = 0.0f;
-#pragma unroll
-      for (int j = 0; j < E; ++j) m = fmaxf(m, fabsf(R[q][j]));
-      const float mw = wave_max_uniform(m);
-      if (lane == 0) wmax[step & 1][wave] = __float_as_uint(mw);
-      __syncthreads();
-      uint32_t mb = 0;
-#pragma unroll
-      for (int w = 0; w < W; ++w) mb = max(mb, wmax[step & 1][w]);
-      const SliceConst<float> kc = slice_const<float>(__uint_as_float(mb), rho);
-      const int t = q == 0 ? s : nhi + s;
-#pragma unroll
-      for (int j = 0; j < E; ++j) {
-        const float rr = R[q][j];
-        float v = (rr + kc.sigma) - kc.sigma;
-        if (kc.zero) v = 0.0f;
-        R[q][j] = rr - v;
-        const int64_t k = (int64_t)j * kResXThreads + tid;
-        if (k < kp) xs[t * kp + k] = slice_value_f32(v, kc.inv);
-      }
-      if (tid == 0) xe[t] = kc.c;
-    }
-  }
-}
-
-// Per-row values kept for the batched fold, in LDS: the pair sums, then per
-// A slice its row scale 2^c and the factor that turns the accumulated sum
-// into the slice product (1, or 2^-c when the unnormalised slice values were
-// summed).
+// Per-row values kept for the batched fold, in LDS: the row and its b, the
+// pair sums, then per A slice its row scale 2^c and the factor that turns the
+// accumulated sum into the slice product (1, or 2^-c when the unnormalised
+// slice values were summed).
 template <int NP, int NT>
 struct ResRow {
+  double b;     // b of the row
+  int64_t row;  // the row
   float p[NP];
   float rs[NT];
   float un[NT];
 };
 
-// One wave per row, rows strided over a persistent grid (one workgroup of
-// kResWaves waves per CU).  Lane l holds elements k = 64 j + l, j < EPL; x's
-// slices live in registers as BF16 pairs (elements j, j + 1).  Per row:
+// One wave per row over a persistent grid (one workgroup of kResWaves waves
+// per CU; rows handed to the waves as described at the row loop).  Lane l
+// holds elements k = 64 j + l, j < EPL; x's slices live in registers as BF16
+// pairs (elements j, j + 1).  Per row:
 //   split into hi / lo parts; lo slice first, so that its registers are free
 //   when the next row's load is issued; then the hi slices.  Each slice is
 //   extracted and immediately dotted (v_dot2_f32_bf16) with the x slices of
@@ -206,9 +146,9 @@ struct ResRow {
 template <int EPL, bool FULL, bool DMA, int NHI, int NLO>
 __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
     const double* __restrict__ A, int64_t N, int64_t K, int64_t lda,
-    const float* __restrict__ xs, const int32_t* __restrict__ xe,
-    int64_t xe_stride, const double* __restrict__ b, int64_t ldb,
-    double* __restrict__ r, int64_t ldr, int rho, uint32_t* __restrict__ flags) {
+    const double* __restrict__ x, int64_t ldx, const double* __restrict__ b,
+    int64_t ldb, double* __restrict__ r, int64_t ldr, int rho,
+    uint32_t* __restrict__ flags) {
   constexpr int NT = NHI + NLO;
   constexpr int NP = pair_count(OZK_PIPE_ONDEVICE, NHI, NLO);
   constexpr int NR = (NP + 3) / 4 * 4;  // pair sums padded for the reduce-scatter
@@ -218,22 +158,15 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
   __shared__ ResRow<NP, NT> red[kResWaves][kResBatch];
   // DMA: each wave's next row, copied into LDS as it lies in memory
   __shared__ double rowbuf[DMA ? kResWaves * KP : 1];
+  __shared__ int queue;  // the workgroup's next row index (see below)
+  if (threadIdx.x == 0) queue = 0;
+  __syncthreads();
 
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int lane = threadIdx.x & 63;
-  uint32_t xp[NT][H];
-#pragma unroll
-  for (int t = 0; t < NT; ++t)
-#pragma unroll
-    for (int i = 0; i < H; ++i)
-      xp[t][i] = pack_bf16x2(xs[t * KP + (2 * i) * 64 + lane],
-                             xs[t * KP + (2 * i + 1) * 64 + lane]);
-  float cs[NT];
-#pragma unroll
-  for (int t = 0; t < NT; ++t) cs[t] = ldexpf(1.0f, xe[t * xe_stride]);
+  uint32_t xp[NT][H];  // x's slices, BF16 pairs (elements j, j + 1)
+  float cs[NT];        // their scales 2^c
 
-  const int64_t nw = (int64_t)gridDim.x * kResWaves;
-  const int64_t first = (int64_t)blockIdx.x * kResWaves + wave;
   double nx[EPL];
   // FULL: rows of exactly 64 EPL elements, loaded without guards; shorter
   // rows read element min(k, K - 1) and replace it by zero past the end
@@ -270,30 +203,78 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
     for (int i = 0; i < KP * 8 / 1024; ++i)
       dma16(myrow_lds + i * 1024, a + i * 1024, 16u * (uint32_t)lane);
   };
-  if (PF && first < N) load_row(first);
-  if (DMA && first < N) dma_row(first);
-  int nb = 0;
-  int64_t row0 = first;
-  ResRow<NP, NT>* rows = red[wave];
-  // b of the batch's rows, lane i holding row row0 + i nw, loaded when the
-  // batch starts
-  auto load_b = [&](int64_t r0) {
-    const int64_t ri = r0 + (int64_t)lane * nw;
-    return lane < kResBatch && ri < N ? b[ri * ldb] : 0.0;
-  };
-  double bb = load_b(row0);
+  // Rows: workgroup g owns rows g + i G (G workgroups), i = 0, 1, ...  Wave
+  // w starts with i = w and i = w + kResWaves; later indices come from the
+  // workgroup's LDS counter in the order the waves ask, so that waves the
+  // hardware serves unevenly (two share a SIMD) still finish together.  A
+  // wave asks for the index after its next one while it works on the
+  // current one and stops at the first row >= N it is given; indices are
+  // handed out in increasing order, so every row is taken exactly once.
+  const int64_t G = gridDim.x;
+  auto row_of = [&](int64_t i) { return (int64_t)blockIdx.x + i * G; };
+  int64_t cur = row_of(wave), nxt = row_of(wave + kResWaves);
+  if (PF && cur < N) load_row(cur);
+  if (DMA && cur < N) dma_row(cur);
 
-  for (int64_t row = first; row < N; row += nw) {
+  // x's slices (x is one column: extract.py:157-191, split matmul.py:204-213),
+  // computed by every wave while its first row is in flight, with the split
+  // and sigma steps of the extraction kernels; normalised slice values are
+  // BF16-exact.  One wave reports a non-finite x.
+  {
+    float X[2][EPL];
+    bool xbad = false;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int k = j * 64 + lane;
+      const double v = k < Ki ? x[(int64_t)k * ldx] : 0.0;
+      xbad |= !isfinite(v);
+      float pr[2];
+      split<float>(v, pr);
+      X[0][j] = pr[0];
+      X[1][j] = pr[1];
+    }
+    if (blockIdx.x == 0 && wave == 0 && xbad) atomicOr(flags, OZK_FLAG_NONFINITE);
+    static_for<0, NT>([&](auto t_c) {
+      constexpr int T = decltype(t_c)::value;
+      constexpr int Q = T < NHI ? 0 : 1;  // hi part, then lo part
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) m = fmaxf(m, fabsf(X[Q][j]));
+      const SliceConst<float> kc = slice_const<float>(wave_max_uniform(m), rho);
+      cs[T] = ldexpf(1.0f, kc.c);
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        float s[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float rr = X[Q][2 * i + e];
+          float v = (rr + kc.sigma) - kc.sigma;
+          if (kc.zero) v = 0.0f;
+          X[Q][2 * i + e] = rr - v;
+          s[e] = slice_value_f32(v, kc.inv);
+        }
+        xp[T][i] = pack_bf16x2(s[0], s[1]);
+      }
+    });
+  }
+  int nb = 0;
+  ResRow<NP, NT>* rows = red[wave];
+
+  while (cur < N) {
     if constexpr (DMA) {
       wait_vm<0>();  // this row's copy has landed in LDS
 #pragma unroll
       for (int j = 0; j < EPL; ++j) nx[j] = myrow[j * 64 + lane];
       // the reads must complete before the buffer is refilled
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (row + nw < N) dma_row(row + nw);
+      if (nxt < N) dma_row(nxt);
     } else if constexpr (!PF) {
-      load_row(row);
+      load_row(cur);
     }
+    const bool take = nxt < N;
+    int q = 0;
+    if (take && lane == 0) q = atomicAdd(&queue, 1);
+    const double bv = lane == 0 ? b[cur * ldb] : 0.0;
     float Rh[EPL], Rl[EPL];
     bool bad = false;
     float mh = 0.0f, ml = 0.0f;
@@ -376,7 +357,7 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
       slice(std::integral_constant<int, NHI + S>{},
             std::integral_constant<bool, (S + 1 < NLO)>{}, Rl, mw, ml);
     });
-    if (PF && row + nw < N) load_row(row + nw);
+    if (PF && nxt < N) load_row(nxt);
     static_for<0, NHI>([&](auto s) {
       constexpr int S = decltype(s)::value;
       const float mw = S == 0 ? mwh0 : wave_max_uniform(mh);
@@ -399,6 +380,8 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
       }
     }
     if (lane == 0) {
+      rr.b = bv;
+      rr.row = cur;
 #pragma unroll
       for (int t = 0; t < NT; ++t) {
         rr.rs[t] = rs[t];
@@ -406,13 +389,12 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
       }
     }
     ++nb;
-    if (nb == kResBatch || row + nw >= N) {
+    if (nb == kResBatch || !take) {
       // LDS accesses of one wave complete in order; the clobber keeps the
       // compiler from moving them across this point
       asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
       if (lane < nb) {
         const ResRow<NP, NT>& s = rows[lane];
-        const int64_t ri = row0 + (int64_t)lane * nw;
         Fold2Sum f;
         f.init();
 #pragma unroll
@@ -421,13 +403,13 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
           f.pair(q, s.p[p] * s.un[q.a], cs[q.b], s.rs[q.a], 0.0, 0.0);
         }
         const double c = f.finish(3);
-        r[ri * ldr] = bb - c;
+        r[s.row * ldr] = s.b - c;
       }
       asm volatile("" ::: "memory");
       nb = 0;
-      row0 = row + nw;
-      bb = load_b(row0);
     }
+    cur = nxt;
+    nxt = take ? row_of(2 * kResWaves + __builtin_amdgcn_readfirstlane(q)) : N;
   }
 }
 
@@ -436,55 +418,45 @@ bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo) {
          ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1));
 }
 
-// Values per lane (EPL) and padded length 64 * EPL of the decoded x slices.
+// Values per lane (EPL): rows (and x) of up to 64 EPL elements.
 static int residual_rows_epl(int64_t K) {
   int epl = 8;
   while (64 * epl < K) epl *= 2;
   return epl;
 }
 
-// Workspace of the row path: x's FP32 slice values, then their exponents.
-size_t residual_rows_xs_bytes(int64_t K, int nhi, int nlo) {
-  return (size_t)(nhi + nlo) * (size_t)(64 * residual_rows_epl(K)) * sizeof(float);
-}
-size_t residual_rows_xe_bytes(int nhi, int nlo) {
-  return (size_t)(nhi + nlo) * sizeof(int32_t);
-}
+int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
 
 // r = b - Ozaki(A, x) for one right-hand side x (K elements, stride ldx):
-// x's slices into xs / xe (workspace), then the row kernel.  Also clears
-// `flags` and sets it for a non-finite x or A.
+// clears `flags`, then runs the row kernel, which sets it for a non-finite x
+// or A.  Needs no workspace.
 int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
                          const double* x, int64_t ldx, const double* b,
                          int64_t ldb, double* r, int64_t ldr, int rho, int nhi,
-                         int nlo, float* xs, int32_t* xe, uint32_t* flags,
-                         hipStream_t st) {
+                         int nlo, uint32_t* flags, hipStream_t st) {
+  const int rc = launch_fill_u32(flags, 0u, st);
+  if (rc) return rc;
   const int epl = residual_rows_epl(K);
-  const int64_t kp = 64 * epl;  // the kernel reads xs[p * kp + j * 64 + lane], j < epl
-  const int64_t xe_stride = 1;
-  hipLaunchKernelGGL(residual_x_kernel, dim3(1), dim3(kResXThreads), 0, st, x, K,
-                     ldx, rho, nhi, nlo, kp, xs, xe, flags);
-  OZK_LAUNCH_CHECK();
   // persistent grid: one workgroup of kResWaves waves per CU
   const int cus = cu_count();
   // every row start 16-byte aligned: the LDS row copy may be used
   const bool dma_ok = ((uintptr_t)A % 16 == 0) && (lda % 2 == 0 || N == 1);
   const int64_t need = (N + kResWaves - 1) / kResWaves;
   const dim3 grid((unsigned)(need < cus ? need : cus));
-#define OZK_RES(E, H, L)                                                           \
-  do {                                                                             \
-    if (K == 64 * (E) && (E) == 32 && dma_ok)                                      \
-      hipLaunchKernelGGL((residual_rows_kernel<E, true, (E) == 32, H, L>), grid,   \
-                         dim3(64 * kResWaves), 0, st, A, N, K, lda, xs, xe,        \
-                         xe_stride, b, ldb, r, ldr, rho, flags);                   \
-    else if (K == 64 * (E))                                                        \
-      hipLaunchKernelGGL((residual_rows_kernel<E, true, false, H, L>), grid,       \
-                         dim3(64 * kResWaves), 0, st, A, N, K, lda, xs, xe,        \
-                         xe_stride, b, ldb, r, ldr, rho, flags);                   \
-    else                                                                           \
-      hipLaunchKernelGGL((residual_rows_kernel<E, false, false, H, L>), grid,      \
-                         dim3(64 * kResWaves), 0, st, A, N, K, lda, xs, xe,        \
-                         xe_stride, b, ldb, r, ldr, rho, flags);                   \
+#define OZK_RES(E, H, L)                                                         \
+  do {                                                                           \
+    if (K == 64 * (E) && (E) == 32 && dma_ok)                                    \
+      hipLaunchKernelGGL((residual_rows_kernel<E, true, (E) == 32, H, L>), grid, \
+                         dim3(64 * kResWaves), 0, st, A, N, K, lda, x, ldx, b,   \
+                         ldb, r, ldr, rho, flags);                               \
+    else if (K == 64 * (E))                                                      \
+      hipLaunchKernelGGL((residual_rows_kernel<E, true, false, H, L>), grid,     \
+                         dim3(64 * kResWaves), 0, st, A, N, K, lda, x, ldx, b,   \
+                         ldb, r, ldr, rho, flags);                               \
+    else                                                                         \
+      hipLaunchKernelGGL((residual_rows_kernel<E, false, false, H, L>), grid,    \
+                         dim3(64 * kResWaves), 0, st, A, N, K, lda, x, ldx, b,   \
+                         ldb, r, ldr, rho, flags);                               \
   } while (0)
 #define OZK_RES_E(H, L)          \
   switch (epl) {                 \
