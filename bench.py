@@ -117,6 +117,18 @@ def accuracy_rows(A, B, C, precision, rows):
             float(np.max(np.abs(C - Ar @ B) / scale)), rho)
 
 
+def copy_calibration(dev):
+    """A plain 1 GiB FP64 elementwise copy (twice), whose HBM byte counters
+    scale those of the measured kernels in the same profiling run."""
+    import torch
+    log("copy calibration: 2 x 1 GiB float64 elementwise copy")
+    src = torch.ones(1 << 27, dtype=torch.float64, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(2):
+        torch.mul(src, 1.0, out=dst)
+    torch.cuda.synchronize()
+
+
 def _timeit(fn, reps, sync):
     fn()
     sync()
@@ -155,6 +167,9 @@ def suite(args):
 
     def want(group):
         return args.suite_filter in group
+
+    if args.copy_calibration:
+        copy_calibration(dev)
 
     # 0: matmul_numpy host pipeline, n_slices=8, 256^3, RandomState(0)
     if want("host"):
@@ -381,12 +396,7 @@ def main():
     dgemm_s = ev0.elapsed_time(ev1) / 1e3 / 3
 
     if args.copy_calibration:
-        log("copy calibration: 2 x 1 GiB float64 elementwise copy")
-        src = torch.ones(1 << 27, dtype=torch.float64, device=dev)
-        dst = torch.empty_like(src)
-        for _ in range(2):
-            torch.mul(src, 1.0, out=dst)
-        torch.cuda.synchronize()
+        copy_calibration(dev)
 
     acc = None
     if not args.no_check:
