@@ -55,7 +55,10 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
 int launch_probe_mfma(int32_t* out, hipStream_t st);
 bool gram_sym_supported(int nhi, int nlo);
 int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
-                    int nlo, double* G, int64_t ldg, hipStream_t st, bool i8, int rho);
+                    int nlo, double* G, int64_t ldg, void* ws, size_t ws_bytes,
+                    hipStream_t st, bool i8, int rho);
+size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int nlo,
+                       bool sym, bool i8);
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo);
 int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
                          const double* x, int64_t ldx, const double* b,
@@ -346,8 +349,11 @@ static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
   SliceSet sa = carve_slices(c, planes, N, K, eb);
   SliceSet sb = carve_slices(c, planes, M, K, eb);
   void* t = c.take(extract_workspace_bytes(K, M, 1));
-  // fold state between sweeps; the 2Sum state bounds every order's
-  const size_t gb = gemm_workspace_bytes(N, M, pipeline, nhi, nlo, OZK_ORDER_2SUM);
+  // fold state between sweeps (the 2Sum state bounds every order's), then
+  // the partial sums of a K-split tail
+  const size_t gb = round_up(gemm_workspace_bytes(N, M, pipeline, nhi, nlo, OZK_ORDER_2SUM),
+                             256) +
+                    gemm_tail_bytes(N, M, K, pipeline, nhi, nlo, false, eb == 1);
   void* g = c.take(gb);
   if (a) *a = sa;
   if (b) *b = sb;
@@ -422,8 +428,12 @@ static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,
   SliceSet ss = carve_slices(c, nhi + nlo, cols, rows,
                              use_i8(OZK_PIPE_ONDEVICE, rows, nhi, nlo) ? 1 : 2);
   void* t = c.take(extract_workspace_bytes(rows, cols, 1));
-  const size_t gb = gemm_workspace_bytes(cols, cols, OZK_PIPE_ONDEVICE, nhi, nlo,
-                                         OZK_ORDER_2SUM);
+  const bool i8 = use_i8(OZK_PIPE_ONDEVICE, rows, nhi, nlo);
+  const size_t gb = round_up(gemm_workspace_bytes(cols, cols, OZK_PIPE_ONDEVICE, nhi, nlo,
+                                                  OZK_ORDER_2SUM),
+                             256) +
+                    gemm_tail_bytes(cols, cols, rows, OZK_PIPE_ONDEVICE, nhi, nlo,
+                                    gram_sym_supported(nhi, nlo), i8);
   void* g = c.take(gb);
   if (s) *s = ss;
   if (tws) *tws = t;
@@ -472,7 +482,8 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
   // high / medium: upper tiles only, the symmetrisation folded into the
   // epilogue.  max (three K sweeps): full product, then symmetrise.
   if (gram_sym_supported(n_hi, n_lo))
-    return launch_gram_sym(s.s, s.e, cols, rows, n_hi, n_lo, G, ldg, st, i8, rho);
+    return launch_gram_sym(s.s, s.e, cols, rows, n_hi, n_lo, G, ldg, gws, gwsb, st, i8,
+                           rho);
   if ((rc = launch_gemm(s.s, s.e, s.s, s.e, cols, cols, rows, OZK_PIPE_ONDEVICE,
                         n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, gws, gwsb, st, i8, rho)))
     return rc;

@@ -425,6 +425,119 @@ template <> struct FoldState<OZK_ORDER_2SUM> {
     s[4 * nm + e] = f.p2;
   }
 };
+// ORDER value of the test hook that writes the per-pair products P.
+constexpr int kOrderProducts = -1;
+
+// Fold and store one output tile (tm, tn) from one wave's accumulators:
+// wave (wr, wc) owns rows 32 wr .. +31 and columns 16 wc .. +15 of the tile
+// as two 16x16 blocks h.  Shared by the all-pairs kernel and the fixup of
+// its K-split tail tiles.
+template <class Op, class SW, int ORDER, int B0, int B1, bool SYM>
+__device__ __forceinline__ void tile_epilogue(
+    const typename Op::acc_t (&acc)[SW::NP][2], int tm, int tn, int wr, int wc,
+    int lane, const int32_t* __restrict__ Ae, const int32_t* __restrict__ Be,
+    int64_t N, int64_t M, int64_t a_lines, int64_t b_lines, float unit2,
+    double* __restrict__ C, int64_t ldc, float* __restrict__ P, int64_t ldp,
+    char* __restrict__ state) {
+  constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
+  constexpr int NBLK = 3;
+  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+
+  // Accumulator register r of lane l of a 16x16 block holds row
+  // 4 * (l / 16) + r, column l % 16.
+  const int64_t col = col0 + 16 * wc + (lane & 15);
+  if constexpr (ORDER == kOrderProducts) {
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = row0 + 32 * wr + 16 * h + 4 * (lane >> 4) + r;
+        if (row < N && col < M) {
+#pragma unroll
+          for (int k = 0; k < NP; ++k)
+            P[((int64_t)(SW::P0 + k) * N + row) * ldp + col] =
+                Op::product(acc[k][h][r], unit2);
+        }
+      }
+    }
+  } else {
+    // Fold in schedule order; carry the state to the next sweep or store C.
+    // The exponents of the lane's column, and per 16-row block those of its
+    // 4 consecutive rows (one 16-byte load per A plane), are loaded
+    // together, so the epilogue waits for memory twice.  Rows and columns
+    // up to the padded line counts lie inside Ae / Be.
+    const int64_t rbase = row0 + 32 * wr + 4 * (lane >> 4);
+    int eb[NB];
+#pragma unroll
+    for (int q = 0; q < NB; ++q) eb[q] = Be[(SW::BB + q) * b_lines + col];
+    const int64_t nm = N * M;
+#pragma unroll
+    for (int h = 0; h < 2; ++h) {
+      int32x4 ea4[NA];
+#pragma unroll
+      for (int q = 0; q < NA; ++q)
+        ea4[q] = *(const int32x4*)(Ae + (SW::A0 + q) * a_lines + rbase + 16 * h);
+      // A sweep that continues the schedule loads the fold state of the
+      // block's 4 rows here too.
+      typename FoldOf<ORDER>::type fr[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        fr[r].init();
+        if constexpr (B0 > 0) {
+          const int64_t row = rbase + 16 * h + r;
+          if (row < N && col < M) FoldState<ORDER>::load(fr[r], state, row * M + col, nm);
+        }
+      }
+      // One wait for all of them here: the folds below sit in branches on
+      // `live`, and a wait placed inside them would also wait for the
+      // previous row's store.  (s_waitcnt vmcnt(0), other counters free.)
+      __builtin_amdgcn_s_waitcnt(0x0f70);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int64_t row = rbase + 16 * h + r;
+        const bool live = row < N && col < M;
+        int ea[NA];
+#pragma unroll
+        for (int q = 0; q < NA; ++q) ea[q] = ea4[q][r];
+        typename FoldOf<ORDER>::type& f = fr[r];
+#pragma unroll
+        for (int k = 0; k < NP; ++k) {
+          const PairInfo q = SW::pair(k);
+          const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
+          f.pair(q, Op::product(acc[k][h][r], unit2), ldexpf(1.0f, ib),
+                 ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+        }
+        if constexpr (SYM) {
+          // Element (col, row) of a gram matrix: its pair (a, b) product is
+          // this lane's pair (b, a) product, its row-side exponents are the
+          // column's and vice versa.  Fold it in schedule order too, then
+          // store (C[i][j] + C[j][i]) * 0.5 at both places (gram.py:37).
+          typename FoldOf<ORDER>::type f2;
+          f2.init();
+#pragma unroll
+          for (int k = 0; k < NP; ++k) {
+            const PairInfo q = SW::pair(k);
+            const int ia = eb[SW::la(k)], ib = ea[SW::lb(k)];
+            f2.pair(q, Op::product(acc[SW::tpair(k)][h][r], unit2), ldexpf(1.0f, ib),
+                    ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+          }
+          const double c1 = f.finish(NBLK), c2 = f2.finish(NBLK);
+          const double out = (c1 + c2) * 0.5;
+          if (live) {
+            C[row * ldc + col] = out;
+            if (tm != tn) C[col * ldc + row] = out;
+          }
+        } else if constexpr (B1 < NBLK - 1) {
+          if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
+        } else {
+          const double out = f.finish(NBLK);
+          if (live) C[row * ldc + col] = out;
+        }
+      }
+    }
+  }
+}
+
 // One K sweep over blocks B0..B1 of the on-device schedule, every pair of
 // those blocks accumulated in registers.  ORDER < 0 writes the per-pair FP32
 // products P[p][row][col] instead (test hook).  A sweep that does not start
@@ -436,7 +549,6 @@ template <> struct FoldState<OZK_ORDER_2SUM> {
 // workgroup b owns tiles b, b + gridDim.x, ... and runs their stages as one
 // sequence through the LDS ring, so the loads of a tile's first stages are
 // issued during the previous tile's last stages and epilogue.
-constexpr int kOrderProducts = -1;
 
 template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM>
 __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
@@ -444,10 +556,9 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     const char* __restrict__ Bs, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t nst, int64_t a_lines, int64_t b_lines,
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
-    int64_t ldp, char* __restrict__ state) {
+    int64_t ldp, char* __restrict__ state, int tail_P, uint32_t* __restrict__ part) {
   typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
-  constexpr int NBLK = 3;
   constexpr int kBuf = SW::S * 4 * 64;  // uint4 per stage buffer
   static_assert(kRing == 4, "wait_stage assumes 4 stage buffers");
   static_assert(SW::S <= 10, "a stage holds at most 10 planes (160 KiB ring)");
@@ -461,12 +572,23 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   static_assert(!SYM || (B0 == 0 && B1 == 2 && ORDER == OZK_ORDER_2SUM),
                 "symmetric products need the single-sweep schedule");
   const int ntiles = SYM ? ntm * (ntm + 1) / 2 : ntm * ntn;
-  const int my_tiles = (ntiles - 1 - bid) / nwg + 1;
   auto coords = [&](int t, int& tm, int& tn) {
     if constexpr (SYM) tile_coords_sym(t, ntm, tm, tn);
     else tile_coords(t, ntm, ntn, tm, tn);
   };
-  const int64_t total = (int64_t)my_tiles * nst;  // stages of this workgroup
+  // Work items of this workgroup: whole tiles bid + j nwg, j < nfull.  With
+  // tail_P > 1 (K-split tail) every workgroup runs the ntiles / nwg whole
+  // rounds, and the ntiles % nwg tail tiles are split along K into tail_P
+  // pieces of about nst / tail_P stages: workgroup bid < tail tiles * tail_P
+  // runs piece bid % tail_P of tail tile bid / tail_P and stores its raw
+  // sums in part (block bid) for gemm_tail_fixup.
+  const int nfull = tail_P ? ntiles / nwg : (ntiles - 1 - bid) / nwg + 1;
+  const bool has_piece = tail_P > 0 && bid < (ntiles % nwg) * tail_P;
+  const int piece_tile = has_piece ? nfull * nwg + bid / tail_P : 0;
+  const int64_t ps0 = has_piece ? (int64_t)(bid % tail_P) * nst / tail_P : 0;
+  const int64_t ps1 = has_piece ? (int64_t)(bid % tail_P + 1) * nst / tail_P : 0;
+  const int nitems = nfull + (has_piece ? 1 : 0);
+  const int64_t total = (int64_t)nfull * nst + (ps1 - ps0);  // stages of this workgroup
   const int64_t a_stage = a_lines * kChunkBytes, b_stage = b_lines * kChunkBytes;
   const int64_t aplane = a_stage * nst, bplane = b_stage * nst;
   const char* Ab = As + SW::A0 * aplane;
@@ -490,13 +612,15 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   const uint32_t lane_bytes = 16u * (uint32_t)lane;
   const uint32_t lds0 = lds_offset(lds);
   int fj = 0;
-  int64_t fs = 0;
-  const char *fA, *fB;
+  int64_t fs = 0, fe = 0;
+  const char *fA = Ab, *fB = Bb;
   auto load_tile = [&](int j) {
     int tm, tn;
-    coords(bid + j * nwg, tm, tn);
+    coords(j < nfull ? bid + j * nwg : piece_tile, tm, tn);
     fA = Ab + (int64_t)tm * kBM * kChunkBytes;
     fB = Bb + (int64_t)tn * kBN * kChunkBytes;
+    fs = j < nfull ? 0 : ps0;
+    fe = j < nfull ? nst : ps1;
   };
   // issue stage g of the sequence into ring buffer g % kRing
   auto fetch = [&](int64_t g) {
@@ -504,19 +628,19 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
       stage_dma<NA, NB>(fA, aplane, a_stage, fB, bplane, b_stage, fs,
                         lds0 + (uint32_t)((g & (kRing - 1)) * kBuf * 16), wave,
                         lane_bytes);
-    if (++fs == nst) {
-      fs = 0;
-      if (++fj < my_tiles) load_tile(fj);
+    if (++fs == fe) {
+      if (++fj < nitems) load_tile(fj);
     }
   };
-  load_tile(0);
+  if (nitems > 0) load_tile(0);
   for (int64_t g = 0; g < kRing - 1 && g < total; ++g) fetch(g);
 
   // Per stage g: wait for this wave's loads of stage g, barrier (stage g is
   // complete in LDS and every wave has finished stage g - 1, whose buffer is
   // refilled next), fetch stage g + kRing - 1, run the MFMAs of stage g;
-  // after a tile's last stage fold and store it.
-  int j = 0;  // tile of the MFMA cursor
+  // after a tile's last stage fold and store it (a tail piece: store its raw
+  // sums).
+  int j = 0;  // work item of the MFMA cursor
   int64_t s = 0;
   for (int64_t g = 0; g < total; ++g) {
     const int64_t later = total - 1 - g < kRing - 2 ? total - 1 - g : kRing - 2;
@@ -524,112 +648,84 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     __syncthreads();
     if (g + kRing - 1 < total) fetch(g + kRing - 1);
     mma(lds + (g & (kRing - 1)) * kBuf);
-    if (++s < nst) continue;
+    if (++s < (j < nfull ? nst : ps1 - ps0)) continue;
     s = 0;
-    int tm, tn;
-    coords(bid + j * nwg, tm, tn);
-    ++j;
-    const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
-
-    // Accumulator register r of lane l of a 16x16 block holds row
-    // 4 * (l / 16) + r, column l % 16.
-    const int64_t col = col0 + 16 * mma.wc + (lane & 15);
-    if constexpr (ORDER == kOrderProducts) {
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t row = row0 + 32 * mma.wr + 16 * h + 4 * (lane >> 4) + r;
-          if (row < N && col < M) {
-#pragma unroll
-            for (int k = 0; k < NP; ++k)
-              P[((int64_t)(SW::P0 + k) * N + row) * ldp + col] =
-                  Op::product(mma.acc[k][h][r], unit2);
-          }
-        }
-      }
+    if (j < nfull) {
+      int tm, tn;
+      coords(bid + j * nwg, tm, tn);
+      tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(mma.acc, tm, tn, mma.wr, mma.wc, lane, Ae,
+                                                Be, N, M, a_lines, b_lines, unit2, C, ldc,
+                                                P, ldp, state);
     } else {
-      // Fold in schedule order; carry the state to the next sweep or store C.
-      // The exponents of the lane's column, and per 16-row block those of its
-      // 4 consecutive rows (one 16-byte load per A plane), are loaded
-      // together, so the epilogue waits for memory twice.  Rows and columns
-      // up to the padded line counts lie inside Ae / Be.
-      const int64_t rbase = row0 + 32 * mma.wr + 4 * (lane >> 4);
-      int eb[NB];
+      // part[bid][thread][k][h]: each thread's sums are contiguous, so the
+      // 16-byte stores take immediate offsets
+      typename Op::acc_t* dst =
+          (typename Op::acc_t*)part + ((int64_t)bid * kThreads16 + threadIdx.x) * NP * 2;
 #pragma unroll
-      for (int q = 0; q < NB; ++q) eb[q] = Be[(SW::BB + q) * b_lines + col];
-      const int64_t nm = N * M;
-#pragma unroll
-      for (int h = 0; h < 2; ++h) {
-        int32x4 ea4[NA];
-#pragma unroll
-        for (int q = 0; q < NA; ++q)
-          ea4[q] = *(const int32x4*)(Ae + (SW::A0 + q) * a_lines + rbase + 16 * h);
-        // A sweep that continues the schedule loads the fold state of the
-        // block's 4 rows here too.
-        typename FoldOf<ORDER>::type fr[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          fr[r].init();
-          if constexpr (B0 > 0) {
-            const int64_t row = rbase + 16 * h + r;
-            if (row < N && col < M) FoldState<ORDER>::load(fr[r], state, row * M + col, nm);
-          }
-        }
-        // One wait for all of them here: the folds below sit in branches on
-        // `live`, and a wait placed inside them would also wait for the
-        // previous row's store.  (s_waitcnt vmcnt(0), other counters free.)
-        __builtin_amdgcn_s_waitcnt(0x0f70);
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int64_t row = rbase + 16 * h + r;
-          const bool live = row < N && col < M;
-          int ea[NA];
-#pragma unroll
-          for (int q = 0; q < NA; ++q) ea[q] = ea4[q][r];
-          typename FoldOf<ORDER>::type& f = fr[r];
-#pragma unroll
-          for (int k = 0; k < NP; ++k) {
-            const PairInfo q = SW::pair(k);
-            const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
-            f.pair(q, Op::product(mma.acc[k][h][r], unit2), ldexpf(1.0f, ib),
-                   ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
-          }
-          if constexpr (SYM) {
-            // Element (col, row) of a gram matrix: its pair (a, b) product is
-            // this lane's pair (b, a) product, its row-side exponents are the
-            // column's and vice versa.  Fold it in schedule order too, then
-            // store (C[i][j] + C[j][i]) * 0.5 at both places (gram.py:37).
-            typename FoldOf<ORDER>::type f2;
-            f2.init();
-#pragma unroll
-            for (int k = 0; k < NP; ++k) {
-              const PairInfo q = SW::pair(k);
-              const int ia = eb[SW::la(k)], ib = ea[SW::lb(k)];
-              f2.pair(q, Op::product(mma.acc[SW::tpair(k)][h][r], unit2), ldexpf(1.0f, ib),
-                      ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
-            }
-            const double c1 = f.finish(NBLK), c2 = f2.finish(NBLK);
-            const double out = (c1 + c2) * 0.5;
-            if (live) {
-              C[row * ldc + col] = out;
-              if (tm != tn) C[col * ldc + row] = out;
-            }
-          } else if constexpr (B1 < NBLK - 1) {
-            if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
-          } else {
-            const double out = f.finish(NBLK);
-            if (live) C[row * ldc + col] = out;
-          }
-        }
+      for (int k = 0; k < NP; ++k) {
+        dst[2 * k] = mma.acc[k][0];
+        dst[2 * k + 1] = mma.acc[k][1];
       }
     }
+    ++j;
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
       mma.acc[k][0] = typename Op::acc_t{};
       mma.acc[k][1] = typename Op::acc_t{};
     }
   }
+}
+
+// Tail tiles split along K: sums the tail_P pieces' raw sums (exact: integer
+// sums, or FP32 sums below 2^24 grid units) and folds the tile like the
+// all-pairs kernel.  One workgroup per (tail tile, wave of the all-pairs
+// workgroup): blockIdx.x = 8 * tail tile + wave slot.  Each of its 8 waves
+// adds up a sixth-or-so of the lane's 2 NP accumulator vectors over all
+// pieces (several pieces' loads in flight), leaves the sums in LDS, and
+// wave 0 folds them.  Tail tile t is tile tile0 + t of the all-pairs order.
+template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM>
+__global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
+    const uint32_t* __restrict__ part, int tail_P, int tile0,
+    const int32_t* __restrict__ Ae, const int32_t* __restrict__ Be, int64_t N,
+    int64_t M, int64_t a_lines, int64_t b_lines, float unit2, double* __restrict__ C,
+    int64_t ldc, float* __restrict__ P, int64_t ldp, char* __restrict__ state) {
+  typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
+  typedef typename Op::acc_t V;
+  constexpr int NP = SW::NP, NV = 2 * NP;  // accumulator vectors per lane
+  constexpr int PER = (NV + 7) / 8;        // vectors per wave
+  __shared__ V sum[NV][64];
+  const int tl = blockIdx.x >> 3, w = blockIdx.x & 7;
+  const int v = threadIdx.x >> 6, lane = threadIdx.x & 63;
+  V s[PER];
+#pragma unroll
+  for (int i = 0; i < PER; ++i) s[i] = V{};
+  // part[slot][thread][2 NP] with slot = tail tile * tail_P + piece and
+  // thread = 64 w + lane of the all-pairs workgroup
+  const V* src = (const V*)part + ((int64_t)tl * tail_P * kThreads16 + w * 64 + lane) * NV;
+  const int64_t piece_stride = (int64_t)kThreads16 * NV;
+#pragma unroll 4
+  for (int q = 0; q < tail_P; ++q) {
+#pragma unroll
+    for (int i = 0; i < PER; ++i)
+      if (v * PER + i < NV) s[i] += src[q * piece_stride + v * PER + i];
+  }
+#pragma unroll
+  for (int i = 0; i < PER; ++i)
+    if (v * PER + i < NV) sum[v * PER + i][lane] = s[i];
+  __syncthreads();
+  if (v != 0) return;
+  V acc[NP][2];
+#pragma unroll
+  for (int k = 0; k < NP; ++k) {
+    acc[k][0] = sum[2 * k][lane];
+    acc[k][1] = sum[2 * k + 1][lane];
+  }
+  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
+  int tm, tn;
+  if constexpr (SYM) tile_coords_sym(tile0 + tl, ntm, tm, tn);
+  else tile_coords(tile0 + tl, ntm, ntn, tm, tn);
+  tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(acc, tm, tn, w >> 2, w & 3, lane, Ae, Be, N, M,
+                                            a_lines, b_lines, unit2, C, ldc, P, ldp, state);
 }
 
 struct OnePairMMA {
@@ -772,9 +868,61 @@ size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
   return (size_t)N * (size_t)M * (size_t)fold_state_bytes(order);
 }
 
+// K-split of the tail.  With R = ntiles / cus whole rounds of one tile per
+// workgroup and T = ntiles % cus tiles left, the last round would keep T
+// CUs busy while the others idle.  Instead each tail tile is split along K
+// into P = min(cus / T, nst / kMinPieceStages) pieces, one per workgroup,
+// whose raw sums gemm_tail_fixup adds up and folds.  Single-sweep schedules
+// only; needs T * P * NP * 8 * kThreads16 * 4 bytes of workspace.
+constexpr int kMinPieceStages = 16;
+
+struct TailPlan {
+  int P = 0;        // pieces per tail tile (0: no split)
+  int64_t T = 0;    // tail tiles
+  int grid = 0;     // all-pairs workgroups
+  size_t bytes = 0; // partial sums
+};
+
+static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np) {
+  TailPlan tp;
+  const int64_t R = ntiles / cus, T = ntiles % cus;
+  if (T == 0) return tp;
+  const int64_t P = cus / T < nst / kMinPieceStages ? cus / T : nst / kMinPieceStages;
+  if (P < 2) return tp;
+  tp.P = (int)P;
+  tp.T = T;
+  tp.grid = R > 0 ? cus : (int)(T * P);
+  tp.bytes = (size_t)(T * P) * (size_t)np * 8 * kThreads16 * sizeof(uint32_t);
+  return tp;
+}
+
+static int64_t allpairs_ntiles(int64_t N, int64_t M, bool sym) {
+  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
+  return sym ? (al / kBM) * (al / kBM + 1) / 2 : (al / kBM) * (bl / kBN);
+}
+
+static int64_t allpairs_nst(int64_t K, bool i8) {
+  // chunks per line: round_up(K, kKPad) elements of 1 or 2 bytes
+  return round_up(K, kKPad) * (i8 ? 1 : 2) / kChunkBytes;
+}
+
+// Workspace of the K-split tail of an N x M (x K) all-pairs product: zero
+// when the product does not split.
+size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int nlo,
+                       bool sym, bool i8) {
+  if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(nhi, nlo) != 1) return 0;
+  return plan_tail(allpairs_ntiles(N, M, sym), cu_count(), allpairs_nst(K, i8),
+                   pair_count(pipe, nhi, nlo))
+      .bytes;
+}
+
 struct ApArgs {
   dim3 grid;
   bool sym;
+  int tail_P;
+  int tile0;  // first tail tile
+  int64_t tail_T;
+  uint32_t* part;
   hipStream_t st;
   const char *As, *Bs;
   const int32_t *Ae, *Be;
@@ -789,9 +937,18 @@ struct ApArgs {
 
 template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
 static void launch_sweep(const ApArgs& a) {
+  const bool split = a.tail_P > 1 && B0 == 0 && B1 == 2;
   hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
                      a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
-                     a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state);
+                     a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
+                     split ? a.tail_P : 0, a.part);
+  if constexpr (B0 == 0 && B1 == 2) {
+    if (split)
+      hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
+                         dim3((unsigned)(a.tail_T * 8)), dim3(kThreads16), 0, a.st, a.part, a.tail_P,
+                         a.tile0, a.Ae, a.Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P,
+                         a.ldp, a.state);
+  }
 }
 
 template <class Op, int NHI, int NLO, int ORDER>
@@ -826,7 +983,8 @@ static void launch_ap_order(int order, const ApArgs& a) {
 
 // All-pairs launch for a preset schedule; `i8` selects the INT8 plane
 // format (rho >= 19).  order = kOrderProducts writes P.  `state` holds
-// gemm_workspace_bytes() for multi-sweep schedules.
+// gemm_workspace_bytes() for multi-sweep schedules; a single-sweep schedule
+// splits its tail along K when `state` also holds gemm_tail_bytes().
 static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
                            const void* Bs, const int32_t* Be, int64_t N,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
@@ -840,11 +998,27 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   }
   ApArgs a;
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
-  const int64_t ntiles = sym ? (al / kBM) * (al / kBM + 1) / 2 : (al / kBM) * (bl / kBN);
+  const int64_t ntiles = allpairs_ntiles(N, M, sym);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
   // persistent: one workgroup per CU (the 160 KiB ring fills its LDS)
   const int cus = cu_count();
   a.grid = dim3((unsigned)(ntiles < cus ? ntiles : cus));
+  a.tail_P = 0;
+  a.tile0 = 0;
+  a.tail_T = 0;
+  a.part = nullptr;
+  if (allpairs_sweeps(nhi, nlo) == 1) {
+    const TailPlan tp = plan_tail(ntiles, cus, allpairs_nst(K, i8),
+                                  pair_count(OZK_PIPE_ONDEVICE, nhi, nlo));
+    const size_t off = round_up((int64_t)need, 256);
+    if (tp.P > 1 && state && state_bytes >= off + tp.bytes) {
+      a.grid = dim3((unsigned)tp.grid);
+      a.tail_P = tp.P;
+      a.tail_T = tp.T;
+      a.tile0 = (int)(ntiles - tp.T);
+      a.part = (uint32_t*)((char*)state + off);
+    }
+  }
   a.sym = sym;
   a.st = st;
   a.As = (const char*)As;
@@ -853,8 +1027,7 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.Be = Be;
   a.N = N;
   a.M = M;
-  // chunks per line: round_up(K, kKPad) elements of 1 or 2 bytes
-  a.nst = round_up(K, kKPad) * (i8 ? 1 : 2) / kChunkBytes;
+  a.nst = allpairs_nst(K, i8);
   a.al = al;
   a.bl = bl;
   a.unit2 = ldexpf(1.0f, 2 * rho - 48);
@@ -882,13 +1055,14 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
 bool gram_sym_supported(int nhi, int nlo) { return nlo == 1 && (nhi == 4 || nhi == 3); }
 
 int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
-                    int nlo, double* G, int64_t ldg, hipStream_t st, bool i8, int rho) {
+                    int nlo, double* G, int64_t ldg, void* ws, size_t ws_bytes,
+                    hipStream_t st, bool i8, int rho) {
   if (!gram_sym_supported(nhi, nlo)) {
     set_error("symmetric gram needs the high or medium preset");
     return OZK_ERR_UNSUPPORTED;
   }
   return launch_allpairs(i8, S, E, S, E, n, n, K, rho, nhi, nlo, OZK_ORDER_2SUM, G, ldg,
-                         nullptr, 0, nullptr, 0, st, true);
+                         nullptr, 0, ws, ws_bytes, st, true);
 }
 
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,

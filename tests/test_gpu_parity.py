@@ -343,6 +343,48 @@ def test_matmul_long_contraction_bit_exact(ozk, precision):
         assert np.array_equal(C, ref())
 
 
+def _tail_split(ntiles, K, i8, cus=256, min_piece=16):
+    """Pieces per tail tile of the all-pairs kernel's K-split tail on a GPU
+    with `cus` CUs (MI355X: 256): 0 when the product does not split."""
+    nst = -(-K // 64) * 64 * (1 if i8 else 2) // 64
+    T = ntiles % cus
+    if T == 0:
+        return 0
+    P = min(cus // T, nst // min_piece)
+    return P if P >= 2 else 0
+
+
+# Products whose tile count leaves a partial last round: the tail tiles are
+# split along K over the workgroups, their raw sums added by the fixup
+# kernel, then folded.  (N, K, M): 100 tiles in no full round; 324 tiles =
+# one round + 68 split tail tiles; BF16 planes (K <= 4096) with 121 tiles.
+@pytest.mark.parametrize("N,K,M", [(640, 8192, 640), (1100, 8192, 1100), (700, 4096, 700)])
+@pytest.mark.parametrize("precision", ["high", "medium"])
+def test_matmul_tail_split_bit_exact(ozk, N, K, M, precision):
+    ntiles = -(-N // 64) * -(-M // 64)
+    assert _tail_split(ntiles, K, K > 4096) >= 2  # the case exercises the split
+    A, B = gen("wide2", (N, K), N + 1), gen("randn", (K, M), M + 2)
+    nh, nl = OP.resolve_precision(precision)
+    rows = np.r_[0:40, N // 2:N // 2 + 24, N - 40:N]  # the last tile rows are tail tiles
+    for acc in ("fused", "host"):
+        case(f"matmul tail split {precision} {acc} ({N},{K},{M})")
+        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=precision)
+        ref = (O.matmul_ondevice_a3(A[rows], B, "raise", nh, nl) if acc == "host"
+               else O.matmul_ondevice_a4(A[rows], B, "raise", nh, nl))
+        assert np.array_equal(C[rows], ref)
+
+
+@pytest.mark.parametrize("precision", ["high", "medium"])
+def test_gram_tail_split_bit_exact(ozk, precision):
+    # 640 columns: 55 upper tiles of K = 8192 stages split 4 ways each
+    A = gen("randn", (8192, 640), 71)
+    assert _tail_split(10 * 11 // 2, 8192, True) == 4
+    case(f"gram tail split {precision} (8192,640)")
+    G = ozk.gram(A, mode="ozaki", precision=precision)
+    assert np.array_equal(G, O.gram_ozaki(A, precision))
+    assert np.array_equal(G, G.T)
+
+
 def test_matmul_numpy_bit_exact(ozk):
     A, B = gen("wide2", (70, 200), 31), gen("wide2", (200, 50), 32)
     case("matmul_numpy host / ondevice (70,200,50)")
