@@ -243,30 +243,29 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 }
 
-// Long FP32-path lines (ld up to 64 Ki elements): the hi part stays on chip
-// (groups j < EPT_R in registers, the others in LDS), the lo part is
-// streamed as in extract_lines_stream.  The first read of the line also
-// gives max|lo| for the lo part's first slice, so n_lo = 1 reads the line
-// twice in all (the streaming kernel reads it n + 1 times for
-// n = max(n_hi, n_lo) slices).  One line per workgroup of BLOCK threads;
-// thread t owns the 4 adjacent elements k = (j * BLOCK + t) * 4 + u of each
-// group j < EPT (EPT * BLOCK * 4 >= ld).
-template <int BLOCK, int EPT, int EPT_R, int FMT>
+// Lines of up to BLOCK * EPT * 4 elements (65536 at BLOCK 1024, EPT 16), FP32
+// path: a line's hi and lo parts (2 x 256 KiB) stay on chip after one read.
+// Thread t owns groups j < EPT of 4 consecutive elements k = (j BLOCK + t) 4 +
+// v.  Its lo parts live in registers (L, 16 float4 at EPT 16); of its hi
+// parts, groups j < EPT_R live in registers (R) and the others in LDS (144
+// KiB at EPT - EPT_R = 9).  Round s reduces the maxima of both parts, then
+// writes hi slice s (s < n0) and lo slice s (s < n1), like extract_lines_reg.
+// VECP (line starts 16-byte aligned, len % 4 == 0) reads a group with two
+// 16-byte loads, else element by element.  Launched for ld > 32768 only, so
+// ld / 4 > t for every thread (the store count below assumes it).
+template <int BLOCK, int EPT, int EPT_R, int FMT, bool VECP>
 __global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
-    const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx,
-    int vec_ok, int rho, int n0, int n1, typename PlaneElem<FMT>::type* __restrict__ S,
+    const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx, int rho,
+    int n0, int n1, typename PlaneElem<FMT>::type* __restrict__ S,
     int64_t ld, int64_t plane, int32_t* __restrict__ E, int64_t eplane,
     uint32_t* __restrict__ flags) {
   constexpr int VEC = 4;
   const float qscale = ldexpf(1.0f, 24 - rho);
   __shared__ float red[2 * (BLOCK / 64)];
-  __shared__ float sig[kMaxSlices], inv[kMaxSlices];
-  __shared__ int zero[kMaxSlices];
   __shared__ float4 hl[(EPT - EPT_R) * BLOCK];  // hi parts of groups EPT_R ..
   const int t = threadIdx.x;
   const int64_t line = xcd_line(blockIdx.x, gridDim.x);
   const bool live = line < lines;
-  const double* x = X + line * ldx;
   typedef typename PlaneElem<FMT>::type T;
   typedef typename PlaneVec<FMT, VEC>::type TV;
   constexpr int kPer = kChunkBytes / (int)sizeof(T);
@@ -274,134 +273,139 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
   const int64_t off0 = plane_offset<sizeof(T)>(line, (int64_t)t * VEC, eplane);
   const int64_t step = (int64_t)(BLOCK * VEC / kPer) * eplane * kPer;
 
-  // The thread's VEC doubles of group j, zero beyond the line.
-  auto load = [&](int j, double (&v)[VEC]) {
-    const int64_t k0 = ((int64_t)j * BLOCK + t) * VEC;
-    if (vec_ok && live && k0 + VEC <= len) {
-#pragma unroll
-      for (int u = 0; u < VEC; u += 2) {
-        const double2 d = *(const double2*)(x + k0 + u);
-        v[u] = d.x;
-        v[u + 1] = d.y;
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < VEC; ++u) v[u] = (live && k0 + u < len) ? x[k0 + u] : 0.0;
-    }
-  };
-  float4 R[EPT_R];
-  // Groups j < EPT_R live in R, the others in hl; every pass below runs
-  // two loops so that R is only ever indexed by unrolled constants.
+  float4 R[EPT_R];  // hi parts of groups j < EPT_R
+  float4 L[EPT];    // lo parts of every group
+  // Groups j >= EPT_R of the hi part live in hl; every pass over the hi part
+  // runs two loops so that R is only ever indexed by unrolled constants.
   float4* const H = hl + t;  // group j >= EPT_R at H[(j - EPT_R) * BLOCK]
 
-  // Read 1: hi parts on chip, max|lo| for the lo part's slice 0.
-  float mlo = 0.0f;
-  bool bad = false;
-  auto read1 = [&](int j) {
-    double v[VEC];
-    load(j, v);
-    float h[VEC];
+  // The one read: split every element into its hi and lo parts.  The loads
+  // are branch-free (an absent element reads the line's first one and is
+  // replaced by zero) and run kDepth groups ahead of the splits; the
+  // scheduling barriers keep the compiler from hoisting every load, which
+  // would hold all EPT groups' doubles in registers at once.
+  constexpr int kDepth = 3;
+  // Largest exponent field seen (0x7ff00000 marks a non-finite element); an
+  // integer in a register, so that the test needs no double kept alive.
+  uint32_t emax = 0;
+  // element indices fit 32 bits: the line is at most BLOCK * EPT * VEC long
+  const int n = live ? (int)len : 0;
+  const int ldi = (int)ld;
+  const double* const xs = X + (live ? line : 0) * ldx;
+  double buf[kDepth][VEC];
+  auto issue = [&](int j) {
+    double(&v)[VEC] = buf[j % kDepth];
+    const int k0 = (j * BLOCK + t) * VEC;
+    if (VECP) {  // len % VEC == 0: a group is whole or absent
+      const double2* const q = (const double2*)(xs + (k0 < n ? k0 : 0));
+      const double2 a = q[0], b = q[1];
+      v[0] = a.x;
+      v[1] = a.y;
+      v[2] = b.x;
+      v[3] = b.y;
+    } else {
+#pragma unroll
+      for (int u = 0; u < VEC; ++u) v[u] = xs[k0 + u < n ? k0 + u : 0];
+    }
+  };
+  auto split_group = [&](int j) {
+    const double(&v)[VEC] = buf[j % kDepth];
+    const int k0 = (j * BLOCK + t) * VEC;
+    float h[VEC], l[VEC];
 #pragma unroll
     for (int u = 0; u < VEC; ++u) {
-      bad |= !isfinite(v[u]);
+      const double d = (VECP ? k0 : k0 + u) < n ? v[u] : 0.0;
+      emax = max(emax, (uint32_t)__double2hiint(d) & 0x7ff00000u);
       float p[2];
-      split<float>(v[u], p);
+      split<float>(d, p);
       h[u] = p[0];
-      mlo = max_w(mlo, fabsf(p[1]));
+      l[u] = p[1];
     }
-    return make_float4(h[0], h[1], h[2], h[3]);
+    // (pins the split here: left alone, the compiler sinks it past the
+    // read and holds the doubles instead, twice the registers)
+#pragma unroll
+    for (int u = 0; u < VEC; ++u) asm volatile("" : "+v"(h[u]), "+v"(l[u]));
+    asm volatile("" : "+v"(emax));
+    L[j] = make_float4(l[0], l[1], l[2], l[3]);
+    const float4 hi = make_float4(h[0], h[1], h[2], h[3]);
+    if (j < EPT_R)
+      R[j < EPT_R ? j : 0] = hi;
+    else
+      H[(j - EPT_R) * BLOCK] = hi;
   };
 #pragma unroll
-  for (int j = 0; j < EPT_R; ++j) R[j] = read1(j);
-#pragma unroll 4
-  for (int j = EPT_R; j < EPT; ++j) H[(j - EPT_R) * BLOCK] = read1(j);
-  if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
-
-  // hi slices (extract_lines_reg, one part); the first round also reduces
-  // max|lo|.  Each thread only touches its own LDS elements, so the
-  // barriers inside block_max2 are the only ordering needed.
-  for (int s = 0; s < n0 || (s == 0 && n1 > 0); ++s) {
-    float m[2];
-    m[0] = 0.0f;
-    auto mx = [&](float4 q) {
-      m[0] = max_w(max_w(m[0], fabsf(q.x)), max_w(fabsf(q.y), max_w(fabsf(q.z), fabsf(q.w))));
-    };
+  for (int j = 0; j < kDepth; ++j) issue(j);
 #pragma unroll
-    for (int j = 0; j < EPT_R; ++j) mx(R[j]);
-#pragma unroll 4
-    for (int j = EPT_R; j < EPT; ++j) mx(H[(j - EPT_R) * BLOCK]);
-    m[1] = mlo;
-    block_max2<float, BLOCK, 1, 2>(m, red);
-    if (s == 0 && n1 > 0 && t == 0) {
-      const SliceConst<float> kc = slice_const<float>(m[1], rho);
-      sig[0] = kc.sigma;
-      inv[0] = kc.inv;
-      zero[0] = kc.zero;
-      E[(int64_t)n0 * eplane + line] = kc.c;
-    }
-    if (s >= n0) break;  // uniform
-    const SliceConst<float> kc = slice_const<float>(m[0], rho);
-    T* out = S + s * plane + off0;
-    auto sl = [&](int j, float4 q) {  // slice step of group j; returns the residual
-      const float r[VEC] = {q.x, q.y, q.z, q.w};
-      float nr[VEC];
-      union {
-        TV w;
-        T e[VEC];
-      } pk;
-#pragma unroll
-      for (int u = 0; u < VEC; ++u) {
-        float v = (r[u] + kc.sigma) - kc.sigma;
-        if (kc.zero) v = 0.0f;
-        nr[u] = r[u] - v;
-        pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
-      }
-      if (((int64_t)j * BLOCK + t) * VEC < ld) *(TV*)(out + j * step) = pk.w;
-      return make_float4(nr[0], nr[1], nr[2], nr[3]);
-    };
-#pragma unroll
-    for (int j = 0; j < EPT_R; ++j) R[j] = sl(j, R[j]);
-#pragma unroll 4
-    for (int j = EPT_R; j < EPT; ++j) H[(j - EPT_R) * BLOCK] = sl(j, H[(j - EPT_R) * BLOCK]);
-    if (t == 0) E[s * eplane + line] = kc.c;
+  for (int j = 0; j < EPT; ++j) {
+    split_group(j);
+    if (j + kDepth < EPT) issue(j + kDepth);
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (n1 == 0) return;
-  __syncthreads();  // sig / inv / zero of lo slice 0 are visible
+  if (emax == 0x7ff00000u) atomicOr(flags, OZK_FLAG_NONFINITE);
+  // Groups this thread stores (k0 < ld), counted from a fresh copy of t so
+  // that the read's indices are not kept alive for the tests below.
+  int tt = t;
+  asm volatile("" : "+v"(tt));
+  const int gst = (ldi / VEC - tt + BLOCK - 1) / BLOCK;
 
-  // lo slices 1 .. n1 - 1: one read each, replaying the earlier lo slices;
-  // then one read that writes the n1 lo planes.
-  for (int s = 1; s <= n1; ++s) {
-    float m = 0.0f;
-    for (int j = 0; j < EPT; ++j) {
-      double v[VEC];
-      load(j, v);
+  auto amax = [](float m, float4 q) {
+    return max_w(max_w(m, fabsf(q.x)), max_w(fabsf(q.y), max_w(fabsf(q.z), fabsf(q.w))));
+  };
+  // Slice step of group j with constants kc into `out`; returns the residual.
+  auto sl = [&](const SliceConst<float>& kc, T* out, int j, float4 q) {
+    const float r[VEC] = {q.x, q.y, q.z, q.w};
+    float nr[VEC];
+    union {
+      TV w;
+      T e[VEC];
+    } pk;
 #pragma unroll
-      for (int u = 0; u < VEC; ++u) {
-        float p[2];
-        split<float>(v[u], p);
-        float r = p[1];
-        for (int q = 0; q < s; ++q) {
-          float w = (r + sig[q]) - sig[q];
-          if (zero[q]) w = 0.0f;
-          if (s == n1 && ((int64_t)j * BLOCK + t) * VEC < ld)
-            S[(int64_t)(n0 + q) * plane + off0 + j * step + u] =
-                PlaneElem<FMT>::make(slice_value_f32(w, inv[q]), qscale);
-          r = r - w;
-        }
-        m = max_w(m, fabsf(r));
-      }
+    for (int u = 0; u < VEC; ++u) {
+      float v = (r[u] + kc.sigma) - kc.sigma;
+      if (kc.zero) v = 0.0f;
+      nr[u] = r[u] - v;
+      // (computes the residual ahead of the store's branch; left alone the
+      // compiler sinks it past the branch, holding v and r alive together)
+      asm volatile("" : "+v"(nr[u]));
+      pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
     }
-    if (s == n1) break;
-    float mm[1] = {m};
-    block_max2<float, BLOCK, 1, 1>(mm, red);
-    if (t == 0) {
-      const SliceConst<float> kc = slice_const<float>(mm[0], rho);
-      sig[s] = kc.sigma;
-      inv[s] = kc.inv;
-      zero[s] = kc.zero;
-      E[(int64_t)(n0 + s) * eplane + line] = kc.c;
+    if (j < gst) *(TV*)(out + j * step) = pk.w;
+    return make_float4(nr[0], nr[1], nr[2], nr[3]);
+  };
+
+  // Each thread only touches its own LDS elements, so the barriers inside
+  // block_max2 are the only ordering needed.
+  const int ns = max(n0, n1);
+  for (int s = 0; s < ns; ++s) {
+    float m[2] = {0.0f, 0.0f};
+    if (s < n0) {
+#pragma unroll
+      for (int j = 0; j < EPT_R; ++j) m[0] = amax(m[0], R[j]);
+#pragma unroll 4
+      for (int j = EPT_R; j < EPT; ++j) m[0] = amax(m[0], H[(j - EPT_R) * BLOCK]);
     }
-    __syncthreads();
+    if (s < n1) {
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) m[1] = amax(m[1], L[j]);
+    }
+    block_max2<float, BLOCK, 1, 2>(m, red);
+    if (s < n0) {  // uniform
+      const SliceConst<float> kc = slice_const<float>(m[0], rho);
+      T* out = S + s * plane + off0;
+#pragma unroll
+      for (int j = 0; j < EPT_R; ++j) R[j] = sl(kc, out, j, R[j]);
+#pragma unroll 4
+      for (int j = EPT_R; j < EPT; ++j)
+        H[(j - EPT_R) * BLOCK] = sl(kc, out, j, H[(j - EPT_R) * BLOCK]);
+      if (t == 0) E[s * eplane + line] = kc.c;
+    }
+    if (s < n1) {  // uniform
+      const SliceConst<float> kc = slice_const<float>(m[1], rho);
+      T* out = S + (n0 + s) * plane + off0;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) L[j] = sl(kc, out, j, L[j]);
+      if (t == 0) E[(n0 + s) * eplane + line] = kc.c;
+    }
   }
 }
 
@@ -506,10 +510,15 @@ static int launch_lines(const double* X, int64_t lines, int64_t len,
       if (ld <= 32768) {
         OZK_REG(512, 16, 1, 4);
         done = true;
-      } else if (ld <= 65536) {  // hi part in registers, lo part streamed
-        hipLaunchKernelGGL((extract_lines_hybrid<1024, 16, 8, FMT>), grid, dim3(1024), 0,
-                           st, X, lines, len, ldx, vec_ok, rho, n0, n1, S, ld, plane, E,
-                           lp, flags);
+      } else if (ld <= 65536) {  // both parts on chip, one read
+        if (vec_ok && len % 4 == 0)
+          hipLaunchKernelGGL((extract_lines_hybrid<1024, 16, 7, FMT, true>), grid, dim3(1024),
+                             0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E, lp,
+                             flags);
+        else
+          hipLaunchKernelGGL((extract_lines_hybrid<1024, 16, 7, FMT, false>), grid, dim3(1024),
+                             0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E, lp,
+                             flags);
         done = true;
       }
     }

@@ -121,12 +121,14 @@ def test_extract_f64_rows_and_cols(ll, shape):
 
 
 # Lines longer than the register-resident kernels hold: up to 64 Ki elements
-# the hi part stays on chip (registers + LDS) and the lo part is streamed;
-# longer lines stream both parts.  (n0, n1) = (2, 3) runs several lo passes.
+# both parts stay on chip (registers + LDS) after one read; longer lines
+# stream them.  (n0, n1) = (2, 3) runs more lo slices than hi slices; lengths
+# that are not a multiple of 4 take the element-wise loads.
 LONG_CASES = [("wide2", (3, 40000), 4, 1, False), ("zerorows", (3, 40000), 4, 1, False),
               ("wide2", (2, 65536), 4, 1, False), ("wide2", (2, 70000), 4, 1, False),
               ("wide2", (3, 40000), 2, 3, False), ("randn", (3, 40000), 4, 1, True),
-              ("wide2", (2, 65536), 5, 4, True)]
+              ("wide2", (2, 65536), 5, 4, True), ("wide2", (3, 40001), 4, 1, False),
+              ("wide2", (2, 49998), 3, 1, True), ("wide2", (2, 65533), 4, 2, False)]
 
 
 @pytest.mark.parametrize("kind,shape,n0,n1,i8", LONG_CASES)
@@ -171,6 +173,23 @@ def test_extract_nonfinite_flag(ll):
     X[2, 3] = np.nan
     case("nonfinite flag (nan) by cols")
     assert ll.extract(X, 1, 17, 4, 1).nonfinite()
+
+
+@pytest.mark.parametrize("length", [40000, 40001])
+def test_extract_nonfinite_flag_long_lines(ll, length):
+    """The on-chip long-line kernel (both load forms) raises the flag too, and
+    only when a line holds a non-finite element."""
+    X = np.ones((3, length))
+    rho = O.rho_f32(length)
+    case(f"nonfinite flag long lines {length}: finite")
+    assert not ll.extract(X, 0, rho, 4, 1).nonfinite()
+    X[2, length - 1] = np.inf
+    case(f"nonfinite flag long lines {length}: inf last element")
+    assert ll.extract(X, 0, rho, 4, 1).nonfinite()
+    X[2, length - 1] = 1.0
+    X[0, 1] = np.nan
+    case(f"nonfinite flag long lines {length}: nan")
+    assert ll.extract(X, 0, rho, 4, 1).nonfinite()
 
 
 # INT8 planes: q = slice * 2^(24 - rho), exact for rho >= 19.  Lines of
