@@ -45,6 +45,7 @@ extern "C" {
 #define OZK_ERR_WORKSPACE (-4)   /* workspace too small */
 
 #define OZK_FLAG_NONFINITE 1u
+#define OZK_FLAG_WAIT_TIMEOUT 2u /* ozk_lu_solve_f32: a row block's wait gave up */
 
 /* Accumulation orders (the four orders of the reference). */
 #define OZK_ORDER_2SUM 0     /* A4: pallas_ops.py:178-239 == matmul.py:382-488 */
@@ -210,6 +211,30 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
                  int64_t N, int64_t K, int64_t ncols, int n_hi, int n_lo,
                  void* workspace, size_t workspace_bytes, uint32_t* flags,
                  void* stream);
+
+/* The FP32 solves of solve(...) (solve.py:154-167): x0 = A32^-1 b and
+ * d = A32^-1 r in each refinement step, which the reference computes with
+ * jnp.linalg.solve(A32, .) (solve.py:159, :164) -- an LU factorisation with
+ * partial pivoting and two triangular solves.  This entry point does the
+ * triangular solves on an existing factor:
+ *     X = U^-1 L^-1 P B   for ncols right-hand sides.
+ * LU is n x n FP32, row-major (lda), as getrf leaves it: unit-diagonal L
+ * below the diagonal, U on and above it.  perm (device int32) is the row
+ * permutation: row i of P B is row perm[i] of B.  B and X are n x ncols FP64
+ * (ldb, ldx); B is rounded to FP32 first (r.astype(float32)) and X is the
+ * FP32 solution widened.  X may alias B.  flags is cleared first and
+ * receives OZK_FLAG_WAIT_TIMEOUT if a row block gave up waiting for the
+ * blocks it depends on (X is then invalid). */
+size_t ozk_lu_solve_workspace_bytes(int64_t n, int64_t ncols);
+int ozk_lu_solve_f32(const float* LU, int64_t lda, const int32_t* perm,
+                     int64_t n, const double* B, int64_t ldb, double* X,
+                     int64_t ldx, int64_t ncols, void* workspace,
+                     size_t workspace_bytes, uint32_t* flags, void* stream);
+
+/* LAPACK getrf pivots -> the permutation ozk_lu_solve_f32 takes.  ipiv is
+ * 1-based: step i swapped rows i and ipiv[i] - 1, for i = 0 .. n-1 in order.
+ * HOST arrays; no device work. */
+int ozk_pivots_to_perm(const int32_t* ipiv, int64_t n, int32_t* perm);
 
 /* np.isfinite(X).all() as a flag (matmul.py:108-109, :623-628). */
 int ozk_check_finite(const double* X, int64_t rows, int64_t cols, int64_t ld,

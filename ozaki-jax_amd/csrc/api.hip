@@ -53,6 +53,10 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho);
 int launch_probe_mfma(int32_t* out, hipStream_t st);
+size_t lu_solve_workspace_bytes(int64_t n, int64_t ncols);
+int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n,
+                    const double* B, int64_t ldb, double* X, int64_t ldx, int64_t ncols,
+                    void* ws, uint32_t* status, hipStream_t st);
 bool gram_sym_supported(int nhi, int nlo);
 int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
                     int nlo, double* G, int64_t ldg, void* ws, size_t ws_bytes,
@@ -571,6 +575,51 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   hipLaunchKernelGGL(sub_from_kernel, dim3(grid_for(N * ncols)), dim3(256), 0,
                      st, b, ldb, y, ncols, r, ldr, N, ncols);
   OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+size_t ozk_lu_solve_workspace_bytes(int64_t n, int64_t ncols) {
+  if (n <= 0 || ncols <= 0) return 0;
+  return lu_solve_workspace_bytes(n, ncols);
+}
+
+int ozk_lu_solve_f32(const float* LU, int64_t lda, const int32_t* perm,
+                     int64_t n, const double* B, int64_t ldb, double* X,
+                     int64_t ldx, int64_t ncols, void* workspace,
+                     size_t workspace_bytes, uint32_t* flags, void* stream) {
+  clear_error();
+  hipStream_t st = (hipStream_t)stream;
+  OZK_CHECK_ARG(n >= 0 && ncols >= 0, "invalid shape");
+  OZK_CHECK_ARG(n <= INT32_MAX, "n above the int32 row indices of perm");
+  OZK_CHECK_ARG((lda >= n || n <= 1) && (ldb >= ncols || n <= 1) &&
+                    (ldx >= ncols || n <= 1),
+                "leading dimension too small");
+  OZK_CHECK_ARG(flags, "null flags pointer");
+  int rc = launch_fill_u32(flags, 0u, st);
+  if (rc || n == 0 || ncols == 0) return rc;
+  OZK_CHECK_ARG(LU && perm && B && X, "null pointer");
+  const size_t need = ozk_lu_solve_workspace_bytes(n, ncols);
+  if (!workspace || workspace_bytes < need) {
+    set_error("lu_solve: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return OZK_ERR_WORKSPACE;
+  }
+  return launch_lu_solve(LU, lda, perm, n, B, ldb, X, ldx, ncols, workspace, flags, st);
+}
+
+int ozk_pivots_to_perm(const int32_t* ipiv, int64_t n, int32_t* perm) {
+  clear_error();
+  OZK_CHECK_ARG(n >= 0 && n <= INT32_MAX, "invalid size");
+  OZK_CHECK_ARG(n == 0 || (ipiv && perm), "null pointer");
+  for (int64_t i = 0; i < n; ++i) perm[i] = (int32_t)i;
+  for (int64_t i = 0; i < n; ++i) {
+    const int64_t p = (int64_t)ipiv[i] - 1;
+    OZK_CHECK_ARG(p >= i && p < n, "pivot %lld of step %lld outside [%lld, %lld)",
+                  (long long)p, (long long)i, (long long)i, (long long)n);
+    const int32_t s = perm[i];
+    perm[i] = perm[p];
+    perm[p] = s;
+  }
   return OZK_OK;
 }
 

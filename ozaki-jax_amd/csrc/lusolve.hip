@@ -1,0 +1,185 @@
+// Triangular solves with an FP32 LU factor: the refinement steps of
+// solve(residual_mode="ozaki") solve A32 d = r with the factor of A32
+// (ozaki_jax/solve.py:159, :164, where jnp.linalg.solve re-solves with the
+// same matrix).  Latency-bound: one right-hand side is a chain of n / 64
+// dependent 64-row blocks.
+#include "common.h"
+
+namespace ozk {
+
+constexpr int kTsRows = 64;   // rows per block (one wave solves a block)
+constexpr int kTsWaves = 4;   // waves per workgroup
+constexpr int kTsThreads = kTsRows * kTsWaves;
+// Polls of a block's flag before the wait is abandoned: a poll takes about a
+// microsecond (an agent-scope load plus s_sleep), a whole solve a few
+// hundred, so this only ends waits that cannot finish.
+constexpr uint32_t kTsSpinLimit = 1u << 21;
+
+// Forward (UPPER false: y = L^-1 P b, L unit lower) or backward (UPPER true:
+// x = U^-1 y) substitution.  LU is n x n row-major with leading dimension
+// lda.  Rows are cut into nb = ceil(n / 64) blocks; workgroup g of G handles
+// blocks g, g + G, ... (counted from the bottom going backward) of
+// right-hand side column c0 + blockIdx.y.
+//
+// Block k needs the solution of every block before it (after it, going
+// backward).  Each wave takes every fourth of those blocks in the order they
+// complete: it loads its 64 x 64 piece of LU (before waiting), polls the
+// block's flag, reads the block's solution from y and accumulates the
+// product.  Wave 0 then sums the four partial products, solves the diagonal
+// block (lane i holds row i; a step broadcasts x_j with lane_value), writes
+// the block's solution to y (and x going backward), and publishes its flag.
+// Dependencies point only to blocks a workgroup reaches earlier, so with all
+// G workgroups resident every wait ends; a wait that still exceeds
+// kTsSpinLimit polls (or sees another one fail) sets OZK_FLAG_WAIT_TIMEOUT
+// and stops waiting, so that every wave exits.
+// Lane j's value, for every lane (the builtin moves 32-bit integers).
+__device__ __forceinline__ float lane_value(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+template <bool UPPER>
+__global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
+    const float* __restrict__ LU, int64_t n, int64_t lda, int vec,
+    const int32_t* __restrict__ perm, const double* __restrict__ B, int64_t ldb,
+    float* __restrict__ y, int64_t ldy, double* __restrict__ X, int64_t ldx,
+    int64_t c0, uint32_t* __restrict__ flags, uint32_t* __restrict__ status) {
+  const int nb = (int)((n + kTsRows - 1) / kTsRows);
+  const int64_t col = c0 + blockIdx.y;
+  uint32_t* const fl = flags + (int64_t)blockIdx.y * nb;
+  __shared__ float part[kTsWaves][kTsRows];
+  const int w = threadIdx.x / kTsRows, lane = threadIdx.x % kTsRows;
+  bool failed = false;
+
+  for (int g = blockIdx.x; g < nb; g += gridDim.x) {
+    const int blk = UPPER ? nb - 1 - g : g;
+    const int64_t row = (int64_t)blk * kTsRows + lane;
+    const bool live = row < n;
+    const float* const lrow = LU + (live ? row : 0) * lda;
+    const int ndep = UPPER ? nb - 1 - blk : blk;
+
+    // Wave 0's right-hand side and diagonal-block row, loaded ahead of the
+    // waits so that the solve after the last one starts at once.
+    float rhs = 0.0f, dg[kTsRows];
+    if (w == 0) {
+      if (live) rhs = UPPER ? y[row * ldy + col] : (float)B[(int64_t)perm[row] * ldb + col];
+      const int64_t k0 = (int64_t)blk * kTsRows;
+#pragma unroll
+      for (int j = 0; j < kTsRows; ++j) dg[j] = (live && k0 + j < n) ? lrow[k0 + j] : 0.0f;
+    }
+
+    float acc = 0.0f;
+    for (int d = w; d < ndep; d += kTsWaves) {
+      const int c = UPPER ? nb - 1 - d : d;
+      const int64_t k0 = (int64_t)c * kTsRows;
+      float a[kTsRows];
+      if (vec && live && k0 + kTsRows <= n) {
+        const float4* const p = (const float4*)(lrow + k0);
+#pragma unroll
+        for (int q = 0; q < kTsRows / 4; ++q) {
+          const float4 v = p[q];
+          a[4 * q] = v.x;
+          a[4 * q + 1] = v.y;
+          a[4 * q + 2] = v.z;
+          a[4 * q + 3] = v.w;
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kTsRows; ++j) a[j] = (live && k0 + j < n) ? lrow[k0 + j] : 0.0f;
+      }
+      if (!failed) {
+        uint32_t spins = 0;
+        while (__hip_atomic_load(fl + c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
+          if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                  OZK_FLAG_WAIT_TIMEOUT ||
+              ++spins > kTsSpinLimit) {
+            failed = true;
+            break;
+          }
+          __builtin_amdgcn_s_sleep(2);
+        }
+      }
+      const float xv = k0 + lane < n ? y[(k0 + lane) * ldy + col] : 0.0f;
+#pragma unroll
+      for (int j = 0; j < kTsRows; ++j) acc = fmaf(a[j], lane_value(xv, j), acc);
+    }
+    part[w][lane] = acc;
+    __syncthreads();
+
+    if (w == 0) {
+      float v = 0.0f;
+      if (live) v = rhs - ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+      if (UPPER) {
+#pragma unroll
+        for (int j = kTsRows - 1; j >= 0; --j) {
+          if (lane == j) v = live ? v / dg[j] : 0.0f;
+          const float xj = lane_value(v, j);
+          if (lane < j) v = fmaf(-dg[j], xj, v);
+        }
+      } else {
+#pragma unroll
+        for (int j = 0; j < kTsRows; ++j) {
+          const float xj = lane_value(v, j);
+          if (lane > j) v = fmaf(-dg[j], xj, v);
+        }
+      }
+      if (live) {
+        y[row * ldy + col] = v;
+        if (UPPER) X[row * ldx + col] = (double)v;
+      }
+      __threadfence();
+      if (lane == 0) __hip_atomic_store(fl + blk, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    __syncthreads();  // part[] is rewritten by the next block
+  }
+  if (failed && lane == 0) atomicOr(status, OZK_FLAG_WAIT_TIMEOUT);
+}
+
+__global__ void fill_u32_array_kernel(uint32_t* p, int64_t count, uint32_t v) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = v;
+}
+
+static int64_t ts_blocks(int64_t n) { return (n + kTsRows - 1) / kTsRows; }
+
+// Columns per launch: the G x chunk workgroups of a launch must be resident
+// together (one per CU suffices).
+static int64_t ts_chunk(int64_t ncols) {
+  const int64_t cus = cu_count();
+  return ncols < cus ? ncols : cus;
+}
+
+size_t lu_solve_workspace_bytes(int64_t n, int64_t ncols) {
+  const size_t yb = (size_t)(n * ncols) * sizeof(float);
+  const size_t fb = (size_t)(2 * ts_blocks(n) * ts_chunk(ncols)) * sizeof(uint32_t);
+  return round_up((int64_t)yb, 256) + fb;
+}
+
+int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n,
+                    const double* B, int64_t ldb, double* X, int64_t ldx, int64_t ncols,
+                    void* ws, uint32_t* status, hipStream_t st) {
+  float* y = (float*)ws;
+  const int64_t nb = ts_blocks(n);
+  const int64_t chunk = ts_chunk(ncols);
+  uint32_t* flags = (uint32_t*)((char*)ws + round_up((int64_t)(n * ncols * sizeof(float)), 256));
+  const int vec = ((uintptr_t)LU % 16 == 0) && (lda % 4 == 0);
+  const int64_t per = cu_count() / chunk;
+  const unsigned G = (unsigned)(nb < per ? nb : (per > 0 ? per : 1));
+  for (int64_t c0 = 0; c0 < ncols; c0 += chunk) {
+    const int64_t nc = ncols - c0 < chunk ? ncols - c0 : chunk;
+    const int64_t nflags = 2 * nb * nc;
+    hipLaunchKernelGGL(fill_u32_array_kernel, dim3((unsigned)((nflags + 255) / 256)),
+                       dim3(256), 0, st, flags, nflags, 0u);
+    OZK_LAUNCH_CHECK();
+    hipLaunchKernelGGL(lu_trsv_kernel<false>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,
+                       LU, n, lda, vec, perm, B, ldb, y, ncols, X, ldx, c0, flags, status);
+    OZK_LAUNCH_CHECK();
+    hipLaunchKernelGGL(lu_trsv_kernel<true>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,
+                       LU, n, lda, vec, perm, B, ldb, y, ncols, X, ldx, c0, flags + nb * nc,
+                       status);
+    OZK_LAUNCH_CHECK();
+  }
+  return OZK_OK;
+}
+
+}  // namespace ozk

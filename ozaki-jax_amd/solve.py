@@ -4,11 +4,12 @@
 residual(mode='ozaki') is b - Ozaki(A, x) with the 2Sum order, computed by the
 HIP kernels (solve.py:38-53, :78-82).  solve(residual_mode='ozaki') is FP32 LU
 plus max_iterations refinement steps whose residuals come from the same
-kernels (solve.py:154-167).  The FP32 LU (jnp.linalg.solve in the
-reference) is a library dependency here: torch.linalg's GPU LU, factored once
-and reused -- the reference re-solves with the same matrix each iteration,
-which yields the same factors.  mode='f64' paths are plain FP64 products
-(rocBLAS DGEMM through torch).
+kernels (solve.py:154-167).  The reference's FP32 jnp.linalg.solve becomes
+an FP32 LU with partial pivoting, factored once and reused (the reference
+re-solves with the same matrix each iteration, which yields the same
+factors), and the library's triangular solves (ozk_lu_solve_f32) on that
+factor.  The factorisation itself is torch.linalg's GPU getrf.  mode='f64'
+paths are plain FP64 products (rocBLAS DGEMM through torch).
 """
 
 from . import _device as D
@@ -135,11 +136,15 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
     vec = bt.dim() == 1
     if vec:
         bt = bt[:, None].contiguous()
-    A32 = At.to(torch.float32)
-    LU, piv = torch.linalg.lu_factor(A32)
+    LU, piv, perm = lu_factor_f32(At, dev)
+    checks = []
 
     def solve32(rhs):
-        return torch.linalg.lu_solve(LU, piv, rhs.to(torch.float32)).to(torch.float64)
+        if rhs.shape[1] > LU_SOLVE_MAX_COLS:  # many columns (inv): a BLAS-3 TRSM
+            return torch.linalg.lu_solve(LU, piv, rhs.to(torch.float32)).to(torch.float64)
+        d, flags = lu_solve_f32(LU, perm, rhs, dev)
+        checks.append(flags)
+        return d
 
     x = solve32(bt)
     if residual_mode == "ozaki":
@@ -150,6 +155,50 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
         else:
             r = ozaki_residual_device(At, x.contiguous(), bt, n_hi, n_lo, dev)
         x = x + solve32(r)
+    if any(D.read_flags(f) & _lib.OZK_FLAG_WAIT_TIMEOUT for f in checks):
+        raise RuntimeError("ozk_lu_solve_f32: a row block gave up waiting for "
+                           "the blocks it depends on (GPU shared with other work?)")
     if vec:
         x = x[:, 0]
     return D.to_family(x, want_torch)
+
+
+# ozk_lu_solve_f32 solves each right-hand side as its own chain of row
+# blocks, re-reading the factor per column; beyond this many columns the
+# solve goes to torch.linalg.lu_solve, whose triangular solves share the
+# factor's reads across columns.
+LU_SOLVE_MAX_COLS = 8
+
+
+def lu_factor_f32(At, dev):
+    """FP32 LU with partial pivoting of the FP64 device matrix At (the
+    factorisation inside the reference's jnp.linalg.solve(A32, .),
+    solve.py:159): (LU row-major FP32, LAPACK pivots, perm device int32 for
+    ozk_lu_solve_f32)."""
+    torch = D.torch
+    lib = _lib.load()
+    n = At.shape[0]
+    LU, piv = torch.linalg.lu_factor(At.to(torch.float32))
+    LU = LU.contiguous()
+    piv_h = piv.to(device="cpu", dtype=torch.int32).contiguous()
+    perm_h = torch.empty(n, dtype=torch.int32)
+    _lib.check(lib.ozk_pivots_to_perm(piv_h.data_ptr(), n, perm_h.data_ptr()))
+    return LU, piv, perm_h.to(dev)
+
+
+def lu_solve_f32(LU, perm, rhs, dev):
+    """d = A32^-1 rhs through ozk_lu_solve_f32 on a factor from
+    lu_factor_f32; rhs is an (n, k) FP64 device tensor, d likewise.  Returns
+    (d, flags); flags holds OZK_FLAG_WAIT_TIMEOUT if the solve gave up."""
+    torch = D.torch
+    lib = _lib.load()
+    n, nc = rhs.shape
+    d = torch.empty((n, nc), dtype=torch.float64, device=dev)
+    flags = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the call
+    wsb = lib.ozk_lu_solve_workspace_bytes(n, nc)
+    ws = D.workspace(wsb, dev)
+    _lib.check(lib.ozk_lu_solve_f32(
+        LU.data_ptr(), D.ld_of(LU), perm.data_ptr(), n, rhs.data_ptr(),
+        D.ld_of(rhs), d.data_ptr(), D.ld_of(d), nc, ws.data_ptr(), wsb,
+        flags.data_ptr(), D.stream_handle()))
+    return d, flags

@@ -127,6 +127,40 @@ def test_argument_errors_before_device_work(lib):
         _lib.check(rc)
 
 
+def test_pivots_to_perm(lib):
+    """LAPACK's sequential swaps -> the permutation: row i of P A is row
+    perm[i] of A, pinned by P A = L U on SciPy's float64 factors."""
+    import scipy.linalg as sla
+    from ozaki_jax_amd import _lib
+    rng = np.random.RandomState(0)
+    for n in (1, 2, 7, 64, 300):
+        A = rng.randn(n, n)
+        lu, piv = sla.lu_factor(A)
+        ipiv = (piv + 1).astype(np.int32)
+        perm = np.empty(n, np.int32)
+        assert lib.ozk_pivots_to_perm(ipiv.ctypes.data, n, perm.ctypes.data) == 0
+        assert sorted(perm) == list(range(n))
+        L = np.tril(lu, -1) + np.eye(n)
+        U = np.triu(lu)
+        assert np.allclose(A[perm], L @ U, rtol=0, atol=1e-12 * n)
+    bad = np.array([2, 1], np.int32)  # step 1 swapping with row 0 < 1
+    perm = np.empty(2, np.int32)
+    assert lib.ozk_pivots_to_perm(bad.ctypes.data, 2, perm.ctypes.data) == _lib.OZK_ERR_INVALID
+    assert b"outside" in lib.ozk_last_error()
+
+
+def test_lu_solve_argument_errors(lib):
+    from ozaki_jax_amd import _lib
+    assert lib.ozk_lu_solve_workspace_bytes(0, 1) == 0
+    assert lib.ozk_lu_solve_workspace_bytes(4096, 1) >= 4096 * 4
+    rc = lib.ozk_lu_solve_f32(None, 4, None, -1, None, 1, None, 1, 1, None, 0, None, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"invalid shape" in lib.ozk_last_error()
+    rc = lib.ozk_lu_solve_f32(None, 2, None, 4, None, 1, None, 1, 1, None, 0, None, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"leading dimension" in lib.ozk_last_error()
+    rc = lib.ozk_lu_solve_f32(None, 4, None, 4, None, 1, None, 1, 1, None, 0, None, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"flags" in lib.ozk_last_error()
+
+
 def test_package_fails_loudly_without_gpu():
     import numpy as np
     import torch
