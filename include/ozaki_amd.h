@@ -46,6 +46,7 @@ extern "C" {
 
 #define OZK_FLAG_NONFINITE 1u
 #define OZK_FLAG_WAIT_TIMEOUT 2u /* ozk_lu_solve_f32: a row block's wait gave up */
+#define OZK_FLAG_SINGULAR 4u     /* ozk_lu_factor_f32: a zero pivot */
 
 /* Accumulation orders (the four orders of the reference). */
 #define OZK_ORDER_2SUM 0     /* A4: pallas_ops.py:178-239 == matmul.py:382-488 */
@@ -211,6 +212,22 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
                  int64_t N, int64_t K, int64_t ncols, int n_hi, int n_lo,
                  void* workspace, size_t workspace_bytes, uint32_t* flags,
                  void* stream);
+
+/* FP32 LU factorisation with partial pivoting, in place: the factorisation
+ * inside the reference's jnp.linalg.solve(A32, .) (solve.py:159).  A is
+ * n x n FP32, row-major (lda); on return it holds the unit-diagonal L below
+ * the diagonal and U on and above it, and perm (device int32, n entries)
+ * the row permutation (row i of P A is row perm[i] of A), the form
+ * ozk_lu_solve_f32 takes.  The pivot of a column is its largest |value| on
+ * or below the diagonal (the lowest row on ties).  flags is cleared first
+ * and receives OZK_FLAG_SINGULAR if a pivot is zero; as in LAPACK's getrf
+ * the factorisation then completes and U has a zero on its diagonal.
+ * n <= ozk_lu_factor_max_n(); larger n return OZK_ERR_UNSUPPORTED. */
+int64_t ozk_lu_factor_max_n(void);
+size_t ozk_lu_factor_workspace_bytes(int64_t n);
+int ozk_lu_factor_f32(float* A, int64_t lda, int64_t n, int32_t* perm,
+                      void* workspace, size_t workspace_bytes, uint32_t* flags,
+                      void* stream);
 
 /* The FP32 solves of solve(...) (solve.py:154-167): x0 = A32^-1 b and
  * d = A32^-1 r in each refinement step, which the reference computes with

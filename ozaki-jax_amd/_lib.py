@@ -19,6 +19,7 @@ OZK_ERR_UNSUPPORTED = -3
 OZK_ERR_WORKSPACE = -4
 OZK_FLAG_NONFINITE = 1
 OZK_FLAG_WAIT_TIMEOUT = 2
+OZK_FLAG_SINGULAR = 4
 
 ORDER_2SUM = 0       # A4  pallas_ops.py:178-239
 ORDER_BLOCK64 = 1    # A3  matmul.py:543-597
@@ -78,6 +79,10 @@ SIGNATURES = {
     "ozk_residual": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,
                               _c_i64, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                               _c_vp, _c_size, _c_vp, _c_vp]),
+    "ozk_lu_factor_max_n": (_c_i64, []),
+    "ozk_lu_factor_workspace_bytes": (_c_size, [_c_i64]),
+    "ozk_lu_factor_f32": (_c_int, [_c_vp, _c_i64, _c_i64, _c_vp, _c_vp, _c_size, _c_vp,
+                                   _c_vp]),
     "ozk_lu_solve_workspace_bytes": (_c_size, [_c_i64, _c_i64]),
     "ozk_lu_solve_f32": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,
                                   _c_i64, _c_i64, _c_vp, _c_size, _c_vp, _c_vp]),

@@ -54,6 +54,10 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t ldp, hipStream_t st, bool i8, int rho);
 int launch_probe_mfma(int32_t* out, hipStream_t st);
 size_t lu_solve_workspace_bytes(int64_t n, int64_t ncols);
+int64_t lu_factor_max_n();
+size_t lu_factor_workspace_bytes();
+int launch_lu_factor(float* A, int64_t lda, int64_t n, int32_t* perm, void* ws,
+                     uint32_t* status, hipStream_t st);
 int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n,
                     const double* B, int64_t ldb, double* X, int64_t ldx, int64_t ncols,
                     void* ws, uint32_t* status, hipStream_t st);
@@ -576,6 +580,36 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
                      st, b, ldb, y, ncols, r, ldr, N, ncols);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
+}
+
+int64_t ozk_lu_factor_max_n(void) { return lu_factor_max_n(); }
+
+size_t ozk_lu_factor_workspace_bytes(int64_t n) {
+  return n > 0 ? lu_factor_workspace_bytes() : 0;
+}
+
+int ozk_lu_factor_f32(float* A, int64_t lda, int64_t n, int32_t* perm,
+                      void* workspace, size_t workspace_bytes, uint32_t* flags,
+                      void* stream) {
+  clear_error();
+  hipStream_t st = (hipStream_t)stream;
+  OZK_CHECK_ARG(n >= 0, "invalid shape");
+  OZK_CHECK_ARG(lda >= n || n <= 1, "leading dimension too small");
+  OZK_CHECK_ARG(flags, "null flags pointer");
+  if (n > lu_factor_max_n()) {
+    set_error("lu_factor: n = %lld above the %lld rows a panel holds", (long long)n,
+              (long long)lu_factor_max_n());
+    return OZK_ERR_UNSUPPORTED;
+  }
+  int rc = launch_fill_u32(flags, 0u, st);
+  if (rc || n == 0) return rc;
+  OZK_CHECK_ARG(A && perm, "null pointer");
+  const size_t need = ozk_lu_factor_workspace_bytes(n);
+  if (!workspace || workspace_bytes < need) {
+    set_error("lu_factor: workspace of %zu bytes needed, %zu given", need, workspace_bytes);
+    return OZK_ERR_WORKSPACE;
+  }
+  return launch_lu_factor(A, lda, n, perm, workspace, flags, st);
 }
 
 size_t ozk_lu_solve_workspace_bytes(int64_t n, int64_t ncols) {

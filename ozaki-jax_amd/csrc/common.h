@@ -5,10 +5,20 @@
 #include <stdint.h>
 
 #include <string>
+#include <type_traits>
 
 #include "../../include/ozaki_amd.h"
 
 namespace ozk {
+
+// f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time.
+template <int B, int E, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(std::integral_constant<int, B>{});
+    static_for<B + 1, E>(f);
+  }
+}
 
 // ---------------------------------------------------------------- errors
 // Thread-local message behind ozk_last_error(); every entry point clears it

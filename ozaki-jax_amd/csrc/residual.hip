@@ -12,21 +12,10 @@
 // result.  The per-row pair products are then folded in schedule order.
 // The work is bound by the read of A and the VALU work of the extraction.
 
-#include <type_traits>
-
 #include "fold.h"
 #include "sigma.h"
 
 namespace ozk {
-
-// f(integral_constant<int, I>) for I = B .. E - 1, unrolled at compile time.
-template <int B, int E, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-  if constexpr (B < E) {
-    f(std::integral_constant<int, B>{});
-    static_for<B + 1, E>(f);
-  }
-}
 
 constexpr int kResWaves = 8;   // waves per workgroup: two per SIMD
 constexpr int kResBatch = 16;  // rows whose pair products are folded together

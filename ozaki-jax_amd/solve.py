@@ -7,9 +7,10 @@ plus max_iterations refinement steps whose residuals come from the same
 kernels (solve.py:154-167).  The reference's FP32 jnp.linalg.solve becomes
 an FP32 LU with partial pivoting, factored once and reused (the reference
 re-solves with the same matrix each iteration, which yields the same
-factors), and the library's triangular solves (ozk_lu_solve_f32) on that
-factor.  The factorisation itself is torch.linalg's GPU getrf.  mode='f64'
-paths are plain FP64 products (rocBLAS DGEMM through torch).
+factors): ozk_lu_factor_f32 up to n = ozk_lu_factor_max_n() (torch.linalg's
+getrf above), then the library's triangular solves (ozk_lu_solve_f32) on that
+factor.  mode='f64' paths are plain FP64 products (rocBLAS DGEMM through
+torch).
 """
 
 from . import _device as D
@@ -136,12 +137,14 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
     vec = bt.dim() == 1
     if vec:
         bt = bt[:, None].contiguous()
-    LU, piv, perm = lu_factor_f32(At, dev)
+    LU, perm = lu_factor_f32(At, dev)
     checks = []
 
     def solve32(rhs):
-        if rhs.shape[1] > LU_SOLVE_MAX_COLS:  # many columns (inv): a BLAS-3 TRSM
-            return torch.linalg.lu_solve(LU, piv, rhs.to(torch.float32)).to(torch.float64)
+        if rhs.shape[1] > LU_SOLVE_MAX_COLS:  # many columns (inv): BLAS-3 TRSMs
+            y = torch.linalg.solve_triangular(LU, rhs.to(torch.float32)[perm.long()],
+                                              upper=False, unitriangular=True)
+            return torch.linalg.solve_triangular(LU, y, upper=True).to(torch.float64)
         d, flags = lu_solve_f32(LU, perm, rhs, dev)
         checks.append(flags)
         return d
@@ -165,25 +168,38 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
 
 # ozk_lu_solve_f32 solves each right-hand side as its own chain of row
 # blocks, re-reading the factor per column; beyond this many columns the
-# solve goes to torch.linalg.lu_solve, whose triangular solves share the
-# factor's reads across columns.
+# solve goes to torch.linalg.solve_triangular, whose triangular solves share
+# the factor's reads across columns.
 LU_SOLVE_MAX_COLS = 8
 
 
 def lu_factor_f32(At, dev):
     """FP32 LU with partial pivoting of the FP64 device matrix At (the
     factorisation inside the reference's jnp.linalg.solve(A32, .),
-    solve.py:159): (LU row-major FP32, LAPACK pivots, perm device int32 for
-    ozk_lu_solve_f32)."""
+    solve.py:159): (LU, perm) with LU an (n, n) row-major FP32 view (unit L
+    below the diagonal, U on and above it) and perm the device int32 row
+    permutation (row i of P A is row perm[i] of A)."""
     torch = D.torch
     lib = _lib.load()
     n = At.shape[0]
+    if n <= lib.ozk_lu_factor_max_n():
+        lda = max(-(-n // 4) * 4, 4)  # 16-byte rows for the kernels' vector loads
+        LU = torch.empty((n, lda), dtype=torch.float32, device=dev)[:, :n]
+        LU.copy_(At)
+        perm = torch.empty(n, dtype=torch.int32, device=dev)
+        flags = torch.empty(1, dtype=torch.int32, device=dev)  # cleared by the call
+        wsb = lib.ozk_lu_factor_workspace_bytes(n)
+        ws = D.workspace(wsb, dev)
+        _lib.check(lib.ozk_lu_factor_f32(LU.data_ptr(), lda, n, perm.data_ptr(),
+                                         ws.data_ptr(), wsb, flags.data_ptr(),
+                                         D.stream_handle()))
+        return LU, perm
     LU, piv = torch.linalg.lu_factor(At.to(torch.float32))
     LU = LU.contiguous()
     piv_h = piv.to(device="cpu", dtype=torch.int32).contiguous()
     perm_h = torch.empty(n, dtype=torch.int32)
     _lib.check(lib.ozk_pivots_to_perm(piv_h.data_ptr(), n, perm_h.data_ptr()))
-    return LU, piv, perm_h.to(dev)
+    return LU, perm_h.to(dev)
 
 
 def lu_solve_f32(LU, perm, rhs, dev):

@@ -149,6 +149,20 @@ def test_pivots_to_perm(lib):
     assert b"outside" in lib.ozk_last_error()
 
 
+def test_lu_factor_limits(lib):
+    from ozaki_jax_amd import _lib
+    nmax = lib.ozk_lu_factor_max_n()
+    assert nmax == 4096
+    assert lib.ozk_lu_factor_workspace_bytes(0) == 0
+    assert lib.ozk_lu_factor_workspace_bytes(nmax) > 0
+    flags = ctypes.c_uint32(0)
+    rc = lib.ozk_lu_factor_f32(None, nmax + 1, nmax + 1, None, None, 0,
+                               ctypes.addressof(flags), None)
+    assert rc == _lib.OZK_ERR_UNSUPPORTED and b"panel" in lib.ozk_last_error()
+    rc = lib.ozk_lu_factor_f32(None, 3, 4, None, None, 0, ctypes.addressof(flags), None)
+    assert rc == _lib.OZK_ERR_INVALID and b"leading dimension" in lib.ozk_last_error()
+
+
 def test_lu_solve_argument_errors(lib):
     from ozaki_jax_amd import _lib
     assert lib.ozk_lu_solve_workspace_bytes(0, 1) == 0

@@ -1,8 +1,14 @@
-"""Triangular solves on an FP32 LU factor (ozk_lu_solve_f32), the FP32 solve
-of solve(...) (ozaki_jax/solve.py:159, :164).
+"""The FP32 solve of solve(...) (ozaki_jax/solve.py:159, :164): the LU
+factorisation with partial pivoting (ozk_lu_factor_f32) and the triangular
+solves on a factor (ozk_lu_solve_f32).
 
-The factors come from SciPy's float32 getrf on the CPU, so the test checks the
-solves alone: the result is compared with the same triangular solves done in
+The factorisation is checked by what defines it: P A = L U to FP32 rounding
+(|P A - L U| <= 8 n eps32 max|A|, a bound that a wrong swap, multiplier or
+update exceeds by orders of magnitude), |L| <= 1 (partial pivoting), perm a
+permutation, and for n <= 64 the same pivots as LAPACK's sgetrf.
+
+For the solves, the factors come from SciPy's float32 getrf on the CPU, so
+the test checks the solves alone: the result is compared with the same triangular solves done in
 float64 on the same FP32 factors.  What is left is the kernel's FP32 rounding,
 bounded through the factors' conditioning: well-conditioned factors (a
 diagonally dominant matrix with its rows shuffled, so that partial pivoting
@@ -126,3 +132,75 @@ def test_solve_uses_native_triangular_solves(ozk):
     x = ozk.solve(A, b, residual_mode="ozaki")
     xr = np.linalg.solve(A, b)
     assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-4
+
+
+def gpu_factor(A32, pad=0):
+    import torch
+    from ozaki_jax_amd import _device as D, _lib
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    n = A32.shape[0]
+    buf = np.zeros((n, n + pad), np.float32)
+    buf[:, :n] = A32
+    At = torch.from_numpy(buf).to(dev)
+    perm = torch.empty(n, dtype=torch.int32, device=dev)
+    flags = torch.full((1,), 7, dtype=torch.int32, device=dev)
+    wsb = lib.ozk_lu_factor_workspace_bytes(n)
+    ws = D.workspace(wsb, dev)
+    _lib.check(lib.ozk_lu_factor_f32(At.data_ptr(), n + pad, n, perm.data_ptr(),
+                                     ws.data_ptr(), wsb, flags.data_ptr(),
+                                     D.stream_handle()))
+    return At.cpu().numpy()[:, :n], perm.cpu().numpy(), int(flags.item())
+
+
+FACTOR_CASES = [(1, 0), (2, 0), (17, 1), (32, 0), (33, 0), (48, 3), (64, 0), (100, 0),
+                (257, 2), (1000, 0), (2048, 1), (4096, 0)]
+
+
+@pytest.mark.parametrize("n,pad", FACTOR_CASES)
+def test_lu_factor_pa_equals_lu(ozk, n, pad):
+    rng = np.random.RandomState(100 + n)
+    A32 = rng.randn(n, n).astype(np.float32)
+    case(f"ozk_lu_factor_f32 n={n} lda=n+{pad}")
+    F, perm, flags = gpu_factor(A32, pad)
+    assert flags == 0
+    assert sorted(perm.tolist()) == list(range(n)), "perm"
+    L = np.tril(F.astype(np.float64), -1) + np.eye(n)
+    U = np.triu(F.astype(np.float64))
+    assert np.abs(np.tril(F, -1)).max(initial=0.0) <= 1.0, "|L| <= 1"
+    err = np.abs(A32.astype(np.float64)[perm] - L @ U).max()
+    assert err <= 8 * n * np.finfo(np.float32).eps * np.abs(A32).max(), err
+    if n <= 64:
+        _, piv = sla.lu_factor(A32)
+        ps = np.arange(n)
+        for i, p in enumerate(piv):
+            ps[i], ps[p] = ps[p], ps[i]
+        assert np.array_equal(ps, perm), "pivots differ from sgetrf"
+
+
+def test_lu_factor_singular_flag(ozk):
+    from ozaki_jax_amd import _lib
+    rng = np.random.RandomState(7)
+    A32 = rng.randn(40, 40).astype(np.float32)
+    case("ozk_lu_factor_f32 nonsingular: no flag")
+    assert gpu_factor(A32)[2] == 0
+    A32[:, 20] = 0.0
+    case("ozk_lu_factor_f32 zero column: singular flag")
+    F, perm, flags = gpu_factor(A32)
+    assert flags & _lib.OZK_FLAG_SINGULAR
+    assert np.isfinite(F).all() and F[20, 20] == 0.0
+
+
+def test_solve_n4096_native_factor_and_solves(ozk):
+    """The C5 solve shape (n = 4096, condition 1e6) end to end through the
+    native factorisation and triangular solves."""
+    rng = np.random.RandomState(3)
+    n = 4096
+    Q1, _ = np.linalg.qr(rng.randn(n, n))
+    Q2, _ = np.linalg.qr(rng.randn(n, n))
+    A = (Q1 * np.logspace(0, 6, n)) @ Q2.T
+    b = rng.randn(n)
+    case("solve ozaki n=4096 cond 1e6")
+    x = ozk.solve(A, b, residual_mode="ozaki")
+    xr = np.linalg.solve(A, b)
+    assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-3
