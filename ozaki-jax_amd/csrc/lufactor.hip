@@ -60,13 +60,15 @@ __device__ __forceinline__ uint32_t lu_wave_reduce(uint32_t u) {
 // registers; the kernel tracks positions instead (LAPACK's row order after
 // its swaps) and stores every row at its final position.
 struct LuPanelShared {
-  uint32_t cv[2][kLuWaves];           // per-wave candidates: |value| bits + 1
-  int cr[2][kLuWaves];                //   their physical rows
+  // per-wave candidates: (|value| bits + 1) << 32 | (INT_MAX - physical row),
+  // so that the largest key is the largest value, then the lowest row
+  uint64_t ckey[2][kLuWaves];
   float crow[2][kLuWaves][kLuSub];    //   and those rows' sub-panel values
   float la[kLuSub][kLuSub];           // the first sub-panel's pivot rows
   float lb[kLuSub][kLuSub];           //   and their second sub-panel columns
   float u01[kLuSub][kLuSub];          // U block right of the first sub-panel
   int piv[kLuPanel];                  // position swapped with column j's diagonal
+  int prow_of[kLuPanel];              // physical pivot row of column j
   int smap[kLuMaxRows];               // position q holds physical row smap[q]
   int inv[kLuMaxRows];                // physical row x sits at position inv[x]
 };
@@ -76,8 +78,8 @@ struct LuPanelShared {
 // rows that are pivots already, and pc[i] receives the column (OFF + j) a
 // row becomes the pivot of.  Column j's pivot is the unused row with the
 // largest |value| (on ties the lowest row of the lowest lane); it takes
-// position OFF + j, swapping with the row there as LAPACK's getf2 swaps, and
-// thread 0 records that in smap, inv and piv.  A zero pivot leaves the
+// position OFF + j, swapping with the row there as LAPACK's getf2 swaps
+// (lu_compose_positions works those out from prow_of).  A zero pivot leaves the
 // column as it is (its unused entries are zero too) and raises
 // OZK_FLAG_SINGULAR.
 template <int OFF>
@@ -97,6 +99,7 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
     int br = INT_MAX;
 #pragma unroll
     for (int i = 0; i < kLuRpt; ++i) {
+      if (i * kLuThreads >= m) break;  // uniform: no thread has row slot i
       const int ph = t + i * kLuThreads;
       const uint32_t bits = __float_as_uint(fabsf(r[i][j])) + 1u;
       if (ph < m && !((used >> i) & 1u) && bits > bb) {
@@ -107,10 +110,7 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
     const uint32_t wb = lu_wave_reduce<true>(bb);
     const uint64_t tie = __ballot(bb == wb);
     const int wr = __builtin_amdgcn_readlane(br, (int)__builtin_ctzll(tie));
-    if (lane == 0) {
-      sh.cv[par][wave] = wb;
-      sh.cr[par][wave] = wr;
-    }
+    if (lane == 0) sh.ckey[par][wave] = (uint64_t)wb << 32 | (uint32_t)(INT_MAX - wr);
     if (wr != INT_MAX && lane == (wr & 63)) {  // the candidate's lane
       const int iw = wr / kLuThreads;          // wave-uniform
       static_for<0, kLuRpt>([&](auto ic) {
@@ -128,51 +128,45 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
     }
     __syncthreads();
 
-    uint32_t pb = sh.cv[par][0];
-    int pr = sh.cr[par][0], pw = 0;
+    // all keys first, then the maximum: one LDS round trip
+    uint64_t keys[kLuWaves];
 #pragma unroll
-    for (int q = 1; q < kLuWaves; ++q) {
-      const uint32_t b2 = sh.cv[par][q];
-      const int r2 = sh.cr[par][q];
-      if (b2 > pb || (b2 == pb && r2 < pr)) {
-        pb = b2;
-        pr = r2;
-        pw = q;
-      }
-    }
-    pr = __builtin_amdgcn_readfirstlane(pr);
-    pw = __builtin_amdgcn_readfirstlane(pw);
+    for (int q = 0; q < kLuWaves; ++q) keys[q] = sh.ckey[par][q];
+    uint64_t best = keys[0];
+#pragma unroll
+    for (int q = 1; q < kLuWaves; ++q) best = keys[q] > best ? keys[q] : best;
+    const int pr = __builtin_amdgcn_readfirstlane(INT_MAX - (int)(uint32_t)best);
+    const int pw = (pr % kLuThreads) / 64;  // the wave holding that row
     float prow[kLuSub];
 #pragma unroll
     for (int k = 0; k < kLuSub; ++k) prow[k] = sh.crow[par][pw][k];
-    if (t == pr % kLuThreads) {
+    {
+      const bool own = t == pr % kLuThreads;
       const int ip = pr / kLuThreads;
 #pragma unroll
-      for (int i = 0; i < kLuRpt; ++i)
-        if (i == ip) {
-          used |= 1u << i;
-          pc[i] = dj;
-        }
+      for (int i = 0; i < kLuRpt; ++i) {
+        const bool hit = own && i == ip;
+        used |= hit ? 1u << i : 0u;
+        pc[i] = hit ? dj : pc[i];
+      }
     }
-    if (t == 0) {  // LAPACK's swap of positions dj and inv[pr]
-      const int pp = sh.inv[pr], q = sh.smap[dj];
-      sh.smap[dj] = pr;
-      sh.smap[pp] = q;
-      sh.inv[pr] = dj;
-      sh.inv[q] = pp;
-      sh.piv[dj] = pp;
-    }
+    if (t == 0) sh.prow_of[dj] = pr;  // positions are composed after the sub-panel
     const float pv = prow[j];
     if (pv != 0.0f) {  // uniform
       // LAPACK's getf2 scales by the reciprocal when it is representable.
       // Pivot rows (old and new) get l = 0, which leaves them as they are.
-      const bool recip = fabsf(pv) >= FLT_MIN;
+      const bool recip = fabsf(pv) >= FLT_MIN;  // uniform
       const float rinv = 1.0f / pv;
 #pragma unroll
       for (int i = 0; i < kLuRpt; ++i) {
+        if (i * kLuThreads >= m) break;  // uniform
         const int ph = t + i * kLuThreads;
         const bool act = ph < m && !((used >> i) & 1u);
-        const float q = recip ? r[i][j] * rinv : r[i][j] / pv;
+        float q;
+        if (recip)  // uniform: the division is only paid for tiny pivots
+          q = r[i][j] * rinv;
+        else
+          q = r[i][j] / pv;
         const float l = act ? q : 0.0f;
         r[i][j] = act ? q : r[i][j];
 #pragma unroll
@@ -182,6 +176,36 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
       atomicOr(status, OZK_FLAG_SINGULAR);
     }
   });
+}
+
+// LAPACK's swap sequence of the panel (column j swaps position j with the
+// position its pivot row sits at) composed by wave 0 after the last column:
+// only the physical rows 0 .. 31 and the pivot rows ever move, so lane k
+// follows one of them (lanes 0-31: rows 0-31, lanes 32-63: the pivot row of
+// column k - 32) through the w swaps.  Writes inv[row] and smap[position]
+// for those rows and piv[j], the position column j swapped with.
+__device__ __forceinline__ void lu_compose_positions(int w, int m, LuPanelShared& sh) {
+  const int t = threadIdx.x;
+  if (t >= 64) return;
+  const int pf = t < kLuPanel && t < w ? sh.prow_of[t] : -1;  // lane j: column j's pivot
+  int row = -1;
+  if (t < kLuPanel) {
+    if (t < m) row = t;
+  } else if (t - kLuPanel < w) {
+    row = sh.prow_of[t - kLuPanel];
+  }
+  int pos = row;
+  for (int j = 0; j < w; ++j) {  // uniform
+    const int pr = __builtin_amdgcn_readlane(pf, j);
+    const uint64_t hit = __ballot(row == pr);  // lane kLuPanel + j at least
+    const int pp = __builtin_amdgcn_readlane(pos, (int)__builtin_ctzll(hit));
+    pos = pos == j ? pp : (pos == pp ? j : pos);
+    if (t == 0) sh.piv[j] = pp;
+  }
+  if (row >= 0) {  // a row followed by two lanes gets the same values twice
+    sh.inv[row] = pos;
+    sh.smap[pos] = row;
+  }
 }
 
 // Rows i in [I0, I1) of a sub-panel from global: r[i][k] = P[ph * lda +
@@ -272,7 +296,7 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
   const int m = n - c;
   const int w0 = w < kLuSub ? w : kLuSub, w1 = w - w0;
   float* const P = A + (int64_t)c * lda + c;
-  for (int q = t; q < m; q += kLuThreads) {
+  for (int q = t; q < m; q += kLuThreads) {  // (ordered by lu_factor_sub's barriers)
     sh.smap[q] = q;
     sh.inv[q] = q;
   }
@@ -283,26 +307,26 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
 
   float a[kLuRpt][kLuSub];
   lu_load_rows<VEC, 0, kLuRpt>(a, P, lda, 0, w0, m);
-  __syncthreads();  // smap / inv initialised before thread 0 swaps in them
   lu_factor_sub<0>(a, used, pc, w0, m, sh, status);
   // The first sub-panel's columns go back to the rows they came from; the
   // panel's permutation moves them at the end.
   lu_store_rows<VEC>(a, P, lda, 0, w0, m, 0u, [](int ph) { return ph; });
 
+  const uint32_t used0 = used;
+  float b[kLuRpt][kLuSub];
   if (w1 > 0) {
-    const uint32_t used0 = used;
 #pragma unroll
     for (int i = 0; i < kLuRpt; ++i)
       if (pc[i] >= 0) {  // a pivot row of the first sub-panel: its L part
 #pragma unroll
         for (int k = 0; k < kLuSub; ++k) sh.la[pc[i]][k] = a[i][k];
       }
-    __syncthreads();  // pivot rows staged, positions of the first sub-panel final
+    __syncthreads();  // pivot rows staged; prow_of of the first sub-panel final
     if (t < 64) {
       // U01 = L00^-1 B0; lane j holds column j's pivot row (position j),
       // whose second sub-panel columns nothing has changed yet
       const int jl = t < kLuSub ? t : 0;
-      const float* const src = P + (int64_t)sh.smap[jl] * lda + kLuSub;
+      const float* const src = P + (int64_t)sh.prow_of[jl] * lda + kLuSub;
       float lrow[kLuSub], u[kLuSub];
 #pragma unroll
       for (int k = 0; k < kLuSub; ++k) {
@@ -323,7 +347,6 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
       }
     }
     __syncthreads();  // U01 in LDS
-    float b[kLuRpt][kLuSub];
     // Half of the rows at a time, so that a and b do not both fill the
     // registers.  The first sub-panel's pivot rows are loaded but left alone.
     lu_load_rows<VEC, 0, kLuRpt / 2>(b, P, lda, kLuSub, w1, m);
@@ -336,11 +359,12 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
       for (int k = 0; k < kLuSub; ++k)
         if (k < w1) P[(int64_t)t * lda + kLuSub + k] = sh.u01[t][k];
     }
-    __syncthreads();  // positions final
-    lu_store_rows<VEC>(b, P, lda, kLuSub, w1, m, used0,
-                       [&](int ph) { return sh.inv[ph]; });
   }
-  __syncthreads();  // positions final; the first sub-panel's stores done
+  __syncthreads();  // prow_of final; the first sub-panel's stores done
+  lu_compose_positions(w, m, sh);
+  __syncthreads();  // inv, smap and piv final
+  if (w1 > 0)
+    lu_store_rows<VEC>(b, P, lda, kLuSub, w1, m, used0, [&](int ph) { return sh.inv[ph]; });
 
   // The first sub-panel's columns of the rows the permutation moves:
   // position q takes physical row smap[q].  Load all, then store.
@@ -435,13 +459,15 @@ __global__ __launch_bounds__(256) void lu_rowfix_trsm_kernel(float* __restrict__
     for (int k = 0; k < kPer; ++k) buf[wv * kPer + k][lane] = v[k];
     __syncthreads();
     if (wv == 0) {  // entries j < w are the diagonal rows c + j, in order
+      // column-oriented: once u[q] is final it updates every later row, so
+      // the dependent chain is 32 steps, not 496
       float u[kLuPanel];
 #pragma unroll
-      for (int j = 0; j < kLuPanel; ++j) {
-        float s = buf[j][lane];
+      for (int j = 0; j < kLuPanel; ++j) u[j] = buf[j][lane];
 #pragma unroll
-        for (int q = 0; q < j; ++q) s = fmaf(-L[j][q], u[q], s);
-        u[j] = s;
+      for (int q = 0; q < kLuPanel - 1; ++q) {
+#pragma unroll
+        for (int j = q + 1; j < kLuPanel; ++j) u[j] = fmaf(-L[j][q], u[q], u[j]);
       }
 #pragma unroll
       for (int j = 0; j < kLuPanel; ++j) buf[j][lane] = u[j];
