@@ -204,3 +204,24 @@ def test_solve_n4096_native_factor_and_solves(ozk):
     x = ozk.solve(A, b, residual_mode="ozaki")
     xr = np.linalg.solve(A, b)
     assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-3
+
+
+def test_solve_above_native_lu_limit(ozk):
+    """n above ozk_lu_factor_max_n(): torch.linalg's getrf, its pivots turned
+    into the permutation by ozk_pivots_to_perm, the library's triangular
+    solves on that factor.  Above K = 4096 the high preset's residual is
+    accurate to about 4e-8 relative (rho = 19; the oracle's residual agrees bit
+    for bit), which bounds what the refinement reaches; f64 residuals reach
+    FP64 accuracy through the same factor."""
+    from ozaki_jax_amd import _lib
+    n = int(_lib.load().ozk_lu_factor_max_n()) + 7
+    rng = np.random.RandomState(11)
+    A = dominant(n, rng)
+    b = rng.randn(n)
+    xr = np.linalg.solve(A, b)
+    case(f"solve ozaki n={n} (library getrf)")
+    x = ozk.solve(A, b, residual_mode="ozaki")
+    assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-5
+    case(f"solve f64 residuals n={n} (library getrf)")
+    x = ozk.solve(A, b)
+    assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-12
