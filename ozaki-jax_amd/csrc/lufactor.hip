@@ -75,8 +75,8 @@ struct LuPanelShared {
 
 // Partial pivoting on one sub-panel in registers: r[i][k] is column OFF + k
 // of physical row t + i * kLuThreads (rows < m); bit i of `used` marks the
-// rows that are pivots already, and pc[i] receives the column (OFF + j) a
-// row becomes the pivot of.  Column j's pivot is the unused row with the
+// rows that are pivots already, and 6-bit field i of pcode receives 1 + the
+// column (OFF + j) a row becomes the pivot of.  Column j's pivot is the unused row with the
 // largest |value| (on ties the lowest row of the lowest lane); it takes
 // position OFF + j, swapping with the row there as LAPACK's getf2 swaps
 // (lu_compose_positions works those out from prow_of).  A zero pivot leaves the
@@ -84,9 +84,12 @@ struct LuPanelShared {
 // OZK_FLAG_SINGULAR.
 template <int OFF>
 __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32_t& used,
-                                              int (&pc)[kLuRpt], int ncols, int m,
+                                              uint64_t& pcode, int ncols, int m,
                                               LuPanelShared& sh, uint32_t* status) {
   const int t = threadIdx.x, wave = t / 64, lane = t % 64;
+  uint32_t present = 0u;  // row slots below the panel's last row
+#pragma unroll
+  for (int i = 0; i < kLuRpt; ++i) present |= (t + i * kLuThreads < m) ? 1u << i : 0u;
   // (a compile-time column index: the loop body is too large for the
   // unroller, and a run-time j would index r through scratch memory)
   static_for<0, kLuSub>([&](auto jc) {
@@ -94,17 +97,17 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
     if (j >= ncols) return;  // uniform
     const int dj = OFF + j;
     const int par = j & 1;
+    const uint32_t avail = present & ~used;  // row slots that can still pivot
     // + 1: an unused row holding 0 still beats a lane with no row (bb = 0)
     uint32_t bb = 0u;
     int br = INT_MAX;
 #pragma unroll
     for (int i = 0; i < kLuRpt; ++i) {
       if (i * kLuThreads >= m) break;  // uniform: no thread has row slot i
-      const int ph = t + i * kLuThreads;
       const uint32_t bits = __float_as_uint(fabsf(r[i][j])) + 1u;
-      if (ph < m && !((used >> i) & 1u) && bits > bb) {
+      if (((avail >> i) & 1u) && bits > bb) {
         bb = bits;
-        br = ph;
+        br = t + i * kLuThreads;
       }
     }
     const uint32_t wb = lu_wave_reduce<true>(bb);
@@ -140,15 +143,10 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
     float prow[kLuSub];
 #pragma unroll
     for (int k = 0; k < kLuSub; ++k) prow[k] = sh.crow[par][pw][k];
-    {
-      const bool own = t == pr % kLuThreads;
+    if (t == pr % kLuThreads) {  // the pivot's owner; its slot ip is uniform
       const int ip = pr / kLuThreads;
-#pragma unroll
-      for (int i = 0; i < kLuRpt; ++i) {
-        const bool hit = own && i == ip;
-        used |= hit ? 1u << i : 0u;
-        pc[i] = hit ? dj : pc[i];
-      }
+      used |= 1u << ip;
+      pcode |= (uint64_t)(dj + 1) << (6 * ip);
     }
     if (t == 0) sh.prow_of[dj] = pr;  // positions are composed after the sub-panel
     const float pv = prow[j];
@@ -157,11 +155,11 @@ __device__ __forceinline__ void lu_factor_sub(float (&r)[kLuRpt][kLuSub], uint32
       // Pivot rows (old and new) get l = 0, which leaves them as they are.
       const bool recip = fabsf(pv) >= FLT_MIN;  // uniform
       const float rinv = 1.0f / pv;
+      const uint32_t act_bits = avail & ~used;  // the new pivot is out too
 #pragma unroll
       for (int i = 0; i < kLuRpt; ++i) {
         if (i * kLuThreads >= m) break;  // uniform
-        const int ph = t + i * kLuThreads;
-        const bool act = ph < m && !((used >> i) & 1u);
+        const bool act = (act_bits >> i) & 1u;
         float q;
         if (recip)  // uniform: the division is only paid for tiny pivots
           q = r[i][j] * rinv;
@@ -301,13 +299,11 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
     sh.inv[q] = q;
   }
   uint32_t used = 0u;
-  int pc[kLuRpt];
-#pragma unroll
-  for (int i = 0; i < kLuRpt; ++i) pc[i] = -1;
+  uint64_t pcode = 0u;
 
   float a[kLuRpt][kLuSub];
   lu_load_rows<VEC, 0, kLuRpt>(a, P, lda, 0, w0, m);
-  lu_factor_sub<0>(a, used, pc, w0, m, sh, status);
+  lu_factor_sub<0>(a, used, pcode, w0, m, sh, status);
   // The first sub-panel's columns go back to the rows they came from; the
   // panel's permutation moves them at the end.
   lu_store_rows<VEC>(a, P, lda, 0, w0, m, 0u, [](int ph) { return ph; });
@@ -316,11 +312,13 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
   float b[kLuRpt][kLuSub];
   if (w1 > 0) {
 #pragma unroll
-    for (int i = 0; i < kLuRpt; ++i)
-      if (pc[i] >= 0) {  // a pivot row of the first sub-panel: its L part
+    for (int i = 0; i < kLuRpt; ++i) {
+      const int col = (int)((pcode >> (6 * i)) & 63u) - 1;
+      if (col >= 0) {  // a pivot row of the first sub-panel: its L part
 #pragma unroll
-        for (int k = 0; k < kLuSub; ++k) sh.la[pc[i]][k] = a[i][k];
+        for (int k = 0; k < kLuSub; ++k) sh.la[col][k] = a[i][k];
       }
+    }
     __syncthreads();  // pivot rows staged; prow_of of the first sub-panel final
     if (t < 64) {
       // U01 = L00^-1 B0; lane j holds column j's pivot row (position j),
@@ -353,7 +351,7 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
     lu_update_rows<0, kLuRpt / 2>(b, a, m, used0, sh);
     lu_load_rows<VEC, kLuRpt / 2, kLuRpt>(b, P, lda, kLuSub, w1, m);
     lu_update_rows<kLuRpt / 2, kLuRpt>(b, a, m, used0, sh);
-    lu_factor_sub<kLuSub>(b, used, pc, w1, m, sh, status);  // its barriers follow every load
+    lu_factor_sub<kLuSub>(b, used, pcode, w1, m, sh, status);  // its barriers follow every load
     if (t < kLuSub) {  // positions 0 .. 15 hold the first sub-panel's pivots
 #pragma unroll
       for (int k = 0; k < kLuSub; ++k)
