@@ -405,14 +405,15 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
 }
 
 // The columns outside the panel [c, c + w), 64 per workgroup (lane = column,
-// wave = a quarter of the permutation's entries), and the permutation
+// wave = an eighth of the permutation's entries), and the permutation
 // vector (the last workgroup): applies the panel's row permutation, every
 // source value read before any is written.  Right of the panel, wave 0 then
 // solves the unit-lower diagonal block for its 64 columns (rows c .. c+w-1
 // become U12) from the values staged in LDS.
 constexpr int kLuFixCols = 64;
+constexpr int kLuFixThreads = 512;  // 8 waves, 8 entries each
 
-__global__ __launch_bounds__(256) void lu_rowfix_trsm_kernel(float* __restrict__ A, int64_t lda,
+__global__ __launch_bounds__(kLuFixThreads) void lu_rowfix_trsm_kernel(float* __restrict__ A, int64_t lda,
                                                              int n, int c,
                                                              const int* __restrict__ maps,
                                                              int32_t* __restrict__ perm) {
@@ -423,7 +424,7 @@ __global__ __launch_bounds__(256) void lu_rowfix_trsm_kernel(float* __restrict__
   const int right = n - c - w;
   const int nleft = (c + kLuFixCols - 1) / kLuFixCols;
   const int nright = (right + kLuFixCols - 1) / kLuFixCols;
-  constexpr int kPer = kLuPairs / 4;  // entries per wave
+  constexpr int kPer = kLuPairs / (kLuFixThreads / 64);  // entries per wave
 
   if ((int)blockIdx.x == nleft + nright) {  // the permutation vector
     int v = 0;
@@ -438,7 +439,7 @@ __global__ __launch_bounds__(256) void lu_rowfix_trsm_kernel(float* __restrict__
                              : (int64_t)blockIdx.x * kLuFixCols + lane;
   const bool live = is_right ? x < n : x < c;
   if (is_right) {
-    for (int q = t; q < kLuPanel * kLuPanel; q += 256) {
+    for (int q = t; q < kLuPanel * kLuPanel; q += kLuFixThreads) {
       const int rr = q / kLuPanel, cc = q % kLuPanel;
       L[rr][cc] = (cc < rr && rr < w) ? A[(int64_t)(c + rr) * lda + c + cc] : 0.0f;
     }
@@ -565,8 +566,8 @@ static int lu_factor_steps(float* A, int64_t lda, int n, int32_t* perm, int* map
     OZK_LAUNCH_CHECK();
     const int right = n - c - w;
     const int groups = (c + kLuFixCols - 1) / kLuFixCols + (right + kLuFixCols - 1) / kLuFixCols;
-    hipLaunchKernelGGL(lu_rowfix_trsm_kernel, dim3(groups + 1), dim3(256), 0, st, A, lda, n, c,
-                       maps, perm);
+    hipLaunchKernelGGL(lu_rowfix_trsm_kernel, dim3(groups + 1), dim3(kLuFixThreads), 0, st, A,
+                       lda, n, c, maps, perm);
     OZK_LAUNCH_CHECK();
     if (right > 0) {
       const unsigned tiles = (unsigned)((right + 63) / 64);
