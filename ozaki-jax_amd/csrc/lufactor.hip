@@ -405,13 +405,13 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
 }
 
 // The columns outside the panel [c, c + w), 64 per workgroup (lane = column,
-// wave = an eighth of the permutation's entries), and the permutation
+// wave = a sixteenth of the permutation's entries), and the permutation
 // vector (the last workgroup): applies the panel's row permutation, every
 // source value read before any is written.  Right of the panel, wave 0 then
 // solves the unit-lower diagonal block for its 64 columns (rows c .. c+w-1
 // become U12) from the values staged in LDS.
 constexpr int kLuFixCols = 64;
-constexpr int kLuFixThreads = 512;  // 8 waves, 8 entries each
+constexpr int kLuFixThreads = 1024;  // 16 waves, 4 entries each
 
 __global__ __launch_bounds__(kLuFixThreads) void lu_rowfix_trsm_kernel(float* __restrict__ A, int64_t lda,
                                                              int n, int c,
