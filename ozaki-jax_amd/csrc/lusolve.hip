@@ -47,6 +47,7 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
   const int64_t col = c0 + blockIdx.y;
   uint32_t* const fl = flags + (int64_t)blockIdx.y * nb;
   __shared__ float part[kTsWaves][kTsRows];
+  __shared__ float4 xs[kTsWaves][kTsRows / 4];  // a wave's copy of a finished block
   const int w = threadIdx.x / kTsRows, lane = threadIdx.x % kTsRows;
   bool failed = false;
 
@@ -99,8 +100,21 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
         }
       }
       const float xv = k0 + lane < n ? y[(k0 + lane) * ldy + col] : 0.0f;
+      // broadcast through LDS (one wave: no barrier), so that the 64 values
+      // need no scalar registers
+      ((float*)xs[w])[lane] = xv;
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 #pragma unroll
-      for (int j = 0; j < kTsRows; ++j) acc = fmaf(a[j], lane_value(xv, j), acc);
+      for (int q = 0; q < kTsRows / 4; ++q) {
+        const float4 x4 = xs[w][q];
+        acc = fmaf(a[4 * q], x4.x, acc);
+        acc = fmaf(a[4 * q + 1], x4.y, acc);
+        acc = fmaf(a[4 * q + 2], x4.z, acc);
+        acc = fmaf(a[4 * q + 3], x4.w, acc);
+      }
+      __builtin_amdgcn_wave_barrier();  // the next block's write waits for these reads
     }
     part[w][lane] = acc;
     __syncthreads();
@@ -108,18 +122,25 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     if (w == 0) {
       float v = 0.0f;
       if (live) v = rhs - ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+      // d = lane - j, stepped with j and opaque to the compiler, so that the
+      // lane tests are made at each step; otherwise all 64 (or 128) lane
+      // masks are hoisted into scalar registers and spilled
       if (UPPER) {
+        int d = lane - (kTsRows - 1);
 #pragma unroll
-        for (int j = kTsRows - 1; j >= 0; --j) {
-          if (lane == j) v = live ? v / dg[j] : 0.0f;
+        for (int j = kTsRows - 1; j >= 0; --j, ++d) {
+          asm volatile("" : "+v"(d));  // (opaque: see above)
+          if (d == 0) v = live ? v / dg[j] : 0.0f;
           const float xj = lane_value(v, j);
-          if (lane < j) v = fmaf(-dg[j], xj, v);
+          v = d < 0 ? fmaf(-dg[j], xj, v) : v;
         }
       } else {
+        int d = lane;
 #pragma unroll
-        for (int j = 0; j < kTsRows; ++j) {
+        for (int j = 0; j < kTsRows; ++j, --d) {
+          asm volatile("" : "+v"(d));
           const float xj = lane_value(v, j);
-          if (lane > j) v = fmaf(-dg[j], xj, v);
+          v = d > 0 ? fmaf(-dg[j], xj, v) : v;
         }
       }
       if (live) {
