@@ -3,9 +3,10 @@
 // ozaki_jax/solve.py:159).  Right-looking and blocked by panels of 32
 // columns; each panel step is three kernels:
 //  1. lu_panel_kernel (one workgroup): factors the panel's rows c .. n-1 in
-//     registers, 16 columns at a time (each column: a pivot search, the row
-//     swap and the rank-1 update of the sub-panel), and writes the
-//     permutation the panel's swaps make of the rows;
+//     registers, 16 columns at a time (each column: a pivot search and the
+//     rank-1 update of the rows not yet pivots; rows stay where they were
+//     read and their final positions are composed after the panel), and
+//     writes the permutation the panel's swaps make of the rows;
 //  2. lu_rowfix_trsm_kernel (64 columns outside the panel per workgroup):
 //     applies that permutation to its columns (and to the permutation
 //     vector) and, right of the panel, solves the unit-lower 32 x 32
@@ -413,10 +414,9 @@ __global__ __launch_bounds__(kLuThreads) void lu_panel_kernel(float* __restrict_
 constexpr int kLuFixCols = 64;
 constexpr int kLuFixThreads = 1024;  // 16 waves, 4 entries each
 
-__global__ __launch_bounds__(kLuFixThreads) void lu_rowfix_trsm_kernel(float* __restrict__ A, int64_t lda,
-                                                             int n, int c,
-                                                             const int* __restrict__ maps,
-                                                             int32_t* __restrict__ perm) {
+__global__ __launch_bounds__(kLuFixThreads) void lu_rowfix_trsm_kernel(
+    float* __restrict__ A, int64_t lda, int n, int c, const int* __restrict__ maps,
+    int32_t* __restrict__ perm) {
   __shared__ float L[kLuPanel][kLuPanel + 1];
   __shared__ float buf[kLuPairs][kLuFixCols + 1];
   const int t = threadIdx.x, lane = t % 64, wv = t / 64;
