@@ -241,7 +241,10 @@ int ozk_lu_factor_f32(float* A, int64_t lda, int64_t n, int32_t* perm,
  * (ldb, ldx); B is rounded to FP32 first (r.astype(float32)) and X is the
  * FP32 solution widened.  X may alias B.  flags is cleared first and
  * receives OZK_FLAG_WAIT_TIMEOUT if a row block gave up waiting for the
- * blocks it depends on (X is then invalid). */
+ * blocks it depends on (X is then invalid).  The workspace (8-byte aligned,
+ * ozk_lu_solve_workspace_bytes(n, ncols) = 16 n ncols bytes) holds the
+ * published solution words; each call clears it first, so calls that share
+ * one must not overlap. */
 size_t ozk_lu_solve_workspace_bytes(int64_t n, int64_t ncols);
 int ozk_lu_solve_f32(const float* LU, int64_t lda, const int32_t* perm,
                      int64_t n, const double* B, int64_t ldb, double* X,

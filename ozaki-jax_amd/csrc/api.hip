@@ -638,6 +638,7 @@ int ozk_lu_solve_f32(const float* LU, int64_t lda, const int32_t* perm,
               workspace_bytes);
     return OZK_ERR_WORKSPACE;
   }
+  OZK_CHECK_ARG((uintptr_t)workspace % 8 == 0, "workspace not 8-byte aligned");
   return launch_lu_solve(LU, lda, perm, n, B, ldb, X, ldx, ncols, workspace, flags, st);
 }
 

@@ -10,10 +10,19 @@ namespace ozk {
 constexpr int kTsRows = 64;   // rows per block (one wave solves a block)
 constexpr int kTsWaves = 4;   // waves per workgroup
 constexpr int kTsThreads = kTsRows * kTsWaves;
-// Polls of a block's flag before the wait is abandoned: a poll takes about a
+// Polls of a block's words before the wait is abandoned: a poll takes about a
 // microsecond (an agent-scope load plus s_sleep), a whole solve a few
 // hundred, so this only ends waits that cannot finish.
 constexpr uint32_t kTsSpinLimit = 1u << 21;
+
+// Lane j's value, for every lane (the builtin moves 32-bit integers).
+__device__ __forceinline__ float lane_value(float v, int j) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
+}
+
+// A solution value is published as one 64-bit word, its FP32 bits below
+// kTsTag: value and readiness arrive together, with no flag or fence.
+constexpr uint32_t kTsTag = 1u;
 
 // Forward (UPPER false: y = L^-1 P b, L unit lower) or backward (UPPER true:
 // x = U^-1 y) substitution.  LU is n x n row-major with leading dimension
@@ -24,28 +33,22 @@ constexpr uint32_t kTsSpinLimit = 1u << 21;
 // Block k needs the solution of every block before it (after it, going
 // backward).  Each wave takes every fourth of those blocks in the order they
 // complete: it loads its 64 x 64 piece of LU (before waiting), polls the
-// block's flag, reads the block's solution from y and accumulates the
+// block's 64 published words until all carry kTsTag, and accumulates the
 // product.  Wave 0 then sums the four partial products, solves the diagonal
-// block (lane i holds row i; a step broadcasts x_j with lane_value), writes
-// the block's solution to y (and x going backward), and publishes its flag.
+// block (lane i holds row i; a step broadcasts x_j with lane_value) and
+// publishes the block's solution (and writes x going backward).
 // Dependencies point only to blocks a workgroup reaches earlier, so with all
 // G workgroups resident every wait ends; a wait that still exceeds
 // kTsSpinLimit polls (or sees another one fail) sets OZK_FLAG_WAIT_TIMEOUT
 // and stops waiting, so that every wave exits.
-// Lane j's value, for every lane (the builtin moves 32-bit integers).
-__device__ __forceinline__ float lane_value(float v, int j) {
-  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), j));
-}
-
 template <bool UPPER>
 __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     const float* __restrict__ LU, int64_t n, int64_t lda, int vec,
     const int32_t* __restrict__ perm, const double* __restrict__ B, int64_t ldb,
-    float* __restrict__ y, int64_t ldy, double* __restrict__ X, int64_t ldx,
-    int64_t c0, uint32_t* __restrict__ flags, uint32_t* __restrict__ status) {
+    const uint64_t* __restrict__ win, uint64_t* __restrict__ wout, int64_t ldw,
+    double* __restrict__ X, int64_t ldx, int64_t c0, uint32_t* __restrict__ status) {
   const int nb = (int)((n + kTsRows - 1) / kTsRows);
   const int64_t col = c0 + blockIdx.y;
-  uint32_t* const fl = flags + (int64_t)blockIdx.y * nb;
   __shared__ float part[kTsWaves][kTsRows];
   __shared__ float4 xs[kTsWaves][kTsRows / 4];  // a wave's copy of a finished block
   const int w = threadIdx.x / kTsRows, lane = threadIdx.x % kTsRows;
@@ -62,7 +65,9 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     // waits so that the solve after the last one starts at once.
     float rhs = 0.0f, dg[kTsRows];
     if (w == 0) {
-      if (live) rhs = UPPER ? y[row * ldy + col] : (float)B[(int64_t)perm[row] * ldb + col];
+      if (live)
+        rhs = UPPER ? __uint_as_float((uint32_t)win[row * ldw + col])
+                    : (float)B[(int64_t)perm[row] * ldb + col];
       const int64_t k0 = (int64_t)blk * kTsRows;
 #pragma unroll
       for (int j = 0; j < kTsRows; ++j) dg[j] = (live && k0 + j < n) ? lrow[k0 + j] : 0.0f;
@@ -87,19 +92,28 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
 #pragma unroll
         for (int j = 0; j < kTsRows; ++j) a[j] = (live && k0 + j < n) ? lrow[k0 + j] : 0.0f;
       }
-      if (!failed) {
-        uint32_t spins = 0;
-        while (__hip_atomic_load(fl + c, __ATOMIC_ACQUIRE, __HIP_MEMORY_SCOPE_AGENT) == 0u) {
-          if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
-                  OZK_FLAG_WAIT_TIMEOUT ||
-              ++spins > kTsSpinLimit) {
-            failed = true;
-            break;
+      // poll the block's words until every lane's value has arrived
+      float xv = 0.0f;
+      bool ready = k0 + lane >= n || failed;
+      uint32_t spins = 0;
+      while (true) {
+        if (!ready) {
+          const uint64_t wd = __hip_atomic_load(wout + (k0 + lane) * ldw + col, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+          if ((uint32_t)(wd >> 32) == kTsTag) {
+            ready = true;
+            xv = __uint_as_float((uint32_t)wd);
           }
-          __builtin_amdgcn_s_sleep(2);
         }
+        if (__all(ready)) break;
+        if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
+                OZK_FLAG_WAIT_TIMEOUT ||
+            ++spins > kTsSpinLimit) {
+          failed = true;
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
-      const float xv = k0 + lane < n ? y[(k0 + lane) * ldy + col] : 0.0f;
       // broadcast through LDS (one wave: no barrier), so that the 64 values
       // need no scalar registers
       ((float*)xs[w])[lane] = xv;
@@ -144,24 +158,22 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
         }
       }
       if (live) {
-        y[row * ldy + col] = v;
+        __hip_atomic_store(wout + row * ldw + col,
+                           (uint64_t)kTsTag << 32 | __float_as_uint(v), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
         if (UPPER) X[row * ldx + col] = (double)v;
       }
-      __threadfence();
-      if (lane == 0) __hip_atomic_store(fl + blk, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();  // part[] is rewritten by the next block
   }
   if (failed && lane == 0) atomicOr(status, OZK_FLAG_WAIT_TIMEOUT);
 }
 
-__global__ void fill_u32_array_kernel(uint32_t* p, int64_t count, uint32_t v) {
+__global__ void fill_u64_array_kernel(uint64_t* p, int64_t count, uint64_t v) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < count;
        i += (int64_t)gridDim.x * blockDim.x)
     p[i] = v;
 }
-
-static int64_t ts_blocks(int64_t n) { return (n + kTsRows - 1) / kTsRows; }
 
 // Columns per launch: the G x chunk workgroups of a launch must be resident
 // together (one per CU suffices).
@@ -170,34 +182,34 @@ static int64_t ts_chunk(int64_t ncols) {
   return ncols < cus ? ncols : cus;
 }
 
+// Two arrays of published words, n x ncols each: the forward pass's and the
+// backward pass's.
 size_t lu_solve_workspace_bytes(int64_t n, int64_t ncols) {
-  const size_t yb = (size_t)(n * ncols) * sizeof(float);
-  const size_t fb = (size_t)(2 * ts_blocks(n) * ts_chunk(ncols)) * sizeof(uint32_t);
-  return round_up((int64_t)yb, 256) + fb;
+  return (size_t)(2 * n * ncols) * sizeof(uint64_t);
 }
 
 int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n,
                     const double* B, int64_t ldb, double* X, int64_t ldx, int64_t ncols,
                     void* ws, uint32_t* status, hipStream_t st) {
-  float* y = (float*)ws;
-  const int64_t nb = ts_blocks(n);
+  uint64_t* const wf = (uint64_t*)ws;
+  uint64_t* const wb = wf + n * ncols;
+  const int64_t nb = (n + kTsRows - 1) / kTsRows;
   const int64_t chunk = ts_chunk(ncols);
-  uint32_t* flags = (uint32_t*)((char*)ws + round_up((int64_t)(n * ncols * sizeof(float)), 256));
   const int vec = ((uintptr_t)LU % 16 == 0) && (lda % 4 == 0);
   const int64_t per = cu_count() / chunk;
   const unsigned G = (unsigned)(nb < per ? nb : (per > 0 ? per : 1));
+  const int64_t words = 2 * n * ncols;
+  const int64_t fb = (words + 255) / 256;
+  hipLaunchKernelGGL(fill_u64_array_kernel, dim3((unsigned)(fb < 4096 ? fb : 4096)), dim3(256), 0,
+                     st, wf, words, (uint64_t)0);
+  OZK_LAUNCH_CHECK();
   for (int64_t c0 = 0; c0 < ncols; c0 += chunk) {
     const int64_t nc = ncols - c0 < chunk ? ncols - c0 : chunk;
-    const int64_t nflags = 2 * nb * nc;
-    hipLaunchKernelGGL(fill_u32_array_kernel, dim3((unsigned)((nflags + 255) / 256)),
-                       dim3(256), 0, st, flags, nflags, 0u);
-    OZK_LAUNCH_CHECK();
     hipLaunchKernelGGL(lu_trsv_kernel<false>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,
-                       LU, n, lda, vec, perm, B, ldb, y, ncols, X, ldx, c0, flags, status);
+                       LU, n, lda, vec, perm, B, ldb, nullptr, wf, ncols, X, ldx, c0, status);
     OZK_LAUNCH_CHECK();
     hipLaunchKernelGGL(lu_trsv_kernel<true>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,
-                       LU, n, lda, vec, perm, B, ldb, y, ncols, X, ldx, c0, flags + nb * nc,
-                       status);
+                       LU, n, lda, vec, perm, B, ldb, wf, wb, ncols, X, ldx, c0, status);
     OZK_LAUNCH_CHECK();
   }
   return OZK_OK;

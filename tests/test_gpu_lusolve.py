@@ -119,6 +119,35 @@ def test_lu_solve_in_place_and_empty(ozk):
     assert gpu_solve(lu, perm, np.zeros((n, 0))).shape == (n, 0)
 
 
+def test_lu_solve_workspace_reused(ozk):
+    """One workspace through calls of different sizes: each call clears the
+    published words it polls, so what an earlier call left there (solution
+    words of a larger system, tagged as ready) is never read as a result."""
+    import torch
+    from ozaki_jax_amd import _device as D, _lib
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    rng = np.random.RandomState(21)
+    wsb = lib.ozk_lu_solve_workspace_bytes(700, 3)
+    ws = D.workspace(wsb, dev)
+    flags = torch.zeros(1, dtype=torch.int32, device=dev)
+    for n, nc in [(700, 3), (300, 2), (700, 3), (129, 1)]:
+        lu, ipiv = factor(dominant(n, rng))
+        perm = perm_of(lib, ipiv)
+        B = rng.randn(n, nc)
+        case(f"ozk_lu_solve_f32 n={n} ncols={nc} on a shared workspace")
+        LUt = torch.from_numpy(np.ascontiguousarray(lu)).to(dev)  # SciPy's is column-major
+        Bt = torch.from_numpy(B).to(dev)
+        Xt = torch.empty_like(Bt)
+        pt = torch.from_numpy(perm).to(dev)
+        _lib.check(lib.ozk_lu_solve_f32(LUt.data_ptr(), n, pt.data_ptr(), n, Bt.data_ptr(), nc,
+                                        Xt.data_ptr(), nc, nc, ws.data_ptr(), wsb,
+                                        flags.data_ptr(), D.stream_handle()))
+        assert int(flags.item()) == 0
+        Xr = ref_solve(lu, perm, B)
+        assert np.linalg.norm(Xt.cpu().numpy() - Xr) <= 2e-5 * np.linalg.norm(Xr)
+
+
 def test_solve_uses_native_triangular_solves(ozk):
     """solve() at one right-hand side goes through ozk_lu_solve_f32 and
     matches LAPACK's FP64 answer on a matrix of condition 1e6 (the C5 form)."""
