@@ -64,20 +64,22 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     // Wave 0's right-hand side and diagonal-block row, loaded ahead of the
     // waits so that the solve after the last one starts at once.
     float rhs = 0.0f, dg[kTsRows];
-    // going backward: the row's diagonal entry u and 1/u, divided here, off
-    // the chain of the diagonal solve
-    float u = 0.0f, ur = 0.0f;
+    // Going backward the row is scaled by 1/u (u its diagonal entry), so that
+    // the diagonal block is unit upper triangular and its solve, like the
+    // forward one, is a broadcast and an FMA per step: the division leaves
+    // the chain of dependent steps.
+    float ur = 0.0f;
     if (w == 0) {
       if (live)
         rhs = UPPER ? __uint_as_float((uint32_t)win[row * ldw + col])
                     : (float)B[(int64_t)perm[row] * ldb + col];
-      if (UPPER && live) {
-        u = lrow[row];
-        ur = 1.0f / u;
-      }
+      if (UPPER && live) ur = 1.0f / lrow[row];
       const int64_t k0 = (int64_t)blk * kTsRows;
 #pragma unroll
-      for (int j = 0; j < kTsRows; ++j) dg[j] = (live && k0 + j < n) ? lrow[k0 + j] : 0.0f;
+      for (int j = 0; j < kTsRows; ++j) {
+        dg[j] = (live && k0 + j < n) ? lrow[k0 + j] : 0.0f;
+        if (UPPER) dg[j] *= ur;
+      }
     }
 
     float acc = 0.0f;
@@ -143,21 +145,15 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     if (w == 0) {
       float v = 0.0f;
       if (live) v = rhs - ((part[0][lane] + part[1][lane]) + (part[2][lane] + part[3][lane]));
+      if (UPPER) v *= ur;  // the scaled row's right-hand side (0 past n)
       // d = lane - j, stepped with j and opaque to the compiler, so that the
-      // lane tests are made at each step; otherwise all 64 (or 128) lane
-      // masks are hoisted into scalar registers and spilled
+      // lane tests are made at each step; otherwise all 64 lane masks are
+      // hoisted into scalar registers and spilled
       if (UPPER) {
         int d = lane - (kTsRows - 1);
 #pragma unroll
         for (int j = kTsRows - 1; j >= 0; --j, ++d) {
           asm volatile("" : "+v"(d));  // (opaque: see above)
-          if (d == 0) {
-            // v / u correctly rounded from the rounded reciprocal (Markstein's
-            // correction: q = v ur, then q + ur (v - u q)), three dependent
-            // operations where a division takes ten; 0 on rows past n
-            const float q = v * ur;
-            v = fmaf(fmaf(-u, q, v), ur, q);
-          }
           const float xj = lane_value(v, j);
           v = d < 0 ? fmaf(-dg[j], xj, v) : v;
         }
