@@ -77,10 +77,11 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
-def cpu_baseline(A, B, precision, rows=2048):
+def cpu_baseline(A, B, precision, rows=2048, runs=3):
     """The oracle's matmul_numpy(pipeline="ondevice") on the first `rows` rows
     of the same A against the full B (same K, rho and slices as the timed
-    workload), rated as 2 * rows * K * M / t."""
+    workload), rated as 2 * rows * K * M / t with t the median of `runs`
+    runs."""
     import oracle
     try:
         from threadpoolctl import threadpool_info
@@ -90,16 +91,22 @@ def cpu_baseline(A, B, precision, rows=2048):
         threads = os.cpu_count() or 1
     K, M = B.shape
     Ar = A[:rows]
-    log(f"cpu baseline: oracle matmul_numpy ondevice {precision} {rows}x{K}x{M}")
-    t0 = time.perf_counter()
-    oracle.matmul_numpy(Ar, B, pipeline="ondevice", precision=precision)
-    t = time.perf_counter() - t0
+    times = []
+    for i in range(runs):
+        log(f"cpu baseline {i + 1}/{runs}: oracle matmul_numpy ondevice {precision} "
+            f"{rows}x{K}x{M}")
+        t0 = time.perf_counter()
+        oracle.matmul_numpy(Ar, B, pipeline="ondevice", precision=precision)
+        times.append(time.perf_counter() - t0)
+    t = float(np.median(times))
     return {"value": 2.0 * rows * K * M / t / 1e12, "unit": "TFLOP/s",
             "cores": int(threads), "kind": "port",
             "sample": f"oracle matmul_numpy(pipeline='ondevice', precision='{precision}') "
                       f"on rows 0..{rows - 1} of the timed A ({rows}x{K}) times the full "
-                      f"B ({K}x{M}), one run of {t:.1f} s including B's extraction "
-                      f"(NumPy/OpenBLAS, {threads} BLAS threads)"}
+                      f"B ({K}x{M}), median of {runs} runs ("
+                      + ", ".join(f"{x:.1f}" for x in times)
+                      + f" s) including B's extraction (NumPy/OpenBLAS, {threads} BLAS "
+                      f"threads)"}
 
 
 def accuracy_rows(A, B, C, precision, rows):
@@ -151,6 +158,7 @@ def suite(args):
     import oracle
     from oracle import pipeline as OP
     import ozaki_jax_amd as ozk
+    from ozaki_jax_amd import _lib
 
     torch.cuda.set_device(0)
     dev = torch.device("cuda", 0)
@@ -201,7 +209,7 @@ def suite(args):
         t_dg = _timeit(lambda: torch.matmul(At, Bt), 3, sync)
         # the whole call's slice-pair rate against the MFMA peak of the plane
         # format it runs on (INT8 for rho_32 >= 19 and a preset, else BF16)
-        i8 = oracle.rho_f32(k) >= 19
+        i8 = _lib.load().ozk_matmul_plane_bytes(_lib.PIPE_ONDEVICE, k, nh, nl) == 1
         pairs = nh * nh + 2 * nh * nl
         d = {"config": name, "ms": t * 1e3, "fp64_eq_tflops": 2.0 * n * k * m / t / 1e12,
              "slice_format": "int8" if i8 else "bf16",
@@ -341,9 +349,11 @@ def main():
     value = 2.0 * n ** 3 / dt / 1e12
     log(f"{dt * 1e3:.2f} ms/step, {value:.2f} FP64-eq TFLOP/s")
 
-    # Fused GEMM kernel alone: HIP events on the stream it is launched on.
+    # Fused GEMM kernel alone: HIP events on the stream it is launched on,
+    # on the plane format ozk_matmul picks for this shape.
     rho = _lib.load().ozk_rho_f32(n)
-    i8 = rho >= 19 and (n_hi, n_lo) in ((4, 1), (3, 1))
+    i8 = _lib.check(_lib.load().ozk_matmul_plane_bytes(_lib.PIPE_ONDEVICE, n, n_hi,
+                                                       n_lo)) == 1
     pa = ll.extract(At, 0, rho, n_hi, n_lo, i8=i8)
     pb = ll.extract(Bt, 1, rho, n_hi, n_lo, i8=i8)
     ll.gemm(pa, pb, ll.PIPE_ONDEVICE, n_hi, n_lo, ll.ORDER_2SUM)
@@ -410,7 +420,9 @@ def main():
 
     ext_bytes = 2 * n * n * (8 + (1 if i8 else 2) * (n_hi + n_lo))
     cpu = None if args.no_cpu else cpu_baseline(A, B, args.precision, min(2048, n))
-    traffic = read_traffic()
+    # HBM bytes per launch come from the committed rocprofv3 counter runs of
+    # this workload (8192^3 high), not from this run
+    traffic = read_traffic() if (n, args.precision) == (8192, "high") else None
     dev_name = torch.cuda.get_device_name(0)
     out = {
         "metric": METRIC,
@@ -437,6 +449,10 @@ def main():
             "bound": "mfma", "achieved": achieved, "peak": peak,
             "unit": "TFLOP/s", "frac": achieved / peak,
             "traffic": traffic,
+            "traffic_source": (f"profile-derived, not measured in this run: "
+                               f"{PROFILE_TRAFFIC.relative_to(ROOT)} (rocprofv3 --pmc "
+                               f"FETCH_SIZE and WRITE_SIZE per dispatch, scaled by a "
+                               f"copy kernel's counters)") if traffic else None,
             "kernel": f"gemm_allpairs<{'OpI8' if i8 else 'OpBf16'},{n_hi},{n_lo},2SUM>",
             "kernel_ms": gemm_s * 1e3,
             "algorithmic_flops_per_launch": flops,

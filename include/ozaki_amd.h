@@ -47,6 +47,23 @@ extern "C" {
 #define OZK_FLAG_NONFINITE 1u
 #define OZK_FLAG_WAIT_TIMEOUT 2u /* ozk_lu_solve_f32: a row block's wait gave up */
 #define OZK_FLAG_SINGULAR 4u     /* ozk_lu_factor_f32: a zero pivot */
+/* INT8 planes: a slice line overflowed with 2^-c > FLT_MAX (see
+ * OZK_EXP_NONFINITE).  The reference's slice then holds +-inf (and NaN where
+ * its value is zero); a product with it may be +-inf rather than NaN, which
+ * the FP64 order OZK_ORDER_BLOCK64 can carry to C.  Rerun such a call with
+ * OZK_PIPE_ONDEVICE_BF16 to get those values; the 2Sum order turns every
+ * non-finite product into NaN, so its results are exact either way. */
+#define OZK_FLAG_INF_SLICE 8u
+
+/* Exponent stored for a slice that INT8 planes cannot represent.  The
+ * reference's FP32 extraction (extract.py:130-148) gives a line non-finite
+ * slices when sigma = 0.75 * 2^(rho + c) or 2^-c overflows FP32 (rho + c >=
+ * 128 or c <= -128) or the line holds NaN/Inf; every product with such a
+ * slice is NaN or +-inf, and its output row / column comes out NaN in the
+ * 2Sum order.  On INT8 planes that slice and every later slice of its part
+ * are stored as zeros with this exponent, and the slice GEMM folds each pair
+ * product with it as NaN. */
+#define OZK_EXP_NONFINITE (-2147483647 - 1)
 
 /* Accumulation orders (the four orders of the reference). */
 #define OZK_ORDER_2SUM 0     /* A4: pallas_ops.py:178-239 == matmul.py:382-488 */
@@ -57,6 +74,10 @@ extern "C" {
 /* Pipelines / pair schedules. */
 #define OZK_PIPE_ONDEVICE 0 /* hh, hl, lh blocks: pallas_gemm_accum.py:26-87 */
 #define OZK_PIPE_HOST 1     /* triangle i+j <= n-1: matmul.py:23-32           */
+/* ozk_matmul / ozk_matmul_workspace_bytes only: the on-device pipeline on
+ * BF16 planes at every contraction length (no INT8 planes).  Same results as
+ * OZK_PIPE_ONDEVICE except where OZK_FLAG_INF_SLICE applies. */
+#define OZK_PIPE_ONDEVICE_BF16 2
 
 /* ---- library --------------------------------------------------------- */
 const char* ozk_last_error(void);
@@ -92,7 +113,9 @@ int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
  * (|q| <= 2^(25 - rho) <= 64; returns OZK_ERR_UNSUPPORTED otherwise).  Same
  * plane layout with 1-byte elements.  No counterpart in the reference: an
  * exact re-encoding of its BF16-exact slices (extract.py:145-151) for the
- * INT8 matrix cores. */
+ * INT8 matrix cores.  Slices the reference makes non-finite are stored as
+ * zeros with exponent OZK_EXP_NONFINITE, and OZK_FLAG_INF_SLICE is set when
+ * one of them may hold +-inf (2^-c overflow). */
 int ozk_extract_f32_i8(const double* X, int64_t rows, int64_t cols,
                        int64_t ldx, int by_cols, int rho, int n_hi, int n_lo,
                        int8_t* slices, int32_t* exps, uint32_t* flags,
@@ -179,12 +202,20 @@ int ozk_accumulate_2sum(const float* products, int64_t n_products,
 /* matmul(A, B, pipeline, accumulation, precision) after preflight:
  * pipeline OZK_PIPE_ONDEVICE: split + FP32 extraction with
  *   rho = ozk_rho_f32(K), n_hi/n_lo slices, order 2SUM or BLOCK64
- *   (matmul.py:641-728);
+ *   (matmul.py:641-728); INT8 planes when rho >= 19 and the schedule is a
+ *   preset (OZK_PIPE_ONDEVICE_BF16 keeps BF16 planes);
  * pipeline OZK_PIPE_HOST: FP64 extraction with rho = ozk_rho_f64(K),
  *   n_hi = n_slices (n_lo ignored), order HOST_JAX or HOST_NP
- *   (matmul.py:823-851, :866-900). */
+ *   (matmul.py:823-851, :866-900).
+ * flags receives OZK_FLAG_NONFINITE (NaN/Inf in A or B) and, on INT8
+ * planes, OZK_FLAG_INF_SLICE. */
 size_t ozk_matmul_workspace_bytes(int64_t N, int64_t K, int64_t M,
                                   int pipeline, int n_hi, int n_lo);
+/* Bytes per slice-plane element ozk_matmul uses for this shape: 1 (INT8
+ * planes, ozk_gemm_i8's kernels) or 2 (BF16 planes); negative on a bad
+ * pipeline or slice count.  No counterpart in the reference (whose slices
+ * are always BF16-valued FP32). */
+int ozk_matmul_plane_bytes(int pipeline, int64_t K, int n_hi, int n_lo);
 int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
                double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
                int pipeline, int n_hi, int n_lo, int order,

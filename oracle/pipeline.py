@@ -213,13 +213,20 @@ def slice_products(A_sl, B_sl, sched):
 
 
 def products_exact_certificate(A_sl, B_sl, sched, unit_a, unit_b):
-    """True when |S_a| @ |S_b| < 2^24 grid units for every pair, i.e. every
-    partial sum of every product is an exactly representable FP32 integer
-    multiple of the grid, so any summation order gives the same bits."""
+    """True when, for every pair and output element, the sum of the positive
+    terms a_k b_k and the sum of the negative ones both stay below 2^24 grid
+    units.  Every partial sum in any summation order lies between those two
+    sums, so each is an integer multiple of the grid below 2^24 units and
+    exactly representable in FP32: any order gives the same bits.  (The
+    terms are integers in grid units, so the FP64 sums below are exact.)"""
     for p in range(sched.n_pairs):
-        a = np.abs(A_sl[sched.pair_a[p]].astype(np.float64)) / unit_a
-        b = np.abs(B_sl[sched.pair_b[p]].astype(np.float64)) / unit_b
-        if (a @ b).max(initial=0.0) >= 2.0 ** 24:
+        a = A_sl[sched.pair_a[p]].astype(np.float64) / unit_a
+        b = B_sl[sched.pair_b[p]].astype(np.float64) / unit_b
+        ap, an = np.maximum(a, 0.0), np.maximum(-a, 0.0)
+        bp, bn = np.maximum(b, 0.0), np.maximum(-b, 0.0)
+        pos = ap @ bp + an @ bn
+        neg = ap @ bn + an @ bp
+        if max(pos.max(initial=0.0), neg.max(initial=0.0)) >= 2.0 ** 24:
             return False
     return True
 

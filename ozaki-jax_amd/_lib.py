@@ -20,6 +20,8 @@ OZK_ERR_WORKSPACE = -4
 OZK_FLAG_NONFINITE = 1
 OZK_FLAG_WAIT_TIMEOUT = 2
 OZK_FLAG_SINGULAR = 4
+OZK_FLAG_INF_SLICE = 8
+OZK_EXP_NONFINITE = -2 ** 31
 
 ORDER_2SUM = 0       # A4  pallas_ops.py:178-239
 ORDER_BLOCK64 = 1    # A3  matmul.py:543-597
@@ -28,6 +30,7 @@ ORDER_HOST_NP = 3    # A1  matmul.py:879-898
 
 PIPE_ONDEVICE = 0
 PIPE_HOST = 1
+PIPE_ONDEVICE_BF16 = 2  # ozk_matmul only: on-device pipeline, BF16 planes at any K
 
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
@@ -68,6 +71,7 @@ SIGNATURES = {
                                     _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_matmul_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int,
                                              _c_int, _c_int]),
+    "ozk_matmul_plane_bytes": (_c_int, [_c_int, _c_i64, _c_int, _c_int]),
     "ozk_matmul": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
                             _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                             _c_vp, _c_size, _c_vp, _c_vp]),

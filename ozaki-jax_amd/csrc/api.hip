@@ -347,12 +347,23 @@ int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
                          n_lo, P, ldp, (hipStream_t)stream, true, rho);
 }
 
+// OZK_PIPE_ONDEVICE_BF16 is the on-device pipeline with the INT8 planes
+// switched off; `i8` says whether a matmul of this shape runs on INT8 planes.
+static int matmul_pipe(int pipeline, int64_t K, int nhi, int nlo, bool* i8) {
+  const bool bf16 = pipeline == OZK_PIPE_ONDEVICE_BF16;
+  const int pipe = bf16 ? OZK_PIPE_ONDEVICE : pipeline;
+  if (i8) *i8 = !bf16 && use_i8(pipe, K, nhi, nlo);
+  return pipe;
+}
+
 static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
                         int nlo, bool carve, void* ws, SliceSet* a,
                         SliceSet* b, void** tws, void** gws = nullptr,
                         size_t* gwsb = nullptr) {
+  bool i8;
+  pipeline = matmul_pipe(pipeline, K, nhi, nlo, &i8);
   const int planes = pipeline == OZK_PIPE_ONDEVICE ? nhi + nlo : nhi;
-  const size_t eb = use_i8(pipeline, K, nhi, nlo) ? 1 : 2;
+  const size_t eb = i8 ? 1 : 2;
   Carver c(carve ? ws : nullptr);
   SliceSet sa = carve_slices(c, planes, N, K, eb);
   SliceSet sb = carve_slices(c, planes, M, K, eb);
@@ -377,12 +388,24 @@ size_t ozk_matmul_workspace_bytes(int64_t N, int64_t K, int64_t M,
                    nullptr, nullptr);
 }
 
+int ozk_matmul_plane_bytes(int pipeline, int64_t K, int n_hi, int n_lo) {
+  clear_error();
+  bool i8 = false;
+  const int pipe = matmul_pipe(pipeline, K, n_hi, n_lo, &i8);
+  const int rc = check_counts(pipe, n_hi, n_lo);
+  if (rc) return rc;
+  return i8 ? 1 : 2;
+}
+
 int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
                double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
                int pipeline, int n_hi, int n_lo, int order, void* workspace,
                size_t workspace_bytes, uint32_t* flags, void* stream) {
   clear_error();
   hipStream_t st = (hipStream_t)stream;
+  const int pipe_arg = pipeline;
+  bool i8 = false;
+  pipeline = matmul_pipe(pipeline, K, n_hi, n_lo, &i8);
   int rc = check_counts(pipeline, n_hi, n_lo);
   if (rc) return rc;
   if ((rc = check_order(order))) return rc;
@@ -394,7 +417,7 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   OZK_CHECK_ARG(flags, "null flags pointer");
   if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
   if (N == 0 || M == 0) return OZK_OK;
-  const size_t need = ozk_matmul_workspace_bytes(N, K, M, pipeline, n_hi, n_lo);
+  const size_t need = ozk_matmul_workspace_bytes(N, K, M, pipe_arg, n_hi, n_lo);
   if (!workspace || workspace_bytes < need) {
     set_error("matmul: workspace of %zu bytes needed, %zu given", need,
               workspace_bytes);
@@ -403,10 +426,9 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   SliceSet sa, sb;
   void *tws, *gws;
   size_t gwsb;
-  matmul_ws(N, K, M, pipeline, n_hi, n_lo, true, workspace, &sa, &sb, &tws, &gws,
+  matmul_ws(N, K, M, pipe_arg, n_hi, n_lo, true, workspace, &sa, &sb, &tws, &gws,
             &gwsb);
   const size_t tbytes = extract_workspace_bytes(K, M, 1);
-  const bool i8 = use_i8(pipeline, K, n_hi, n_lo);
   int rho;
   if (pipeline == OZK_PIPE_ONDEVICE) {
     rho = rho_generic(K, 24);

@@ -35,6 +35,40 @@ template <> struct PlaneElem<kFmtI8> {
   }
 };
 
+// Slices the INT8 format cannot hold.  The reference's slice of a line is
+// non-finite when sigma = 0.75 * 2^(rho + c) or 2^-c overflows FP32
+// (extract.py:134-136, :145-148), and a NaN / Inf element makes every slice
+// of its line non-finite.  Each product with such a slice is NaN or +-inf,
+// so the output row / column is NaN in the 2Sum order whichever slice it
+// was.  INT8 planes store the slice as zeros (v = 0, so the residual and
+// with it the overflow carry into the next slice, which is stored the same
+// way) with exponent OZK_EXP_NONFINITE; the slice GEMM folds every product
+// with it as NaN.  A 2^-c overflow can leave the reference's slice all +-inf
+// with no NaN, whose products may then be +-inf: OZK_FLAG_INF_SLICE.
+// Returns the exponent to store; `leader` is one thread of the line.
+template <int FMT, typename W>
+__device__ __forceinline__ int plane_exponent(SliceConst<W>& kc, int rho,
+                                              uint32_t* flags, bool leader) {
+  if constexpr (FMT == kFmtI8) {
+    if (!kc.zero && (rho + kc.c >= 128 || kc.c <= -128)) {
+      if (kc.c <= -128 && leader) atomicOr(flags, OZK_FLAG_INF_SLICE);
+      kc.zero = true;
+      kc.inv = W(1);
+      return OZK_EXP_NONFINITE;
+    }
+  }
+  return kc.c;
+}
+
+// Line-maximum contribution of a thread that read a NaN / Inf element: on
+// INT8 planes +inf, whose exponent plane_exponent classifies as overflow in
+// every slice of the line.  (The BF16 format carries such values itself.)
+template <int FMT, typename W>
+__device__ __forceinline__ W line_max_input(W m, bool bad) {
+  if constexpr (FMT == kFmtI8) return bad ? W(INFINITY) : m;
+  return m;
+}
+
 // Line maxima of up to two parts at once: wave butterfly then LDS combine
 // over the BLOCK / 64 waves of the thread's line (a workgroup holds LPB
 // lines of BLOCK threads each).
@@ -143,13 +177,15 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
       m[q] = W(0);
 #pragma unroll
       for (int j = 0; j < EPT * VEC; ++j) m[q] = max_w(m[q], fabs(R[q][j]));
+      m[q] = line_max_input<FMT>(m[q], bad);
     }
     block_max2<W, BLOCK, LPB, NP>(m, red);
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
       const int nq = q == 0 ? n0 : n1;
       if (s >= nq) continue;  // uniform
-      const SliceConst<W> kc = slice_const<W>(m[q], rho);
+      SliceConst<W> kc = slice_const<W>(m[q], rho);
+      const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
       const int pl = (q == 0 ? 0 : n0) + s;
       T* out = S + pl * plane + off0;
 #pragma unroll
@@ -168,7 +204,7 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
         }
         if (((int64_t)j * BLOCK + t) * VEC < ld) *(TV*)(out + j * step) = pk.w;
       }
-      if (t == 0) E[pl * eplane + line] = kc.c;
+      if (t == 0) E[pl * eplane + line] = ce;
     }
   }
 }
@@ -225,17 +261,20 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
       }
     }
     if (s == ns) break;
+#pragma unroll
+    for (int q = 0; q < NP; ++q) m[q] = line_max_input<FMT>(m[q], bad);
     block_max2<W, BLOCK, 1, NP>(m, red);
     if (threadIdx.x == 0) {
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
         const int nq = q == 0 ? n0 : n1;
         if (s >= nq) continue;
-        const SliceConst<W> kc = slice_const<W>(m[q], rho);
+        SliceConst<W> kc = slice_const<W>(m[q], rho);
+        const int ce = plane_exponent<FMT>(kc, rho, flags, true);
         sig[q][s] = kc.sigma;
         inv[q][s] = kc.inv;
         zero[q][s] = kc.zero;
-        E[((q == 0 ? 0 : n0) + s) * eplane + line] = kc.c;
+        E[((q == 0 ? 0 : n0) + s) * eplane + line] = ce;
       }
     }
     __syncthreads();
@@ -341,7 +380,8 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
     if (j + kDepth < EPT) issue(j + kDepth);
     __builtin_amdgcn_sched_barrier(0);
   }
-  if (emax == 0x7ff00000u) atomicOr(flags, OZK_FLAG_NONFINITE);
+  const bool bad = emax == 0x7ff00000u;
+  if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
   // Groups this thread stores (k0 < ld), counted from a fresh copy of t so
   // that the read's indices are not kept alive for the tests below.
   int tt = t;
@@ -388,23 +428,27 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
 #pragma unroll
       for (int j = 0; j < EPT; ++j) m[1] = amax(m[1], L[j]);
     }
+    m[0] = line_max_input<FMT>(m[0], bad);
+    m[1] = line_max_input<FMT>(m[1], bad);
     block_max2<float, BLOCK, 1, 2>(m, red);
     if (s < n0) {  // uniform
-      const SliceConst<float> kc = slice_const<float>(m[0], rho);
+      SliceConst<float> kc = slice_const<float>(m[0], rho);
+      const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
       T* out = S + s * plane + off0;
 #pragma unroll
       for (int j = 0; j < EPT_R; ++j) R[j] = sl(kc, out, j, R[j]);
 #pragma unroll 4
       for (int j = EPT_R; j < EPT; ++j)
         H[(j - EPT_R) * BLOCK] = sl(kc, out, j, H[(j - EPT_R) * BLOCK]);
-      if (t == 0) E[s * eplane + line] = kc.c;
+      if (t == 0) E[s * eplane + line] = ce;
     }
     if (s < n1) {  // uniform
-      const SliceConst<float> kc = slice_const<float>(m[1], rho);
+      SliceConst<float> kc = slice_const<float>(m[1], rho);
+      const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
       T* out = S + (n0 + s) * plane + off0;
 #pragma unroll
       for (int j = 0; j < EPT; ++j) L[j] = sl(kc, out, j, L[j]);
-      if (t == 0) E[(n0 + s) * eplane + line] = kc.c;
+      if (t == 0) E[(n0 + s) * eplane + line] = ce;
     }
   }
 }

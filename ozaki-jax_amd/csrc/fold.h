@@ -55,6 +55,18 @@ __host__ __device__ constexpr PairInfo pair_info(int pipe, int nhi, int nlo,
 
 // ---------------------------------------------------------------- fold
 
+// Scale 2^e of a slice exponent, as the reference forms it (FP32:
+// pallas_ops.py:126-164, matmul.py:558-561; FP64: matmul.py:553-556).  The
+// exponent OZK_EXP_NONFINITE marks a slice the reference makes NaN / +-inf
+// (INT8 planes store zeros there): its scale is NaN, so every product with
+// the slice folds as NaN.
+__device__ __forceinline__ float scale32(int e) {
+  return e == OZK_EXP_NONFINITE ? __builtin_nanf("") : ldexpf(1.0f, e);
+}
+__device__ __forceinline__ double scale64(int e) {
+  return e == OZK_EXP_NONFINITE ? __builtin_nan("") : ldexp(1.0, e);
+}
+
 __device__ __forceinline__ void twosum(float& s, float& l, float x) {
   const float t = s + x;
   const float e = (s - t) + x;

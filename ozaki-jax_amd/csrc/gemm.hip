@@ -504,8 +504,8 @@ __device__ __forceinline__ void tile_epilogue(
         for (int k = 0; k < NP; ++k) {
           const PairInfo q = SW::pair(k);
           const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
-          f.pair(q, Op::product(acc[k][h][r], unit2), ldexpf(1.0f, ib),
-                 ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+          f.pair(q, Op::product(acc[k][h][r], unit2), scale32(ib), scale32(ia),
+                 scale64(ib), scale64(ia));
         }
         if constexpr (SYM) {
           // Element (col, row) of a gram matrix: its pair (a, b) product is
@@ -518,8 +518,8 @@ __device__ __forceinline__ void tile_epilogue(
           for (int k = 0; k < NP; ++k) {
             const PairInfo q = SW::pair(k);
             const int ia = eb[SW::la(k)], ib = ea[SW::lb(k)];
-            f2.pair(q, Op::product(acc[SW::tpair(k)][h][r], unit2), ldexpf(1.0f, ib),
-                    ldexpf(1.0f, ia), ldexp(1.0, ib), ldexp(1.0, ia));
+            f2.pair(q, Op::product(acc[SW::tpair(k)][h][r], unit2), scale32(ib),
+                    scale32(ia), scale64(ib), scale64(ia));
           }
           const double c1 = f.finish(NBLK), c2 = f2.finish(NBLK);
           const double out = (c1 + c2) * 0.5;
@@ -785,13 +785,13 @@ __global__ __launch_bounds__(kThreads) void gemm_pairwise(
       continue;
     }
     const int eb = Be[q.b * b_lines + col];
-    const float cs32 = ldexpf(1.0f, eb);
-    const double cs64 = ldexp(1.0, eb);
+    const float cs32 = scale32(eb);
+    const double cs64 = scale64(eb);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
       const int ea = Ae[q.a * a_lines + row];
-      f[r].pair(q, mma.acc[r], cs32, ldexpf(1.0f, ea), cs64, ldexp(1.0, ea));
+      f[r].pair(q, mma.acc[r], cs32, scale32(ea), cs64, scale64(ea));
     }
   }
   if (MODE == 1) return;

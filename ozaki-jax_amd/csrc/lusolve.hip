@@ -3,6 +3,8 @@
 // (ozaki_jax/solve.py:159, :164, where jnp.linalg.solve re-solves with the
 // same matrix).  Latency-bound: one right-hand side is a chain of n / 64
 // dependent 64-row blocks.
+#include <cfloat>
+
 #include "common.h"
 
 namespace ozk {
@@ -68,12 +70,20 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     // the diagonal block is unit upper triangular and its solve, like the
     // forward one, is a broadcast and an FMA per step: the division leaves
     // the chain of dependent steps.
-    float ur = 0.0f;
+    // A block with a diagonal entry below FLT_MIN, whose reciprocal can
+    // overflow (0 * inf would then turn the row's zeros into NaN), is left
+    // unscaled instead and divides in the chain (`plain`, wave-uniform).
+    float ur = 0.0f, u = 1.0f;
+    bool plain = false;
     if (w == 0) {
       if (live)
         rhs = UPPER ? __uint_as_float((uint32_t)win[row * ldw + col])
                     : (float)B[(int64_t)perm[row] * ldb + col];
-      if (UPPER && live) ur = 1.0f / lrow[row];
+      if (UPPER) {
+        if (live) u = lrow[row];
+        plain = __any(!(fabsf(u) >= FLT_MIN));
+        if (live) ur = plain ? 1.0f : 1.0f / u;
+      }
       const int64_t k0 = (int64_t)blk * kTsRows;
 #pragma unroll
       for (int j = 0; j < kTsRows; ++j) {
@@ -149,11 +159,20 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
       // d = lane - j, stepped with j and opaque to the compiler, so that the
       // lane tests are made at each step; otherwise all 64 lane masks are
       // hoisted into scalar registers and spilled
-      if (UPPER) {
+      if (UPPER && !plain) {
         int d = lane - (kTsRows - 1);
 #pragma unroll
         for (int j = kTsRows - 1; j >= 0; --j, ++d) {
           asm volatile("" : "+v"(d));  // (opaque: see above)
+          const float xj = lane_value(v, j);
+          v = d < 0 ? fmaf(-dg[j], xj, v) : v;
+        }
+      } else if (UPPER) {  // unscaled rows: lane j divides by u before step j
+        int d = lane - (kTsRows - 1);
+#pragma unroll
+        for (int j = kTsRows - 1; j >= 0; --j, ++d) {
+          asm volatile("" : "+v"(d));
+          v = d == 0 ? v / u : v;
           const float xj = lane_value(v, j);
           v = d < 0 ? fmaf(-dg[j], xj, v) : v;
         }

@@ -113,7 +113,13 @@ def _unsafe(reasons, safe_mode, At, Bt):
 
 
 def _run_matmul(At, Bt, pipeline, n_hi, n_lo, order, dev):
-    """ozk_matmul on device tensors; returns (C tensor, nonfinite flag)."""
+    """ozk_matmul on device tensors; returns (C tensor, nonfinite flag).
+
+    INT8 slice planes (K > 4096) store a slice that the reference's
+    extraction makes non-finite as zeros with a NaN scale.  In the FP64 block
+    order (accumulation='host') a slice of +-inf can give C = +-inf where
+    that folds to NaN; the library flags such slices, and the call is then
+    repeated on BF16 planes, which hold the infinities themselves."""
     lib = _lib.load()
     N, K = At.shape
     M = Bt.shape[1]
@@ -121,13 +127,21 @@ def _run_matmul(At, Bt, pipeline, n_hi, n_lo, order, dev):
     flags = D.new_flags(dev)
     if N == 0 or M == 0:
         return C, 0
-    wsb = lib.ozk_matmul_workspace_bytes(N, K, M, pipeline, n_hi, n_lo)
-    ws = D.workspace(wsb, dev)
-    _lib.check(lib.ozk_matmul(
-        At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
-        D.ld_of(C), N, K, M, pipeline, n_hi, n_lo, order, ws.data_ptr(), wsb,
-        flags.data_ptr(), D.stream_handle()))
-    return C, D.read_flags(flags) & _lib.OZK_FLAG_NONFINITE
+
+    def run(pipe):
+        wsb = lib.ozk_matmul_workspace_bytes(N, K, M, pipe, n_hi, n_lo)
+        ws = D.workspace(wsb, dev)
+        _lib.check(lib.ozk_matmul(
+            At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
+            D.ld_of(C), N, K, M, pipe, n_hi, n_lo, order, ws.data_ptr(), wsb,
+            flags.data_ptr(), D.stream_handle()))
+        return D.read_flags(flags)
+
+    fl = run(pipeline)
+    if (fl & _lib.OZK_FLAG_INF_SLICE and order == _lib.ORDER_BLOCK64
+            and pipeline == _lib.PIPE_ONDEVICE):
+        fl = run(_lib.PIPE_ONDEVICE_BF16)
+    return C, fl & _lib.OZK_FLAG_NONFINITE
 
 
 def _matmul_ondevice(At, Bt, safe_mode, accumulation, n_hi, n_lo, dev):

@@ -82,10 +82,15 @@ def dominant(n, rng):
     return A[rng.permutation(n)]
 
 
+# (4096, 8) and (2100, 8): 8 columns leave 32 workgroups per column for 64
+# and 33 row blocks, so one workgroup runs several blocks in order.  (300,
+# 300): more columns than compute units, solved in launches of one chunk of
+# columns each, one workgroup per column.
 CASES = [(1, 1, 0, "dominant"), (5, 1, 0, "randn"), (64, 1, 0, "dominant"),
          (65, 2, 0, "dominant"), (127, 1, 3, "randn"), (300, 3, 0, "dominant"),
          (1000, 1, 0, "randn"), (1000, 2, 1, "dominant"), (2100, 1, 0, "dominant"),
-         (4096, 1, 0, "dominant")]
+         (4096, 1, 0, "dominant"), (4096, 8, 0, "dominant"), (2100, 8, 1, "randn"),
+         (300, 300, 0, "dominant")]
 
 
 @pytest.mark.parametrize("n,nc,pad,kind", CASES)
@@ -102,6 +107,48 @@ def test_lu_solve_matches_float64_solves(ozk, n, nc, pad, kind):
     Xr = ref_solve(lu, perm, B)
     err = np.linalg.norm(X - Xr) / np.linalg.norm(Xr)
     assert err <= (2e-5 if kind == "dominant" else 1e-3), err
+
+
+def test_lu_solve_subnormal_pivot(ozk):
+    """A diagonal entry of U below 2^-128 (its reciprocal overflows FP32):
+    that row block is solved unscaled, dividing in the chain, so the zeros
+    of its rows stay zeros and the solution stays finite."""
+    rng = np.random.RandomState(9)
+    n = 200
+    lu = np.triu(rng.randn(n, n) * 0.1 + np.diag(2.0 + rng.rand(n))).astype(np.float32)
+    lu[10, 11:] = 0.0
+    lu[10, 10] = np.float32(1e-39)        # subnormal pivot
+    b = rng.randn(n, 1)
+    b[10, 0] = float(np.float32(3e-39))
+    perm = np.arange(n, dtype=np.int32)
+    case("ozk_lu_solve_f32 subnormal pivot")
+    X = gpu_solve(lu, perm, b)
+    Xr = ref_solve(lu, perm, b)
+    assert np.isfinite(X).all() and abs(X[10, 0] - 3.0) < 1e-5
+    assert np.linalg.norm(X - Xr) <= 2e-5 * np.linalg.norm(Xr)
+
+
+def test_solve_eight_columns_n4096(ozk):
+    """solve() with an 8-column right-hand side at n = 4096: the native
+    solves with several row blocks per workgroup.  The refined error against
+    LAPACK's FP64 answer (bounded by the high preset's residual accuracy at
+    rho = 18) is within 2x of the oracle's refinement."""
+    import oracle as O
+    rng = np.random.RandomState(12)
+    n = 4096
+    A = dominant(n, rng)
+    B = rng.randn(n, 8)
+    case("solve ozaki n=4096 with 8 right-hand sides")
+    X = ozk.solve(A, B, residual_mode="ozaki")
+    Xr = np.linalg.solve(A, B)
+    assert X.shape == (n, 8)
+
+    def err(x):
+        return np.linalg.norm(x - Xr) / np.linalg.norm(Xr)
+
+    e_ref = err(O.solve_ozaki(A, B))
+    assert err(X) <= 2.0 * e_ref
+    assert e_ref < err(O.solve_ozaki(A, B, max_iterations=0)) / 10.0
 
 
 def test_lu_solve_in_place_and_empty(ozk):

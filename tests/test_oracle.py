@@ -266,6 +266,83 @@ def test_slice_products_exact_integers():
     assert P.products_exact_certificate(a, b, sched, float(unit), float(unit))
 
 
+def test_products_certificate_bounds_every_order():
+    """The certificate holds exactly when no summation order can round: with
+    it, the FP32 sums of the terms in many orders (sorted both ways,
+    shuffled) all equal the exact sum; a positive-term total one grid step
+    past 2^24 fails it, and the descending order then rounds."""
+    rng = np.random.RandomState(11)
+    K = 1 << 15
+    sched = O.ondevice_schedule(1, 1)
+    # terms of both signs whose |.| total exceeds 2^24 while each sign's
+    # total stays below: the |.| bound would refuse, this one accepts
+    qa = rng.choice([-1.0, 1.0], K) * 23.0
+    qb = np.where(qa > 0, 23.0, -23.0)[None, :].T.copy()
+    qb[1::2] *= -1.0
+    a, b = qa[None, :], qb
+    t = (qa * qb[:, 0])
+    assert np.abs(t).sum() >= 2 ** 24 and max(t[t > 0].sum(), -t[t < 0].sum()) < 2 ** 24
+    S = np.stack([a, a]).astype(np.float32)
+    T = np.stack([b, b]).astype(np.float32)
+    assert P.products_exact_certificate(S, T, sched, 1.0, 1.0)
+    exact = t.sum()
+    for order in [np.argsort(t), np.argsort(-t)] + [rng.permutation(K) for _ in range(20)]:
+        acc = np.float32(0)
+        for v in t[order].astype(np.float32):
+            acc = np.float32(acc + v)
+        assert float(acc) == exact
+    # one sign's total one step past 2^24, with an odd term: refused, and
+    # the descending order rounds
+    t2 = np.full(K, 512.0)
+    t2[0] = 1.0
+    t2 = np.concatenate([t2, [512.0]])
+    assert t2.sum() > 2 ** 24
+    S2 = np.stack([t2[None, :]] * 2).astype(np.float32)
+    T2 = np.ones((2, t2.size, 1), np.float32)
+    assert not P.products_exact_certificate(S2, T2, sched, 1.0, 1.0)
+    acc = np.float32(0)
+    for v in np.sort(t2)[::-1].astype(np.float32):
+        acc = np.float32(acc + v)
+    assert float(acc) != t2.sum()
+
+
+def test_nonfinite_lines_give_nan_rows_and_columns():
+    """The rule the INT8 planes rely on, checked on the oracle: a line is
+    non-finite in some slice exactly when one of its slice exponents makes
+    sigma = 0.75 * 2^(rho + c) or 2^-c overflow FP32 (rho + c >= 128,
+    c <= -128; c is inf / NaN for a line holding inf / NaN), and its whole
+    output row (A) or column (B) is then NaN in the 2Sum order; every other
+    element is finite.  Rows scaled by 2^-103 overflow only in the later lo
+    slices that precision 'max' extracts."""
+    import warnings
+    rng = np.random.RandomState(5)
+    N, K, M = 12, 8192, 10
+    A, B = rng.randn(N, K), rng.randn(K, M)
+    A[1] *= 2.0 ** -110
+    A[3] *= 2.0 ** -103
+    A[5] *= 2.0 ** 110
+    A[7] *= 2.0 ** -140
+    A[9, 4] = 1e300
+    B[:, 2] *= 2.0 ** -112
+    B[:, 4] *= 2.0 ** 108
+    B[:, 6] *= 2.0 ** -100
+    rho = O.rho_f32(K)
+    with warnings.catch_warnings(), np.errstate(all="ignore"):
+        warnings.simplefilter("ignore")
+        for prec in ("high", "medium", "max"):
+            nh, nl = P.resolve_precision(prec)
+            _, ae, _, be = O.ondevice_slices(A, B, rho, nh, nl)
+
+            def special(e):
+                return (~np.isfinite(e) | (rho + e >= 128) | (e <= -128)).any(axis=0)
+
+            expect = special(ae)[:, None] | special(be)[None, :]
+            C = O.matmul_ondevice_a4(A, B, "raise", nh, nl)
+            assert np.array_equal(np.isnan(C), expect), prec
+            assert np.isfinite(C[~expect]).all()
+            assert expect[3].all() == (prec == "max")
+
+
 # ---------------------------------------------------------------- orders
 
 def _np32(x):
