@@ -222,6 +222,22 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
                void* workspace, size_t workspace_bytes, uint32_t* flags,
                void* stream);
 
+/* ozk_matmul without a workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  The
+ * workspace is the library's own device array of OZK_NOALLOC_SCRATCH_BYTES
+ * (128 MiB), which each GPU the library runs on holds until the process
+ * ends; shapes whose ozk_matmul_workspace_bytes exceeds it return
+ * OZK_ERR_WORKSPACE (e.g. 2048^3 high needs 112 MiB and fits, 4096^3 high
+ * needs 448 MiB and does not).  The call allocates nothing: no hipMalloc,
+ * no hipFree.  All calls on one GPU share that GPU's array, so calls that
+ * overlap on a GPU (other streams, other threads) race. */
+#define OZK_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int ozk_matmul_noalloc(const double* A, int64_t lda, const double* B, int64_t ldb,
+                       double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
+                       int pipeline, int n_hi, int n_lo, int order,
+                       uint32_t* flags, void* stream);
+
 /* gram(A, mode="ozaki"): G = Ozaki(A^T, A) in order 2SUM with
  * rho = ozk_rho_f32(rows), then G = (G + G^T) * 0.5 (gram.py:19-37, :92-95).
  * A is rows x cols; G is cols x cols.  One column extraction of A serves

@@ -75,6 +75,9 @@ SIGNATURES = {
     "ozk_matmul": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
                             _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                             _c_vp, _c_size, _c_vp, _c_vp]),
+    "ozk_matmul_noalloc": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
+                                    _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
+                                    _c_vp, _c_vp]),
     "ozk_gram_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_int]),
     "ozk_gram": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp,
                           _c_i64, _c_vp, _c_size, _c_vp, _c_vp]),
