@@ -1,31 +1,187 @@
-"""Device-memory plumbing for the ctypes calls.
+"""Device memory, streams and FP64 helper products for the ctypes calls, per
+array family.
 
-PyTorch-ROCm provides the device allocations (its caching allocator) and the
-current HIP stream; every computation is done by libozaki_amd.so.  Arrays
-cross into the library as (device pointer, leading dimension) pairs.
+NumPy family (NumPy arrays and array-likes): device arrays from the HIP
+runtime (``_hip``), copies on the null stream, FP64 products by rocBLAS; no
+PyTorch involved.  Torch family (torch tensors, the optional on-device
+type): PyTorch-ROCm's allocator and current stream; FP64 products through
+torch (rocBLAS underneath).  Every Ozaki computation is done by
+libozaki_amd.so in both.  Arrays cross into the library as (device pointer,
+leading dimension) pairs.
 """
 
 import numpy as np
 
+from . import _hip
 from . import _lib
 
-try:
+try:  # imported before the library loads, so both share torch's HIP runtime
     import torch
-except ImportError:  # pragma: no cover - torch is part of the image
+except ImportError:  # pragma: no cover - torch is optional
     torch = None
 
 
 def is_torch(x):
-    return torch is not None and isinstance(x, torch.Tensor)
+    """A torch tensor?  Decided from the type alone: NumPy inputs never
+    touch the torch module."""
+    return type(x).__module__.split(".")[0] == "torch"
 
+
+def ld_of(t):
+    """Leading dimension (row stride in elements) of a 2-D device array."""
+    if t.dim() != 2:
+        raise ValueError("expected a 2-D array")
+    return max(int(t.stride(0)), int(t.shape[1]), 1)
+
+
+_NO_GPU = ("ozaki_jax_amd needs a ROCm GPU; there is no CPU implementation "
+           "(no HIP device found).")
+
+
+class _TorchFamily:
+    """Torch tensors on torch's current device and stream."""
+
+    def __init__(self):
+        if torch is None or not torch.cuda.is_available():
+            raise RuntimeError(
+                "ozaki_jax_amd needs a ROCm GPU (torch.cuda.is_available() is "
+                "False); there is no CPU implementation.")
+        _lib.load()
+        self.dev = torch.device("cuda", torch.cuda.current_device())
+
+    def stream(self):
+        return torch.cuda.current_stream().cuda_stream
+
+    def f64(self, x):
+        """float64 device tensor with contiguous rows holding x's values;
+        never aliases a NumPy input."""
+        if is_torch(x):
+            t = x.detach()
+            if t.dtype != torch.float64:
+                t = t.to(torch.float64)
+            if t.device != self.dev:
+                t = t.to(self.dev)
+        else:
+            a = np.ascontiguousarray(np.asarray(x, dtype=np.float64))
+            t = torch.from_numpy(a).to(self.dev)
+        if t.dim() >= 1 and t.numel() > 0 and t.stride(-1) != 1:
+            t = t.contiguous()
+        if t.dim() == 2 and t.numel() > 0 and t.stride(0) < max(t.shape[1], 1):
+            t = t.contiguous()
+        return t
+
+    def empty(self, shape, dtype=np.float64):
+        return torch.empty(shape, dtype=_TORCH_DTYPES[np.dtype(dtype)], device=self.dev)
+
+    def workspace(self, nbytes):
+        return torch.empty(max(int(nbytes), 1), dtype=torch.uint8, device=self.dev)
+
+    def flags(self):
+        """A flag word for a call that clears it itself."""
+        return torch.empty(1, dtype=torch.int32, device=self.dev)
+
+    def zero_flags(self):
+        return torch.zeros(1, dtype=torch.int32, device=self.dev)
+
+    def read_flags(self, f):
+        """Synchronising read of a device flag word."""
+        return int(f.item()) & 0xffffffff
+
+    def column(self, v):
+        return v[:, None].contiguous()
+
+    def flat(self, v):
+        return v[:, 0]
+
+    def out(self, t, want_torch):
+        return t if want_torch else t.cpu().numpy()
+
+    def matmul(self, A, B):
+        """FP64 A @ B."""
+        return torch.matmul(A, B)
+
+    def gram_f64(self, A):
+        G = torch.matmul(A.T, A)
+        return (G + G.T) * 0.5
+
+    def residual_f64(self, A, x, b):
+        return b - torch.matmul(A, x)
+
+
+class _HipFamily:
+    """NumPy inputs: device arrays of the HIP runtime on the null stream."""
+
+    def __init__(self):
+        if _hip.device_count() < 1:
+            raise RuntimeError(_NO_GPU)
+
+    def stream(self):
+        return None
+
+    def f64(self, x):
+        if is_torch(x):  # matmul_numpy takes any array-like
+            x = x.detach().cpu().numpy()
+        return _hip.DeviceArray.from_numpy(np.asarray(x, dtype=np.float64))
+
+    def empty(self, shape, dtype=np.float64):
+        return _hip.DeviceArray(shape, dtype)
+
+    def workspace(self, nbytes):
+        return _hip.DeviceArray((max(int(nbytes), 1),), np.uint8)
+
+    def flags(self):
+        return _hip.DeviceArray((1,), np.int32)
+
+    def zero_flags(self):
+        return _hip.DeviceArray.from_numpy(np.zeros(1, np.int32))
+
+    def read_flags(self, f):
+        return int(f.numpy()[0]) & 0xffffffff
+
+    def column(self, v):
+        return v.column()
+
+    def flat(self, v):
+        return v.flat()
+
+    def out(self, t, want_torch):
+        if want_torch:
+            raise TypeError("a NumPy-family result cannot be returned as a tensor")
+        return t.numpy()
+
+    def matmul(self, A, B):
+        C = _hip.DeviceArray((A.shape[0], B.shape[1]))
+        return _hip.blas().matmul(A, B, C)
+
+    def gram_f64(self, A):
+        n = A.shape[1]
+        G = _hip.blas().gram(A, _hip.DeviceArray((n, n)))
+        return _hip.blas().half_sum_transpose(G, _hip.DeviceArray((n, n)))
+
+    def residual_f64(self, A, x, b):
+        r = _hip.DeviceArray(b.shape)
+        r.copy_from(b)
+        return _hip.blas().matmul(A, x, r, alpha=-1.0, beta=1.0)
+
+
+_TORCH_DTYPES = {}
+if torch is not None:
+    _TORCH_DTYPES = {np.dtype(np.float64): torch.float64, np.dtype(np.float32): torch.float32,
+                     np.dtype(np.int32): torch.int32, np.dtype(np.uint8): torch.uint8}
+
+
+def family(want_torch):
+    """The device family of a call: torch tensors in -> torch, else the
+    HIP-runtime NumPy family."""
+    return _TorchFamily() if want_torch else _HipFamily()
+
+
+# ---- helpers of the torch-only modules (solve, lstsq, norm, inv, extract,
+# accumulate, lowlevel), which take their FP32 factorisations from torch.linalg
 
 def require_gpu():
-    if torch is None or not torch.cuda.is_available():
-        raise RuntimeError(
-            "ozaki_jax_amd needs a ROCm GPU (torch.cuda.is_available() is "
-            "False); there is no CPU implementation.")
-    _lib.load()
-    return torch.device("cuda", torch.cuda.current_device())
+    fam = _TorchFamily()
+    return fam.dev
 
 
 def stream_handle():
@@ -34,38 +190,11 @@ def stream_handle():
 
 
 def to_device_f64(x, dev):
-    """Return a float64 device tensor whose rows are contiguous (stride 1 in
-    the last dimension) holding the values of `x` (NumPy array, array-like or
-    torch tensor).  Never aliases a NumPy input."""
-    if is_torch(x):
-        t = x.detach()
-        if t.dtype != torch.float64:
-            t = t.to(torch.float64)
-        if t.device != dev:
-            t = t.to(dev)
-    else:
-        a = np.ascontiguousarray(np.asarray(x, dtype=np.float64))
-        t = torch.from_numpy(a).to(dev)
-    if t.dim() >= 1 and t.numel() > 0 and t.stride(-1) != 1:
-        t = t.contiguous()
-    if t.dim() == 2 and t.numel() > 0 and t.stride(0) < max(t.shape[1], 1):
-        t = t.contiguous()
-    return t
-
-
-def ld_of(t):
-    """Leading dimension (row stride in elements) of a 2-D device tensor."""
-    if t.dim() != 2:
-        raise ValueError("expected a 2-D tensor")
-    return max(int(t.stride(0)), int(t.shape[1]), 1)
-
-
-def ptr(t):
-    return ctypes_ptr(t.data_ptr()) if t is not None else None
-
-
-def ctypes_ptr(v):
-    return v if v else None
+    """float64 device tensor with contiguous rows holding the values of `x`
+    (NumPy array, array-like or torch tensor).  Never aliases NumPy input."""
+    fam = _TorchFamily.__new__(_TorchFamily)
+    fam.dev = dev
+    return fam.f64(x)
 
 
 def workspace(nbytes, dev):
@@ -86,3 +215,7 @@ def to_family(t, want_torch):
     if want_torch:
         return t
     return t.cpu().numpy()
+
+
+def ptr(t):
+    return t.data_ptr() if t is not None else None

@@ -1,0 +1,296 @@
+"""HIP runtime and rocBLAS through ctypes: device memory, copies and FP64
+products for the NumPy array family, which therefore needs no PyTorch.
+
+The HIP runtime is reached by its soname after libozaki_amd.so has been
+loaded, so this module and the library always share the one copy of the
+runtime in the process (PyTorch ships one under the same soname; whichever
+was loaded first serves both).  All work runs on the null stream, in order
+with the library's kernels, which this family launches there too.
+
+Device memory comes from a caching pool: blocks are rounded to size classes
+and kept for reuse after their arrays are garbage collected, so repeated
+calls of one shape allocate nothing after the first.
+"""
+
+import ctypes
+import os
+import threading
+
+import numpy as np
+
+from . import _lib
+
+_ROCM_LIB = "/opt/rocm/lib"
+_H2D, _D2H, _D2D = 1, 2, 3
+_OP_N, _OP_T = 111, 112  # rocblas_operation_none / _transpose
+
+
+def _open(soname):
+    """The library of this soname already in the process, else ROCm's."""
+    try:
+        return ctypes.CDLL(soname)
+    except OSError:
+        return ctypes.CDLL(os.path.join(_ROCM_LIB, soname))
+
+
+class _Runtime:
+    def __init__(self):
+        _lib.load()  # pulls libamdhip64.so.7 in through its runpath
+        h = _open("libamdhip64.so.7")
+        vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
+        for name, args in [("hipMalloc", [ctypes.POINTER(vp), sz]), ("hipFree", [vp]),
+                           ("hipMemcpy", [vp, vp, sz, i]),
+                           ("hipStreamSynchronize", [vp]),
+                           ("hipGetDeviceCount", [ctypes.POINTER(i)]),
+                           ("hipGetLastError", [])]:
+            fn = getattr(h, name)
+            fn.restype = i
+            fn.argtypes = args
+        h.hipGetErrorString.restype = ctypes.c_char_p
+        h.hipGetErrorString.argtypes = [i]
+        self.h = h
+
+    def check(self, rc, what):
+        if rc != 0:
+            msg = self.h.hipGetErrorString(rc).decode(errors="replace")
+            raise _lib.OzakiError(f"{what} failed: {msg} ({rc})")
+
+    def device_count(self):
+        n = ctypes.c_int(0)
+        rc = self.h.hipGetDeviceCount(ctypes.byref(n))
+        if rc != 0:
+            self.h.hipGetLastError()  # clear the sticky "no device" status
+            return 0
+        return n.value
+
+    def malloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self.check(self.h.hipMalloc(ctypes.byref(p), nbytes), f"hipMalloc({nbytes})")
+        return p.value
+
+    def free(self, ptr):
+        self.check(self.h.hipFree(ptr), "hipFree")
+
+    def copy(self, dst, src, nbytes, kind):
+        if nbytes:
+            self.check(self.h.hipMemcpy(dst, src, nbytes, kind), "hipMemcpy")
+
+    def sync(self):
+        self.check(self.h.hipStreamSynchronize(None), "hipStreamSynchronize")
+
+
+class _Pool:
+    """Device blocks by size class: powers of two below 1 MiB, multiples of
+    2 MiB above.  Released blocks are kept up to `keep` bytes in all."""
+
+    def __init__(self, rt, keep=64 << 30):
+        self.rt, self.keep, self.cached = rt, keep, 0
+        self.free = {}
+        self.lock = threading.Lock()
+
+    @staticmethod
+    def size_class(n):
+        n = max(int(n), 256)
+        if n < (1 << 20):
+            return 1 << (n - 1).bit_length()
+        return -(-n // (2 << 20)) * (2 << 20)
+
+    def take(self, n):
+        c = self.size_class(n)
+        with self.lock:
+            lst = self.free.get(c)
+            if lst:
+                self.cached -= c
+                return lst.pop(), c
+        return self.rt.malloc(c), c
+
+    def give(self, ptr, c):
+        with self.lock:
+            if self.cached + c <= self.keep:
+                self.free.setdefault(c, []).append(ptr)
+                self.cached += c
+                return
+        self.rt.free(ptr)
+
+
+class _Block:
+    """One pool block, returned to the pool when the last array using it is
+    collected.  Work that still reads it was queued on the null stream
+    before any later use of the block, so reuse stays in order."""
+    __slots__ = ("ptr", "cls", "__weakref__")
+
+    def __init__(self, nbytes):
+        self.ptr, self.cls = _pool().take(nbytes)
+
+    def __del__(self):
+        try:
+            _pool().give(self.ptr, self.cls)
+        except Exception:  # interpreter shutdown
+            pass
+
+
+class DeviceArray:
+    """A device array of the NumPy family: C-ordered rows, with `ld`
+    elements from one row to the next (2-D) or contiguous (1-D)."""
+
+    def __init__(self, shape, dtype=np.float64, ld=None, block=None, offset=0):
+        self.shape = tuple(int(s) for s in shape)
+        self.dtype = np.dtype(dtype)
+        cols = self.shape[1] if len(self.shape) == 2 else 1
+        self.ld = int(ld) if ld is not None else max(cols, 1)
+        rows = self.shape[0] if self.shape else 1
+        nbytes = (max(rows - 1, 0) * self.ld + cols) * self.dtype.itemsize
+        self._block = block if block is not None else _Block(max(nbytes, 1))
+        self._offset = offset
+
+    # the protocol the host layer uses (shared with torch tensors)
+    def data_ptr(self):
+        return self._block.ptr + self._offset
+
+    def dim(self):
+        return len(self.shape)
+
+    @property
+    def ndim(self):
+        return len(self.shape)
+
+    def numel(self):
+        return int(np.prod(self.shape)) if self.shape else 1
+
+    def stride(self, d):
+        return (self.ld, 1)[d] if len(self.shape) == 2 else 1
+
+    def element_size(self):
+        return self.dtype.itemsize
+
+    def column(self):
+        """A 1-D array as its (n, 1) matrix (same memory)."""
+        return DeviceArray((self.shape[0], 1), self.dtype, 1, self._block, self._offset)
+
+    def flat(self):
+        """An (n, 1) matrix as its 1-D array (same memory)."""
+        return DeviceArray((self.shape[0],), self.dtype, None, self._block, self._offset)
+
+    @classmethod
+    def from_numpy(cls, a):
+        a = np.ascontiguousarray(a)
+        d = cls(a.shape, a.dtype)
+        _rt().copy(d.data_ptr(), a.ctypes.data, a.nbytes, _H2D)
+        return d
+
+    def numpy(self):
+        """Synchronising copy to a new NumPy array."""
+        out = np.empty(self.shape, self.dtype)
+        if out.size == 0:
+            return out
+        if self.dim() == 2 and self.ld != self.shape[1]:
+            full = np.empty((self.shape[0], self.ld), self.dtype)
+            n = ((self.shape[0] - 1) * self.ld + self.shape[1]) * self.dtype.itemsize
+            _rt().copy(full.ctypes.data, self.data_ptr(), n, _D2H)
+            out[:] = full[:, :self.shape[1]]
+        else:
+            _rt().copy(out.ctypes.data, self.data_ptr(), out.nbytes, _D2H)
+        return out
+
+    def copy_from(self, other):
+        """Device-to-device copy of an array of the same shape and layout."""
+        n = ((self.shape[0] - 1) * self.ld + self.shape[1]) * self.dtype.itemsize \
+            if self.dim() == 2 else self.numel() * self.dtype.itemsize
+        _rt().copy(self.data_ptr(), other.data_ptr(), n, _D2D)
+
+
+class _Blas:
+    """rocBLAS FP64 products on the null stream.  Row-major matrices are
+    column-major transposes, so C = A B is computed as C^T = B^T A^T."""
+
+    def __init__(self):
+        _rt()
+        b = _open("librocblas.so.5")
+        vp, i = ctypes.c_void_p, ctypes.c_int
+        dp = ctypes.POINTER(ctypes.c_double)
+        b.rocblas_create_handle.restype = i
+        b.rocblas_create_handle.argtypes = [ctypes.POINTER(vp)]
+        b.rocblas_set_stream.restype = i
+        b.rocblas_set_stream.argtypes = [vp, vp]
+        b.rocblas_dgemm.restype = i
+        b.rocblas_dgemm.argtypes = [vp, i, i, i, i, i, dp, vp, i, vp, i, dp, vp, i]
+        b.rocblas_dgeam.restype = i
+        b.rocblas_dgeam.argtypes = [vp, i, i, i, i, dp, vp, i, dp, vp, i, vp, i]
+        h = vp()
+        self._chk(b.rocblas_create_handle(ctypes.byref(h)), "rocblas_create_handle")
+        self._chk(b.rocblas_set_stream(h, None), "rocblas_set_stream")
+        self.b, self.h = b, h
+
+    @staticmethod
+    def _chk(rc, what):
+        if rc != 0:
+            raise _lib.OzakiError(f"{what} failed: rocblas status {rc}")
+
+    @staticmethod
+    def _c(x):
+        return ctypes.byref(ctypes.c_double(x))
+
+    def matmul(self, A, B, C, alpha=1.0, beta=0.0):
+        """C = alpha A B + beta C (row-major A: N x K, B: K x M, C: N x M)."""
+        N, K = A.shape
+        M = B.shape[1]
+        if N == 0 or M == 0:
+            return C
+        if K == 0:
+            raise ValueError("contraction length 0")
+        self._chk(self.b.rocblas_dgemm(self.h, _OP_N, _OP_N, M, N, K, self._c(alpha),
+                                       B.data_ptr(), B.ld, A.data_ptr(), A.ld, self._c(beta),
+                                       C.data_ptr(), C.ld), "rocblas_dgemm")
+        return C
+
+    def gram(self, A, G):
+        """G = A^T A (row-major A: rows x cols, G: cols x cols)."""
+        rows, cols = A.shape
+        self._chk(self.b.rocblas_dgemm(self.h, _OP_N, _OP_T, cols, cols, rows, self._c(1.0),
+                                       A.data_ptr(), A.ld, A.data_ptr(), A.ld, self._c(0.0),
+                                       G.data_ptr(), G.ld), "rocblas_dgemm")
+        return G
+
+    def half_sum_transpose(self, G, out):
+        """out = G * 0.5 + G^T * 0.5, which equals (G + G^T) * 0.5 exactly
+        (halving is exact, and one rounding of the same sum)."""
+        n = G.shape[0]
+        self._chk(self.b.rocblas_dgeam(self.h, _OP_N, _OP_T, n, n, self._c(0.5), G.data_ptr(),
+                                       G.ld, self._c(0.5), G.data_ptr(), G.ld,
+                                       out.data_ptr(), out.ld), "rocblas_dgeam")
+        return out
+
+
+_state = {}
+_state_lock = threading.Lock()
+
+
+def _get(name, make):
+    v = _state.get(name)
+    if v is None:
+        with _state_lock:
+            v = _state.get(name)
+            if v is None:
+                v = make()
+                _state[name] = v
+    return v
+
+
+def _rt():
+    return _get("rt", _Runtime)
+
+
+def _pool():
+    return _get("pool", lambda: _Pool(_rt()))
+
+
+def blas():
+    return _get("blas", _Blas)
+
+
+def device_count():
+    return _rt().device_count()
+
+
+def sync():
+    _rt().sync()

@@ -4,7 +4,7 @@ mode='ozaki' runs the Ozaki pipeline on the GPU: one column extraction of A
 serves as both operands (row extraction of A^T equals column extraction of
 A), the fused slice-pair kernel accumulates in the 2Sum order, and the result
 is symmetrised as (G + G^T) * 0.5 (gram.py:19-37).  mode='f64' is the plain
-FP64 product (gram.py:40-44), computed by rocBLAS DGEMM through torch.
+FP64 product (gram.py:40-44), computed by rocBLAS DGEMM.
 """
 
 from . import _device as D
@@ -28,28 +28,28 @@ def gram(A, precision="high", accumulation="bf16_interleaved", mode="f64"):
     if A.ndim != 2:
         raise ValueError(f"A must be 2D, got ndim={A.ndim}.")
     want_torch = D.is_torch(A)
-    dev = D.require_gpu()
-    At = D.to_device_f64(A, dev)
+    fam = D.family(want_torch)
+    At = fam.f64(A)
     rows, cols = At.shape
     if mode == "f64":
-        G = D.torch.matmul(At.T, At)
-        G = (G + G.T) * 0.5
-        return D.to_family(G, want_torch)
+        return fam.out(fam.gram_f64(At), want_torch)
     n_hi, n_lo = _resolve_precision(precision)
     lib = _lib.load()
-    G = D.torch.empty((cols, cols), dtype=D.torch.float64, device=dev)
+    G = fam.empty((cols, cols))
     if cols == 0:
-        return D.to_family(G, want_torch)
+        return fam.out(G, want_torch)
     if rows == 0:
         raise ValueError("zero-size array to reduction operation maximum "
                          "which has no identity")
-    flags = D.new_flags(dev)
+    # A NaN / Inf in A gives NaN rows and columns of G, as in the reference,
+    # which runs no preflight here; the flag word needs no host action.
+    flags = fam.flags()
     wsb = lib.ozk_gram_workspace_bytes(rows, cols, n_hi, n_lo)
-    ws = D.workspace(wsb, dev)
+    ws = fam.workspace(wsb)
     _lib.check(lib.ozk_gram(At.data_ptr(), D.ld_of(At), rows, cols, n_hi, n_lo,
                             G.data_ptr(), D.ld_of(G), ws.data_ptr(), wsb,
-                            flags.data_ptr(), D.stream_handle()))
-    return D.to_family(G, want_torch)
+                            flags.data_ptr(), fam.stream()))
+    return fam.out(G, want_torch)
 
 
 __all__ = ["gram", "rho_f32"]

@@ -83,37 +83,31 @@ def _check_safe_mode(safe_mode):
             f"{sorted(allowed)}.")
 
 
-def _nonfinite(tensors, dev):
+def _nonfinite(fam, tensors):
     """np.isfinite(...).all() on the device (matmul.py:108-109, :623-628)."""
     lib = _lib.load()
-    flags = D.new_flags(dev)
+    flags = fam.zero_flags()
     for t in tensors:
         if t.numel() == 0:
             continue
         _lib.check(lib.ozk_check_finite(t.data_ptr(), t.shape[0], t.shape[1],
-                                        D.ld_of(t), flags.data_ptr(),
-                                        D.stream_handle()))
-    return D.read_flags(flags) & _lib.OZK_FLAG_NONFINITE
+                                        D.ld_of(t), flags.data_ptr(), fam.stream()))
+    return fam.read_flags(flags) & _lib.OZK_FLAG_NONFINITE
 
 
-def _fp64_fallback(At, Bt):
-    """safe_mode='fallback' result (matmul.py:133-134): the plain FP64
-    product, computed on the GPU by rocBLAS DGEMM through torch.matmul."""
-    return D.torch.matmul(At, Bt)
-
-
-def _unsafe(reasons, safe_mode, At, Bt):
-    """matmul.py:127-135 once the reasons are known."""
+def _unsafe(fam, reasons, safe_mode, At, Bt):
+    """matmul.py:127-135 once the reasons are known.  The fallback result is
+    the plain FP64 product, computed on the GPU by rocBLAS DGEMM."""
     if not reasons:
         return None
     if safe_mode == "fallback":
-        return _fp64_fallback(At, Bt)
+        return fam.matmul(At, Bt)
     raise ValueError("Ozaki preflight marked this input as unsafe: "
                      + "; ".join(reasons))
 
 
-def _run_matmul(At, Bt, pipeline, n_hi, n_lo, order, dev):
-    """ozk_matmul on device tensors; returns (C tensor, nonfinite flag).
+def _run_matmul(fam, At, Bt, pipeline, n_hi, n_lo, order):
+    """ozk_matmul on device arrays; returns (C, nonfinite flag).
 
     INT8 slice planes (K > 4096) store a slice that the reference's
     extraction makes non-finite as zeros with a NaN scale.  In the FP64 block
@@ -123,19 +117,19 @@ def _run_matmul(At, Bt, pipeline, n_hi, n_lo, order, dev):
     lib = _lib.load()
     N, K = At.shape
     M = Bt.shape[1]
-    C = D.torch.empty((N, M), dtype=D.torch.float64, device=dev)
-    flags = D.new_flags(dev)
+    C = fam.empty((N, M))
     if N == 0 or M == 0:
         return C, 0
+    flags = fam.flags()  # cleared by the call
 
     def run(pipe):
         wsb = lib.ozk_matmul_workspace_bytes(N, K, M, pipe, n_hi, n_lo)
-        ws = D.workspace(wsb, dev)
+        ws = fam.workspace(wsb)
         _lib.check(lib.ozk_matmul(
             At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
             D.ld_of(C), N, K, M, pipe, n_hi, n_lo, order, ws.data_ptr(), wsb,
-            flags.data_ptr(), D.stream_handle()))
-        return D.read_flags(flags)
+            flags.data_ptr(), fam.stream()))
+        return fam.read_flags(flags)
 
     fl = run(pipeline)
     if (fl & _lib.OZK_FLAG_INF_SLICE and order == _lib.ORDER_BLOCK64
@@ -144,7 +138,7 @@ def _run_matmul(At, Bt, pipeline, n_hi, n_lo, order, dev):
     return C, fl & _lib.OZK_FLAG_NONFINITE
 
 
-def _matmul_ondevice(At, Bt, safe_mode, accumulation, n_hi, n_lo, dev):
+def _matmul_ondevice(fam, At, Bt, safe_mode, accumulation, n_hi, n_lo):
     """matmul.py:641-728: preflight, then split + FP32 extraction + fused
     slice GEMMs with the accumulation order of `accumulation`
     ('fused' / 'bf16_interleaved' / 'ondevice' -> 2Sum A4; 'host' -> A3)."""
@@ -158,17 +152,17 @@ def _matmul_ondevice(At, Bt, safe_mode, accumulation, n_hi, n_lo, dev):
     reasons = _kbound_reasons(K, bits, "large for FP32 extraction")
     _check_safe_mode(safe_mode)
     if reasons:
-        if _nonfinite((At, Bt), dev):
+        if _nonfinite(fam, (At, Bt)):
             reasons.append("inputs contain NaN or Inf")
-        return _unsafe(reasons, safe_mode, At, Bt)
+        return _unsafe(fam, reasons, safe_mode, At, Bt)
     order = _lib.ORDER_BLOCK64 if accumulation == "host" else _lib.ORDER_2SUM
-    C, bad = _run_matmul(At, Bt, _lib.PIPE_ONDEVICE, n_hi, n_lo, order, dev)
+    C, bad = _run_matmul(fam, At, Bt, _lib.PIPE_ONDEVICE, n_hi, n_lo, order)
     if bad:
-        return _unsafe(["inputs contain NaN or Inf"], safe_mode, At, Bt)
+        return _unsafe(fam, ["inputs contain NaN or Inf"], safe_mode, At, Bt)
     return C
 
 
-def _matmul_host(At, Bt, n_slices, safe_mode, order, dev):
+def _matmul_host(fam, At, Bt, n_slices, safe_mode, order):
     """matmul.py:826-851 / :866-900: FP64 extraction (rho from
     `_compute_rho`), triangular slice pairs i + j <= n_slices - 1, FP64
     accumulation in order A2 (matmul) or A1 (matmul_numpy)."""
@@ -187,14 +181,14 @@ def _matmul_host(At, Bt, n_slices, safe_mode, order, dev):
                        f"{n_slices * max(bits, 0)} < 53")
     _check_safe_mode(safe_mode)
     if reasons:
-        if _nonfinite((At, Bt), dev):
+        if _nonfinite(fam, (At, Bt)):
             reasons.append("inputs contain NaN or Inf")
-        return _unsafe(reasons, safe_mode, At, Bt)
+        return _unsafe(fam, reasons, safe_mode, At, Bt)
     if n_slices > 32:
         raise NotImplementedError("n_slices > 32 is not supported")
-    C, bad = _run_matmul(At, Bt, _lib.PIPE_HOST, n_slices, 0, order, dev)
+    C, bad = _run_matmul(fam, At, Bt, _lib.PIPE_HOST, n_slices, 0, order)
     if bad:
-        return _unsafe(["inputs contain NaN or Inf"], safe_mode, At, Bt)
+        return _unsafe(fam, ["inputs contain NaN or Inf"], safe_mode, At, Bt)
     return C
 
 
@@ -220,18 +214,18 @@ def matmul(A, B, n_slices=8, safe_mode="raise", pipeline="host",
     follows the input family.
     """
     want_torch = _families(A, B)
-    dev = D.require_gpu()
+    fam = D.family(want_torch)
     if pipeline == "ondevice":
         n_hi, n_lo = _resolve_precision(precision)
-        At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
-        C = _matmul_ondevice(At, Bt, safe_mode, accumulation, n_hi, n_lo, dev)
-        return D.to_family(C, want_torch)
+        At, Bt = fam.f64(A), fam.f64(B)
+        C = _matmul_ondevice(fam, At, Bt, safe_mode, accumulation, n_hi, n_lo)
+        return fam.out(C, want_torch)
     if pipeline != "host":
         raise ValueError(
             f"Unknown pipeline={pipeline!r}; expected 'host' or 'ondevice'.")
-    At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
-    C = _matmul_host(At, Bt, n_slices, safe_mode, _lib.ORDER_HOST_JAX, dev)
-    return D.to_family(C, False)
+    At, Bt = fam.f64(A), fam.f64(B)
+    C = _matmul_host(fam, At, Bt, n_slices, safe_mode, _lib.ORDER_HOST_JAX)
+    return fam.out(C, False)
 
 
 def matmul_numpy(A_f64, B_f64, n_slices=8, safe_mode="raise", pipeline="host",
@@ -240,17 +234,15 @@ def matmul_numpy(A_f64, B_f64, n_slices=8, safe_mode="raise", pipeline="host",
     NumPy pipeline -- accumulation order A1 for pipeline='host' and A3
     (`_accumulate_block_products`) for 'ondevice' -- computed by the same
     GPU kernels.  Accepts array-likes; returns NumPy."""
-    dev = D.require_gpu()
-    A = np.asarray(A_f64, dtype=np.float64) if not D.is_torch(A_f64) else A_f64
-    B = np.asarray(B_f64, dtype=np.float64) if not D.is_torch(B_f64) else B_f64
+    want_torch = D.is_torch(A_f64) and D.is_torch(B_f64)
+    fam = D.family(want_torch)
+    At, Bt = fam.f64(A_f64), fam.f64(B_f64)
     if pipeline == "ondevice":
         n_hi, n_lo = _resolve_precision(precision)
-        At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
-        C = _matmul_ondevice(At, Bt, safe_mode, "host", n_hi, n_lo, dev)
-        return D.to_family(C, False)
+        C = _matmul_ondevice(fam, At, Bt, safe_mode, "host", n_hi, n_lo)
+        return fam.out(C, False)
     if pipeline != "host":
         raise ValueError(
             f"Unknown pipeline={pipeline!r}; expected 'host' or 'ondevice'.")
-    At, Bt = D.to_device_f64(A, dev), D.to_device_f64(B, dev)
-    C = _matmul_host(At, Bt, n_slices, safe_mode, _lib.ORDER_HOST_NP, dev)
-    return D.to_family(C, False)
+    C = _matmul_host(fam, At, Bt, n_slices, safe_mode, _lib.ORDER_HOST_NP)
+    return fam.out(C, False)

@@ -76,51 +76,51 @@ def _asarray(v):
     return np.asarray(v)
 
 
-def ozaki_residual_device(At, xt, bt, n_hi, n_lo, dev):
-    """r = b - Ozaki(A, x) on device tensors (x, b 2-D)."""
+def ozaki_residual_device(fam, At, xt, bt, n_hi, n_lo):
+    """r = b - Ozaki(A, x) on device arrays of family `fam` (x, b 2-D)."""
     lib = _lib.load()
     N, K = At.shape
     nc = xt.shape[1]
-    r = D.torch.empty((N, nc), dtype=D.torch.float64, device=dev)
+    r = fam.empty((N, nc))
     if N == 0 or nc == 0:
         return r
     if K == 0:
         raise ValueError("zero-size array to reduction operation maximum "
                          "which has no identity")
-    # ozk_residual clears the flag word itself
-    flags = D.torch.empty(1, dtype=D.torch.int32, device=dev)
+    flags = fam.flags()  # ozk_residual clears the flag word itself
     wsb = lib.ozk_residual_workspace_bytes(N, K, nc, n_hi, n_lo)
-    ws = D.workspace(wsb, dev)
+    ws = fam.workspace(wsb)
     _lib.check(lib.ozk_residual(
         At.data_ptr(), D.ld_of(At), xt.data_ptr(), D.ld_of(xt), bt.data_ptr(),
         D.ld_of(bt), r.data_ptr(), D.ld_of(r), N, K, nc, n_hi, n_lo,
-        ws.data_ptr(), wsb, flags.data_ptr(), D.stream_handle()))
+        ws.data_ptr(), wsb, flags.data_ptr(), fam.stream()))
     return r
 
 
 def residual(A, x, b, precision="high", accumulation="bf16_interleaved",
              mode="f64"):
-    """solve.py:91-151: b - A @ x; same family and shape as b."""
+    """solve.py:91-151: b - A @ x; same family and shape as b.  Runs no
+    preflight, as the reference: NaN / Inf give NaN entries of r."""
     _check_mode(mode, accumulation, "mode")
     A, x, b = _asarray(A), _asarray(x), _asarray(b)
     want_torch = D.is_torch(A)
     _validate_residual_inputs(A, x, b)
-    dev = D.require_gpu()
-    At = D.to_device_f64(A, dev)
-    xt = D.to_device_f64(x, dev)
-    bt = D.to_device_f64(b, dev)
+    fam = D.family(want_torch)
+    At = fam.f64(A)
+    xt = fam.f64(x)
+    bt = fam.f64(b)
     vec = xt.dim() == 1
     if vec:
-        xt = xt[:, None].contiguous()
-        bt = bt[:, None].contiguous()
+        xt = fam.column(xt)
+        bt = fam.column(bt)
     if mode == "f64":
-        r = bt - D.torch.matmul(At, xt)
+        r = fam.residual_f64(At, xt, bt)
     else:
         n_hi, n_lo = _resolve_precision(precision)
-        r = ozaki_residual_device(At, xt, bt, n_hi, n_lo, dev)
+        r = ozaki_residual_device(fam, At, xt, bt, n_hi, n_lo)
     if vec:
-        r = r[:, 0]
-    return D.to_family(r, want_torch)
+        r = fam.flat(r)
+    return fam.out(r, want_torch)
 
 
 def solve(A, b, precision="high", accumulation="bf16_interleaved",
@@ -131,6 +131,7 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
     want_torch = D.is_torch(A)
     _validate_solve_inputs(A, b)
     dev = D.require_gpu()
+    fam = D.family(True)
     torch = D.torch
     At = D.to_device_f64(A, dev)
     bt = D.to_device_f64(b, dev)
@@ -161,7 +162,7 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
         if residual_mode == "f64":
             r = bt - torch.matmul(At, x)
         else:
-            r = ozaki_residual_device(At, x.contiguous(), bt, n_hi, n_lo, dev)
+            r = ozaki_residual_device(fam, At, x.contiguous(), bt, n_hi, n_lo)
         x = x + solve32(r)
     if vec:
         x = x[:, 0]

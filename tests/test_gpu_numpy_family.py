@@ -1,0 +1,134 @@
+"""The NumPy family runs without PyTorch.
+
+The reference's matmul_numpy and the NumPy branch of matmul need nothing but
+NumPy (matmul.py:823-858).  Here NumPy inputs go through the HIP runtime and
+rocBLAS by ctypes (ozaki_jax_amd._hip); PyTorch is only the optional tensor
+family.  These tests replace the package's torch module with a stub that
+fails on any use, then run matmul / matmul_numpy / gram / residual on NumPy
+inputs against the oracle, bit for bit.
+"""
+
+import sys
+import warnings
+
+import numpy as np
+import pytest
+
+import oracle as O
+from oracle import pipeline as OP
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+class _NoTorch:
+    def __getattr__(self, name):
+        raise AssertionError(f"torch.{name} used by the NumPy family")
+
+
+@pytest.fixture
+def no_torch(ozk, monkeypatch):
+    from ozaki_jax_amd import _device as D
+    monkeypatch.setattr(D, "torch", _NoTorch())
+    return ozk
+
+
+def test_matmul_without_torch(no_torch):
+    ozk = no_torch
+    rng = np.random.RandomState(3)
+    for (N, K, M), prec, acc in [((150, 300, 90), "high", "fused"),
+                                 ((150, 300, 90), "max", "host"),
+                                 ((40, 6000, 70), "high", "fused"),
+                                 ((40, 6000, 70), "medium", "host")]:
+        A, B = rng.randn(N, K), rng.randn(K, M)
+        nh, nl = OP.resolve_precision(prec)
+        case(f"matmul ondevice {prec} {acc} ({N},{K},{M}) without torch")
+        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=prec)
+        f = O.matmul_ondevice_a3 if acc == "host" else O.matmul_ondevice_a4
+        assert isinstance(C, np.ndarray) and np.array_equal(C, f(A, B, "raise", nh, nl))
+    A, B = rng.randn(70, 200), rng.randn(200, 50)
+    case("matmul host pipeline without torch")
+    assert np.array_equal(ozk.matmul(A, B), OP.matmul_host_a2(A, B))
+    case("matmul_numpy host / ondevice without torch (lists accepted)")
+    assert np.array_equal(ozk.matmul_numpy(A.tolist(), B.tolist()), O.matmul_numpy(A, B))
+    assert np.array_equal(ozk.matmul_numpy(A, B, pipeline="ondevice", precision="max"),
+                          O.matmul_numpy(A, B, pipeline="ondevice", precision="max"))
+
+
+def test_preflight_and_fallback_without_torch(no_torch):
+    ozk = no_torch
+    rng = np.random.RandomState(4)
+    A, B = rng.randn(8, 16), rng.randn(16, 4)
+    bad = A.copy()
+    bad[1, 1] = np.nan
+    case("preflight NaN without torch")
+    with pytest.raises(ValueError, match="NaN or Inf"):
+        ozk.matmul(bad, B, pipeline="ondevice")
+    case("safe_mode fallback (rocBLAS DGEMM) without torch")
+    fb = ozk.matmul(bad, B, pipeline="ondevice", safe_mode="fallback")
+    assert np.isnan(fb[1]).all() and np.allclose(fb[0], (bad @ B)[0], rtol=1e-14)
+    Ab, Bb = rng.randn(2, 10000), rng.randn(10000, 2)
+    Cf = ozk.matmul(Ab, Bb, safe_mode="fallback")  # host pipeline: unsafe budget
+    assert np.allclose(Cf, Ab @ Bb, rtol=1e-13, atol=1e-12)
+
+
+def test_gram_and_residual_without_torch(no_torch):
+    ozk = no_torch
+    rng = np.random.RandomState(5)
+    for shape, prec in [((300, 40), "high"), ((5000, 24), "max"), ((8192, 70), "high")]:
+        A = rng.randn(*shape)
+        case(f"gram ozaki {shape} {prec} without torch")
+        G = ozk.gram(A, mode="ozaki", precision=prec)
+        assert np.array_equal(G, O.gram_ozaki(A, prec)) and np.array_equal(G, G.T)
+    A = rng.randn(200, 64)
+    case("gram f64 (rocBLAS) without torch")
+    G = ozk.gram(A)
+    assert np.array_equal(G, G.T) and np.allclose(G, A.T @ A, rtol=1e-13, atol=1e-12)
+    for (N, K), nc in [((300, 2048), None), ((37, 5000), None), ((64, 700), 3)]:
+        A = rng.randn(N, K)
+        x = rng.randn(K) if nc is None else rng.randn(K, nc)
+        b = rng.randn(N) if nc is None else rng.randn(N, nc)
+        case(f"residual ozaki ({N},{K}) ncols={nc} without torch")
+        r = ozk.residual(A, x, b, mode="ozaki")
+        assert r.shape == b.shape
+        assert np.array_equal(r, O.residual_ozaki(A, x, b))
+        case(f"residual f64 (rocBLAS) ({N},{K}) without torch")
+        r = ozk.residual(A, x, b)
+        assert np.allclose(r, b - A @ x, rtol=1e-12, atol=1e-10)
+    A = rng.randn(40, 8192)
+    A[3] *= 2.0 ** 110
+    x, b = rng.randn(8192), rng.randn(40)
+    case("residual ozaki with an overflowing row, without torch")
+    with warnings.catch_warnings(), np.errstate(all="ignore"):
+        warnings.simplefilter("ignore")
+        ref = O.residual_ozaki(A, x, b)
+    assert np.array_equal(ozk.residual(A, x, b, mode="ozaki"), ref, equal_nan=True)
+
+
+def test_device_pool_reuses_blocks(no_torch):
+    """Repeated calls of one shape take their device memory from the pool."""
+    from ozaki_jax_amd import _hip
+    ozk = no_torch
+    A, B = np.random.RandomState(6).randn(256, 512), np.random.RandomState(7).randn(512, 128)
+    ozk.matmul(A, B, pipeline="ondevice")
+    pool = _hip._pool()
+    before = sum(len(v) for v in pool.free.values())
+    case("matmul x 3 on one shape: no new device blocks")
+    calls = {"n": 0}
+    real = pool.rt.malloc
+
+    def counting(n):
+        calls["n"] += 1
+        return real(n)
+
+    pool.rt.malloc = counting
+    try:
+        for _ in range(3):
+            ozk.matmul(A, B, pipeline="ondevice")
+    finally:
+        pool.rt.malloc = real
+    assert calls["n"] == 0 and sum(len(v) for v in pool.free.values()) >= before
