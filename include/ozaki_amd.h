@@ -168,6 +168,20 @@ int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
                 double* C, int64_t ldc, void* workspace, size_t workspace_bytes,
                 void* stream);
 
+/* The fused slice GEMM of `fused_gemm_accum` (pallas_gemm_accum.py:191-275):
+ * the on-device (n_hi, n_lo) schedule in the 2Sum order, returning the
+ * double-float pair (C_hi, C_lo) of pallas_gemm_accum.py:181-186 (whose FP64
+ * sum ozk_gemm writes) as two FP32 N x M arrays with leading dimension ldc.
+ * plane_bytes 2: BF16 planes (ozk_extract_f32; rho is not used); 1: INT8
+ * planes (ozk_extract_f32_i8 with this rho >= 19, preset schedules).
+ * Workspace: ozk_gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, n_hi, n_lo,
+ * OZK_ORDER_2SUM). */
+int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
+                       const void* b_slices, const int32_t* b_exps,
+                       int64_t N, int64_t M, int64_t K, int plane_bytes, int rho,
+                       int n_hi, int n_lo, float* C_hi, float* C_lo, int64_t ldc,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Test hook: the per-pair FP32 products P[p] = S^A_a(p) . S^B_b(p) written
  * to P[p][N][ldp] in schedule order (matmul.py:216-233, :757-773, :885-887). */
 int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,

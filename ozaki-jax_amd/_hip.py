@@ -53,6 +53,7 @@ class _Runtime:
     def check(self, rc, what):
         if rc != 0:
             msg = self.h.hipGetErrorString(rc).decode(errors="replace")
+            self.h.hipGetLastError()  # leave no error behind for other users of the runtime
             raise _lib.OzakiError(f"{what} failed: {msg} ({rc})")
 
     def device_count(self):
@@ -130,17 +131,21 @@ class _Block:
 
 
 class DeviceArray:
-    """A device array of the NumPy family: C-ordered rows, with `ld`
-    elements from one row to the next (2-D) or contiguous (1-D)."""
+    """A device array of the NumPy family: a 2-D array has C-ordered rows
+    with `ld` elements from one row to the next; other ranks are contiguous."""
 
     def __init__(self, shape, dtype=np.float64, ld=None, block=None, offset=0):
         self.shape = tuple(int(s) for s in shape)
         self.dtype = np.dtype(dtype)
-        cols = self.shape[1] if len(self.shape) == 2 else 1
-        self.ld = int(ld) if ld is not None else max(cols, 1)
-        rows = self.shape[0] if self.shape else 1
-        nbytes = (max(rows - 1, 0) * self.ld + cols) * self.dtype.itemsize
-        self._block = block if block is not None else _Block(max(nbytes, 1))
+        if len(self.shape) == 2:
+            rows, cols = self.shape
+            self.ld = int(ld) if ld is not None else max(cols, 1)
+            count = max(rows - 1, 0) * self.ld + cols if rows and cols else 0
+        else:
+            self.ld = None
+            count = int(np.prod(self.shape)) if self.shape else 1
+        self.nbytes = count * self.dtype.itemsize
+        self._block = block if block is not None else _Block(max(self.nbytes, 1))
         self._offset = offset
 
     # the protocol the host layer uses (shared with torch tensors)
@@ -175,6 +180,7 @@ class DeviceArray:
     def from_numpy(cls, a):
         a = np.ascontiguousarray(a)
         d = cls(a.shape, a.dtype)
+        assert d.nbytes == a.nbytes
         _rt().copy(d.data_ptr(), a.ctypes.data, a.nbytes, _H2D)
         return d
 
@@ -185,8 +191,7 @@ class DeviceArray:
             return out
         if self.dim() == 2 and self.ld != self.shape[1]:
             full = np.empty((self.shape[0], self.ld), self.dtype)
-            n = ((self.shape[0] - 1) * self.ld + self.shape[1]) * self.dtype.itemsize
-            _rt().copy(full.ctypes.data, self.data_ptr(), n, _D2H)
+            _rt().copy(full.ctypes.data, self.data_ptr(), self.nbytes, _D2H)
             out[:] = full[:, :self.shape[1]]
         else:
             _rt().copy(out.ctypes.data, self.data_ptr(), out.nbytes, _D2H)
@@ -194,9 +199,9 @@ class DeviceArray:
 
     def copy_from(self, other):
         """Device-to-device copy of an array of the same shape and layout."""
-        n = ((self.shape[0] - 1) * self.ld + self.shape[1]) * self.dtype.itemsize \
-            if self.dim() == 2 else self.numel() * self.dtype.itemsize
-        _rt().copy(self.data_ptr(), other.data_ptr(), n, _D2D)
+        if other.shape != self.shape or other.nbytes != self.nbytes:
+            raise ValueError("copy between arrays of different shape or layout")
+        _rt().copy(self.data_ptr(), other.data_ptr(), self.nbytes, _D2D)
 
 
 class _Blas:

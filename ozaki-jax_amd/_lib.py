@@ -65,6 +65,9 @@ SIGNATURES = {
     "ozk_gemm_i8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                              _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp,
                              _c_size, _c_vp]),
+    "ozk_gemm_2sum_pair": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_i64,
+                                    _c_vp, _c_size, _c_vp]),
     "ozk_slice_products_i8": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                        _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_slice_products": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,

@@ -49,6 +49,10 @@ int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho);
 size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
                             int order);
+int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
+                     const int32_t* Be, int64_t N, int64_t M, int64_t K, int nhi,
+                     int nlo, float* C_hi, float* C_lo, int64_t ldc, void* ws,
+                     size_t ws_bytes, hipStream_t st, bool i8, int rho);
 int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho);
@@ -315,6 +319,38 @@ int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
   return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K,
                      OZK_PIPE_ONDEVICE, n_hi, n_lo, order, C, ldc, workspace,
                      workspace_bytes, (hipStream_t)stream, true, rho);
+}
+
+int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
+                       const void* b_slices, const int32_t* b_exps, int64_t N,
+                       int64_t M, int64_t K, int plane_bytes, int rho, int n_hi,
+                       int n_lo, float* C_hi, float* C_lo, int64_t ldc,
+                       void* workspace, size_t workspace_bytes, void* stream) {
+  clear_error();
+  int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
+  if (rc) return rc;
+  OZK_CHECK_ARG(plane_bytes == 1 || plane_bytes == 2, "plane_bytes=%d is not 1 or 2",
+                plane_bytes);
+  OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape N=%lld M=%lld K=%lld",
+                (long long)N, (long long)M, (long long)K);
+  OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
+  const bool i8 = plane_bytes == 1;
+  if (i8 && (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo))) {
+    set_error("int8 planes need rho >= 19 and a preset schedule (rho=%d, (%d, %d))",
+              rho, n_hi, n_lo);
+    return OZK_ERR_UNSUPPORTED;
+  }
+  if (N == 0 || M == 0) return OZK_OK;
+  OZK_CHECK_ARG(a_slices && a_exps && b_slices && b_exps && C_hi && C_lo, "null pointer");
+  const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, n_hi, n_lo, OZK_ORDER_2SUM);
+  if (workspace_bytes < need || (need && !workspace)) {
+    set_error("gemm_2sum_pair: workspace of %zu bytes needed, %zu given", need,
+              workspace_bytes);
+    return OZK_ERR_WORKSPACE;
+  }
+  return launch_gemm_pair(a_slices, a_exps, b_slices, b_exps, N, M, K, n_hi, n_lo, C_hi,
+                          C_lo, ldc, workspace, workspace_bytes, (hipStream_t)stream, i8,
+                          rho);
 }
 
 int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,

@@ -96,11 +96,20 @@ struct Fold2Sum {
       }
     }
   }
-  __device__ __forceinline__ double finish(int nblocks) {
+  // The blocks' lo parts after their hi parts (pallas_ops.py:230-237): the
+  // double-float pair (C_hi, C_lo) ...
+  __device__ __forceinline__ void finish_pair(int nblocks, float& hi, float& lo) {
     twosum(ct, cl, p0);
     if (nblocks > 1) twosum(ct, cl, p1);
     if (nblocks > 2) twosum(ct, cl, p2);
-    return (double)ct + (double)cl;
+    hi = ct;
+    lo = cl;
+  }
+  // ... and its FP64 combine (matmul.py:526, :540).
+  __device__ __forceinline__ double finish(int nblocks) {
+    float hi, lo;
+    finish_pair(nblocks, hi, lo);
+    return (double)hi + (double)lo;
   }
 };
 

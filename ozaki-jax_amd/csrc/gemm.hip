@@ -427,6 +427,12 @@ template <> struct FoldState<OZK_ORDER_2SUM> {
 };
 // ORDER value of the test hook that writes the per-pair products P.
 constexpr int kOrderProducts = -1;
+// ORDER value of the 2Sum order written as its double-float pair (C_hi,
+// C_lo) (pallas_gemm_accum.py:181-186) instead of their FP64 sum: C_hi goes
+// to P and C_lo to C, which then points at FP32 values; both use ldp.
+constexpr int kOrderPair = -2;
+template <> struct FoldOf<kOrderPair> { typedef Fold2Sum type; };
+template <> struct FoldState<kOrderPair> : FoldState<OZK_ORDER_2SUM> {};
 
 // Fold and store one output tile (tm, tn) from one wave's accumulators:
 // wave (wr, wc) owns rows 32 wr .. +31 and columns 16 wc .. +15 of the tile
@@ -529,6 +535,13 @@ __device__ __forceinline__ void tile_epilogue(
           }
         } else if constexpr (B1 < NBLK - 1) {
           if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
+        } else if constexpr (ORDER == kOrderPair) {
+          float hi, lo;
+          f.finish_pair(NBLK, hi, lo);
+          if (live) {
+            P[row * ldp + col] = hi;
+            ((float*)C)[row * ldp + col] = lo;
+          }
         } else {
           const double out = f.finish(NBLK);
           if (live) C[row * ldc + col] = out;
@@ -798,8 +811,17 @@ __global__ __launch_bounds__(kThreads) void gemm_pairwise(
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const int64_t row = row0 + 32 * mma.wm + acc_row(r, lane);
-    const double out = f[r].finish(nblocks);
-    if (row < N && col < M) C[row * ldc + col] = out;
+    if constexpr (ORDER == kOrderPair) {
+      float hi, lo;
+      f[r].finish_pair(nblocks, hi, lo);
+      if (row < N && col < M) {
+        P[row * ldp + col] = hi;
+        ((float*)C)[row * ldp + col] = lo;
+      }
+    } else {
+      const double out = f[r].finish(nblocks);
+      if (row < N && col < M) C[row * ldc + col] = out;
+    }
   }
 }
 
@@ -977,6 +999,7 @@ static void launch_ap_order(int order, const ApArgs& a) {
     case OZK_ORDER_BLOCK64: launch_schedule<Op, NHI, NLO, OZK_ORDER_BLOCK64>(a); break;
     case OZK_ORDER_HOST_JAX: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a); break;
     case OZK_ORDER_HOST_NP: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a); break;
+    case kOrderPair: launch_schedule<Op, NHI, NLO, kOrderPair>(a); break;
     default: launch_schedule<Op, NHI, NLO, kOrderProducts>(a); break;
   }
 }
@@ -1094,6 +1117,30 @@ int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
     default: OZK_PW(OZK_ORDER_HOST_NP); break;
   }
 #undef OZK_PW
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+// The on-device schedule of (nhi, nlo) in the 2Sum order, written as the
+// pair (C_hi, C_lo), FP32, both with leading dimension ldc.
+int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
+                     const int32_t* Be, int64_t N, int64_t M, int64_t K, int nhi,
+                     int nlo, float* C_hi, float* C_lo, int64_t ldc, void* ws,
+                     size_t ws_bytes, hipStream_t st, bool i8, int rho) {
+  if (allpairs_schedule(OZK_PIPE_ONDEVICE, nhi, nlo))
+    return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, kOrderPair,
+                           (double*)C_lo, ldc, C_hi, ldc, ws, ws_bytes, st);
+  if (i8) {
+    set_error("int8 slice planes need a preset on-device schedule");
+    return OZK_ERR_UNSUPPORTED;
+  }
+  const int64_t ld = round_up(K, kKPad);
+  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
+  const int64_t ntiles = (al / kBM) * (bl / kBN);
+  OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
+  hipLaunchKernelGGL((gemm_pairwise<kOrderPair, 0>), dim3((unsigned)ntiles), dim3(kThreads),
+                     0, st, (const uint16_t*)As, Ae, (const uint16_t*)Bs, Be, N, M, ld, al,
+                     bl, (int)OZK_PIPE_ONDEVICE, nhi, nlo, (double*)C_lo, ldc, C_hi, ldc);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }

@@ -126,6 +126,23 @@ def gemm(a, b, pipeline, n_hi, n_lo, order):
     return C
 
 
+def gemm_pair(a, b, n_hi, n_lo):
+    """ozk_gemm_2sum_pair on two Planes -> (C_hi, C_lo) float32 (N, M)."""
+    lib = _lib.load()
+    dev = a.s.device
+    N, M, K = a.lines, b.lines, a.length
+    C_hi = D.torch.empty((N, M), dtype=D.torch.float32, device=dev)
+    C_lo = D.torch.empty((N, M), dtype=D.torch.float32, device=dev)
+    wsb = lib.ozk_gemm_workspace_bytes(N, M, PIPE_ONDEVICE, n_hi, n_lo, ORDER_2SUM)
+    ws = D.workspace(wsb, dev)
+    _lib.check(lib.ozk_gemm_2sum_pair(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
+                                      b.e.data_ptr(), N, M, K, 1 if a.i8 else 2,
+                                      a.rho or 0, n_hi, n_lo, C_hi.data_ptr(),
+                                      C_lo.data_ptr(), max(M, 1), ws.data_ptr(), wsb,
+                                      D.stream_handle()))
+    return C_hi, C_lo
+
+
 def slice_products(a, b, pipeline, n_hi, n_lo):
     """ozk_slice_products -> float32 (n_pairs, N, M) device tensor."""
     lib = _lib.load()
