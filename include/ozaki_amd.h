@@ -45,7 +45,8 @@ extern "C" {
 #define OZK_ERR_WORKSPACE (-4)   /* workspace too small */
 
 #define OZK_FLAG_NONFINITE 1u
-#define OZK_FLAG_WAIT_TIMEOUT 2u /* ozk_lu_solve_f32: a row block's wait gave up */
+#define OZK_FLAG_WAIT_TIMEOUT 2u /* a bounded wait between workgroups gave up (column
+                                   extraction, ozk_lu_solve_f32): results not valid */
 #define OZK_FLAG_SINGULAR 4u     /* ozk_lu_factor_f32: a zero pivot */
 /* INT8 planes: a slice line overflowed with 2^-c > FLT_MAX (see
  * OZK_EXP_NONFINITE).  The reference's slice then holds +-inf (and NaN where
@@ -100,7 +101,12 @@ int64_t ozk_slice_lines(int64_t lines);
  * sigma-trick extraction: n_hi slices of hi then n_lo slices of lo
  * (extract.py:197-286; NumPy twin extract.py:116-191).  by_cols = 0 extracts
  * per row of X (rows x cols), by_cols = 1 per column; in both cases a line
- * is stored contiguously (columns are transposed through the workspace).
+ * is stored contiguously.  Columns of up to 8192 rows are extracted in place
+ * by groups of workgroups that exchange their per-slice column maxima through
+ * the workspace (a bounded wait that gives up sets OZK_FLAG_WAIT_TIMEOUT in
+ * flags: the planes are then not valid); longer columns are transposed
+ * through the workspace.  ozk_extract_workspace_bytes covers both this and
+ * ozk_extract_f64 (whose columns are always transposed).
  * Output planes: n_hi + n_lo. */
 size_t ozk_extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols);
 int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,

@@ -32,6 +32,15 @@ PIPE_ONDEVICE = 0
 PIPE_HOST = 1
 PIPE_ONDEVICE_BF16 = 2  # ozk_matmul only: on-device pipeline, BF16 planes at any K
 
+
+def check_flags(fl):
+    """Raise if a kernel's bounded wait gave up (OZK_FLAG_WAIT_TIMEOUT): the
+    results of that call are not valid.  Returns the flag word."""
+    if fl & OZK_FLAG_WAIT_TIMEOUT:
+        raise RuntimeError("ozaki_amd: a bounded wait between workgroups gave up "
+                           "(OZK_FLAG_WAIT_TIMEOUT); the result is not valid")
+    return fl
+
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
 _c_size = ctypes.c_size_t

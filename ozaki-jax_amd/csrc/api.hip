@@ -38,7 +38,7 @@ template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
             int by_cols, int rho, int n0, int n1, void* S, int32_t* E,
             uint32_t* flags, void* ws, size_t wsb, hipStream_t st, bool i8);
-size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols);
+size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols, bool f64);
 int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
 int launch_check_finite(const double* X, int64_t rows, int64_t cols,
                         int64_t ld, uint32_t* flags, hipStream_t st);
@@ -213,7 +213,9 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo) {
 }
 
 size_t ozk_extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols) {
-  return extract_workspace_bytes(rows, cols, by_cols);
+  const size_t a = extract_workspace_bytes(rows, cols, by_cols, false);
+  const size_t b = extract_workspace_bytes(rows, cols, by_cols, true);
+  return a > b ? a : b;
 }
 
 int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
@@ -403,7 +405,7 @@ static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
   Carver c(carve ? ws : nullptr);
   SliceSet sa = carve_slices(c, planes, N, K, eb);
   SliceSet sb = carve_slices(c, planes, M, K, eb);
-  void* t = c.take(extract_workspace_bytes(K, M, 1));
+  void* t = c.take(extract_workspace_bytes(K, M, 1, pipeline != OZK_PIPE_ONDEVICE));
   // fold state between sweeps (the 2Sum state bounds every order's), then
   // the partial sums of a K-split tail
   const size_t gb = round_up(gemm_workspace_bytes(N, M, pipeline, nhi, nlo, OZK_ORDER_2SUM),
@@ -464,7 +466,7 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   size_t gwsb;
   matmul_ws(N, K, M, pipe_arg, n_hi, n_lo, true, workspace, &sa, &sb, &tws, &gws,
             &gwsb);
-  const size_t tbytes = extract_workspace_bytes(K, M, 1);
+  const size_t tbytes = extract_workspace_bytes(K, M, 1, pipeline != OZK_PIPE_ONDEVICE);
   int rho;
   if (pipeline == OZK_PIPE_ONDEVICE) {
     rho = rho_generic(K, 24);
@@ -493,7 +495,7 @@ static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,
   Carver c(ws);
   SliceSet ss = carve_slices(c, nhi + nlo, cols, rows,
                              use_i8(OZK_PIPE_ONDEVICE, rows, nhi, nlo) ? 1 : 2);
-  void* t = c.take(extract_workspace_bytes(rows, cols, 1));
+  void* t = c.take(extract_workspace_bytes(rows, cols, 1, false));
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, rows, nhi, nlo);
   const size_t gb = round_up(gemm_workspace_bytes(cols, cols, OZK_PIPE_ONDEVICE, nhi, nlo,
                                                   OZK_ORDER_2SUM),
@@ -542,7 +544,7 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
   const int rho = rho_generic(rows, 24);
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, rows, n_hi, n_lo);
   if ((rc = extract<float>(A, rows, cols, lda, 1, rho, n_hi, n_lo, s.s, s.e,
-                           flags, tws, extract_workspace_bytes(rows, cols, 1), st,
+                           flags, tws, extract_workspace_bytes(rows, cols, 1, false), st,
                            i8)))
     return rc;
   // high / medium: upper tiles only, the symmetrisation folded into the
@@ -573,7 +575,7 @@ static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
   SliceSet sa = carve_slices(c, nhi + nlo, N, K, eb);
   SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
   double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
-  void* t = c.take(extract_workspace_bytes(K, ncols, 1));
+  void* t = c.take(extract_workspace_bytes(K, ncols, 1, false));
   const size_t gb = gemm_workspace_bytes(N, ncols, OZK_PIPE_ONDEVICE, nhi, nlo,
                                          OZK_ORDER_2SUM);
   void* g = c.take(gb);
@@ -625,7 +627,7 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
   if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,
-                           flags, tws, extract_workspace_bytes(K, ncols, 1), st,
+                           flags, tws, extract_workspace_bytes(K, ncols, 1, false), st,
                            i8)))
     return rc;
   if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,

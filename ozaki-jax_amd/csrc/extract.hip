@@ -453,6 +453,221 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
   }
 }
 
+// Column extraction without a transposed copy of X.  The columns are cut
+// into panels of kGangPW = 16 (a 128-byte row segment of X) and each panel's
+// rows into runs of kGangRun; workgroup ("member") m of the panel's gang of
+// G = ceil(rows / kGangRun) holds run m of all 16 columns in registers
+// (thread t: columns 2 (t % 8) and 2 (t % 8) + 1, rows 8 (t / 8) .. +7 of
+// the run, read as 16-byte pairs), so X is read once, in whole 128-byte row
+// segments, and every plane element is written once.  The arithmetic is
+// extract_lines_reg's; only the per-slice line maxima cross workgroups.
+//
+// Exchange, per (panel, slice): a record of G lines of 128 bytes, zeroed
+// before the launch.  Member m stores its 32 partial maxima (2 parts x 16
+// columns) as order keys, which are never 0, into line m, then waits until
+// every line is complete and combines them.  Every word is written once per
+// launch, so a reader that sees a nonzero word sees its final value: relaxed
+// agent-scope atomic loads and stores suffice (no fences, and no
+// read-modify-write on shared words).
+//
+// Progress: a member's place (panel, m) comes from a ticket taken when it
+// starts, so all members of the gangs before the first incomplete one have
+// started, and those gangs finish; the incomplete gang's remaining members
+// then need only free slots (G <= kGangMaxMembers workgroups resident at
+// once).  Every wait is bounded all the same: after kGangSpin polls it sets
+// OZK_FLAG_WAIT_TIMEOUT (the slices are then not valid) and the member waits
+// no more in later slices.
+constexpr int kGangPW = 16;
+constexpr int kGangRowsPT = 8;
+constexpr int kGangThreads = 512;
+constexpr int kGangRun = kGangThreads / (kGangPW / 2) * kGangRowsPT;  // 512 rows
+constexpr int kGangMaxMembers = 16;
+constexpr int kGangSpin = 1 << 18;
+constexpr int kGangKeys = 2 * kGangPW;  // keys per record line
+constexpr int64_t kGangLine = 128;      // bytes per record line
+constexpr int64_t kGangHeader = 256;    // the ticket word, padded
+
+__host__ __device__ constexpr int gang_members(int64_t ld) {
+  return (int)((ld + kGangRun - 1) / kGangRun);
+}
+
+// Order key of a partial maximum (a non-negative float or NaN): the key of
+// a maximum is the maximum of the keys under fmaxf's rule (NaN only when
+// every part is NaN), and no key is 0.
+__device__ __forceinline__ uint32_t max_key(float m) {
+  return m != m ? 1u : __float_as_uint(m) + 2u;
+}
+__device__ __forceinline__ float key_max(uint32_t k) {
+  return k == 1u ? __builtin_nanf("") : __uint_as_float(k - 2u);
+}
+
+// Bounded wait for a nonzero word; 0 after kGangSpin polls (and the flag).
+__device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags) {
+  for (int spin = 0; spin < kGangSpin; ++spin) {
+    const uint32_t k = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (k) return k;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  atomicOr(flags, OZK_FLAG_WAIT_TIMEOUT);
+  return 0u;
+}
+
+template <int FMT, bool VEC>
+__global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
+    const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
+    int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
+    int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G) {
+  typedef typename PlaneElem<FMT>::type T;
+  constexpr int NP = 2, CP = kGangPW / 2, NW = kGangThreads / 64, R = kGangRowsPT;
+  constexpr int NG = kGangThreads / kGangKeys;  // key groups of a workgroup
+  constexpr int64_t kWords = kGangLine / 4;
+  const float qscale = ldexpf(1.0f, 24 - rho);
+  __shared__ float red[NW][NP][kGangPW];
+  __shared__ float fin[NP][kGangPW];
+  __shared__ uint32_t comb[NG][kGangKeys];
+  __shared__ uint32_t place;
+  __shared__ int gave_up;
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if (t == 0) {
+    place = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    gave_up = 0;
+  }
+  __syncthreads();
+  const int64_t panel = place / (uint32_t)G;
+  const int member = (int)(place % (uint32_t)G);
+  const int ns = max(n0, n1);
+  uint32_t* const my = rec + panel * ns * G * kWords;
+  const int cp = t % CP;
+  const int64_t r0 = (int64_t)member * kGangRun + R * (t / CP);
+  const int64_t c0 = panel * kGangPW + 2 * cp;  // the thread's first line (column)
+
+  // The one read.  The empty asm pins each part where it is made, so the
+  // compiler does not hold the doubles until the non-finite check.
+  float Rg[NP][2][R];
+  bool bad[2] = {false, false};
+  const bool full = VEC && c0 + 1 < M;
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
+    const int64_t row = r0 + i;
+    const double* x = X + (row < K ? row : 0) * ldx + c0;
+    double v[2];
+    if (full) {
+      const double2 d = *(const double2*)x;
+      v[0] = d.x;
+      v[1] = d.y;
+    } else {
+      v[0] = c0 < M ? x[0] : 0.0;
+      v[1] = c0 + 1 < M ? x[1] : 0.0;
+    }
+#pragma unroll
+    for (int c = 0; c < 2; ++c) {
+      const double xv = row < K ? v[c] : 0.0;
+      bad[c] |= !isfinite(xv);
+      float p[NP];
+      split<float>(xv, p);
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        asm volatile("" : "+v"(p[q]));
+        Rg[q][c][i] = p[q];
+      }
+    }
+  }
+  if (bad[0] || bad[1]) atomicOr(flags, OZK_FLAG_NONFINITE);
+
+  const bool store = r0 < ld;  // the R rows lie in one padded unit
+  for (int s = 0; s < ns; ++s) {
+    uint32_t* const rs = my + s * G * kWords;  // this slice's record
+    float m[NP][2];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        float mm = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; ++i) mm = max_w(mm, fabsf(Rg[q][c][i]));
+        mm = line_max_input<FMT>(mm, bad[c]);
+#pragma unroll
+        for (int off = CP; off < 64; off <<= 1) mm = max_w(mm, __shfl_xor(mm, off));
+        m[q][c] = mm;
+      }
+    }
+    __syncthreads();  // the previous slice's readers of fin are done
+    if (lane < CP) {
+#pragma unroll
+      for (int q = 0; q < NP; ++q) {
+        red[wave][q][2 * lane] = m[q][0];
+        red[wave][q][2 * lane + 1] = m[q][1];
+      }
+    }
+    __syncthreads();
+    // Publish: wave 0, one lane per key (part t / 16, column t % 16).
+    if (t < kGangKeys) {
+      const int q = t / kGangPW, col = t % kGangPW;
+      float mm = red[0][q][col];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) mm = max_w(mm, red[w][q][col]);
+      __hip_atomic_store(rs + member * kWords + t, max_key(mm), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // Combine: thread t waits for key t % 32 of members t / 32, t / 32 +
+    // NG, ..., then the groups' maxima meet in LDS.
+    {
+      uint32_t k = 0u;
+      if (!gave_up) {
+        for (int mb = t / kGangKeys; mb < G; mb += NG) {
+          const uint32_t km = wait_key(rs + mb * kWords + t % kGangKeys, flags);
+          if (!km) gave_up = 1;
+          k = max(k, km);
+        }
+      }
+      comb[t / kGangKeys][t % kGangKeys] = k;
+    }
+    __syncthreads();
+    if (t < kGangKeys) {
+      uint32_t kk = comb[0][t];
+#pragma unroll
+      for (int g = 1; g < NG; ++g) kk = max(kk, comb[g][t]);
+      fin[t / kGangPW][t % kGangPW] = key_max(kk);
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int nq = q == 0 ? n0 : n1;
+      if (s >= nq) continue;  // uniform
+      const int pl = (q == 0 ? 0 : n0) + s;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        SliceConst<float> kc = slice_const<float>(fin[q][2 * cp + c], rho);
+        const int ce = plane_exponent<FMT>(kc, rho, flags, r0 == 0);
+        const int64_t line = c0 + c;
+        union {
+          typename std::conditional<FMT == kFmtI8, uint2, uint4>::type w;
+          T e[R];
+        } out;
+#pragma unroll
+        for (int i = 0; i < R; ++i) {
+          const float r = Rg[q][c][i];
+          float v = (r + kc.sigma) - kc.sigma;
+          if (kc.zero) v = 0.0f;
+          Rg[q][c][i] = r - v;
+          out.e[i] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+        }
+        if (store)
+          *(decltype(out.w)*)(S + pl * plane + plane_offset<sizeof(T)>(line, r0, eplane)) =
+              out.w;
+        if (r0 == 0) E[pl * eplane + line] = ce;
+      }
+    }
+  }
+}
+
+__global__ void zero_u32x4_kernel(uint4* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // X (rows x cols, ldx) -> XT (cols x rows, contiguous) through LDS tiles of
 // 128 rows x 64 columns: each wave reads 512 contiguous bytes of a row of X
 // and writes 512 contiguous bytes of a row of XT.
@@ -582,13 +797,64 @@ int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st) {
   return OZK_OK;
 }
 
-size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols) {
-  return by_cols ? (size_t)(rows * cols) * sizeof(double) : 0;
+// FP32 column extraction of columns up to kGangRun * kGangMaxMembers rows
+// runs on gangs; FP64 column extraction, and longer columns, go through an
+// FP64 transpose of X into the workspace.
+static bool gang_columns(int64_t rows) {
+  return round_up(rows, kKPad) <= (int64_t)kGangRun * kGangMaxMembers;
 }
 
-// Extraction entry shared by the FP32 and FP64 paths.  For column extraction
-// X is first transposed into the workspace so each column is contiguous.
-// int8 planes (FP32 path only) need rho >= 19 so that |q| <= 64.
+static size_t gang_workspace_bytes(int64_t rows, int64_t cols, int nslices) {
+  const int64_t G = gang_members(round_up(rows, kKPad));
+  return (size_t)kGangHeader +
+         (size_t)(round_up(cols, kLinePad) / kGangPW) * nslices * G * kGangLine;
+}
+
+size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols, bool f64) {
+  if (!by_cols) return 0;
+  if (!f64 && gang_columns(rows)) return gang_workspace_bytes(rows, cols, kMaxSlices);
+  return (size_t)(rows * cols) * sizeof(double);
+}
+
+template <int FMT>
+static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+                            int rho, int n0, int n1, void* Sv, int32_t* E, uint32_t* flags,
+                            void* ws, size_t wsb, hipStream_t st) {
+  typedef typename PlaneElem<FMT>::type T;
+  if (rows <= 0 || cols <= 0) return OZK_OK;
+  const int ns = n0 > n1 ? n0 : n1;
+  const size_t need = gang_workspace_bytes(rows, cols, ns);
+  if (wsb < need || !ws) {
+    set_error("extract: workspace of %zu bytes needed, %zu given", need, wsb);
+    return OZK_ERR_WORKSPACE;
+  }
+  const int64_t ld = round_up(rows, kKPad), lp = round_up(cols, kLinePad);
+  const int64_t plane = lp * ld, npanels = lp / kGangPW;
+  const int G = gang_members(ld);
+  // the ticket and the exchange records start at zero
+  const int64_t n16 = (int64_t)need / 16;
+  hipLaunchKernelGGL(zero_u32x4_kernel, dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)),
+                     dim3(256), 0, st, (uint4*)ws, n16);
+  OZK_LAUNCH_CHECK();
+  uint32_t* ticket = (uint32_t*)ws;
+  uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
+  const dim3 grid((unsigned)(npanels * G));
+  if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
+    hipLaunchKernelGGL((extract_cols_gang<FMT, true>), grid, dim3(kGangThreads), 0, st, X,
+                       rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
+                       ticket, G);
+  else
+    hipLaunchKernelGGL((extract_cols_gang<FMT, false>), grid, dim3(kGangThreads), 0, st, X,
+                       rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
+                       ticket, G);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
+// Extraction entry shared by the FP32 and FP64 paths.  FP32 columns go to
+// the gangs; other columns are first transposed into the workspace so each
+// is contiguous.  int8 planes (FP32 path only) need rho >= 19 so that
+// |q| <= 64.
 template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
             int by_cols, int rho, int n0, int n1, void* S, int32_t* E,
@@ -599,8 +865,17 @@ int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
   }
   const double* src = X;
   int64_t lines = rows, len = cols, lds = ldx;
+  if constexpr (sizeof(W) == 4) {
+    if (by_cols && gang_columns(rows)) {
+      if (i8)
+        return launch_cols_gang<kFmtI8>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, ws,
+                                        wsb, st);
+      return launch_cols_gang<kFmtBf16>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, ws,
+                                        wsb, st);
+    }
+  }
   if (by_cols) {
-    const size_t need = extract_workspace_bytes(rows, cols, 1);
+    const size_t need = extract_workspace_bytes(rows, cols, 1, sizeof(W) == 8);
     if (wsb < need || (need && !ws)) {
       set_error("extract: workspace of %zu bytes needed, %zu given", need, wsb);
       return OZK_ERR_WORKSPACE;

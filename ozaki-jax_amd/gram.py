@@ -42,13 +42,15 @@ def gram(A, precision="high", accumulation="bf16_interleaved", mode="f64"):
         raise ValueError("zero-size array to reduction operation maximum "
                          "which has no identity")
     # A NaN / Inf in A gives NaN rows and columns of G, as in the reference,
-    # which runs no preflight here; the flag word needs no host action.
+    # which runs no preflight here; the flag word is read only for
+    # OZK_FLAG_WAIT_TIMEOUT.
     flags = fam.flags()
     wsb = lib.ozk_gram_workspace_bytes(rows, cols, n_hi, n_lo)
     ws = fam.workspace(wsb)
     _lib.check(lib.ozk_gram(At.data_ptr(), D.ld_of(At), rows, cols, n_hi, n_lo,
                             G.data_ptr(), D.ld_of(G), ws.data_ptr(), wsb,
                             flags.data_ptr(), fam.stream()))
+    _lib.check_flags(fam.read_flags(flags))
     return fam.out(G, want_torch)
 
 

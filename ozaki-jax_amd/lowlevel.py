@@ -101,6 +101,7 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False, i8=False):
                 n1, s.data_ptr(), e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
                 wsb, D.stream_handle())
     _lib.check(rc)
+    _lib.check_flags(D.read_flags(flags))
     return Planes(s, e, lines, length, flags, rho if i8 else None)
 
 

@@ -129,7 +129,7 @@ def _run_matmul(fam, At, Bt, pipeline, n_hi, n_lo, order):
             At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
             D.ld_of(C), N, K, M, pipe, n_hi, n_lo, order, ws.data_ptr(), wsb,
             flags.data_ptr(), fam.stream()))
-        return fam.read_flags(flags)
+        return _lib.check_flags(fam.read_flags(flags))
 
     fl = run(pipeline)
     if (fl & _lib.OZK_FLAG_INF_SLICE and order == _lib.ORDER_BLOCK64

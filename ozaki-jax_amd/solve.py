@@ -94,6 +94,7 @@ def ozaki_residual_device(fam, At, xt, bt, n_hi, n_lo):
         At.data_ptr(), D.ld_of(At), xt.data_ptr(), D.ld_of(xt), bt.data_ptr(),
         D.ld_of(bt), r.data_ptr(), D.ld_of(r), N, K, nc, n_hi, n_lo,
         ws.data_ptr(), wsb, flags.data_ptr(), fam.stream()))
+    _lib.check_flags(fam.read_flags(flags))
     return r
 
 

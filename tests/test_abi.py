@@ -60,21 +60,35 @@ def test_host_functions(lib):
     assert b"outside" in lib.ozk_last_error()
 
 
+def gang_bytes(rows, cols):
+    """Column extraction of up to 65536 rows on the FP32 path: the ticket
+    word and, per (16-column panel, slice) for up to 32 slices, one
+    128-byte exchange line per 512-row run of a column."""
+    G = -(-(-(-rows // 64) * 64) // 512)
+    return 256 + (-(-cols // 64) * 64 // 16) * 32 * G * 128
+
+
 def test_workspace_sizes(lib):
-    # A and B slice planes + exponents + the FP64 transpose of B; planes are
-    # INT8 when K > 4096 (rho >= 19) and the schedule is a preset, else BF16
+    # A and B slice planes + exponents + B's column-extraction exchange
+    # records; planes are INT8 when K > 4096 (rho >= 19) and the schedule is
+    # a preset, else BF16
     for K, eb in [(8192, 1), (4096, 2)]:
         N = M = 8192
         for nh, nl in [(4, 1), (3, 1)]:
             ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, nh, nl)
             planes = 2 * (nh + nl) * 8192 * K * eb
             extra = 2 * (nh + nl) * 8192 * 4 + 4096
-            assert planes + 8 * K * M <= ws <= planes + 8 * K * M + extra, (K, nh, nl)
-    # max (5, 4): INT8 planes + transpose + the 2Sum fold state between its
-    # three sweeps (5 FP32 fields per output element)
+            assert planes + gang_bytes(K, M) <= ws <= planes + gang_bytes(K, M) + extra, (K, nh, nl)
+    # max (5, 4): INT8 planes + exchange records + the 2Sum fold state
+    # between its three sweeps (5 FP32 fields per output element)
     ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
-    base = 2 * 9 * 8192 * 8192 + 8 * 8192 * 8192 + 20 * 8192 * 8192
+    base = 2 * 9 * 8192 * 8192 + gang_bytes(8192, 8192) + 20 * 8192 * 8192
     assert base <= ws <= base + 2 * 9 * 8192 * 4 + 8192
+    # columns longer than 65536 rows, and the FP64 (host) pipeline, transpose B
+    ws = lib.ozk_matmul_workspace_bytes(64, 70000, 64, 0, 4, 1)
+    assert ws >= 8 * 70000 * 64
+    ws = lib.ozk_matmul_workspace_bytes(64, 1000, 64, 1, 8, 0)
+    assert ws >= 8 * 1000 * 64
 
 
 def test_gemm_workspace_bytes(lib):
@@ -86,7 +100,10 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == 100 * 70 * 8
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == 0
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
-    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == 100 * 50 * 8
+    # the larger of the FP32 (exchange records) and FP64 (transpose) needs
+    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == max(100 * 50 * 8, gang_bytes(100, 50))
+    assert lib.ozk_extract_workspace_bytes(8, 5000, 1) == gang_bytes(8, 5000)
+    assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 70000 * 3 * 8
 
 
 def test_int8_entry_points_reject_before_device_work(lib):
@@ -206,3 +223,11 @@ def test_plane_layout_decode_matches_header_formula(eb, lines, ld):
     st = torch.from_numpy(store.view(dt).reshape(P, lines, ld).copy())
     pl = Planes(st, None, lines, ld, None, rho=19 if eb == 1 else None)
     assert np.array_equal(pl.grid().numpy(), grid)
+
+
+def test_check_flags_raises_on_wait_timeout():
+    from ozaki_jax_amd import _lib
+    assert _lib.check_flags(0) == 0
+    assert _lib.check_flags(_lib.OZK_FLAG_NONFINITE) == _lib.OZK_FLAG_NONFINITE
+    with pytest.raises(RuntimeError, match="OZK_FLAG_WAIT_TIMEOUT"):
+        _lib.check_flags(_lib.OZK_FLAG_WAIT_TIMEOUT | _lib.OZK_FLAG_NONFINITE)
