@@ -74,8 +74,8 @@ size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int n
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo);
 int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
                          const double* x, int64_t ldx, const double* b,
-                         int64_t ldb, double* r, int64_t ldr, int rho, int nhi,
-                         int nlo, uint32_t* flags, hipStream_t st);
+                         int64_t ldb, double* r, int64_t ldr, int64_t ncols, int rho,
+                         int nhi, int nlo, uint32_t* flags, hipStream_t st);
 
 constexpr int kMaxSlices = 32;
 constexpr size_t kAlign = 256;
@@ -617,7 +617,7 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   }
   const int rho = rho_generic(K, 24);
   if (residual_rows_supported(K, ncols, n_hi, n_lo))  // clears and sets flags
-    return launch_residual_rows(A, N, K, lda, x, ldx, b, ldb, r, ldr, rho, n_hi,
+    return launch_residual_rows(A, N, K, lda, x, ldx, b, ldb, r, ldr, ncols, rho, n_hi,
                                 n_lo, flags, st);
   SliceSet sa, sx;
   double* y;

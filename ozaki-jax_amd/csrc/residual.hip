@@ -402,8 +402,271 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
   }
 }
 
+// Rows longer than one wave holds (K up to 64 EPL W): a workgroup of W waves
+// per row over a persistent grid, wave w holding elements k = 64 EPL w +
+// 64 j + l, j < EPL, in lane l, with the arithmetic of residual_rows_kernel.
+// What crosses waves goes through LDS: the row maxima of every slice (each
+// wave's maximum as a bit pattern, then the maximum of the W, so every wave
+// gets the same slice constants) and, per row, the waves' pair sums, which
+// wave 0 adds and folds.  Every partial sum of a slice product lies on one
+// grid below 2^24 units, so the sum over the waves is exact in any order.
+// x's slices are extracted the same way, once.
+template <int EPL, bool FULL, int W, int NHI, int NLO>
+__global__ __launch_bounds__(64 * W) void residual_split_kernel(
+    const double* __restrict__ A, int64_t N, int64_t K, int64_t lda,
+    const double* __restrict__ x, int64_t ldx, const double* __restrict__ b,
+    int64_t ldb, double* __restrict__ r, int64_t ldr, int rho,
+    uint32_t* __restrict__ flags) {
+  constexpr int NT = NHI + NLO;
+  constexpr int NP = pair_count(OZK_PIPE_ONDEVICE, NHI, NLO);
+  constexpr int NR = (NP + 3) / 4 * 4;  // pair sums padded for the reduce-scatter
+  constexpr int KW = 64 * EPL, H = EPL / 2;
+  static_assert(EPL % 2 == 0 && NP <= 64, "elements are paired; one lane per pair");
+  __shared__ ResRow<NP, NT> rows[kResBatch];
+  __shared__ uint32_t gm[2][W][2];  // the waves' maxima, alternating buffers
+  __shared__ float part[W][NR];     // the waves' pair sums of the row
+
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int kw0 = wave * KW;  // this wave's first element
+  const int Ki = (int)K;
+  int ph = 0;
+  // Maxima over the row of two wave-uniform values (non-negative floats or
+  // NaN, compared as bit patterns like wave_max_uniform).  The buffers
+  // alternate, so that one barrier per exchange suffices: a buffer is
+  // rewritten two exchanges later, after every wave has read it.
+  auto row_max2 = [&](float& u, float& v) {
+    if (lane == 0) {
+      gm[ph][wave][0] = __float_as_uint(u);
+      gm[ph][wave][1] = __float_as_uint(v);
+    }
+    __syncthreads();
+    uint32_t mu = 0u, mv = 0u;
+#pragma unroll
+    for (int w = 0; w < W; ++w) {
+      mu = max(mu, gm[ph][w][0]);
+      mv = max(mv, gm[ph][w][1]);
+    }
+    u = __uint_as_float(__builtin_amdgcn_readfirstlane(mu));
+    v = __uint_as_float(__builtin_amdgcn_readfirstlane(mv));
+    ph ^= 1;
+  };
+  auto row_max = [&](float u) {
+    float v = 0.0f;
+    row_max2(u, v);
+    return u;
+  };
+
+  uint32_t xp[NT][H];  // x's slices, BF16 pairs (elements j, j + 1)
+  float cs[NT];        // their scales 2^c
+  {
+    float X[2][EPL];
+    bool xbad = false;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int k = kw0 + j * 64 + lane;
+      const double v = k < Ki ? x[(int64_t)k * ldx] : 0.0;
+      xbad |= !isfinite(v);
+      float pr[2];
+      split<float>(v, pr);
+      X[0][j] = pr[0];
+      X[1][j] = pr[1];
+    }
+    if (blockIdx.x == 0 && xbad) atomicOr(flags, OZK_FLAG_NONFINITE);
+    static_for<0, NT>([&](auto t_c) {
+      constexpr int T = decltype(t_c)::value;
+      constexpr int Q = T < NHI ? 0 : 1;  // hi part, then lo part
+      float m = 0.0f;
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) m = fmaxf(m, fabsf(X[Q][j]));
+      const SliceConst<float> kc = slice_const<float>(row_max(wave_max_uniform(m)), rho);
+      cs[T] = ldexpf(1.0f, kc.c);
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        float s[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float rr = X[Q][2 * i + e];
+          float v = (rr + kc.sigma) - kc.sigma;
+          if (kc.zero) v = 0.0f;
+          X[Q][2 * i + e] = rr - v;
+          s[e] = slice_value_f32(v, kc.inv);
+        }
+        xp[T][i] = pack_bf16x2(s[0], s[1]);
+      }
+    });
+  }
+
+  double nx[EPL];
+  auto load_row = [&](int64_t row) {
+    const char* a = (const char*)(A + row * lda);
+    int Kr = Ki;
+    asm volatile("" : "+s"(Kr));
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      const int k = kw0 + j * 64 + lane;
+      if constexpr (FULL) {
+        nx[j] = *(const double*)(a + (uint32_t)k * 8u);
+      } else {
+        const double v = *(const double*)(a + (uint32_t)(k < Kr ? k : Kr - 1) * 8u);
+        nx[j] = k < Kr ? v : 0.0;
+      }
+    }
+  };
+  constexpr bool PF = EPL <= 16;  // the next row's prefetch fits in registers
+  const int64_t G = gridDim.x;
+  int64_t cur = blockIdx.x;
+  if (PF && cur < N) load_row(cur);
+  int nb = 0;
+
+  while (cur < N) {  // uniform over the workgroup
+    const int64_t nxt = cur + G;
+    if constexpr (!PF) load_row(cur);
+    const double bv = (wave == 0 && lane == 0) ? b[cur * ldb] : 0.0;
+    float Rh[EPL], Rl[EPL];
+    bool bad = false;
+    float mh = 0.0f, ml = 0.0f;
+#pragma unroll
+    for (int j = 0; j < EPL; ++j) {
+      bad |= !isfinite(nx[j]);
+      float pr[2];
+      split<float>(nx[j], pr);
+      Rh[j] = pr[0];
+      Rl[j] = pr[1];
+      if (j & 1) {
+        mh = max3_abs(mh, Rh[j - 1], Rh[j]);
+        ml = max3_abs(ml, Rl[j - 1], Rl[j]);
+      }
+    }
+    if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
+
+    float acc[NR];
+#pragma unroll
+    for (int p = 0; p < NR; ++p) acc[p] = 0.0f;
+    float rs[NT], un[NT];
+
+    auto slice_loop = [&](auto a_c, auto maxnext_c, auto norm_c, float (&R)[EPL],
+                          const SliceConst<float>& kc) {
+      constexpr int a = decltype(a_c)::value;
+      constexpr bool MAXNEXT = decltype(maxnext_c)::value;
+      constexpr bool NORM = decltype(norm_c)::value;
+      float mn = 0.0f;
+#pragma unroll
+      for (int i = 0; i < H; ++i) {
+        float v[2];
+#pragma unroll
+        for (int e = 0; e < 2; ++e) {
+          const float rr = R[2 * i + e];
+          v[e] = (rr + kc.sigma) - kc.sigma;
+          if (MAXNEXT) R[2 * i + e] = rr - v[e];
+          if (NORM) v[e] = slice_value_f32(v[e], kc.inv);
+        }
+        if (MAXNEXT) mn = max3_abs(mn, R[2 * i], R[2 * i + 1]);
+        const uint32_t pk = pack_bf16x2(v[0], v[1]);
+#pragma unroll
+        for (int p = 0; p < NP; ++p) {
+          const PairInfo q = pair_info(OZK_PIPE_ONDEVICE, NHI, NLO, p);
+          if (q.a == a) acc[p] = dot2(pk, xp[q.b][i], acc[p]);
+        }
+      }
+      return mn;
+    };
+    // The slice constants come from the row maximum mw, the same in every
+    // wave, so the zero / normalised branches are uniform over the row.
+    auto slice = [&](auto a_c, auto maxnext_c, float (&R)[EPL], float mw, float& m) {
+      constexpr int a = decltype(a_c)::value;
+      const SliceConst<float> kc = slice_const<float>(mw, rho);
+      rs[a] = ldexpf(1.0f, kc.c);
+      un[a] = 1.0f;
+      if (kc.zero) {
+        m = 0.0f;
+        return;
+      }
+      if (kc.c >= -100 && kc.c <= 100) {
+        un[a] = ldexpf(1.0f, -kc.c);
+        m = slice_loop(a_c, maxnext_c, std::false_type{}, R, kc);
+      } else {
+        m = slice_loop(a_c, maxnext_c, std::true_type{}, R, kc);
+      }
+    };
+
+    float mwl0 = wave_max_uniform(ml), mwh0 = wave_max_uniform(mh);
+    row_max2(mwl0, mwh0);
+    static_for<0, NLO>([&](auto s) {
+      constexpr int S = decltype(s)::value;
+      const float mw = S == 0 ? mwl0 : row_max(wave_max_uniform(ml));
+      slice(std::integral_constant<int, NHI + S>{},
+            std::integral_constant<bool, (S + 1 < NLO)>{}, Rl, mw, ml);
+    });
+    if (PF && nxt < N) load_row(nxt);
+    static_for<0, NHI>([&](auto s) {
+      constexpr int S = decltype(s)::value;
+      const float mw = S == 0 ? mwh0 : row_max(wave_max_uniform(mh));
+      slice(std::integral_constant<int, S>{},
+            std::integral_constant<bool, (S + 1 < NHI)>{}, Rh, mw, mh);
+    });
+
+    // reduce-scatter within the wave (z[k] of row q of lanes holds pair
+    // k + q * NR / 4), then the waves' sums meet in LDS
+    float y[NR / 2], z[NR / 4];
+#pragma unroll
+    for (int k = 0; k < NR / 2; ++k) y[k] = swap32_sum(acc[k], acc[k + NR / 2]);
+#pragma unroll
+    for (int k = 0; k < NR / 4; ++k) z[k] = row_sum(swap16_sum(y[k], y[k + NR / 4]));
+    if ((lane & 15) == 0) {
+#pragma unroll
+      for (int k = 0; k < NR / 4; ++k) part[wave][k + (lane >> 4) * (NR / 4)] = z[k];
+    }
+    __syncthreads();
+    if (wave == 0) {
+      ResRow<NP, NT>& rr = rows[nb];
+      if (lane < NP) {
+        float s = part[0][lane];
+#pragma unroll
+        for (int w = 1; w < W; ++w) s += part[w][lane];
+        rr.p[lane] = s;
+      }
+      if (lane == 0) {
+        rr.b = bv;
+        rr.row = cur;
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+          rr.rs[t] = rs[t];
+          rr.un[t] = un[t];
+        }
+      }
+      ++nb;
+      if (nb == kResBatch || nxt >= N) {
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (lane < nb) {
+          const ResRow<NP, NT>& s = rows[lane];
+          Fold2Sum f;
+          f.init();
+#pragma unroll
+          for (int p = 0; p < NP; ++p) {
+            const PairInfo q = pair_info(OZK_PIPE_ONDEVICE, NHI, NLO, p);
+            f.pair(q, s.p[p] * s.un[q.a], cs[q.b], s.rs[q.a], 0.0, 0.0);
+          }
+          const double c = f.finish(3);
+          r[s.row * ldr] = s.b - c;
+        }
+        asm volatile("" ::: "memory");
+        nb = 0;
+      }
+    }
+    cur = nxt;
+  }
+}
+
+// Right-hand sides and row lengths the fused kernels take: up to
+// kResMaxCols columns, each a launch of its own (A is read once per column,
+// 8 B an element, against the ~28 B of the slice-GEMM route's plane round
+// trip), and K <= 64 * 32 * 8 (eight waves of 2048 elements per row).
+constexpr int64_t kResMaxCols = 4;
+constexpr int64_t kResMaxK = 64 * 32 * 8;
+
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo) {
-  return ncols == 1 && K >= 1 && K <= 64 * 32 &&
+  return ncols >= 1 && ncols <= kResMaxCols && K >= 1 && K <= kResMaxK &&
          ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1));
 }
 
@@ -416,15 +679,11 @@ static int residual_rows_epl(int64_t K) {
 
 int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
 
-// r = b - Ozaki(A, x) for one right-hand side x (K elements, stride ldx):
-// clears `flags`, then runs the row kernel, which sets it for a non-finite x
-// or A.  Needs no workspace.
-int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
-                         const double* x, int64_t ldx, const double* b,
-                         int64_t ldb, double* r, int64_t ldr, int rho, int nhi,
-                         int nlo, uint32_t* flags, hipStream_t st) {
-  const int rc = launch_fill_u32(flags, 0u, st);
-  if (rc) return rc;
+// One right-hand side on the one-wave-per-row kernel (K <= 2048).
+static void launch_rows_1(const double* A, int64_t N, int64_t K, int64_t lda,
+                          const double* x, int64_t ldx, const double* b, int64_t ldb,
+                          double* r, int64_t ldr, int rho, int nhi, uint32_t* flags,
+                          hipStream_t st) {
   const int epl = residual_rows_epl(K);
   // persistent grid: one workgroup of kResWaves waves per CU
   const int cus = cu_count();
@@ -460,7 +719,59 @@ int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
   }
 #undef OZK_RES_E
 #undef OZK_RES
-  OZK_LAUNCH_CHECK();
+}
+
+// One right-hand side on the split-row kernel (2048 < K <= kResMaxK): W = 4
+// waves of 1024 elements up to K = 4096, else 8 waves of 1024 or 2048.
+static void launch_rows_split(const double* A, int64_t N, int64_t K, int64_t lda,
+                              const double* x, int64_t ldx, const double* b, int64_t ldb,
+                              double* r, int64_t ldr, int rho, int nhi, uint32_t* flags,
+                              hipStream_t st) {
+  // persistent grid: 8 / W workgroups per CU
+  const int64_t cus = cu_count();
+#define OZK_SPLIT(E, W, H)                                                           \
+  do {                                                                               \
+    const int64_t g = cus * (8 / (W));                                               \
+    const dim3 grid((unsigned)(N < g ? N : g));                                      \
+    if (K == 64 * (E) * (W))                                                         \
+      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, 1>), grid, dim3(64 * (W)), \
+                         0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, rho, flags);   \
+    else                                                                             \
+      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, 1>), grid, dim3(64 * (W)), \
+                         0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, rho, flags);   \
+  } while (0)
+#define OZK_SPLIT_K(H)                          \
+  if (K <= 64 * 16 * 4) OZK_SPLIT(16, 4, H);    \
+  else if (K <= 64 * 16 * 8) OZK_SPLIT(16, 8, H); \
+  else OZK_SPLIT(32, 8, H);
+  if (nhi == 4) {
+    OZK_SPLIT_K(4);
+  } else {
+    OZK_SPLIT_K(3);
+  }
+#undef OZK_SPLIT_K
+#undef OZK_SPLIT
+}
+
+// r = b - Ozaki(A, x) for up to kResMaxCols right-hand sides (column j of x,
+// b and r at x + j, b + j, r + j with strides ldx, ldb, ldr): clears `flags`,
+// then runs the row kernel once per column; it sets the flag for a
+// non-finite x or A.  Needs no workspace.
+int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
+                         const double* x, int64_t ldx, const double* b,
+                         int64_t ldb, double* r, int64_t ldr, int64_t ncols, int rho,
+                         int nhi, int nlo, uint32_t* flags, hipStream_t st) {
+  (void)nlo;
+  const int rc = launch_fill_u32(flags, 0u, st);
+  if (rc) return rc;
+  for (int64_t j = 0; j < ncols; ++j) {
+    if (K <= 64 * 32)
+      launch_rows_1(A, N, K, lda, x + j, ldx, b + j, ldb, r + j, ldr, rho, nhi, flags, st);
+    else
+      launch_rows_split(A, N, K, lda, x + j, ldx, b + j, ldb, r + j, ldr, rho, nhi, flags,
+                        st);
+    OZK_LAUNCH_CHECK();
+  }
   return OZK_OK;
 }
 

@@ -545,11 +545,14 @@ def test_residual_bit_exact(ozk, shape):
     assert np.array_equal(R, O.residual_ozaki(A, X, Bm))
 
 
-@pytest.mark.parametrize("N,K", [(37, 1), (37, 1100), (129, 4096), (5, 513)])
+@pytest.mark.parametrize("N,K", [(37, 1), (37, 1100), (129, 4096), (5, 513), (70, 2049),
+                                 (33, 3000), (40, 8192), (9, 12000), (17, 16384),
+                                 (6, 16385)])
 @pytest.mark.parametrize("precision", ["high", "medium", "max"])
 def test_residual_fused_rows_bit_exact(ozk, N, K, precision):
-    # one right-hand side with K <= 2048 (high, medium) runs the fused row
-    # kernel; K = 4096 and max take the slice-GEMM route
+    # high / medium: K <= 2048 runs the one-wave-per-row kernel, K <= 16384
+    # the split-row kernel (4 waves of 1024 elements up to K = 4096, then 8
+    # waves of 1024 or 2048); K = 16385 and max take the slice-GEMM route
     rng = np.random.RandomState(N + K)
     A = (rng.rand(N, K) - 0.5) * np.exp(2.0 * rng.randn(N, K))
     x, b = rng.randn(K), rng.randn(N)
@@ -558,20 +561,36 @@ def test_residual_fused_rows_bit_exact(ozk, N, K, precision):
     assert np.array_equal(r, O.residual_ozaki(A, x, b, precision))
 
 
-@pytest.mark.parametrize("K", [2048, 1500, 1024, 700])
+@pytest.mark.parametrize("K,ncols", [(700, 2), (2048, 4), (5000, 3), (9000, 5)])
+def test_residual_fused_columns_bit_exact(ozk, K, ncols):
+    # up to 4 right-hand sides run the row kernels once per column; 5 take
+    # the slice-GEMM route; x and b strided (columns of matrices)
+    rng = np.random.RandomState(K + ncols)
+    N = 150
+    A = rng.randn(N, K) * np.exp(rng.randn(N, 1))
+    X, Bm = rng.randn(K, ncols), rng.randn(N, ncols)
+    case(f"residual fused columns K={K} ncols={ncols}")
+    R = ozk.residual(A, X, Bm, mode="ozaki")
+    assert R.shape == (N, ncols)
+    assert np.array_equal(R, O.residual_ozaki(A, X, Bm))
+
+
+@pytest.mark.parametrize("K", [2048, 1500, 1024, 700, 4096, 6000, 16384])
 @pytest.mark.parametrize("precision", ["high", "medium"])
 def test_residual_rows_batches_and_edge_rows(ozk, K, precision):
-    """40000 rows: every wave of the row kernel's persistent grid (one
-    workgroup of 8 waves per CU) takes more than one batch of 16 rows, the
-    last one partial.  K = 2048 / 1024 are whole 64 x EPL rows, 1500 / 700
-    take the guarded loads.  Special rows: all zero (no slice), one nonzero,
+    """40000 rows (fewer for K > 2048, about 80 M elements): every wave of
+    the one-wave-per-row kernel's persistent grid (one workgroup of 8 waves
+    per CU), and every workgroup of the split-row kernel's, takes more than
+    one batch of 16 rows, the last one partial.  K = 2048 / 1024 / 4096 /
+    16384 are whole rows of the kernels, 1500 / 700 / 6000 take the guarded
+    loads.  Special rows: all zero (no slice), one nonzero,
     scaled by 2^-103 (slice exponents below -100: normalised dot products,
     subnormal lo parts), 2^105 (exponents above 100), a wide row, and one
     scaled by 2^-110, where 2^-c overflows FP32 in the reference's
     extraction and its result is NaN (extract.py:145-148; at K = 1024 the
     2^-103 row's last slices do too); the kernel must give NaN there too.  Rows are independent, so three row ranges are
     checked against the oracle on those rows alone."""
-    N = 40000
+    N = 40000 if K <= 2048 else 80_000_000 // K
     rng = np.random.RandomState(K + (7 if precision == "high" else 11))
     A = rng.randn(N, K)
     A[3] = 0.0
@@ -585,19 +604,19 @@ def test_residual_rows_batches_and_edge_rows(ozk, K, precision):
     b[[3, 5, 100, 101, 102, N - 2]] = 0.0  # r = -Ozaki(A, x) exactly there
     case(f"residual rows N={N} K={K} {precision}")
     r = ozk.residual(A, x, b, mode="ozaki", precision=precision)
-    sel = np.r_[0:300, 16300:16400, N - 300:N]
+    sel = np.r_[0:300, N // 2:N // 2 + 100, N - 300:N]
     with np.errstate(over="ignore", invalid="ignore"):
         ref = O.residual_ozaki(A[sel], x, b[sel], precision)
     assert np.isnan(ref[-2]) and np.isfinite(ref).sum() >= len(sel) - 2
     assert np.array_equal(r[sel], ref, equal_nan=True)
 
 
-@pytest.mark.parametrize("K", [2048, 700, 4096])
+@pytest.mark.parametrize("K", [2048, 700, 4096, 9000, 20000])
 def test_residual_flags_through_c_abi(ozk, K):
     """ozk_residual clears the flag word itself, whatever it held, and sets
-    OZK_FLAG_NONFINITE for a NaN/Inf in x or in A: on the fused row path
-    (K <= 2048), where the x-slice kernel writes the word, and on the
-    slice-GEMM path (K = 4096)."""
+    OZK_FLAG_NONFINITE for a NaN/Inf in x or in A: on the fused row paths
+    (K <= 16384), where the row kernels write the word, and on the
+    slice-GEMM path (K = 20000)."""
     import torch
     from ozaki_jax_amd import _lib, _device as D
     lib = _lib.load()
