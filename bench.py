@@ -59,13 +59,14 @@ def parse_args():
     ap.add_argument("--suite", action="store_true",
                     help="instead of the metric line, time every workload "
                          "configuration (host 256, 4096 high, 8192 medium/max "
-                         "wide range, gram / residual 32768x2048, long K, "
-                         "solve) and print one JSON line each")
+                         "wide range, gram / residual 32768x2048, residual "
+                         "8192^2 and 4096^2 x 4, long K, solve) and print one "
+                         "JSON line each")
     ap.add_argument("--suite-out", default=None,
                     help="also write the suite's JSON lines to this file")
     ap.add_argument("--suite-filter", default="",
                     help="run only the suite groups whose name contains this "
-                         "text: host, 4096, 8192, gram, long, solve")
+                         "text: host, 4096, 8192, gram, residual, long, solve")
     return ap.parse_args()
 
 
@@ -243,6 +244,8 @@ def suite(args):
     A = B = None
     if want("gram"):
         suite_gram(emit, ozk, oracle, dev, sync)
+    if want("residual"):
+        suite_residual(emit, ozk, oracle, dev, sync)
     if want("long"):
         suite_long(emit, ondevice)
     if want("solve"):
@@ -276,6 +279,28 @@ def suite_gram(emit, ozk, oracle, dev, sync):
           "GB_per_s_of_A": A.nbytes / t / 1e9,
           "frac_of_hbm_peak": A.nbytes / t / 1e9 / PEAK_HBM_GBS,
           "bit_exact_vs_oracle": bool(np.array_equal(r, oracle.residual_ozaki(A, x, b)))})
+
+
+def suite_residual(emit, ozk, oracle, dev, sync):
+    import torch
+    # residual rows longer than one wave holds (split-row kernel) and several
+    # right-hand sides, N(0,1); sampled rows checked (rows are independent)
+    for n, nc in ((8192, 1), (4096, 4)):
+        rs = np.random.RandomState(5)
+        A = rs.randn(n, n)
+        x, b = rs.randn(n, nc), rs.randn(n, nc)
+        At = torch.from_numpy(A).to(dev)
+        xt, bt = torch.from_numpy(x).to(dev), torch.from_numpy(b).to(dev)
+        log(f"suite: residual {n}x{n}, {nc} right-hand side(s)")
+        t = _timeit(lambda: ozk.residual(At, xt, bt, mode="ozaki"), 10, sync)
+        r = ozk.residual(At, xt, bt, mode="ozaki").cpu().numpy()
+        rows = np.array([0, n // 2, n - 1])
+        emit({"config": f"residual ozaki high {n}x{n} N(0,1), {nc} right-hand side(s)",
+              "ms": t * 1e3, "GB_per_s_of_A": A.nbytes * nc / t / 1e9,
+              "frac_of_hbm_peak": A.nbytes * nc / t / 1e9 / PEAK_HBM_GBS,
+              "bit_exact_vs_oracle": bool(np.array_equal(
+                  r[rows], oracle.residual_ozaki(A[rows], x, b[rows])))})
+        del At, xt, bt
 
 
 def suite_long(emit, ondevice):
