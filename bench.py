@@ -59,14 +59,15 @@ def parse_args():
     ap.add_argument("--suite", action="store_true",
                     help="instead of the metric line, time every workload "
                          "configuration (host 256, 4096 high, 8192 medium/max "
-                         "wide range, gram / residual 32768x2048, residual "
-                         "8192^2 and 4096^2 x 4, long K, solve) and print one "
-                         "JSON line each")
+                         "wide range, custom schedules 8192, gram / residual "
+                         "32768x2048, residual 8192^2 and 4096^2 x 4, long K, "
+                         "solve) and print one JSON line each")
     ap.add_argument("--suite-out", default=None,
                     help="also write the suite's JSON lines to this file")
     ap.add_argument("--suite-filter", default="",
                     help="run only the suite groups whose name contains this "
-                         "text: host, 4096, 8192, gram, residual, long, solve")
+                         "text: host, 4096, 8192, custom, gram, residual, long, "
+                         "solve")
     return ap.parse_args()
 
 
@@ -209,7 +210,8 @@ def suite(args):
         ref = oracle.matmul_ondevice_a4(A[rows], B, "raise", nh, nl)
         t_dg = _timeit(lambda: torch.matmul(At, Bt), 3, sync)
         # the whole call's slice-pair rate against the MFMA peak of the plane
-        # format it runs on (INT8 for rho_32 >= 19 and a preset, else BF16)
+        # format it runs on (INT8 for rho_32 >= 19 and an all-pairs schedule,
+        # else BF16)
         i8 = _lib.load().ozk_matmul_plane_bytes(_lib.PIPE_ONDEVICE, k, nh, nl) == 1
         pairs = nh * nh + 2 * nh * nl
         d = {"config": name, "ms": t * 1e3, "fp64_eq_tflops": 2.0 * n * k * m / t / 1e12,
@@ -241,6 +243,12 @@ def suite(args):
                 d = ondevice(f"matmul ondevice fused {prec} 8192^3 wide phi_A={pa} phi_B={pb}",
                              A, B, prec, rows)
                 emit(d)
+    # custom (n_hi, n_lo) schedules at 8192^3, N(0,1): (2, 2) and (3, 2) on
+    # the all-pairs kernel (INT8 planes), (4, 2) on the pairwise kernel
+    for prec in ((2, 2), (3, 2), (4, 2)) if want("custom") else ():
+        rs = np.random.RandomState(0)
+        A, B = rs.randn(n, n), rs.randn(n, n)
+        emit(ondevice(f"matmul ondevice fused custom {prec} 8192^3 N(0,1)", A, B, prec, rows))
     A = B = None
     if want("gram"):
         suite_gram(emit, ozk, oracle, dev, sync)

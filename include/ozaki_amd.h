@@ -148,12 +148,15 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * matmul_numpy host loop (matmul.py:879-898).  A planes are rows of A
  * (N lines), B planes are columns of B (M lines); both of length K.
  * The drivers below use INT8 planes (ozk_gemm_i8) instead when the
- * contraction length gives rho >= 19 and the schedule is a preset.
+ * contraction length gives rho >= 19 and the schedule is an all-pairs one.
  *
- * The on-device presets high (4,1) and medium (3,1) run in one K sweep;
- * max (5,4) runs its hh, hl and lh blocks (matmul.py:670-674) as three
- * sweeps and keeps the fold state between them in the workspace
- * (ozk_gemm_workspace_bytes; 0 bytes for the other schedules). */
+ * All-pairs schedules: the on-device presets high (4,1) and medium (3,1),
+ * which run in one K sweep, max (5,4), which runs its hh, hl and lh blocks
+ * (matmul.py:670-674) as three sweeps and keeps the fold state between them
+ * in the workspace (ozk_gemm_workspace_bytes; 0 bytes for the other
+ * schedules), and the custom schedules (1,2), (1,3), (1,4), (2,1), (2,2),
+ * (2,3) and (3,2), which fit one sweep.  Other schedules, and the host
+ * pipeline, run one pair at a time on BF16 planes. */
 size_t ozk_gemm_workspace_bytes(int64_t N, int64_t M, int pipeline, int n_hi,
                                 int n_lo, int order);
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
@@ -166,7 +169,7 @@ int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
 /* ozk_gemm on INT8 planes (ozk_extract_f32_i8 with the same rho): INT8 MFMA
  * with exact INT32 sums; each pair product is the integer sum times
  * 2^(2 rho - 48), the FP32 product of the BF16 path whenever that one is
- * exact.  On-device preset schedules (4,1), (3,1) and (5,4). */
+ * exact.  All-pairs on-device schedules (see ozk_gemm). */
 int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
                 const int8_t* b_slices, const int32_t* b_exps,
                 int64_t N, int64_t M, int64_t K, int rho,
@@ -179,7 +182,7 @@ int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
  * double-float pair (C_hi, C_lo) of pallas_gemm_accum.py:181-186 (whose FP64
  * sum ozk_gemm writes) as two FP32 N x M arrays with leading dimension ldc.
  * plane_bytes 2: BF16 planes (ozk_extract_f32; rho is not used); 1: INT8
- * planes (ozk_extract_f32_i8 with this rho >= 19, preset schedules).
+ * planes (ozk_extract_f32_i8 with this rho >= 19, all-pairs schedules).
  * Workspace: ozk_gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, n_hi, n_lo,
  * OZK_ORDER_2SUM). */
 int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
@@ -222,8 +225,8 @@ int ozk_accumulate_2sum(const float* products, int64_t n_products,
 /* matmul(A, B, pipeline, accumulation, precision) after preflight:
  * pipeline OZK_PIPE_ONDEVICE: split + FP32 extraction with
  *   rho = ozk_rho_f32(K), n_hi/n_lo slices, order 2SUM or BLOCK64
- *   (matmul.py:641-728); INT8 planes when rho >= 19 and the schedule is a
- *   preset (OZK_PIPE_ONDEVICE_BF16 keeps BF16 planes);
+ *   (matmul.py:641-728); INT8 planes when rho >= 19 and the schedule is an
+ *   all-pairs one (ozk_gemm; OZK_PIPE_ONDEVICE_BF16 keeps BF16 planes);
  * pipeline OZK_PIPE_HOST: FP64 extraction with rho = ozk_rho_f64(K),
  *   n_hi = n_slices (n_lo ignored), order HOST_JAX or HOST_NP
  *   (matmul.py:823-851, :866-900).

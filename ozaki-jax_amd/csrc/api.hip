@@ -313,7 +313,7 @@ int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
                 (long long)N, (long long)M, (long long)K);
   OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
   if (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
-    set_error("int8 planes need rho >= 19 and a preset schedule (rho=%d, (%d, %d))",
+    set_error("int8 planes need rho >= 19 and an all-pairs schedule (rho=%d, (%d, %d))",
               rho, n_hi, n_lo);
     return OZK_ERR_UNSUPPORTED;
   }
@@ -338,7 +338,7 @@ int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
   OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
   const bool i8 = plane_bytes == 1;
   if (i8 && (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo))) {
-    set_error("int8 planes need rho >= 19 and a preset schedule (rho=%d, (%d, %d))",
+    set_error("int8 planes need rho >= 19 and an all-pairs schedule (rho=%d, (%d, %d))",
               rho, n_hi, n_lo);
     return OZK_ERR_UNSUPPORTED;
   }
@@ -377,7 +377,7 @@ int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
   OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape");
   OZK_CHECK_ARG(ldp >= M, "ldp < M");
   if (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
-    set_error("int8 planes need rho >= 19 and a preset schedule");
+    set_error("int8 planes need rho >= 19 and an all-pairs schedule");
     return OZK_ERR_UNSUPPORTED;
   }
   if (N == 0 || M == 0) return OZK_OK;

@@ -278,7 +278,7 @@ struct AllPairsMMA {
   // j + kDepth is issued before the MFMAs of block j.  Scheduling barriers
   // keep the reads where they are.
   static constexpr int kBlocks = NA * 2, kDepth = 3;
-  static_assert(kBlocks >= kDepth + 2, "the opening fills blocks 2 .. 4");
+  static_assert(kBlocks >= kDepth + 1, "the opening fills blocks 2, 3 (and 4 when there)");
 
   __device__ __forceinline__ uint4 read_a(const uint4* buf, int j) const {
     return buf[((j >> 1) * 4 + 2 * wr + (j & 1)) * 64 + fl];
@@ -330,7 +330,7 @@ struct AllPairsMMA {
       if constexpr (K == kA0 - 2) af[2] = read_a(buf, 2);
       if constexpr (K == kA0 - 1) af[3] = read_a(buf, 3);
       acc[k][0] = Op::mma(af[0], bf[b], acc[k][0]);
-      if constexpr (K == kA0 - 1) af[0] = read_a(buf, 4);
+      if constexpr (K == kA0 - 1 && kBlocks > 4) af[0] = read_a(buf, 4);
       acc[k][1] = Op::mma(af[1], bf[b], acc[k][1]);
       __builtin_amdgcn_sched_barrier(0);
       opening<K + 1>(buf, af, bf);
@@ -865,17 +865,43 @@ __global__ void probe_mfma16_kernel(int32_t* out) {
 
 // Schedules with an all-pairs instantiation: high (4,1) and medium (3,1)
 // in one sweep, max (5,4) in three (hh, hl, lh; at most 25 pairs and 10
-// planes each).
+// planes each), the custom schedules that fit one sweep (at most 10 planes,
+// n_hi + n_lo <= 5, and 21 pairs), and (4,2) and (3,3) in two (hh + hl,
+// then lh).  Custom schedules take the on-device orders only (2Sum, FP64
+// block, and the pair and per-product forms).
+constexpr bool allpairs_two_sweeps(int nhi, int nlo) {
+  return (nhi == 4 && nlo == 2) || (nhi == 3 && nlo == 3);
+}
+
+constexpr bool allpairs_preset(int nhi, int nlo) {
+  return (nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1) || (nhi == 5 && nlo == 4);
+}
+
+// Orders the all-pairs kernel runs for schedule (nhi, nlo): every order for
+// the presets, the on-device ones for the custom schedules.
+static bool allpairs_order(int nhi, int nlo, int order) {
+  return allpairs_preset(nhi, nlo) ||
+         (order != OZK_ORDER_HOST_JAX && order != OZK_ORDER_HOST_NP);
+}
+
+static bool allpairs_custom(int nhi, int nlo) {
+  return (nhi == 1 && nlo >= 1 && nlo <= 4) || (nhi == 2 && nlo >= 1 && nlo <= 3) ||
+         (nhi == 3 && nlo == 2) || allpairs_two_sweeps(nhi, nlo);
+}
+
 static bool allpairs_schedule(int pipe, int nhi, int nlo) {
   return pipe == OZK_PIPE_ONDEVICE &&
-         ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1) || (nhi == 5 && nlo == 4));
+         ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1) || (nhi == 5 && nlo == 4) ||
+          allpairs_custom(nhi, nlo));
 }
 
 bool allpairs_supported(int pipe, int nhi, int nlo) {
   return allpairs_schedule(pipe, nhi, nlo);
 }
 
-static int allpairs_sweeps(int nhi, int nlo) { return nhi == 5 && nlo == 4 ? 3 : 1; }
+static int allpairs_sweeps(int nhi, int nlo) {
+  return nhi == 5 && nlo == 4 ? 3 : (allpairs_two_sweeps(nhi, nlo) ? 2 : 1);
+}
 
 static int fold_state_bytes(int order) {
   return order == OZK_ORDER_2SUM ? FoldState<OZK_ORDER_2SUM>::kBytes
@@ -884,8 +910,8 @@ static int fold_state_bytes(int order) {
 
 size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
                             int order) {
-  if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(nhi, nlo) == 1 ||
-      order < 0)
+  if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(nhi, nlo, order) ||
+      allpairs_sweeps(nhi, nlo) == 1 || order < 0)
     return 0;
   return (size_t)N * (size_t)M * (size_t)fold_state_bytes(order);
 }
@@ -979,6 +1005,9 @@ static void launch_schedule(const ApArgs& a) {
     launch_sweep<Op, NHI, NLO, ORDER, 0, 0>(a);
     launch_sweep<Op, NHI, NLO, ORDER, 1, 1>(a);
     launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
+  } else if constexpr (allpairs_two_sweeps(NHI, NLO)) {
+    launch_sweep<Op, NHI, NLO, ORDER, 0, 1>(a);
+    launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
   } else {
     launch_sweep<Op, NHI, NLO, ORDER, 0, 2>(a);
   }
@@ -988,7 +1017,7 @@ template <class Op, int NHI, int NLO>
 static void launch_ap_order(int order, const ApArgs& a) {
   switch (order) {
     case OZK_ORDER_2SUM:
-      if constexpr (NLO == 1) {  // single-sweep presets: symmetric form available
+      if constexpr (NLO == 1 && NHI >= 3) {  // high, medium: symmetric form available
         if (a.sym) {
           launch_sweep<Op, NHI, NLO, OZK_ORDER_2SUM, 0, 2, true>(a);
           break;
@@ -997,14 +1026,20 @@ static void launch_ap_order(int order, const ApArgs& a) {
       launch_schedule<Op, NHI, NLO, OZK_ORDER_2SUM>(a);
       break;
     case OZK_ORDER_BLOCK64: launch_schedule<Op, NHI, NLO, OZK_ORDER_BLOCK64>(a); break;
-    case OZK_ORDER_HOST_JAX: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a); break;
-    case OZK_ORDER_HOST_NP: launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a); break;
+    case OZK_ORDER_HOST_JAX:  // presets only (allpairs_order)
+      if constexpr (allpairs_preset(NHI, NLO))
+        launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a);
+      break;
+    case OZK_ORDER_HOST_NP:
+      if constexpr (allpairs_preset(NHI, NLO))
+        launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a);
+      break;
     case kOrderPair: launch_schedule<Op, NHI, NLO, kOrderPair>(a); break;
     default: launch_schedule<Op, NHI, NLO, kOrderProducts>(a); break;
   }
 }
 
-// All-pairs launch for a preset schedule; `i8` selects the INT8 plane
+// All-pairs launch for an all-pairs schedule; `i8` selects the INT8 plane
 // format (rho >= 19).  order = kOrderProducts writes P.  `state` holds
 // gemm_workspace_bytes() for multi-sweep schedules; a single-sweep schedule
 // splits its tail along K when `state` also holds gemm_tail_bytes().
@@ -1059,11 +1094,21 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.P = P;
   a.ldp = ldp;
   a.state = (char*)state;
-#define OZK_AP_ALL(Op)                                       \
-  do {                                                       \
-    if (nhi == 4) launch_ap_order<Op, 4, 1>(order, a);       \
-    else if (nhi == 3) launch_ap_order<Op, 3, 1>(order, a);  \
-    else launch_ap_order<Op, 5, 4>(order, a);                \
+#define OZK_AP_ALL(Op)                                                    \
+  do {                                                                    \
+    if (nhi == 4 && nlo == 1) launch_ap_order<Op, 4, 1>(order, a);        \
+    else if (nhi == 3 && nlo == 1) launch_ap_order<Op, 3, 1>(order, a);   \
+    else if (nhi == 5 && nlo == 4) launch_ap_order<Op, 5, 4>(order, a);   \
+    else if (nhi == 1 && nlo == 1) launch_ap_order<Op, 1, 1>(order, a);   \
+    else if (nhi == 1 && nlo == 2) launch_ap_order<Op, 1, 2>(order, a);   \
+    else if (nhi == 1 && nlo == 3) launch_ap_order<Op, 1, 3>(order, a);   \
+    else if (nhi == 1 && nlo == 4) launch_ap_order<Op, 1, 4>(order, a);   \
+    else if (nhi == 2 && nlo == 1) launch_ap_order<Op, 2, 1>(order, a);   \
+    else if (nhi == 2 && nlo == 2) launch_ap_order<Op, 2, 2>(order, a);   \
+    else if (nhi == 2 && nlo == 3) launch_ap_order<Op, 2, 3>(order, a);   \
+    else if (nhi == 3 && nlo == 2) launch_ap_order<Op, 3, 2>(order, a);   \
+    else if (nhi == 4 && nlo == 2) launch_ap_order<Op, 4, 2>(order, a);   \
+    else launch_ap_order<Op, 3, 3>(order, a);                             \
   } while (0)
   if (i8) OZK_AP_ALL(OpI8);
   else OZK_AP_ALL(OpBf16);
@@ -1092,11 +1137,11 @@ int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
                 void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho) {
-  if (allpairs_schedule(pipe, nhi, nlo))
+  if (allpairs_schedule(pipe, nhi, nlo) && allpairs_order(nhi, nlo, order))
     return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, order,
                            C, ldc, nullptr, 0, ws, ws_bytes, st);
   if (i8) {
-    set_error("int8 slice planes need a preset on-device schedule");
+    set_error("int8 slice planes need an all-pairs on-device schedule");
     return OZK_ERR_UNSUPPORTED;
   }
   const int64_t ld = round_up(K, kKPad);
@@ -1131,7 +1176,7 @@ int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
     return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, kOrderPair,
                            (double*)C_lo, ldc, C_hi, ldc, ws, ws_bytes, st);
   if (i8) {
-    set_error("int8 slice planes need a preset on-device schedule");
+    set_error("int8 slice planes need an all-pairs on-device schedule");
     return OZK_ERR_UNSUPPORTED;
   }
   const int64_t ld = round_up(K, kKPad);
@@ -1145,8 +1190,8 @@ int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
   return OZK_OK;
 }
 
-// Per-pair products.  Preset schedules run the all-pairs kernel (the one the
-// drivers use); other schedules (BF16 only) the pairwise kernel.
+// Per-pair products.  All-pairs schedules run the all-pairs kernel (the one
+// the drivers use); other schedules (BF16 only) the pairwise kernel.
 int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho) {
@@ -1154,7 +1199,7 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
     return launch_allpairs(i8, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
                            kOrderProducts, nullptr, 0, P, ldp, nullptr, 0, st);
   if (i8) {
-    set_error("int8 slice planes need a preset on-device schedule");
+    set_error("int8 slice planes need an all-pairs on-device schedule");
     return OZK_ERR_UNSUPPORTED;
   }
   const int64_t ld = round_up(K, kKPad);

@@ -108,17 +108,20 @@ def test_gemm_workspace_bytes(lib):
 
 def test_int8_entry_points_reject_before_device_work(lib):
     from ozaki_jax_amd import _lib
-    # INT8 planes need rho >= 19 (|q| <= 64) and a preset schedule
+    # INT8 planes need rho >= 19 (|q| <= 64) and an all-pairs schedule: the
+    # presets and the custom schedules (1,1)-(1,4), (2,1)-(2,3), (3,2), (3,3)
+    # and (4,2); others, such as (5,1), (2,4) and (4,4), run on BF16 planes
     rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, 18, 4, 1, None, None, None, None, 0, None)
     assert rc == _lib.OZK_ERR_UNSUPPORTED and b"rho >= 19" in lib.ozk_last_error()
     rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 18, 4, 1, 0, None, 4,
                          None, 0, None)
     assert rc == _lib.OZK_ERR_UNSUPPORTED
-    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 2, 3, 0, None, 4,
-                         None, 0, None)
-    assert rc == _lib.OZK_ERR_UNSUPPORTED
-    rc = lib.ozk_slice_products_i8(None, None, 4, 4, 8192, 19, 2, 3, None, 4, None)
-    assert rc == _lib.OZK_ERR_UNSUPPORTED
+    for nh, nl in ((5, 1), (2, 4), (4, 4)):
+        rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, nh, nl, 0, None, 4,
+                             None, 0, None)
+        assert rc == _lib.OZK_ERR_UNSUPPORTED and b"all-pairs" in lib.ozk_last_error()
+        rc = lib.ozk_slice_products_i8(None, None, 4, 4, 8192, 19, nh, nl, None, 4, None)
+        assert rc == _lib.OZK_ERR_UNSUPPORTED
     rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4,
                          None, 0, None)
     assert rc == _lib.OZK_ERR_INVALID

@@ -25,10 +25,11 @@ def _oracle_pair(A, B, rho, nh, nl):
     return (a, ae, b, be), OP.accumulate_a4(OP.slice_products(a, b, sched), sched, ae, be)
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 3)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 3), (4, 2), (5, 1)])
 def test_fused_gemm_accum_pair(ozk, nh, nl):
     """Caller-held slices (the oracle's) through the NumPy family: all-pairs
-    kernel for the presets, pairwise kernel for (2, 3)."""
+    kernel for the presets, (2, 3) (one sweep) and (4, 2) (two sweeps; the
+    fold state crosses the workspace), pairwise kernel for (5, 1)."""
     from ozaki_jax_amd.pallas_gemm_accum import fused_gemm_accum
     rng = np.random.RandomState(nh * 10 + nl)
     A = (rng.rand(96, 200) - 0.5) * np.exp(2 * rng.randn(96, 200))
@@ -43,14 +44,14 @@ def test_fused_gemm_accum_pair(ozk, nh, nl):
                           O.matmul_ondevice_a4(A, B, "raise", nh, nl))
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (5, 4)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (5, 4), (4, 2)])
 def test_gemm_pair_int8_planes(ozk, nh, nl):
     """INT8 planes (K = 5000 and 4200, rho = 19), 16 and 324 tiles."""
     import torch
     from ozaki_jax_amd import lowlevel as ll
     rng = np.random.RandomState(nh)
     for N, K, M in [(70, 5000, 60), (1100, 4200, 1100)]:
-        if nl == 4 and N > 100:
+        if nl > 1 and N > 100:
             continue
         A, B = rng.randn(N, K), (rng.rand(K, M) - 0.5) * np.exp(2 * rng.randn(K, M))
         rho = O.rho_f32(K)

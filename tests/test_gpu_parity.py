@@ -230,8 +230,11 @@ def test_extract_i8_rejects_coarse_grid(ll):
 
 # ---------------------------------------------------------------- products
 
+# (2, 3), (1, 2), (2, 1), (1, 1): one-sweep custom schedules on the
+# all-pairs kernel; (4, 2): two sweeps of it; (5, 1): the pairwise kernel
 SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
-             ("ondevice", 2, 3), ("host", 8, 0)]
+             ("ondevice", 2, 3), ("ondevice", 1, 2), ("ondevice", 2, 1),
+             ("ondevice", 1, 1), ("ondevice", 4, 2), ("ondevice", 5, 1), ("host", 8, 0)]
 
 
 def _slices(ll, A, B, pipe, nh, nl):
@@ -281,7 +284,8 @@ def _slices_i8(ll, A, B, nh, nl, rho_fixed):
     return a, b, O.ondevice_slices(A, B, rho, nh, nl), O.ondevice_schedule(nh, nl), rho
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 2), (1, 4), (3, 2), (1, 1), (4, 2),
+                                   (3, 3)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
@@ -294,7 +298,8 @@ def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
     assert np.array_equal(P, O.slice_products(oa, ob, sched))
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 2), (1, 4), (3, 2), (1, 1), (4, 2),
+                                   (3, 3)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_gemm_i8_orders_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
@@ -333,7 +338,8 @@ def test_gemm_orders_bit_exact(ll, pipe, nh, nl, shape):
 
 # ---------------------------------------------------------------- public API
 
-@pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (2, 2)])
+@pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (2, 2), (1, 1), (1, 2),
+                                       (1, 4), (2, 1), (2, 3), (3, 2), (3, 3), (5, 1)])
 @pytest.mark.parametrize("accumulation", ["fused", "bf16_interleaved", "ondevice", "host"])
 def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
     A, B = gen("randn", (150, 300), 21), gen("randn", (300, 90), 22)
@@ -350,9 +356,12 @@ def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
     assert np.all(np.abs(C - ref) <= 2.0 ** -51 * (np.abs(A) @ np.abs(B)))
 
 
-@pytest.mark.parametrize("precision", ["high", "medium", "max"])
+@pytest.mark.parametrize("precision", ["high", "medium", "max", (1, 1), (1, 2), (1, 3), (2, 1),
+                                       (2, 2), (2, 3), (3, 2), (3, 3), (4, 2), (5, 1)])
 def test_matmul_long_contraction_bit_exact(ozk, precision):
-    # K > 4096: rho >= 19, the presets run on INT8 planes
+    # K > 4096: rho >= 19, the presets and the custom schedules of the
+    # all-pairs kernel run on INT8 planes ((4, 2) and (3, 3) in two sweeps);
+    # (5, 1) on BF16 planes in the pairwise kernel
     A, B = gen("randn", (40, 6000), 23), gen("wide2", (6000, 70), 24)
     nh, nl = OP.resolve_precision(precision)
     for acc, ref in [("fused", lambda: O.matmul_ondevice_a4(A, B, "raise", nh, nl)),
