@@ -47,6 +47,7 @@ extern "C" {
 #define OZK_FLAG_NONFINITE 1u
 #define OZK_FLAG_WAIT_TIMEOUT 2u /* a bounded wait between workgroups gave up (column
                                    extraction, ozk_lu_solve_f32): results not valid */
+
 #define OZK_FLAG_SINGULAR 4u     /* ozk_lu_factor_f32: a zero pivot */
 /* INT8 planes: a slice line overflowed with 2^-c > FLT_MAX (see
  * OZK_EXP_NONFINITE).  The reference's slice then holds +-inf (and NaN where
@@ -65,6 +66,14 @@ extern "C" {
  * are stored as zeros with this exponent, and the slice GEMM folds each pair
  * product with it as NaN. */
 #define OZK_EXP_NONFINITE (-2147483647 - 1)
+
+/* Test hook, no counterpart in the reference: the poll limit of every
+ * bounded wait between workgroups (column extraction, ozk_lu_solve_f32) for
+ * the kernels launched after the call; 0 restores the built-in limits.  A
+ * tiny limit makes those waits give up, so that a test can check
+ * OZK_FLAG_WAIT_TIMEOUT and the callers' handling of it while every kernel
+ * still exits normally. */
+void ozk_set_wait_polls(uint32_t polls);
 
 /* Accumulation orders (the four orders of the reference). */
 #define OZK_ORDER_2SUM 0     /* A4: pallas_ops.py:178-239 == matmul.py:382-488 */

@@ -50,6 +50,7 @@ _c_vp = ctypes.c_void_p
 SIGNATURES = {
     "ozk_last_error": (ctypes.c_char_p, []),
     "ozk_abi_version": (_c_int, []),
+    "ozk_set_wait_polls": (None, [ctypes.c_uint32]),
     "ozk_device_info": (_c_int, [ctypes.c_char_p, _c_size, ctypes.POINTER(_c_int)]),
     "ozk_rho_f64": (_c_int, [_c_i64]),
     "ozk_rho_f32": (_c_int, [_c_i64]),

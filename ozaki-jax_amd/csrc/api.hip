@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <atomic>
+
 #include "common.h"
 
 namespace ozk {
@@ -31,6 +33,13 @@ int cu_count() {
     cus = 256;
   if (dev >= 0 && dev < 64) cache[dev] = cus;
   return cus;
+}
+
+static std::atomic<uint32_t> g_wait_polls{0};
+
+uint32_t wait_polls(uint32_t dflt) {
+  const uint32_t v = g_wait_polls.load(std::memory_order_relaxed);
+  return v ? v : dflt;
 }
 
 // Implemented in extract.hip / gemm.hip.
@@ -185,6 +194,10 @@ extern "C" {
 const char* ozk_last_error(void) { return g_error.c_str(); }
 
 int ozk_abi_version(void) { return 2; }
+
+void ozk_set_wait_polls(uint32_t polls) {
+  ozk::g_wait_polls.store(polls, std::memory_order_relaxed);
+}
 
 int ozk_device_info(char* buf, size_t len, int* cu_count) {
   clear_error();

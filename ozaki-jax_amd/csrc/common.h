@@ -56,6 +56,10 @@ void clear_error();
 // query fails).  Persistent kernels size their grids with it.
 int cu_count();
 
+// Poll limit of the kernels' bounded waits between workgroups: `dflt`, or
+// the limit a test set with ozk_set_wait_polls.
+uint32_t wait_polls(uint32_t dflt);
+
 // ---------------------------------------------------------------- layout
 // Slice planes hold BF16 bit patterns or INT8 grid counts with lines padded
 // to kLinePad and k padded to kKPad elements; padding holds zeros, so the

@@ -474,15 +474,16 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
 // starts, so all members of the gangs before the first incomplete one have
 // started, and those gangs finish; the incomplete gang's remaining members
 // then need only free slots (G <= kGangMaxMembers workgroups resident at
-// once).  Every wait is bounded all the same: after kGangSpin polls it sets
-// OZK_FLAG_WAIT_TIMEOUT (the slices are then not valid) and the member waits
-// no more in later slices.
+// once).  Every wait is bounded all the same: after kGangSpin polls (or the
+// limit a test set with ozk_set_wait_polls) it sets OZK_FLAG_WAIT_TIMEOUT
+// (the slices are then not valid) and the member waits no more in later
+// slices.
 constexpr int kGangPW = 16;
 constexpr int kGangRowsPT = 8;
 constexpr int kGangThreads = 512;
 constexpr int kGangRun = kGangThreads / (kGangPW / 2) * kGangRowsPT;  // 512 rows
 constexpr int kGangMaxMembers = 16;
-constexpr int kGangSpin = 1 << 18;
+constexpr uint32_t kGangSpin = 1u << 18;
 constexpr int kGangKeys = 2 * kGangPW;  // keys per record line
 constexpr int64_t kGangLine = 128;      // bytes per record line
 constexpr int64_t kGangHeader = 256;    // the ticket word, padded
@@ -501,9 +502,10 @@ __device__ __forceinline__ float key_max(uint32_t k) {
   return k == 1u ? __builtin_nanf("") : __uint_as_float(k - 2u);
 }
 
-// Bounded wait for a nonzero word; 0 after kGangSpin polls (and the flag).
-__device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags) {
-  for (int spin = 0; spin < kGangSpin; ++spin) {
+// Bounded wait for a nonzero word; 0 after `polls` polls (and the flag).
+__device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
+                                             uint32_t polls) {
+  for (uint32_t spin = 0; spin < polls; ++spin) {
     const uint32_t k = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (k) return k;
     __builtin_amdgcn_s_sleep(1);
@@ -517,7 +519,7 @@ __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
     const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
-    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G) {
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls) {
   typedef typename PlaneElem<FMT>::type T;
   constexpr int NP = 2, CP = kGangPW / 2, NW = kGangThreads / 64, R = kGangRowsPT;
   constexpr int NG = kGangThreads / kGangKeys;  // key groups of a workgroup
@@ -616,7 +618,7 @@ __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
       uint32_t k = 0u;
       if (!gave_up) {
         for (int mb = t / kGangKeys; mb < G; mb += NG) {
-          const uint32_t km = wait_key(rs + mb * kWords + t % kGangKeys, flags);
+          const uint32_t km = wait_key(rs + mb * kWords + t % kGangKeys, flags, polls);
           if (!km) gave_up = 1;
           k = max(k, km);
         }
@@ -839,14 +841,15 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
   uint32_t* ticket = (uint32_t*)ws;
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
   const dim3 grid((unsigned)(npanels * G));
+  const uint32_t polls = wait_polls(kGangSpin);
   if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
     hipLaunchKernelGGL((extract_cols_gang<FMT, true>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G);
+                       ticket, G, polls);
   else
     hipLaunchKernelGGL((extract_cols_gang<FMT, false>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G);
+                       ticket, G, polls);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }

@@ -41,14 +41,16 @@ constexpr uint32_t kTsTag = 1u;
 // publishes the block's solution (and writes x going backward).
 // Dependencies point only to blocks a workgroup reaches earlier, so with all
 // G workgroups resident every wait ends; a wait that still exceeds
-// kTsSpinLimit polls (or sees another one fail) sets OZK_FLAG_WAIT_TIMEOUT
+// spin_limit polls (kTsSpinLimit unless a test set another limit with
+// ozk_set_wait_polls), or sees another one fail, sets OZK_FLAG_WAIT_TIMEOUT
 // and stops waiting, so that every wave exits.
 template <bool UPPER>
 __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
     const float* __restrict__ LU, int64_t n, int64_t lda, int vec,
     const int32_t* __restrict__ perm, const double* __restrict__ B, int64_t ldb,
     const uint64_t* __restrict__ win, uint64_t* __restrict__ wout, int64_t ldw,
-    double* __restrict__ X, int64_t ldx, int64_t c0, uint32_t* __restrict__ status) {
+    double* __restrict__ X, int64_t ldx, int64_t c0, uint32_t* __restrict__ status,
+    uint32_t spin_limit) {
   const int nb = (int)((n + kTsRows - 1) / kTsRows);
   const int64_t col = c0 + blockIdx.y;
   __shared__ float part[kTsWaves][kTsRows];
@@ -127,7 +129,7 @@ __global__ __launch_bounds__(kTsThreads) void lu_trsv_kernel(
         if (__all(ready)) break;
         if (__hip_atomic_load(status, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) &
                 OZK_FLAG_WAIT_TIMEOUT ||
-            ++spins > kTsSpinLimit) {
+            ++spins > spin_limit) {
           failed = true;
           break;
         }
@@ -231,13 +233,16 @@ int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n
   hipLaunchKernelGGL(fill_u64_array_kernel, dim3((unsigned)(fb < 4096 ? fb : 4096)), dim3(256), 0,
                      st, wf, words, (uint64_t)0);
   OZK_LAUNCH_CHECK();
+  const uint32_t spin_limit = wait_polls(kTsSpinLimit);
   for (int64_t c0 = 0; c0 < ncols; c0 += chunk) {
     const int64_t nc = ncols - c0 < chunk ? ncols - c0 : chunk;
     hipLaunchKernelGGL(lu_trsv_kernel<false>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,
-                       LU, n, lda, vec, perm, B, ldb, nullptr, wf, ncols, X, ldx, c0, status);
+                       LU, n, lda, vec, perm, B, ldb, nullptr, wf, ncols, X, ldx, c0, status,
+                       spin_limit);
     OZK_LAUNCH_CHECK();
     hipLaunchKernelGGL(lu_trsv_kernel<true>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,
-                       LU, n, lda, vec, perm, B, ldb, wf, wb, ncols, X, ldx, c0, status);
+                       LU, n, lda, vec, perm, B, ldb, wf, wb, ncols, X, ldx, c0, status,
+                       spin_limit);
     OZK_LAUNCH_CHECK();
   }
   return OZK_OK;

@@ -1,0 +1,94 @@
+"""Bounded waits between workgroups, made to give up from the host.
+
+ozk_set_wait_polls(1) limits every wait of the kernels launched afterwards
+to one poll: the gangs of the column extraction (a member that gives up sets
+OZK_FLAG_WAIT_TIMEOUT and waits no more, so every kernel still exits) and
+the row-block chains of the LU triangular solves.  The package raises on the
+flag after an extraction (matmul, gram, residual, lowlevel.extract); solve()
+redoes a triangular solve that gave up on torch.linalg's path.  After
+ozk_set_wait_polls(0) the same calls are exact again, so nothing stale is
+left behind.
+"""
+
+import sys
+
+import numpy as np
+import pytest
+
+import oracle as O
+
+pytestmark = pytest.mark.gpu
+
+
+def case(msg):
+    print(f"[case] {msg}", flush=True)
+    sys.stdout.flush()
+
+
+@pytest.fixture
+def set_polls(ozk):
+    from ozaki_jax_amd import _lib
+    lib = _lib.load()
+    yield lib.ozk_set_wait_polls
+    lib.ozk_set_wait_polls(0)
+
+
+def test_column_extraction_gives_up_then_recovers(ozk, set_polls):
+    from ozaki_jax_amd import lowlevel as ll
+    rng = np.random.RandomState(3)
+    X = rng.randn(8192, 512)  # 32 panels, gangs of 16 workgroups
+    rho = O.rho_f32(8192)
+    set_polls(1)
+    case("ozk_extract_f32_i8 by columns (8192, 512), one poll per wait")
+    with pytest.raises(RuntimeError, match="OZK_FLAG_WAIT_TIMEOUT"):
+        ll.extract(X, 1, rho, 4, 1, i8=True)
+    case("matmul 64 x 8192 x 512, one poll per wait")
+    with pytest.raises(RuntimeError, match="OZK_FLAG_WAIT_TIMEOUT"):
+        ozk.matmul(rng.randn(64, 8192), X, pipeline="ondevice")
+    set_polls(0)
+    case("ozk_extract_f32_i8 by columns (8192, 512), built-in limit")
+    pl = ll.extract(X, 1, rho, 4, 1, i8=True)
+    cols = np.r_[0:20, 500:512]
+    hi, lo = O.split_hi_lo(X[:, cols])
+    sh, eh = O.extract_cols_f32(hi, rho, 4)
+    sl, el = O.extract_cols_f32(lo, rho, 1)
+    ref = np.concatenate([sh, sl]).transpose(0, 2, 1) * 2.0 ** (24 - rho)
+    assert np.array_equal(pl.grid().cpu().numpy()[:, cols, :8192], ref.astype(np.int8))
+    assert np.array_equal(pl.exponents().cpu().numpy()[:, cols],
+                          np.concatenate([eh, el]).astype(np.int32))
+
+
+def test_lu_solve_gives_up_and_solve_falls_back(ozk, set_polls):
+    import importlib
+
+    import torch
+    from ozaki_jax_amd import _device as D, _lib
+    S = importlib.import_module("ozaki_jax_amd.solve")  # the module, not solve()
+    n = 2100
+    rng = np.random.RandomState(5)
+    A = rng.randn(n, n) + n * np.eye(n)
+    b = rng.randn(n)
+    dev = torch.device("cuda", 0)
+    At = torch.from_numpy(A).to(dev)
+    LU, perm = S.lu_factor_f32(At, dev)
+    rhs = torch.from_numpy(b[:, None].copy()).to(dev)
+    set_polls(1)
+    case(f"ozk_lu_solve_f32 n={n}, one poll per wait")
+    _, flags = S.lu_solve_f32(LU, perm, rhs, dev)
+    assert D.read_flags(flags) & _lib.OZK_FLAG_WAIT_TIMEOUT
+    # the bounds of the solve tests: FP64 residuals reach FP64 accuracy, the
+    # Ozaki residual (high, K = 2100) bounds the refinement near 1e-8
+    case(f"solve n={n} with the triangular solves giving up")
+    xr = np.linalg.solve(A, b)
+    x = ozk.solve(A, b)
+    assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-12
+    x = ozk.solve(A, b, residual_mode="ozaki")
+    assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-5
+    set_polls(0)
+    case(f"ozk_lu_solve_f32 n={n}, built-in limit")
+    d, flags = S.lu_solve_f32(LU, perm, rhs, dev)
+    assert not D.read_flags(flags) & _lib.OZK_FLAG_WAIT_TIMEOUT
+    d32 = torch.linalg.solve_triangular(
+        LU, torch.linalg.solve_triangular(LU, rhs.to(torch.float32)[perm.long()], upper=False,
+                                          unitriangular=True), upper=True)
+    assert np.allclose(d.cpu().numpy(), d32.cpu().numpy(), rtol=1e-4, atol=1e-6)
