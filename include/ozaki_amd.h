@@ -114,8 +114,11 @@ int64_t ozk_slice_lines(int64_t lines);
  * by groups of workgroups that exchange their per-slice column maxima through
  * the workspace (a bounded wait that gives up sets OZK_FLAG_WAIT_TIMEOUT in
  * flags: the planes are then not valid); longer columns are transposed
- * through the workspace.  ozk_extract_workspace_bytes covers both this and
- * ozk_extract_f64 (whose columns are always transposed).
+ * through the workspace.  Lines of 32769 to 262144 elements (rows, or the
+ * transposed columns) are likewise held by groups of workgroups exchanging
+ * their line maxima through the workspace, so row extraction needs one too.
+ * ozk_extract_workspace_bytes covers both this and ozk_extract_f64 (whose
+ * columns are always transposed).
  * Output planes: n_hi + n_lo. */
 size_t ozk_extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols);
 int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,

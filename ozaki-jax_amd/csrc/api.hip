@@ -407,6 +407,15 @@ static int matmul_pipe(int pipeline, int64_t K, int nhi, int nlo, bool* i8) {
   return pipe;
 }
 
+// Extraction workspace of the rows of A (N x K) and the columns of B
+// (K x M), extracted one after the other on one stream: one buffer serves
+// both.
+static size_t extract_pair_bytes(int64_t N, int64_t K, int64_t M, bool f64) {
+  const size_t a = extract_workspace_bytes(N, K, 0, f64);
+  const size_t b = extract_workspace_bytes(K, M, 1, f64);
+  return a > b ? a : b;
+}
+
 static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
                         int nlo, bool carve, void* ws, SliceSet* a,
                         SliceSet* b, void** tws, void** gws = nullptr,
@@ -418,7 +427,7 @@ static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
   Carver c(carve ? ws : nullptr);
   SliceSet sa = carve_slices(c, planes, N, K, eb);
   SliceSet sb = carve_slices(c, planes, M, K, eb);
-  void* t = c.take(extract_workspace_bytes(K, M, 1, pipeline != OZK_PIPE_ONDEVICE));
+  void* t = c.take(extract_pair_bytes(N, K, M, pipeline != OZK_PIPE_ONDEVICE));
   // fold state between sweeps (the 2Sum state bounds every order's), then
   // the partial sums of a K-split tail
   const size_t gb = round_up(gemm_workspace_bytes(N, M, pipeline, nhi, nlo, OZK_ORDER_2SUM),
@@ -479,12 +488,12 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   size_t gwsb;
   matmul_ws(N, K, M, pipe_arg, n_hi, n_lo, true, workspace, &sa, &sb, &tws, &gws,
             &gwsb);
-  const size_t tbytes = extract_workspace_bytes(K, M, 1, pipeline != OZK_PIPE_ONDEVICE);
+  const size_t tbytes = extract_pair_bytes(N, K, M, pipeline != OZK_PIPE_ONDEVICE);
   int rho;
   if (pipeline == OZK_PIPE_ONDEVICE) {
     rho = rho_generic(K, 24);
     if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                             nullptr, 0, st, i8)))
+                             tws, tbytes, st, i8)))
       return rc;
     if ((rc = extract<float>(B, K, M, ldb, 1, rho, n_hi, n_lo, sb.s, sb.e, flags,
                              tws, tbytes, st, i8)))
@@ -492,7 +501,7 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   } else {
     rho = rho_generic(K, 53);
     if ((rc = extract<double>(A, N, K, lda, 0, rho, n_hi, 0, sa.s, sa.e, flags,
-                              nullptr, 0, st, false)))
+                              tws, tbytes, st, false)))
       return rc;
     if ((rc = extract<double>(B, K, M, ldb, 1, rho, n_hi, 0, sb.s, sb.e, flags,
                               tws, tbytes, st, false)))
@@ -574,10 +583,10 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
   return OZK_OK;
 }
 
-// Residual workspace.  One right-hand side with K <= 2048 (presets high and
-// medium) takes the fused row kernel, which needs none; otherwise A and x are
-// extracted to planes for the slice GEMM, whose FP64 product y is subtracted
-// from b afterwards.
+// Residual workspace.  Up to 4 right-hand sides with K <= 16384 (presets
+// high and medium) take the fused row kernels, which need none; otherwise A
+// and x are extracted to planes for the slice GEMM, whose FP64 product y is
+// subtracted from b afterwards.
 static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
                           int nlo, void* ws, SliceSet* a, SliceSet* x,
                           double** y, void** tws, void** gws = nullptr,
@@ -588,7 +597,7 @@ static size_t residual_ws(int64_t N, int64_t K, int64_t ncols, int nhi,
   SliceSet sa = carve_slices(c, nhi + nlo, N, K, eb);
   SliceSet sx = carve_slices(c, nhi + nlo, ncols, K, eb);
   double* yy = (double*)c.take((size_t)N * ncols * sizeof(double));
-  void* t = c.take(extract_workspace_bytes(K, ncols, 1, false));
+  void* t = c.take(extract_pair_bytes(N, K, ncols, false));
   const size_t gb = gemm_workspace_bytes(N, ncols, OZK_PIPE_ONDEVICE, nhi, nlo,
                                          OZK_ORDER_2SUM);
   void* g = c.take(gb);
@@ -639,12 +648,12 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   residual_ws(N, K, ncols, n_hi, n_lo, workspace, &sa, &sx, &y, &tws, &gws, &gwsb);
   if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
+  const size_t tbytes = extract_pair_bytes(N, K, ncols, false);
   if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,
-                           flags, tws, extract_workspace_bytes(K, ncols, 1, false), st,
-                           i8)))
+                           flags, tws, tbytes, st, i8)))
     return rc;
   if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                           nullptr, 0, st, i8)))
+                           tws, tbytes, st, i8)))
     return rc;
   if ((rc = launch_gemm(sa.s, sa.e, sx.s, sx.e, N, ncols, K, OZK_PIPE_ONDEVICE,
                         n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, gws, gwsb, st, i8, rho)))

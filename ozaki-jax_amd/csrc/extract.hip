@@ -4,6 +4,9 @@
 // extraction) and keeps the whole line's residual in registers, so X is read
 // from HBM once and every slice plane is written once.  Per slice the line
 // maximum comes from a wavefront butterfly + an LDS combine across waves.
+// Lines too long for one workgroup, and columns read in place, are held by
+// gangs of workgroups that exchange their partial maxima through global
+// memory; lines longer still are streamed.
 //
 // Arithmetic per slice (reference extract.py:124-152 for FP32, :28-63 for
 // FP64; split matmul.py:204-213):
@@ -282,177 +285,6 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 }
 
-// Lines of up to BLOCK * EPT * 4 elements (65536 at BLOCK 1024, EPT 16), FP32
-// path: a line's hi and lo parts (2 x 256 KiB) stay on chip after one read.
-// Thread t owns groups j < EPT of 4 consecutive elements k = (j BLOCK + t) 4 +
-// v.  Its lo parts live in registers (L, 16 float4 at EPT 16); of its hi
-// parts, groups j < EPT_R live in registers (R) and the others in LDS (144
-// KiB at EPT - EPT_R = 9).  Round s reduces the maxima of both parts, then
-// writes hi slice s (s < n0) and lo slice s (s < n1), like extract_lines_reg.
-// VECP (line starts 16-byte aligned, len % 4 == 0) reads a group with two
-// 16-byte loads, else element by element.  Launched for ld > 32768 only, so
-// ld / 4 > t for every thread (the store count below assumes it).
-template <int BLOCK, int EPT, int EPT_R, int FMT, bool VECP>
-__global__ __launch_bounds__(BLOCK) void extract_lines_hybrid(
-    const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx, int rho,
-    int n0, int n1, typename PlaneElem<FMT>::type* __restrict__ S,
-    int64_t ld, int64_t plane, int32_t* __restrict__ E, int64_t eplane,
-    uint32_t* __restrict__ flags) {
-  constexpr int VEC = 4;
-  const float qscale = ldexpf(1.0f, 24 - rho);
-  __shared__ float red[2 * (BLOCK / 64)];
-  __shared__ float4 hl[(EPT - EPT_R) * BLOCK];  // hi parts of groups EPT_R ..
-  const int t = threadIdx.x;
-  const int64_t line = xcd_line(blockIdx.x, gridDim.x);
-  const bool live = line < lines;
-  typedef typename PlaneElem<FMT>::type T;
-  typedef typename PlaneVec<FMT, VEC>::type TV;
-  constexpr int kPer = kChunkBytes / (int)sizeof(T);
-  static_assert((BLOCK * VEC) % kPer == 0, "BLOCK * VEC must hold whole chunks");
-  const int64_t off0 = plane_offset<sizeof(T)>(line, (int64_t)t * VEC, eplane);
-  const int64_t step = (int64_t)(BLOCK * VEC / kPer) * eplane * kPer;
-
-  float4 R[EPT_R];  // hi parts of groups j < EPT_R
-  float4 L[EPT];    // lo parts of every group
-  // Groups j >= EPT_R of the hi part live in hl; every pass over the hi part
-  // runs two loops so that R is only ever indexed by unrolled constants.
-  float4* const H = hl + t;  // group j >= EPT_R at H[(j - EPT_R) * BLOCK]
-
-  // The one read: split every element into its hi and lo parts.  The loads
-  // are branch-free (an absent element reads the line's first one and is
-  // replaced by zero) and run kDepth groups ahead of the splits; the
-  // scheduling barriers keep the compiler from hoisting every load, which
-  // would hold all EPT groups' doubles in registers at once.
-  constexpr int kDepth = 3;
-  // Largest exponent field seen (0x7ff00000 marks a non-finite element); an
-  // integer in a register, so that the test needs no double kept alive.
-  uint32_t emax = 0;
-  // element indices fit 32 bits: the line is at most BLOCK * EPT * VEC long
-  const int n = live ? (int)len : 0;
-  const int ldi = (int)ld;
-  const double* const xs = X + (live ? line : 0) * ldx;
-  double buf[kDepth][VEC];
-  auto issue = [&](int j) {
-    double(&v)[VEC] = buf[j % kDepth];
-    const int k0 = (j * BLOCK + t) * VEC;
-    if (VECP) {  // len % VEC == 0: a group is whole or absent
-      const double2* const q = (const double2*)(xs + (k0 < n ? k0 : 0));
-      const double2 a = q[0], b = q[1];
-      v[0] = a.x;
-      v[1] = a.y;
-      v[2] = b.x;
-      v[3] = b.y;
-    } else {
-#pragma unroll
-      for (int u = 0; u < VEC; ++u) v[u] = xs[k0 + u < n ? k0 + u : 0];
-    }
-  };
-  auto split_group = [&](int j) {
-    const double(&v)[VEC] = buf[j % kDepth];
-    const int k0 = (j * BLOCK + t) * VEC;
-    float h[VEC], l[VEC];
-#pragma unroll
-    for (int u = 0; u < VEC; ++u) {
-      const double d = (VECP ? k0 : k0 + u) < n ? v[u] : 0.0;
-      emax = max(emax, (uint32_t)__double2hiint(d) & 0x7ff00000u);
-      float p[2];
-      split<float>(d, p);
-      h[u] = p[0];
-      l[u] = p[1];
-    }
-    // (pins the split here: left alone, the compiler sinks it past the
-    // read and holds the doubles instead, twice the registers)
-#pragma unroll
-    for (int u = 0; u < VEC; ++u) asm volatile("" : "+v"(h[u]), "+v"(l[u]));
-    asm volatile("" : "+v"(emax));
-    L[j] = make_float4(l[0], l[1], l[2], l[3]);
-    const float4 hi = make_float4(h[0], h[1], h[2], h[3]);
-    if (j < EPT_R)
-      R[j < EPT_R ? j : 0] = hi;
-    else
-      H[(j - EPT_R) * BLOCK] = hi;
-  };
-#pragma unroll
-  for (int j = 0; j < kDepth; ++j) issue(j);
-#pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    split_group(j);
-    if (j + kDepth < EPT) issue(j + kDepth);
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  const bool bad = emax == 0x7ff00000u;
-  if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
-  // Groups this thread stores (k0 < ld), counted from a fresh copy of t so
-  // that the read's indices are not kept alive for the tests below.
-  int tt = t;
-  asm volatile("" : "+v"(tt));
-  const int gst = (ldi / VEC - tt + BLOCK - 1) / BLOCK;
-
-  auto amax = [](float m, float4 q) {
-    return max_w(max_w(m, fabsf(q.x)), max_w(fabsf(q.y), max_w(fabsf(q.z), fabsf(q.w))));
-  };
-  // Slice step of group j with constants kc into `out`; returns the residual.
-  auto sl = [&](const SliceConst<float>& kc, T* out, int j, float4 q) {
-    const float r[VEC] = {q.x, q.y, q.z, q.w};
-    float nr[VEC];
-    union {
-      TV w;
-      T e[VEC];
-    } pk;
-#pragma unroll
-    for (int u = 0; u < VEC; ++u) {
-      float v = (r[u] + kc.sigma) - kc.sigma;
-      if (kc.zero) v = 0.0f;
-      nr[u] = r[u] - v;
-      // (computes the residual ahead of the store's branch; left alone the
-      // compiler sinks it past the branch, holding v and r alive together)
-      asm volatile("" : "+v"(nr[u]));
-      pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
-    }
-    if (j < gst) *(TV*)(out + j * step) = pk.w;
-    return make_float4(nr[0], nr[1], nr[2], nr[3]);
-  };
-
-  // Each thread only touches its own LDS elements, so the barriers inside
-  // block_max2 are the only ordering needed.
-  const int ns = max(n0, n1);
-  for (int s = 0; s < ns; ++s) {
-    float m[2] = {0.0f, 0.0f};
-    if (s < n0) {
-#pragma unroll
-      for (int j = 0; j < EPT_R; ++j) m[0] = amax(m[0], R[j]);
-#pragma unroll 4
-      for (int j = EPT_R; j < EPT; ++j) m[0] = amax(m[0], H[(j - EPT_R) * BLOCK]);
-    }
-    if (s < n1) {
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) m[1] = amax(m[1], L[j]);
-    }
-    m[0] = line_max_input<FMT>(m[0], bad);
-    m[1] = line_max_input<FMT>(m[1], bad);
-    block_max2<float, BLOCK, 1, 2>(m, red);
-    if (s < n0) {  // uniform
-      SliceConst<float> kc = slice_const<float>(m[0], rho);
-      const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
-      T* out = S + s * plane + off0;
-#pragma unroll
-      for (int j = 0; j < EPT_R; ++j) R[j] = sl(kc, out, j, R[j]);
-#pragma unroll 4
-      for (int j = EPT_R; j < EPT; ++j)
-        H[(j - EPT_R) * BLOCK] = sl(kc, out, j, H[(j - EPT_R) * BLOCK]);
-      if (t == 0) E[s * eplane + line] = ce;
-    }
-    if (s < n1) {  // uniform
-      SliceConst<float> kc = slice_const<float>(m[1], rho);
-      const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
-      T* out = S + (n0 + s) * plane + off0;
-#pragma unroll
-      for (int j = 0; j < EPT; ++j) L[j] = sl(kc, out, j, L[j]);
-      if (t == 0) E[(n0 + s) * eplane + line] = ce;
-    }
-  }
-}
-
 // Column extraction without a transposed copy of X.  The columns are cut
 // into panels of kGangPW = 16 (a 128-byte row segment of X) and each panel's
 // rows into runs of kGangRun; workgroup ("member") m of the panel's gang of
@@ -664,6 +496,142 @@ __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
   }
 }
 
+// Row extraction of lines longer than one workgroup holds (FP32 path,
+// padded length 32769 .. kRowRun * kRowMaxMembers): each line is cut into
+// runs of kRowRun elements, one per workgroup ("member") of the line's gang
+// of G = ceil(ld / kRowRun), which holds its run in registers with
+// extract_lines_reg's layout (thread t: elements base + (512 j + t) * 4 + v)
+// and arithmetic.  Per slice the members exchange the run maxima of both
+// parts, as extract_cols_gang does: member m stores its two order keys
+// into words 2 m, 2 m + 1 of the (line, slice) record (128 bytes, zeroed
+// before the launch), then every member waits for all 2 G words.  Places
+// come from a ticket, and every wait is bounded, as for the column gangs.
+constexpr int kRowThreads = 512, kRowEPT = 8, kRowVEC = 4;
+constexpr int kRowRun = kRowThreads * kRowEPT * kRowVEC;  // 16384 elements
+constexpr int kRowMaxMembers = 16;
+constexpr int64_t kRowRecBytes = 8 * kRowMaxMembers;  // two keys per member
+
+template <int FMT, bool VEC>
+__global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
+    const double* __restrict__ X, int64_t len, int64_t ldx, int rho, int n0, int n1,
+    typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
+    int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls) {
+  typedef typename PlaneElem<FMT>::type T;
+  typedef typename PlaneVec<FMT, kRowVEC>::type TV;
+  constexpr int NP = 2, EPT = kRowEPT, V = kRowVEC;
+  constexpr int kPer = kChunkBytes / (int)sizeof(T);
+  static_assert(kRowRun % kPer == 0 && (kRowThreads * V) % kPer == 0, "whole chunks");
+  constexpr int64_t kWords = kRowRecBytes / 4;
+  const float qscale = ldexpf(1.0f, 24 - rho);
+  __shared__ float red[NP * (kRowThreads / 64)];
+  __shared__ uint32_t comb[2 * kRowMaxMembers];
+  __shared__ uint32_t place;
+  __shared__ int gave_up;
+  const int t = threadIdx.x;
+  if (t == 0) {
+    place = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    gave_up = 0;
+  }
+  __syncthreads();
+  // the grid holds exactly lines * G workgroups, so every place is a member
+  const int64_t line = place / (uint32_t)G;
+  const int member = (int)(place % (uint32_t)G);
+  const int ns = max(n0, n1);
+  const int64_t base = (int64_t)member * kRowRun;
+  const double* x = X + line * ldx;
+  // base is a whole number of chunks, so as in extract_lines_reg the
+  // in-chunk position is fixed per thread and j advances whole chunks
+  const int64_t off0 = plane_offset<sizeof(T)>(line, base + (int64_t)t * V, eplane);
+  const int64_t step = (int64_t)(kRowThreads * V / kPer) * eplane * kPer;
+  uint32_t* const my = rec + line * ns * kWords;
+
+  float R[NP][EPT * V];
+  bool bad = false;
+#pragma unroll
+  for (int j = 0; j < EPT; ++j) {
+    const int64_t k0 = base + ((int64_t)j * kRowThreads + t) * V;
+    double v[V];
+    if (VEC && k0 + V <= len) {
+#pragma unroll
+      for (int u = 0; u < V; u += 2) {
+        const double2 d = *(const double2*)(x + k0 + u);
+        v[u] = d.x;
+        v[u + 1] = d.y;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < V; ++u) v[u] = k0 + u < len ? x[k0 + u] : 0.0;
+    }
+#pragma unroll
+    for (int u = 0; u < V; ++u) {
+      bad |= !isfinite(v[u]);
+      float p[NP];
+      split<float>(v[u], p);
+#pragma unroll
+      for (int q = 0; q < NP; ++q) R[q][j * V + u] = p[q];
+    }
+  }
+  if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
+
+  for (int s = 0; s < ns; ++s) {
+    uint32_t* const rs = my + s * kWords;  // this slice's record
+    float m[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      m[q] = 0.0f;
+#pragma unroll
+      for (int j = 0; j < EPT * V; ++j) m[q] = max_w(m[q], fabsf(R[q][j]));
+      m[q] = line_max_input<FMT>(m[q], bad);
+    }
+    block_max2<float, kRowThreads, 1, NP>(m, red);  // the run's maxima
+    if (t < NP)
+      __hip_atomic_store(rs + 2 * member + t, max_key(m[t]), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (t < 2 * G) {  // every member's maxima
+      uint32_t k = 0u;
+      if (!gave_up) {
+        k = wait_key(rs + t, flags, polls);
+        if (!k) gave_up = 1;
+      }
+      comb[t] = k;
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      uint32_t kk = 0u;
+      for (int mb = 0; mb < G; ++mb) kk = max(kk, comb[2 * mb + q]);
+      m[q] = key_max(kk);
+    }
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int nq = q == 0 ? n0 : n1;
+      if (s >= nq) continue;  // uniform
+      SliceConst<float> kc = slice_const<float>(m[q], rho);
+      const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0 && member == 0);
+      const int pl = (q == 0 ? 0 : n0) + s;
+      T* out = S + pl * plane + off0;
+#pragma unroll
+      for (int j = 0; j < EPT; ++j) {
+        union {
+          TV w;
+          T e[V];
+        } pk;
+#pragma unroll
+        for (int u = 0; u < V; ++u) {
+          const float r = R[q][j * V + u];
+          float v = (r + kc.sigma) - kc.sigma;
+          if (kc.zero) v = 0.0f;
+          R[q][j * V + u] = r - v;
+          pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+        }
+        if (base + ((int64_t)j * kRowThreads + t) * V < ld) *(TV*)(out + j * step) = pk.w;
+      }
+      if (t == 0 && member == 0) E[pl * eplane + line] = ce;
+    }
+  }
+}
+
 __global__ void zero_u32x4_kernel(uint4* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -735,10 +703,62 @@ __global__ void fill_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
 
 // ---------------------------------------------------------------- launchers
 
+// FP32 lines longer than one workgroup holds and at most
+// kRowRun * kRowMaxMembers long run on row gangs.
+static bool gang_rows(int64_t len) {
+  const int64_t ld = round_up(len, kKPad);
+  return ld > 32768 && ld <= (int64_t)kRowRun * kRowMaxMembers;
+}
+
+static size_t row_gang_bytes(int64_t lines, int nslices) {
+  return (size_t)kGangHeader + (size_t)round_up(lines, kLinePad) * nslices * kRowRecBytes;
+}
+
+template <int FMT>
+static int launch_rows_gang(const double* X, int64_t lines, int64_t len, int64_t ldx,
+                            int rho, int n0, int n1, void* Sv, int32_t* E, uint32_t* flags,
+                            void* ws, size_t wsb, hipStream_t st) {
+  typedef typename PlaneElem<FMT>::type T;
+  const int ns = n0 > n1 ? n0 : n1;
+  const size_t need = row_gang_bytes(lines, ns);
+  if (wsb < need || !ws) {
+    set_error("extract: workspace of %zu bytes needed, %zu given", need, wsb);
+    return OZK_ERR_WORKSPACE;
+  }
+  const int64_t ld = round_up(len, kKPad), lp = round_up(lines, kLinePad);
+  const int64_t plane = lp * ld;
+  const int G = (int)((ld + kRowRun - 1) / kRowRun);
+  // the ticket and the exchange records start at zero
+  const int64_t n16 = (int64_t)need / 16;
+  hipLaunchKernelGGL(zero_u32x4_kernel,
+                     dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)),
+                     dim3(256), 0, st, (uint4*)ws, n16);
+  OZK_LAUNCH_CHECK();
+  uint32_t* ticket = (uint32_t*)ws;
+  uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
+  const dim3 grid((unsigned)(lines * G));
+  const uint32_t polls = wait_polls(kGangSpin);
+  if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
+    hipLaunchKernelGGL((extract_lines_gang<FMT, true>), grid, dim3(kRowThreads), 0, st, X,
+                       len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec, ticket, G,
+                       polls);
+  else
+    hipLaunchKernelGGL((extract_lines_gang<FMT, false>), grid, dim3(kRowThreads), 0, st, X,
+                       len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec, ticket, G,
+                       polls);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
 template <typename W, int FMT>
 static int launch_lines(const double* X, int64_t lines, int64_t len,
                         int64_t ldx, int rho, int n0, int n1, void* Sv,
-                        int32_t* E, uint32_t* flags, hipStream_t st) {
+                        int32_t* E, uint32_t* flags, void* ws, size_t wsb, hipStream_t st) {
+  if constexpr (sizeof(W) == 4) {
+    if (gang_rows(len) && lines > 0)
+      return launch_rows_gang<FMT>(X, lines, len, ldx, rho, n0, n1, Sv, E, flags, ws, wsb,
+                                   st);
+  }
   typedef typename PlaneElem<FMT>::type T;
   T* S = (T*)Sv;
   const int64_t ld = round_up(len, kKPad);
@@ -771,19 +791,9 @@ static int launch_lines(const double* X, int64_t lines, int64_t len,
       if (ld <= 32768) {
         OZK_REG(512, 16, 1, 4);
         done = true;
-      } else if (ld <= 65536) {  // both parts on chip, one read
-        if (vec_ok && len % 4 == 0)
-          hipLaunchKernelGGL((extract_lines_hybrid<1024, 16, 7, FMT, true>), grid, dim3(1024),
-                             0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E, lp,
-                             flags);
-        else
-          hipLaunchKernelGGL((extract_lines_hybrid<1024, 16, 7, FMT, false>), grid, dim3(1024),
-                             0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E, lp,
-                             flags);
-        done = true;
       }
     }
-    if (!done)
+    if (!done)  // FP64 lines, and FP32 lines longer than the row gangs take
       hipLaunchKernelGGL((extract_lines_stream<W, 1024, FMT>), grid, dim3(1024),
                          0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E,
                          lp, flags);
@@ -812,10 +822,15 @@ static size_t gang_workspace_bytes(int64_t rows, int64_t cols, int nslices) {
          (size_t)(round_up(cols, kLinePad) / kGangPW) * nslices * G * kGangLine;
 }
 
+// Offset of the row-gang records after the transposed copy.
+static size_t transpose_bytes(int64_t rows, int64_t cols) {
+  return (size_t)round_up(rows * cols * (int64_t)sizeof(double), 256);
+}
+
 size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols, bool f64) {
-  if (!by_cols) return 0;
+  if (!by_cols) return !f64 && gang_rows(cols) ? row_gang_bytes(rows, kMaxSlices) : 0;
   if (!f64 && gang_columns(rows)) return gang_workspace_bytes(rows, cols, kMaxSlices);
-  return (size_t)(rows * cols) * sizeof(double);
+  return transpose_bytes(rows, cols) + (!f64 && gang_rows(rows) ? row_gang_bytes(cols, kMaxSlices) : 0);
 }
 
 template <int FMT>
@@ -891,9 +906,14 @@ int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
     lines = cols;
     len = rows;
     lds = rows;
+    const size_t tb = transpose_bytes(rows, cols);  // the rest holds row-gang records
+    ws = wsb > tb ? (void*)((char*)ws + tb) : nullptr;
+    wsb = wsb > tb ? wsb - tb : 0;
   }
-  if (i8) return launch_lines<W, kFmtI8>(src, lines, len, lds, rho, n0, n1, S, E, flags, st);
-  return launch_lines<W, kFmtBf16>(src, lines, len, lds, rho, n0, n1, S, E, flags, st);
+  if (i8)
+    return launch_lines<W, kFmtI8>(src, lines, len, lds, rho, n0, n1, S, E, flags, ws, wsb, st);
+  return launch_lines<W, kFmtBf16>(src, lines, len, lds, rho, n0, n1, S, E, flags, ws, wsb,
+                                   st);
 }
 
 template int extract<float>(const double*, int64_t, int64_t, int64_t, int, int,

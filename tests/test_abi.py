@@ -68,6 +68,12 @@ def gang_bytes(rows, cols):
     return 256 + (-(-cols // 64) * 64 // 16) * 32 * G * 128
 
 
+def row_gang_bytes(lines):
+    """FP32 lines of 32769 to 262144 elements: the ticket word and, per
+    (line, slice) for up to 32 slices, one 128-byte exchange record."""
+    return 256 + -(-lines // 64) * 64 * 32 * 128
+
+
 def test_workspace_sizes(lib):
     # A and B slice planes + exponents + B's column-extraction exchange
     # records; planes are INT8 when K > 4096 (rho >= 19) and the schedule is
@@ -84,9 +90,15 @@ def test_workspace_sizes(lib):
     ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
     base = 2 * 9 * 8192 * 8192 + gang_bytes(8192, 8192) + 20 * 8192 * 8192
     assert base <= ws <= base + 2 * 9 * 8192 * 4 + 8192
-    # columns longer than 65536 rows, and the FP64 (host) pipeline, transpose B
+    # columns longer than 8192 rows, and the FP64 (host) pipeline, transpose B;
+    # one extraction buffer serves A's rows and B's columns in turn
     ws = lib.ozk_matmul_workspace_bytes(64, 70000, 64, 0, 4, 1)
-    assert ws >= 8 * 70000 * 64
+    assert ws >= 8 * 70000 * 64 + row_gang_bytes(64)
+    N, K, M = 1024, 65536, 1024
+    ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, 4, 1)
+    planes = 5 * (N + M) * K + 5 * (N + M) * 4
+    ex = max(row_gang_bytes(N), 8 * K * M + row_gang_bytes(M))
+    assert planes + ex <= ws <= planes + ex + 4096
     ws = lib.ozk_matmul_workspace_bytes(64, 1000, 64, 1, 8, 0)
     assert ws >= 8 * 1000 * 64
 
@@ -100,10 +112,19 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == 100 * 70 * 8
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == 0
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
-    # the larger of the FP32 (exchange records) and FP64 (transpose) needs
-    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == max(100 * 50 * 8, gang_bytes(100, 50))
+    assert lib.ozk_extract_workspace_bytes(100, 32768, 0) == 0
+    # rows of 32769 to 262144 elements: row gangs; longer lines stream
+    assert lib.ozk_extract_workspace_bytes(3, 32769, 0) == row_gang_bytes(3)
+    assert lib.ozk_extract_workspace_bytes(100, 262144, 0) == row_gang_bytes(100)
+    assert lib.ozk_extract_workspace_bytes(3, 262145, 0) == 0
+    # the larger of the FP32 (exchange records) and FP64 (transpose, rounded
+    # up to 256 bytes) needs
+    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == max(40192, gang_bytes(100, 50))
     assert lib.ozk_extract_workspace_bytes(8, 5000, 1) == gang_bytes(8, 5000)
-    assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 70000 * 3 * 8
+    # longer columns: the transposed copy (256-byte aligned), then the row
+    # gangs' records while the transposed lines are within their reach
+    assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 1680128 + row_gang_bytes(3)
+    assert lib.ozk_extract_workspace_bytes(300000, 3, 1) == 300000 * 3 * 8
 
 
 def test_int8_entry_points_reject_before_device_work(lib):

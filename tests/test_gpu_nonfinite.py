@@ -58,12 +58,12 @@ def edge_operands(N, K, M, seed):
 
 # ---------------------------------------------------------------- extraction
 
-@pytest.mark.parametrize("length", [5000, 8192, 40000, 70000])
+@pytest.mark.parametrize("length", [5000, 8192, 40000, 70000, 150000, 300000])
 def test_extract_i8_nonfinite_lines(ll, length):
     """Slices of a line up to its first non-finite one (per part) equal the
     oracle's; from there on they are zeros with exponent OZK_EXP_NONFINITE.
-    Covers the register kernel (5000, 8192), the on-chip long-line kernel
-    (40000) and the streaming kernel (70000)."""
+    Covers the register kernel (5000, 8192), lines held by 3, 5 and 10
+    workgroups (40000, 70000, 150000) and the streaming kernel (300000)."""
     rng = np.random.RandomState(length)
     X = rng.randn(10, length)
     X[1] *= 2.0 ** -110

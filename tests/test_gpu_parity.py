@@ -120,15 +120,20 @@ def test_extract_f64_rows_and_cols(ll, shape):
         assert np.array_equal(v, s) and np.array_equal(e, ee.astype(np.int32))
 
 
-# Lines longer than the register-resident kernels hold: up to 64 Ki elements
-# both parts stay on chip (registers + LDS) after one read; longer lines
-# stream them.  (n0, n1) = (2, 3) runs more lo slices than hi slices; lengths
-# that are not a multiple of 4 take the element-wise loads.
+# Lines longer than one workgroup holds in registers: up to 256 Ki elements
+# (FP32 path) a line is held by 3 to 16 workgroups that exchange their
+# per-slice maxima; longer lines stream.  (n0, n1) = (2, 3) runs more lo
+# slices than hi slices; lengths that are not a multiple of 4 take the
+# element-wise loads; 33000 is the shortest such line (3 workgroups),
+# 262144 the longest (16), 262145 streams.
 LONG_CASES = [("wide2", (3, 40000), 4, 1, False), ("zerorows", (3, 40000), 4, 1, False),
               ("wide2", (2, 65536), 4, 1, False), ("wide2", (2, 70000), 4, 1, False),
               ("wide2", (3, 40000), 2, 3, False), ("randn", (3, 40000), 4, 1, True),
               ("wide2", (2, 65536), 5, 4, True), ("wide2", (3, 40001), 4, 1, False),
-              ("wide2", (2, 49998), 3, 1, True), ("wide2", (2, 65533), 4, 2, False)]
+              ("wide2", (2, 49998), 3, 1, True), ("wide2", (2, 65533), 4, 2, False),
+              ("randn", (70, 33000), 3, 1, False), ("wide2", (2, 131072), 4, 1, True),
+              ("zerorows", (3, 100003), 4, 1, False), ("wide2", (1, 262144), 4, 1, False),
+              ("wide2", (1, 262145), 4, 1, False)]
 
 
 @pytest.mark.parametrize("kind,shape,n0,n1,i8", LONG_CASES)
@@ -175,10 +180,10 @@ def test_extract_nonfinite_flag(ll):
     assert ll.extract(X, 1, 17, 4, 1).nonfinite()
 
 
-@pytest.mark.parametrize("length", [40000, 40001])
+@pytest.mark.parametrize("length", [40000, 40001, 200000])
 def test_extract_nonfinite_flag_long_lines(ll, length):
-    """The on-chip long-line kernel (both load forms) raises the flag too, and
-    only when a line holds a non-finite element."""
+    """The long-line kernels (both load forms) raise the flag too, and only
+    when a line holds a non-finite element."""
     X = np.ones((3, length))
     rho = O.rho_f32(length)
     case(f"nonfinite flag long lines {length}: finite")

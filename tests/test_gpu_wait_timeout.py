@@ -1,8 +1,9 @@
 """Bounded waits between workgroups, made to give up from the host.
 
 ozk_set_wait_polls(1) limits every wait of the kernels launched afterwards
-to one poll: the gangs of the column extraction (a member that gives up sets
-OZK_FLAG_WAIT_TIMEOUT and waits no more, so every kernel still exits) and
+to one poll: the gangs of the column and long-row extraction (a member that
+gives up sets OZK_FLAG_WAIT_TIMEOUT and waits no more, so every kernel still
+exits) and
 the row-block chains of the LU triangular solves.  The package raises on the
 flag after an extraction (matmul, gram, residual, lowlevel.extract); solve()
 redoes a triangular solve that gave up on torch.linalg's path.  After
@@ -55,6 +56,31 @@ def test_column_extraction_gives_up_then_recovers(ozk, set_polls):
     ref = np.concatenate([sh, sl]).transpose(0, 2, 1) * 2.0 ** (24 - rho)
     assert np.array_equal(pl.grid().cpu().numpy()[:, cols, :8192], ref.astype(np.int8))
     assert np.array_equal(pl.exponents().cpu().numpy()[:, cols],
+                          np.concatenate([eh, el]).astype(np.int32))
+
+
+def test_row_extraction_gives_up_then_recovers(ozk, set_polls):
+    from ozaki_jax_amd import lowlevel as ll
+    rng = np.random.RandomState(4)
+    X = rng.randn(256, 131072)  # gangs of 8 workgroups per row
+    rho = O.rho_f32(131072)
+    set_polls(1)
+    case("ozk_extract_f32_i8 by rows (256, 131072), one poll per wait")
+    with pytest.raises(RuntimeError, match="OZK_FLAG_WAIT_TIMEOUT"):
+        ll.extract(X, 0, rho, 4, 1, i8=True)
+    case("matmul 64 x 70000 x 8 (row gangs for A and the transposed B), one poll per wait")
+    with pytest.raises(RuntimeError, match="OZK_FLAG_WAIT_TIMEOUT"):
+        ozk.matmul(rng.randn(64, 70000), rng.randn(70000, 8), pipeline="ondevice")
+    set_polls(0)
+    case("ozk_extract_f32_i8 by rows (256, 131072), built-in limit")
+    pl = ll.extract(X, 0, rho, 4, 1, i8=True)
+    rows = np.r_[0:3, 254:256]
+    hi, lo = O.split_hi_lo(X[rows])
+    sh, eh = O.extract_rows_f32(hi, rho, 4)
+    sl, el = O.extract_rows_f32(lo, rho, 1)
+    ref = np.concatenate([sh, sl]) * 2.0 ** (24 - rho)
+    assert np.array_equal(pl.grid().cpu().numpy()[:, rows, :131072], ref.astype(np.int8))
+    assert np.array_equal(pl.exponents().cpu().numpy()[:, rows],
                           np.concatenate([eh, el]).astype(np.int32))
 
 
