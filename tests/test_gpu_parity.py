@@ -376,6 +376,29 @@ def test_matmul_long_contraction_bit_exact(ozk, precision):
         assert np.array_equal(C, ref())
 
 
+@pytest.mark.parametrize("K", [5000, 8192, 4100])
+@pytest.mark.parametrize("aligned", [True, False])
+def test_matmul_operand_strides_bit_exact(ozk, K, aligned):
+    """Torch views with odd leading dimensions and, unaligned, an 8-byte
+    offset (element-wise loads for both operands), at K where A's rows fit
+    one workgroup and B's columns are extracted in place by gangs.  N = 65
+    and M = 70 leave padding lines in both plane sets."""
+    import torch
+    N, M = 65, 70
+    rng = np.random.RandomState(K + aligned)
+    Abig = torch.tensor(rng.randn(N, K + 3), device="cuda")
+    Bbig = torch.tensor((rng.rand(K, M + 3) - 0.5) * np.exp(2.0 * rng.randn(K, M + 3)),
+                        device="cuda")
+    o = 0 if aligned else 1
+    At, Bt = Abig[:, o:o + K], Bbig[:, o:o + M]
+    A, B = At.cpu().numpy(), Bt.cpu().numpy()
+    for precision in ("high", "medium", (5, 1)):
+        nh, nl = OP.resolve_precision(precision)
+        case(f"matmul strided views ({N},{K},{M}) aligned={aligned} {precision}")
+        C = ozk.matmul(At, Bt, pipeline="ondevice", precision=precision)
+        assert np.array_equal(C.cpu().numpy(), O.matmul_ondevice_a4(A, B, "raise", nh, nl))
+
+
 def _tail_split(ntiles, K, i8, cus=256, min_piece=16):
     """Pieces per tail tile of the all-pairs kernel's K-split tail on a GPU
     with `cus` CUs (MI355X: 256): 0 when the product does not split."""
