@@ -416,8 +416,9 @@ def main():
 
     def extract_both():
         for X, by, p in ((At, 0, pa), (Bt, 1, pb)):
+            sums = (p.sums.data_ptr(),) if i8 else ()  # INT8: line sums of the counts
             _lib.check(ext_fn(X.data_ptr(), n, n, n, by, rho, n_hi, n_lo,
-                              p.s.data_ptr(), p.e.data_ptr(), flags.data_ptr(),
+                              p.s.data_ptr(), p.e.data_ptr(), *sums, flags.data_ptr(),
                               ext_ws.data_ptr(), ext_wsb, hs))
 
     extract_both()

@@ -61,7 +61,7 @@ SIGNATURES = {
                                  _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
                                  _c_size, _c_vp]),
     "ozk_extract_f32_i8": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
-                                    _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp,
+                                    _c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_size, _c_vp]),
     "ozk_extract_f64": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
                                  _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_size,
@@ -72,14 +72,14 @@ SIGNATURES = {
     "ozk_gemm": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
                           _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp,
                           _c_size, _c_vp]),
-    "ozk_gemm_i8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
-                             _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp,
+    "ozk_gemm_i8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                             _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp,
                              _c_size, _c_vp]),
-    "ozk_gemm_2sum_pair": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
-                                    _c_int, _c_int, _c_int, _c_int, _c_vp, _c_vp, _c_i64,
-                                    _c_vp, _c_size, _c_vp]),
-    "ozk_slice_products_i8": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
-                                       _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
+    "ozk_gemm_2sum_pair": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                    _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int, _c_vp,
+                                    _c_vp, _c_i64, _c_vp, _c_size, _c_vp]),
+    "ozk_slice_products_i8": (_c_int, [_c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                       _c_int, _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_slice_products": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                     _c_int, _c_int, _c_vp, _c_i64, _c_vp]),
     "ozk_matmul_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int,

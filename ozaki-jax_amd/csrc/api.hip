@@ -46,7 +46,8 @@ uint32_t wait_polls(uint32_t dflt) {
 template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
             int by_cols, int rho, int n0, int n1, void* S, int32_t* E,
-            uint32_t* flags, void* ws, size_t wsb, hipStream_t st, bool i8);
+            uint32_t* flags, void* ws, size_t wsb, hipStream_t st, bool i8,
+            int32_t* sums);
 size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols, bool f64);
 int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
 int launch_check_finite(const double* X, int64_t rows, int64_t cols,
@@ -55,16 +56,19 @@ bool allpairs_supported(int pipe, int nhi, int nlo);
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
-                void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho);
+                void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho,
+                const int32_t* Asum, const int32_t* Bsum);
 size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
                             int order);
 int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
                      const int32_t* Be, int64_t N, int64_t M, int64_t K, int nhi,
                      int nlo, float* C_hi, float* C_lo, int64_t ldc, void* ws,
-                     size_t ws_bytes, hipStream_t st, bool i8, int rho);
+                     size_t ws_bytes, hipStream_t st, bool i8, int rho,
+                     const int32_t* Asum, const int32_t* Bsum);
 int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
-                    int64_t ldp, hipStream_t st, bool i8, int rho);
+                    int64_t ldp, hipStream_t st, bool i8, int rho, const int32_t* Asum,
+                    const int32_t* Bsum);
 int launch_probe_mfma(int32_t* out, hipStream_t st);
 size_t lu_solve_workspace_bytes(int64_t n, int64_t ncols);
 int64_t lu_factor_max_n();
@@ -77,7 +81,7 @@ int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n
 bool gram_sym_supported(int nhi, int nlo);
 int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
                     int nlo, double* G, int64_t ldg, void* ws, size_t ws_bytes,
-                    hipStream_t st, bool i8, int rho);
+                    hipStream_t st, bool i8, int rho, const int32_t* Ssum);
 size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int nlo,
                        bool sym, bool i8);
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo);
@@ -112,9 +116,11 @@ struct Carver {
   }
 };
 
+// Slice planes, their exponents and, for INT8 planes, their line sums.
 struct SliceSet {
   void* s;
   int32_t* e;
+  int32_t* sum;
 };
 
 static SliceSet carve_slices(Carver& c, int planes, int64_t lines, int64_t len,
@@ -123,6 +129,7 @@ static SliceSet carve_slices(Carver& c, int planes, int64_t lines, int64_t len,
   SliceSet r;
   r.s = c.take((size_t)planes * lp * ld * elem_bytes);
   r.e = (int32_t*)c.take((size_t)planes * lp * sizeof(int32_t));
+  r.sum = elem_bytes == 1 ? (int32_t*)c.take((size_t)planes * lp * sizeof(int32_t)) : nullptr;
   return r;
 }
 
@@ -193,7 +200,7 @@ extern "C" {
 
 const char* ozk_last_error(void) { return g_error.c_str(); }
 
-int ozk_abi_version(void) { return 2; }
+int ozk_abi_version(void) { return 3; }
 
 void ozk_set_wait_polls(uint32_t polls) {
   ozk::g_wait_polls.store(polls, std::memory_order_relaxed);
@@ -248,12 +255,12 @@ int ozk_extract_f32(const double* X, int64_t rows, int64_t cols, int64_t ldx,
   OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
   return extract<float>(X, rows, cols, ldx, by_cols, rho, n_hi, n_lo, slices,
                         exps, flags, workspace, workspace_bytes,
-                        (hipStream_t)stream, false);
+                        (hipStream_t)stream, false, nullptr);
 }
 
 int ozk_extract_f32_i8(const double* X, int64_t rows, int64_t cols,
                        int64_t ldx, int by_cols, int rho, int n_hi, int n_lo,
-                       int8_t* slices, int32_t* exps, uint32_t* flags,
+                       int8_t* slices, int32_t* exps, int32_t* sums, uint32_t* flags,
                        void* workspace, size_t workspace_bytes, void* stream) {
   clear_error();
   OZK_CHECK_ARG(rows >= 0 && cols >= 0, "negative shape");
@@ -262,15 +269,15 @@ int ozk_extract_f32_i8(const double* X, int64_t rows, int64_t cols,
   OZK_CHECK_ARG(n_hi >= 1 && n_hi <= kMaxSlices && n_lo >= 0 && n_lo <= kMaxSlices,
                 "slice counts (%d, %d) outside [1, %d] x [0, %d]", n_hi, n_lo,
                 kMaxSlices, kMaxSlices);
-  if (rho < 19) {
-    set_error("int8 slice planes need rho >= 19 (got %d)", rho);
+  if (rho < 19 || rho > 24) {
+    set_error("int8 slice planes need 19 <= rho <= 24 (got %d)", rho);
     return OZK_ERR_UNSUPPORTED;
   }
   if (rows == 0 || cols == 0) return OZK_OK;
-  OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
+  OZK_CHECK_ARG(X && slices && exps && sums && flags, "null pointer");
   return extract<float>(X, rows, cols, ldx, by_cols, rho, n_hi, n_lo, slices,
                         exps, flags, workspace, workspace_bytes,
-                        (hipStream_t)stream, true);
+                        (hipStream_t)stream, true, sums);
 }
 
 int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
@@ -286,7 +293,7 @@ int ozk_extract_f64(const double* X, int64_t rows, int64_t cols, int64_t ldx,
   OZK_CHECK_ARG(X && slices && exps && flags, "null pointer");
   return extract<double>(X, rows, cols, ldx, by_cols, rho, n_slices, 0, slices,
                          exps, flags, workspace, workspace_bytes,
-                         (hipStream_t)stream, false);
+                         (hipStream_t)stream, false, nullptr);
 }
 
 size_t ozk_gemm_workspace_bytes(int64_t N, int64_t M, int pipeline, int n_hi,
@@ -310,12 +317,12 @@ int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
   if (N == 0 || M == 0) return OZK_OK;
   return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K, pipeline,
                      n_hi, n_lo, order, C, ldc, workspace, workspace_bytes,
-                     (hipStream_t)stream, false, 0);
+                     (hipStream_t)stream, false, 0, nullptr, nullptr);
 }
 
-int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
-                const int8_t* b_slices, const int32_t* b_exps, int64_t N,
-                int64_t M, int64_t K, int rho, int n_hi, int n_lo, int order,
+int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps, const int32_t* a_sums,
+                const int8_t* b_slices, const int32_t* b_exps, const int32_t* b_sums,
+                int64_t N, int64_t M, int64_t K, int rho, int n_hi, int n_lo, int order,
                 double* C, int64_t ldc, void* workspace, size_t workspace_bytes,
                 void* stream) {
   clear_error();
@@ -325,19 +332,21 @@ int ozk_gemm_i8(const int8_t* a_slices, const int32_t* a_exps,
   OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape N=%lld M=%lld K=%lld",
                 (long long)N, (long long)M, (long long)K);
   OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
-  if (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
-    set_error("int8 planes need rho >= 19 and an all-pairs schedule (rho=%d, (%d, %d))",
+  if (rho < 19 || rho > 24 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
+    set_error("int8 planes need 19 <= rho <= 24 and an all-pairs schedule (rho=%d, (%d, %d))",
               rho, n_hi, n_lo);
     return OZK_ERR_UNSUPPORTED;
   }
   if (N == 0 || M == 0) return OZK_OK;
+  OZK_CHECK_ARG(a_sums && b_sums, "null pointer");
   return launch_gemm(a_slices, a_exps, b_slices, b_exps, N, M, K,
                      OZK_PIPE_ONDEVICE, n_hi, n_lo, order, C, ldc, workspace,
-                     workspace_bytes, (hipStream_t)stream, true, rho);
+                     workspace_bytes, (hipStream_t)stream, true, rho, a_sums, b_sums);
 }
 
 int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
-                       const void* b_slices, const int32_t* b_exps, int64_t N,
+                       const int32_t* a_sums, const void* b_slices,
+                       const int32_t* b_exps, const int32_t* b_sums, int64_t N,
                        int64_t M, int64_t K, int plane_bytes, int rho, int n_hi,
                        int n_lo, float* C_hi, float* C_lo, int64_t ldc,
                        void* workspace, size_t workspace_bytes, void* stream) {
@@ -350,13 +359,14 @@ int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
                 (long long)N, (long long)M, (long long)K);
   OZK_CHECK_ARG(ldc >= M || N <= 1, "ldc < M");
   const bool i8 = plane_bytes == 1;
-  if (i8 && (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo))) {
-    set_error("int8 planes need rho >= 19 and an all-pairs schedule (rho=%d, (%d, %d))",
+  if (i8 && (rho < 19 || rho > 24 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo))) {
+    set_error("int8 planes need 19 <= rho <= 24 and an all-pairs schedule (rho=%d, (%d, %d))",
               rho, n_hi, n_lo);
     return OZK_ERR_UNSUPPORTED;
   }
   if (N == 0 || M == 0) return OZK_OK;
   OZK_CHECK_ARG(a_slices && a_exps && b_slices && b_exps && C_hi && C_lo, "null pointer");
+  OZK_CHECK_ARG(!i8 || (a_sums && b_sums), "null pointer");
   const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, n_hi, n_lo, OZK_ORDER_2SUM);
   if (workspace_bytes < need || (need && !workspace)) {
     set_error("gemm_2sum_pair: workspace of %zu bytes needed, %zu given", need,
@@ -365,7 +375,7 @@ int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
   }
   return launch_gemm_pair(a_slices, a_exps, b_slices, b_exps, N, M, K, n_hi, n_lo, C_hi,
                           C_lo, ldc, workspace, workspace_bytes, (hipStream_t)stream, i8,
-                          rho);
+                          rho, i8 ? a_sums : nullptr, i8 ? b_sums : nullptr);
 }
 
 int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
@@ -378,10 +388,11 @@ int ozk_slice_products(const uint16_t* a_slices, const uint16_t* b_slices,
   OZK_CHECK_ARG(ldp >= M, "ldp < M");
   if (N == 0 || M == 0) return OZK_OK;
   return launch_products(a_slices, b_slices, N, M, K, pipeline, n_hi, n_lo, P,
-                         ldp, (hipStream_t)stream, false, 0);
+                         ldp, (hipStream_t)stream, false, 0, nullptr, nullptr);
 }
 
-int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
+int ozk_slice_products_i8(const int8_t* a_slices, const int32_t* a_sums,
+                          const int8_t* b_slices, const int32_t* b_sums,
                           int64_t N, int64_t M, int64_t K, int rho, int n_hi,
                           int n_lo, float* P, int64_t ldp, void* stream) {
   clear_error();
@@ -389,13 +400,14 @@ int ozk_slice_products_i8(const int8_t* a_slices, const int8_t* b_slices,
   if (rc) return rc;
   OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape");
   OZK_CHECK_ARG(ldp >= M, "ldp < M");
-  if (rho < 19 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
-    set_error("int8 planes need rho >= 19 and an all-pairs schedule");
+  if (rho < 19 || rho > 24 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
+    set_error("int8 planes need 19 <= rho <= 24 and an all-pairs schedule");
     return OZK_ERR_UNSUPPORTED;
   }
   if (N == 0 || M == 0) return OZK_OK;
+  OZK_CHECK_ARG(a_sums && b_sums, "null pointer");
   return launch_products(a_slices, b_slices, N, M, K, OZK_PIPE_ONDEVICE, n_hi,
-                         n_lo, P, ldp, (hipStream_t)stream, true, rho);
+                         n_lo, P, ldp, (hipStream_t)stream, true, rho, a_sums, b_sums);
 }
 
 // OZK_PIPE_ONDEVICE_BF16 is the on-device pipeline with the INT8 planes
@@ -493,22 +505,22 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
   if (pipeline == OZK_PIPE_ONDEVICE) {
     rho = rho_generic(K, 24);
     if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                             tws, tbytes, st, i8)))
+                             tws, tbytes, st, i8, sa.sum)))
       return rc;
     if ((rc = extract<float>(B, K, M, ldb, 1, rho, n_hi, n_lo, sb.s, sb.e, flags,
-                             tws, tbytes, st, i8)))
+                             tws, tbytes, st, i8, sb.sum)))
       return rc;
   } else {
     rho = rho_generic(K, 53);
     if ((rc = extract<double>(A, N, K, lda, 0, rho, n_hi, 0, sa.s, sa.e, flags,
-                              tws, tbytes, st, false)))
+                              tws, tbytes, st, false, nullptr)))
       return rc;
     if ((rc = extract<double>(B, K, M, ldb, 1, rho, n_hi, 0, sb.s, sb.e, flags,
-                              tws, tbytes, st, false)))
+                              tws, tbytes, st, false, nullptr)))
       return rc;
   }
   return launch_gemm(sa.s, sa.e, sb.s, sb.e, N, M, K, pipeline, n_hi, n_lo,
-                     order, C, ldc, gws, gwsb, st, i8, rho);
+                     order, C, ldc, gws, gwsb, st, i8, rho, sa.sum, sb.sum);
 }
 
 static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,
@@ -567,15 +579,16 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, rows, n_hi, n_lo);
   if ((rc = extract<float>(A, rows, cols, lda, 1, rho, n_hi, n_lo, s.s, s.e,
                            flags, tws, extract_workspace_bytes(rows, cols, 1, false), st,
-                           i8)))
+                           i8, s.sum)))
     return rc;
   // high / medium: upper tiles only, the symmetrisation folded into the
   // epilogue.  max (three K sweeps): full product, then symmetrise.
   if (gram_sym_supported(n_hi, n_lo))
     return launch_gram_sym(s.s, s.e, cols, rows, n_hi, n_lo, G, ldg, gws, gwsb, st, i8,
-                           rho);
+                           rho, s.sum);
   if ((rc = launch_gemm(s.s, s.e, s.s, s.e, cols, cols, rows, OZK_PIPE_ONDEVICE,
-                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, gws, gwsb, st, i8, rho)))
+                        n_hi, n_lo, OZK_ORDER_2SUM, G, ldg, gws, gwsb, st, i8, rho, s.sum,
+                        s.sum)))
     return rc;
   hipLaunchKernelGGL(symmetrize_kernel, dim3(grid_for(cols * cols)), dim3(256),
                      0, st, G, cols, ldg);
@@ -650,13 +663,14 @@ int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,
   const bool i8 = use_i8(OZK_PIPE_ONDEVICE, K, n_hi, n_lo);
   const size_t tbytes = extract_pair_bytes(N, K, ncols, false);
   if ((rc = extract<float>(x, K, ncols, ldx, 1, rho, n_hi, n_lo, sx.s, sx.e,
-                           flags, tws, tbytes, st, i8)))
+                           flags, tws, tbytes, st, i8, sx.sum)))
     return rc;
   if ((rc = extract<float>(A, N, K, lda, 0, rho, n_hi, n_lo, sa.s, sa.e, flags,
-                           tws, tbytes, st, i8)))
+                           tws, tbytes, st, i8, sa.sum)))
     return rc;
   if ((rc = launch_gemm(sa.s, sa.e, sx.s, sx.e, N, ncols, K, OZK_PIPE_ONDEVICE,
-                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, gws, gwsb, st, i8, rho)))
+                        n_hi, n_lo, OZK_ORDER_2SUM, y, ncols, gws, gwsb, st, i8, rho,
+                        sa.sum, sx.sum)))
     return rc;
   hipLaunchKernelGGL(sub_from_kernel, dim3(grid_for(N * ncols)), dim3(256), 0,
                      st, b, ldb, y, ncols, r, ldr, N, ncols);

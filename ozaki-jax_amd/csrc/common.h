@@ -78,6 +78,10 @@ constexpr int kChunkBytes = 64;
 
 inline int64_t round_up(int64_t x, int64_t m) { return (x + m - 1) / m * m; }
 
+// Offset of the INT8 plane format: a grid count q (|q| <= 2^(25 - rho),
+// rho >= 19) is stored as q + i8_offset(rho), in [-1, 127].
+__host__ __device__ inline int32_t i8_offset(int rho) { return (1 << (25 - rho)) - 1; }
+
 __host__ __device__ __forceinline__ int unit_swizzle(int64_t line) {
   const int r = (int)(line & 15);
   return ((r >> 1) ^ (r >> 2)) & 3;

@@ -21,8 +21,12 @@ namespace ozk {
 
 // Slice plane formats.  BF16: the FP32 slice value's BF16 bits.  I8: the
 // slice as an integer count of its grid step, q = slice * 2^(24 - rho)
-// (FP32 path only; |q| <= 2^(25 - rho) <= 64 for rho >= 19, so exact).
+// (FP32 path only; |q| <= 2^(25 - rho) <= 64 for rho >= 19, so exact),
+// stored as q + 2^(25 - rho) - 1 (i8_offset), with the sum of q over each
+// plane line written beside the plane (see the slice GEMM's I8Fix).
 constexpr int kFmtBf16 = 0, kFmtI8 = 1;
+constexpr int kMaxSlices = 32;
+constexpr int kMaxPlanes = 2 * kMaxSlices;
 
 template <int FMT> struct PlaneElem;
 template <> struct PlaneElem<kFmtBf16> {
@@ -33,10 +37,25 @@ template <> struct PlaneElem<kFmtBf16> {
 };
 template <> struct PlaneElem<kFmtI8> {
   typedef int8_t type;
+  // qscale = 2^(24 - rho), so 2 qscale - 1 is the offset
   static __device__ __forceinline__ int8_t make(float s, float qscale) {
-    return (int8_t)(int)(s * qscale);
+    return (int8_t)((int)(s * qscale) + (int)(2.0f * qscale) - 1);
   }
 };
+
+// Sum over the 64 lanes of a wave.
+// acc + the sum of the signed bytes of w (one dot product with ones)
+__device__ __forceinline__ int byte_sum(uint32_t w, int acc) {
+  return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
+}
+__device__ __forceinline__ int byte_sum(uint16_t w, int acc) { return byte_sum((uint32_t)w, acc); }
+__device__ __forceinline__ int byte_sum(uint2 w, int acc) { return byte_sum(w.y, byte_sum(w.x, acc)); }
+
+__device__ __forceinline__ int wave_sum(int v) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
+  return v;
+}
 
 // Slices the INT8 format cannot hold.  The reference's slice of a line is
 // non-finite when sigma = 0.75 * 2^(rho + c) or 2^-c overflows FP32
@@ -126,13 +145,21 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
     const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx,
     int vec_ok, int rho, int n0, int n1, typename PlaneElem<FMT>::type* __restrict__ S,
     int64_t ld, int64_t plane, int32_t* __restrict__ E, int64_t eplane,
-    uint32_t* __restrict__ flags) {
+    uint32_t* __restrict__ flags, int32_t* __restrict__ Sg) {
   static_assert(VEC == 2 || VEC == 4, "VEC doubles are read as 16-byte pairs");
   const float qscale = ldexpf(1.0f, 24 - rho);
   constexpr int NP = Parts<W>::N;
   __shared__ W red[NP * (BLOCK / 64) * LPB];
+  // INT8: line sums of q per plane.  Every thread adds up the bytes it packs
+  // (q + offset, the elements past the line's end included: their q is 0),
+  // the waves meet in LDS, and offset x BLOCK * EPT * VEC comes off at the end.
+  __shared__ int ssum[FMT == kFmtI8 ? kMaxPlanes * LPB : 1];
+  if constexpr (FMT == kFmtI8) {
+    for (int i = threadIdx.x; i < kMaxPlanes * LPB; i += BLOCK * LPB) ssum[i] = 0;
+  }
   const int t = threadIdx.x % BLOCK;
-  const int64_t line = xcd_line(blockIdx.x, gridDim.x) * LPB + threadIdx.x / BLOCK;
+  const int64_t grp = xcd_line(blockIdx.x, gridDim.x);
+  const int64_t line = grp * LPB + threadIdx.x / BLOCK;
   const bool live = line < lines;
   const double* x = X + line * ldx;
   // Plane offset of the thread's first element: BLOCK * VEC is a multiple of
@@ -191,6 +218,7 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
       const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
       const int pl = (q == 0 ? 0 : n0) + s;
       T* out = S + pl * plane + off0;
+      int qs = 0;
 #pragma unroll
       for (int j = 0; j < EPT; ++j) {
         union {
@@ -203,19 +231,30 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
           W v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = W(0);
           R[q][j * VEC + u] = r - v;
-          pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+          const float sv = slice_value_f32(v, kc.inv);
+          pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
         }
+        if constexpr (FMT == kFmtI8) qs = byte_sum(pk.w, qs);
         if (((int64_t)j * BLOCK + t) * VEC < ld) *(TV*)(out + j * step) = pk.w;
+      }
+      if constexpr (FMT == kFmtI8) {
+        qs = wave_sum(qs);
+        if ((threadIdx.x & 63) == 0) atomicAdd(&ssum[pl * LPB + threadIdx.x / BLOCK], qs);
       }
       if (t == 0) E[pl * eplane + line] = ce;
     }
+  }
+  if constexpr (FMT == kFmtI8) {
+    __syncthreads();
+    for (int i = threadIdx.x; i < (n0 + n1) * LPB; i += BLOCK * LPB)
+      Sg[(i / LPB) * eplane + grp * LPB + i % LPB] =
+          ssum[i] - i8_offset(rho) * (BLOCK * EPT * VEC);
   }
 }
 
 // Streaming extraction for lines too long for registers: every pass re-reads
 // the line and replays the previous slices' sigma steps (R_s depends only on
 // x and sigma_1..sigma_{s-1}), so only the per-slice constants are stored.
-constexpr int kMaxSlices = 32;
 
 template <typename W, int BLOCK, int FMT>
 __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
@@ -346,12 +385,17 @@ __device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
   return 0u;
 }
 
+// INT8: `part` receives member m's sums of q over its rows, per plane pl and
+// column at part[(pl G + m) eplane + column] (added up by i8_sum_parts):
+// the packed bytes (q + offset) of all kGangRun rows, rows past the column's
+// end included (q = 0 there), less offset x kGangRun.
 template <int FMT, bool VEC>
 __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
     const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
-    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls) {
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls,
+    int32_t* __restrict__ part) {
   typedef typename PlaneElem<FMT>::type T;
   constexpr int NP = 2, CP = kGangPW / 2, NW = kGangThreads / 64, R = kGangRowsPT;
   constexpr int NG = kGangThreads / kGangKeys;  // key groups of a workgroup
@@ -362,7 +406,11 @@ __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
   __shared__ uint32_t comb[NG][kGangKeys];
   __shared__ uint32_t place;
   __shared__ int gave_up;
+  __shared__ int ssum[FMT == kFmtI8 ? kMaxPlanes * kGangPW : 1];
   const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if constexpr (FMT == kFmtI8) {
+    for (int i = t; i < kMaxPlanes * kGangPW; i += kGangThreads) ssum[i] = 0;
+  }
   if (t == 0) {
     place = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     gave_up = 0;
@@ -479,20 +527,35 @@ __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
           typename std::conditional<FMT == kFmtI8, uint2, uint4>::type w;
           T e[R];
         } out;
+        int qs = 0;
 #pragma unroll
         for (int i = 0; i < R; ++i) {
           const float r = Rg[q][c][i];
           float v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = 0.0f;
           Rg[q][c][i] = r - v;
-          out.e[i] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+          const float sv = slice_value_f32(v, kc.inv);
+          out.e[i] = PlaneElem<FMT>::make(sv, qscale);
         }
+        if constexpr (FMT == kFmtI8) qs = byte_sum(out.w, qs);
         if (store)
           *(decltype(out.w)*)(S + pl * plane + plane_offset<sizeof(T)>(line, r0, eplane)) =
               out.w;
+        if constexpr (FMT == kFmtI8) {
+          // the wave's lanes of this column pair: lane % CP
+#pragma unroll
+          for (int off = CP; off < 64; off <<= 1) qs += __shfl_xor(qs, off);
+          if (lane < CP) atomicAdd(&ssum[pl * kGangPW + 2 * cp + c], qs);
+        }
         if (r0 == 0) E[pl * eplane + line] = ce;
       }
     }
+  }
+  if constexpr (FMT == kFmtI8) {
+    __syncthreads();
+    for (int i = t; i < (n0 + n1) * kGangPW; i += kGangThreads)
+      part[((int64_t)(i / kGangPW) * G + member) * eplane + panel * kGangPW + i % kGangPW] =
+          ssum[i] - i8_offset(rho) * kGangRun;
   }
 }
 
@@ -511,12 +574,17 @@ constexpr int kRowRun = kRowThreads * kRowEPT * kRowVEC;  // 16384 elements
 constexpr int kRowMaxMembers = 16;
 constexpr int64_t kRowRecBytes = 8 * kRowMaxMembers;  // two keys per member
 
+// INT8: `part` receives member m's sum of q per plane pl at
+// part[(pl G + m) eplane + line] (added up by i8_sum_parts): the packed bytes
+// of its run, less offset x kRowRun, as in extract_lines_reg.
 template <int FMT, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
-    const double* __restrict__ X, int64_t len, int64_t ldx, int rho, int n0, int n1,
+    const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx, int rho, int n0,
+    int n1,
     typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
-    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls) {
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls,
+    int32_t* __restrict__ part) {
   typedef typename PlaneElem<FMT>::type T;
   typedef typename PlaneVec<FMT, kRowVEC>::type TV;
   constexpr int NP = 2, EPT = kRowEPT, V = kRowVEC;
@@ -528,18 +596,24 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
   __shared__ uint32_t comb[2 * kRowMaxMembers];
   __shared__ uint32_t place;
   __shared__ int gave_up;
+  __shared__ int ssum[FMT == kFmtI8 ? kMaxPlanes : 1];
   const int t = threadIdx.x;
+  if constexpr (FMT == kFmtI8) {
+    if (t < kMaxPlanes) ssum[t] = 0;
+  }
   if (t == 0) {
     place = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     gave_up = 0;
   }
   __syncthreads();
-  // the grid holds exactly lines * G workgroups, so every place is a member
+  // the grid holds exactly G workgroups per padded line, so every place is a
+  // member; the padding lines (no reads) store zero slices
   const int64_t line = place / (uint32_t)G;
   const int member = (int)(place % (uint32_t)G);
+  const bool live = line < lines;
   const int ns = max(n0, n1);
   const int64_t base = (int64_t)member * kRowRun;
-  const double* x = X + line * ldx;
+  const double* x = X + (live ? line : 0) * ldx;
   // base is a whole number of chunks, so as in extract_lines_reg the
   // in-chunk position is fixed per thread and j advances whole chunks
   const int64_t off0 = plane_offset<sizeof(T)>(line, base + (int64_t)t * V, eplane);
@@ -552,7 +626,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
   for (int j = 0; j < EPT; ++j) {
     const int64_t k0 = base + ((int64_t)j * kRowThreads + t) * V;
     double v[V];
-    if (VEC && k0 + V <= len) {
+    if (VEC && live && k0 + V <= len) {
 #pragma unroll
       for (int u = 0; u < V; u += 2) {
         const double2 d = *(const double2*)(x + k0 + u);
@@ -561,7 +635,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
       }
     } else {
 #pragma unroll
-      for (int u = 0; u < V; ++u) v[u] = k0 + u < len ? x[k0 + u] : 0.0;
+      for (int u = 0; u < V; ++u) v[u] = live && k0 + u < len ? x[k0 + u] : 0.0;
     }
 #pragma unroll
     for (int u = 0; u < V; ++u) {
@@ -611,6 +685,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
       const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0 && member == 0);
       const int pl = (q == 0 ? 0 : n0) + s;
       T* out = S + pl * plane + off0;
+      int qs = 0;
 #pragma unroll
       for (int j = 0; j < EPT; ++j) {
         union {
@@ -623,12 +698,23 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
           float v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = 0.0f;
           R[q][j * V + u] = r - v;
-          pk.e[u] = PlaneElem<FMT>::make(slice_value_f32(v, kc.inv), qscale);
+          const float sv = slice_value_f32(v, kc.inv);
+          pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
         }
+        if constexpr (FMT == kFmtI8) qs = byte_sum(pk.w, qs);
         if (base + ((int64_t)j * kRowThreads + t) * V < ld) *(TV*)(out + j * step) = pk.w;
+      }
+      if constexpr (FMT == kFmtI8) {
+        qs = wave_sum(qs);
+        if ((t & 63) == 0) atomicAdd(&ssum[pl], qs);
       }
       if (t == 0 && member == 0) E[pl * eplane + line] = ce;
     }
+  }
+  if constexpr (FMT == kFmtI8) {
+    __syncthreads();
+    if (t < n0 + n1)
+      part[((int64_t)t * G + member) * eplane + line] = ssum[t] - i8_offset(rho) * kRowRun;
   }
 }
 
@@ -701,6 +787,52 @@ __global__ void check_finite_kernel(const double* __restrict__ X, int64_t rows,
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
 
+// INT8 line sums from the gangs' partial sums: sums[pl eplane + l] =
+// sum over members m of part[(pl G + m) eplane + l] for lines l < valid
+// (0 for the padding lines, which a row gang does not visit).
+__global__ void i8_sum_parts_kernel(const int32_t* __restrict__ part, int G, int planes,
+                                    int64_t eplane, int64_t valid, int32_t* __restrict__ sums) {
+  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (i >= planes * eplane) return;
+  const int64_t pl = i / eplane, l = i - pl * eplane;
+  int v = 0;
+  if (l < valid)
+    for (int m = 0; m < G; ++m) v += part[(pl * G + m) * eplane + l];
+  sums[i] = v;
+}
+
+// INT8 line sums read back from stored planes (the streaming path): 64
+// lines per workgroup, four threads per line, each summing one 16-byte unit
+// of every chunk; the stored values are q + off.
+__global__ __launch_bounds__(256) void i8_plane_sums_kernel(const int8_t* __restrict__ S,
+                                                            int64_t lp, int64_t ld, int off,
+                                                            int32_t* __restrict__ sums) {
+  const int t = threadIdx.x;
+  const int64_t pl = blockIdx.y, line = (int64_t)blockIdx.x * 64 + t / 4;
+  const int8_t* base = S + pl * lp * ld + line * kChunkBytes + 16 * (t % 4);
+  int v = 0;
+  for (int64_t c = 0; c < ld / kChunkBytes; ++c) {
+    const int4 w = *(const int4*)(base + c * lp * kChunkBytes);
+    const int ws[4] = {w.x, w.y, w.z, w.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      v += (int)(int8_t)ws[i] + (int)(int8_t)(ws[i] >> 8) + (int)(int8_t)(ws[i] >> 16) +
+           (ws[i] >> 24);
+  }
+  v += __shfl_xor(v, 1);
+  v += __shfl_xor(v, 2);
+  if (t % 4 == 0) sums[pl * lp + line] = v - (int)ld * off;
+}
+
+static int launch_sum_parts(const int32_t* part, int G, int planes, int64_t eplane,
+                            int64_t valid, int32_t* sums, hipStream_t st) {
+  const int64_t n = planes * eplane;
+  hipLaunchKernelGGL(i8_sum_parts_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
+                     part, G, planes, eplane, valid, sums);
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
 // ---------------------------------------------------------------- launchers
 
 // FP32 lines longer than one workgroup holds and at most
@@ -710,17 +842,24 @@ static bool gang_rows(int64_t len) {
   return ld > 32768 && ld <= (int64_t)kRowRun * kRowMaxMembers;
 }
 
-static size_t row_gang_bytes(int64_t lines, int nslices) {
-  return (size_t)kGangHeader + (size_t)round_up(lines, kLinePad) * nslices * kRowRecBytes;
+// Ticket and exchange records (zeroed per launch), then the INT8 partial
+// line sums (2 nslices planes x G members x padded lines).
+static size_t row_gang_records(int64_t lines, int nslices) {
+  return (size_t)round_up(kGangHeader + round_up(lines, kLinePad) * nslices * kRowRecBytes, 256);
+}
+static size_t row_gang_bytes(int64_t lines, int64_t len, int nslices) {
+  const int64_t G = (round_up(len, kKPad) + kRowRun - 1) / kRowRun;
+  return row_gang_records(lines, nslices) +
+         (size_t)(2 * nslices * G * round_up(lines, kLinePad)) * sizeof(int32_t);
 }
 
 template <int FMT>
 static int launch_rows_gang(const double* X, int64_t lines, int64_t len, int64_t ldx,
                             int rho, int n0, int n1, void* Sv, int32_t* E, uint32_t* flags,
-                            void* ws, size_t wsb, hipStream_t st) {
+                            void* ws, size_t wsb, hipStream_t st, int32_t* Sg) {
   typedef typename PlaneElem<FMT>::type T;
   const int ns = n0 > n1 ? n0 : n1;
-  const size_t need = row_gang_bytes(lines, ns);
+  const size_t need = row_gang_bytes(lines, len, ns);
   if (wsb < need || !ws) {
     set_error("extract: workspace of %zu bytes needed, %zu given", need, wsb);
     return OZK_ERR_WORKSPACE;
@@ -729,35 +868,39 @@ static int launch_rows_gang(const double* X, int64_t lines, int64_t len, int64_t
   const int64_t plane = lp * ld;
   const int G = (int)((ld + kRowRun - 1) / kRowRun);
   // the ticket and the exchange records start at zero
-  const int64_t n16 = (int64_t)need / 16;
+  const size_t recb = row_gang_records(lines, ns);
+  const int64_t n16 = (int64_t)recb / 16;
   hipLaunchKernelGGL(zero_u32x4_kernel,
                      dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)),
                      dim3(256), 0, st, (uint4*)ws, n16);
   OZK_LAUNCH_CHECK();
   uint32_t* ticket = (uint32_t*)ws;
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
-  const dim3 grid((unsigned)(lines * G));
+  int32_t* part = (int32_t*)((char*)ws + recb);
+  const dim3 grid((unsigned)(lp * G));
   const uint32_t polls = wait_polls(kGangSpin);
   if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
     hipLaunchKernelGGL((extract_lines_gang<FMT, true>), grid, dim3(kRowThreads), 0, st, X,
-                       len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec, ticket, G,
-                       polls);
+                       lines, len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
+                       ticket, G, polls, part);
   else
     hipLaunchKernelGGL((extract_lines_gang<FMT, false>), grid, dim3(kRowThreads), 0, st, X,
-                       len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec, ticket, G,
-                       polls);
+                       lines, len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
+                       ticket, G, polls, part);
   OZK_LAUNCH_CHECK();
+  if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;
 }
 
 template <typename W, int FMT>
 static int launch_lines(const double* X, int64_t lines, int64_t len,
                         int64_t ldx, int rho, int n0, int n1, void* Sv,
-                        int32_t* E, uint32_t* flags, void* ws, size_t wsb, hipStream_t st) {
+                        int32_t* E, uint32_t* flags, void* ws, size_t wsb, hipStream_t st,
+                        int32_t* Sg) {
   if constexpr (sizeof(W) == 4) {
     if (gang_rows(len) && lines > 0)
       return launch_rows_gang<FMT>(X, lines, len, ldx, rho, n0, n1, Sv, E, flags, ws, wsb,
-                                   st);
+                                   st, Sg);
   }
   typedef typename PlaneElem<FMT>::type T;
   T* S = (T*)Sv;
@@ -770,7 +913,7 @@ static int launch_lines(const double* X, int64_t lines, int64_t len,
 #define OZK_REG(B, EPT, LPB, V)                                                        \
   hipLaunchKernelGGL((extract_lines_reg<W, B, EPT, LPB, FMT, V>),                      \
                      dim3((unsigned)(lp / LPB)), dim3(B * LPB), 0, st, X, lines, len, ldx, \
-                     vec_ok, rho, n0, n1, S, ld, plane, E, lp, flags)
+                     vec_ok, rho, n0, n1, S, ld, plane, E, lp, flags, Sg)
   // Shapes measured per line-length bucket (one or two lines per workgroup
   // so that several workgroups share a CU and overlap loads with stores).
   if (ld <= 256) {
@@ -793,10 +936,16 @@ static int launch_lines(const double* X, int64_t lines, int64_t len,
         done = true;
       }
     }
-    if (!done)  // FP64 lines, and FP32 lines longer than the row gangs take
+    if (!done) {  // FP64 lines, and FP32 lines longer than the row gangs take
       hipLaunchKernelGGL((extract_lines_stream<W, 1024, FMT>), grid, dim3(1024),
                          0, st, X, lines, len, ldx, rho, n0, n1, S, ld, plane, E,
                          lp, flags);
+      if constexpr (FMT == kFmtI8) {
+        OZK_LAUNCH_CHECK();
+        hipLaunchKernelGGL(i8_plane_sums_kernel, dim3((unsigned)(lp / 64), (unsigned)(n0 + n1)),
+                           dim3(256), 0, st, (const int8_t*)S, lp, ld, i8_offset(rho), Sg);
+      }
+    }
   }
 #undef OZK_REG
   OZK_LAUNCH_CHECK();
@@ -816,10 +965,17 @@ static bool gang_columns(int64_t rows) {
   return round_up(rows, kKPad) <= (int64_t)kGangRun * kGangMaxMembers;
 }
 
+// Ticket and exchange records (zeroed per launch), then the INT8 partial
+// line sums (2 nslices planes x G members x padded columns).
+static size_t gang_records(int64_t rows, int64_t cols, int nslices) {
+  const int64_t G = gang_members(round_up(rows, kKPad));
+  return (size_t)round_up(
+      kGangHeader + (round_up(cols, kLinePad) / kGangPW) * nslices * G * kGangLine, 256);
+}
 static size_t gang_workspace_bytes(int64_t rows, int64_t cols, int nslices) {
   const int64_t G = gang_members(round_up(rows, kKPad));
-  return (size_t)kGangHeader +
-         (size_t)(round_up(cols, kLinePad) / kGangPW) * nslices * G * kGangLine;
+  return gang_records(rows, cols, nslices) +
+         (size_t)(2 * nslices * G * round_up(cols, kLinePad)) * sizeof(int32_t);
 }
 
 // Offset of the row-gang records after the transposed copy.
@@ -828,15 +984,16 @@ static size_t transpose_bytes(int64_t rows, int64_t cols) {
 }
 
 size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols, bool f64) {
-  if (!by_cols) return !f64 && gang_rows(cols) ? row_gang_bytes(rows, kMaxSlices) : 0;
+  if (!by_cols) return !f64 && gang_rows(cols) ? row_gang_bytes(rows, cols, kMaxSlices) : 0;
   if (!f64 && gang_columns(rows)) return gang_workspace_bytes(rows, cols, kMaxSlices);
-  return transpose_bytes(rows, cols) + (!f64 && gang_rows(rows) ? row_gang_bytes(cols, kMaxSlices) : 0);
+  return transpose_bytes(rows, cols) +
+         (!f64 && gang_rows(rows) ? row_gang_bytes(cols, rows, kMaxSlices) : 0);
 }
 
 template <int FMT>
 static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t ldx,
                             int rho, int n0, int n1, void* Sv, int32_t* E, uint32_t* flags,
-                            void* ws, size_t wsb, hipStream_t st) {
+                            void* ws, size_t wsb, hipStream_t st, int32_t* Sg) {
   typedef typename PlaneElem<FMT>::type T;
   if (rows <= 0 || cols <= 0) return OZK_OK;
   const int ns = n0 > n1 ? n0 : n1;
@@ -849,23 +1006,26 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
   const int64_t plane = lp * ld, npanels = lp / kGangPW;
   const int G = gang_members(ld);
   // the ticket and the exchange records start at zero
-  const int64_t n16 = (int64_t)need / 16;
+  const size_t recb = gang_records(rows, cols, ns);
+  const int64_t n16 = (int64_t)recb / 16;
   hipLaunchKernelGGL(zero_u32x4_kernel, dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)),
                      dim3(256), 0, st, (uint4*)ws, n16);
   OZK_LAUNCH_CHECK();
   uint32_t* ticket = (uint32_t*)ws;
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
+  int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(npanels * G));
   const uint32_t polls = wait_polls(kGangSpin);
   if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
     hipLaunchKernelGGL((extract_cols_gang<FMT, true>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, polls);
+                       ticket, G, polls, part);
   else
     hipLaunchKernelGGL((extract_cols_gang<FMT, false>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, polls);
+                       ticket, G, polls, part);
   OZK_LAUNCH_CHECK();
+  if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;
 }
 
@@ -876,10 +1036,15 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
 template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
             int by_cols, int rho, int n0, int n1, void* S, int32_t* E,
-            uint32_t* flags, void* ws, size_t wsb, hipStream_t st, bool i8) {
-  if (i8 && (sizeof(W) != 4 || rho < 19)) {
-    set_error("int8 slice planes need the FP32 path with rho >= 19 (rho=%d)", rho);
+            uint32_t* flags, void* ws, size_t wsb, hipStream_t st, bool i8,
+            int32_t* sums) {
+  if (i8 && (sizeof(W) != 4 || rho < 19 || rho > 24)) {
+    set_error("int8 slice planes need the FP32 path with 19 <= rho <= 24 (rho=%d)", rho);
     return OZK_ERR_UNSUPPORTED;
+  }
+  if (i8 && !sums) {
+    set_error("int8 slice planes need a line-sum array");
+    return OZK_ERR_INVALID;
   }
   const double* src = X;
   int64_t lines = rows, len = cols, lds = ldx;
@@ -887,9 +1052,9 @@ int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
     if (by_cols && gang_columns(rows)) {
       if (i8)
         return launch_cols_gang<kFmtI8>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, ws,
-                                        wsb, st);
+                                        wsb, st, sums);
       return launch_cols_gang<kFmtBf16>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, ws,
-                                        wsb, st);
+                                        wsb, st, nullptr);
     }
   }
   if (by_cols) {
@@ -911,17 +1076,18 @@ int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
     wsb = wsb > tb ? wsb - tb : 0;
   }
   if (i8)
-    return launch_lines<W, kFmtI8>(src, lines, len, lds, rho, n0, n1, S, E, flags, ws, wsb, st);
+    return launch_lines<W, kFmtI8>(src, lines, len, lds, rho, n0, n1, S, E, flags, ws, wsb, st,
+                                   sums);
   return launch_lines<W, kFmtBf16>(src, lines, len, lds, rho, n0, n1, S, E, flags, ws, wsb,
-                                   st);
+                                   st, nullptr);
 }
 
 template int extract<float>(const double*, int64_t, int64_t, int64_t, int, int,
                             int, int, void*, int32_t*, uint32_t*, void*,
-                            size_t, hipStream_t, bool);
+                            size_t, hipStream_t, bool, int32_t*);
 template int extract<double>(const double*, int64_t, int64_t, int64_t, int, int,
                              int, int, void*, int32_t*, uint32_t*, void*,
-                             size_t, hipStream_t, bool);
+                             size_t, hipStream_t, bool, int32_t*);
 
 int launch_check_finite(const double* X, int64_t rows, int64_t cols,
                         int64_t ld, uint32_t* flags, hipStream_t st) {

@@ -434,10 +434,39 @@ constexpr int kOrderPair = -2;
 template <> struct FoldOf<kOrderPair> { typedef Fold2Sum type; };
 template <> struct FoldState<kOrderPair> : FoldState<OZK_ORDER_2SUM> {};
 
+// INT8 planes store each grid count q with the offset o = 2^(25 - rho) - 1
+// (q + o in [-1, 2^(26 - rho) - 1]: mostly non-negative operands, which the
+// matrix cores multiply at a lower power, so a higher clock), and every
+// plane line comes with its sum of q.  The exact sum of a pair's products
+// is then
+//   S = sum_k (qa + o)(qb + o) - o (sum_k qa + sum_k qb) - Kp o^2
+// over the Kp padded positions (padding holds q = 0).  Under the rho rule
+// every term is an integer below 2^31 in magnitude; the arithmetic is done
+// modulo 2^32 (as the matrix cores add), which gives S exactly whenever S
+// itself fits.  as / bs: sums per (plane, line), plane stride a_lines /
+// b_lines; kpo2 = Kp o^2 modulo 2^32.
+struct I8Fix {
+  const int32_t* as;
+  const int32_t* bs;
+  uint32_t off, kpo2;
+};
+
+// Minus the INT8 offset's part (I8Fix) of a pair's sum at the lane's 4 rows
+// (line sums sa) and its column (sb): the accumulator value a whole tile
+// starts from.
+__device__ __forceinline__ int32x4 i8_start(const I8Fix& fix, int32x4 sa, int sb) {
+  const uint32_t c = fix.off * (uint32_t)sb + fix.kpo2;
+  int32x4 r;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = (int32_t)(0u - (fix.off * (uint32_t)sa[i] + c));
+  return r;
+}
+
 // Fold and store one output tile (tm, tn) from one wave's accumulators:
 // wave (wr, wc) owns rows 32 wr .. +31 and columns 16 wc .. +15 of the tile
 // as two 16x16 blocks h.  Shared by the all-pairs kernel and the fixup of
 // its K-split tail tiles.
+
 template <class Op, class SW, int ORDER, int B0, int B1, bool SYM>
 __device__ __forceinline__ void tile_epilogue(
     const typename Op::acc_t (&acc)[SW::NP][2], int tm, int tn, int wr, int wc,
@@ -569,7 +598,8 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     const char* __restrict__ Bs, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t nst, int64_t a_lines, int64_t b_lines,
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
-    int64_t ldp, char* __restrict__ state, int tail_P, uint32_t* __restrict__ part) {
+    int64_t ldp, char* __restrict__ state, int tail_P, uint32_t* __restrict__ part,
+    I8Fix fix) {
   typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
   constexpr int kBuf = SW::S * 4 * 64;  // uint4 per stage buffer
@@ -614,11 +644,39 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   mma.fl = frag_lane(lane);
   mma.wr = wave >> 2;
   mma.wc = wave & 3;
+  // Accumulators of work item jj: zero, or on INT8 planes for a whole tile
+  // minus the offset's part (I8Fix); a K-split piece stores raw sums and
+  // its fixup removes that part once.
+  auto start_item = [&](int jj) {
+    if constexpr (std::is_same<Op, OpI8>::value) {
+      if (jj < nfull) {
+        int tm, tn;
+        coords(bid + jj * nwg, tm, tn);
+        const int64_t col = (int64_t)tn * kBN + 16 * mma.wc + (lane & 15);
+        const int64_t rb = (int64_t)tm * kBM + 32 * mma.wr + 4 * (lane >> 4);
+        int sb[NB];
 #pragma unroll
-  for (int k = 0; k < NP; ++k) {
-    mma.acc[k][0] = typename Op::acc_t{};
-    mma.acc[k][1] = typename Op::acc_t{};
-  }
+        for (int q = 0; q < NB; ++q) sb[q] = fix.bs[(SW::BB + q) * b_lines + col];
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+          int32x4 sa[NA];
+#pragma unroll
+          for (int q = 0; q < NA; ++q)
+            sa[q] = *(const int32x4*)(fix.as + (SW::A0 + q) * a_lines + rb + 16 * h);
+#pragma unroll
+          for (int k = 0; k < NP; ++k)
+            mma.acc[k][h] = i8_start(fix, sa[SW::la(k)], sb[SW::lb(k)]);
+        }
+        return;
+      }
+    }
+#pragma unroll
+    for (int k = 0; k < NP; ++k) {
+      mma.acc[k][0] = typename Op::acc_t{};
+      mma.acc[k][1] = typename Op::acc_t{};
+    }
+  };
+  start_item(0);
 
   // Load cursor: chunk fs of this workgroup's tile fj, whose first lines
   // are fA / fB.
@@ -681,11 +739,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
       }
     }
     ++j;
-#pragma unroll
-    for (int k = 0; k < NP; ++k) {
-      mma.acc[k][0] = typename Op::acc_t{};
-      mma.acc[k][1] = typename Op::acc_t{};
-    }
+    start_item(j);
   }
 }
 
@@ -701,7 +755,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     const uint32_t* __restrict__ part, int tail_P, int tile0,
     const int32_t* __restrict__ Ae, const int32_t* __restrict__ Be, int64_t N,
     int64_t M, int64_t a_lines, int64_t b_lines, float unit2, double* __restrict__ C,
-    int64_t ldc, float* __restrict__ P, int64_t ldp, char* __restrict__ state) {
+    int64_t ldc, float* __restrict__ P, int64_t ldp, char* __restrict__ state, I8Fix fix) {
   typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
   typedef typename Op::acc_t V;
   constexpr int NP = SW::NP, NV = 2 * NP;  // accumulator vectors per lane
@@ -722,6 +776,26 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     for (int i = 0; i < PER; ++i)
       if (v * PER + i < NV) s[i] += src[q * piece_stride + v * PER + i];
   }
+  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
+  int tm, tn;
+  if constexpr (SYM) tile_coords_sym(tile0 + tl, ntm, tm, tn);
+  else tile_coords(tile0 + tl, ntm, ntn, tm, tn);
+  if constexpr (std::is_same<Op, OpI8>::value) {
+    // the offset's part (I8Fix) out of the pieces' raw sums
+    const int64_t col = (int64_t)tn * kBN + 16 * (w & 3) + (lane & 15);
+    const int64_t rb = (int64_t)tm * kBM + 32 * (w >> 2) + 4 * (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < PER; ++i) {
+      const int idx = v * PER + i;  // vector idx = 2 k + h
+      if (idx < NV) {
+        const int k = idx >> 1, h = idx & 1;
+        const int32x4 sa = *(const int32x4*)(fix.as + (SW::A0 + SW::la(k)) * a_lines + rb +
+                                              16 * h);
+        const int sb = fix.bs[(SW::BB + SW::lb(k)) * b_lines + col];
+        s[i] += i8_start(fix, sa, sb);
+      }
+    }
+  }
 #pragma unroll
   for (int i = 0; i < PER; ++i)
     if (v * PER + i < NV) sum[v * PER + i][lane] = s[i];
@@ -733,10 +807,6 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     acc[k][0] = sum[2 * k][lane];
     acc[k][1] = sum[2 * k + 1][lane];
   }
-  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
-  int tm, tn;
-  if constexpr (SYM) tile_coords_sym(tile0 + tl, ntm, tm, tn);
-  else tile_coords(tile0 + tl, ntm, ntn, tm, tn);
   tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(acc, tm, tn, w >> 2, w & 3, lane, Ae, Be, N, M,
                                             a_lines, b_lines, unit2, C, ldc, P, ldp, state);
 }
@@ -981,6 +1051,7 @@ struct ApArgs {
   float* P;
   int64_t ldp;
   char* state;
+  I8Fix fix;
 };
 
 template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
@@ -989,13 +1060,13 @@ static void launch_sweep(const ApArgs& a) {
   hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
                      a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
                      a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
-                     split ? a.tail_P : 0, a.part);
+                     split ? a.tail_P : 0, a.part, a.fix);
   if constexpr (B0 == 0 && B1 == 2) {
     if (split)
       hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
                          dim3((unsigned)(a.tail_T * 8)), dim3(kThreads16), 0, a.st, a.part, a.tail_P,
                          a.tile0, a.Ae, a.Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P,
-                         a.ldp, a.state);
+                         a.ldp, a.state, a.fix);
   }
 }
 
@@ -1048,7 +1119,12 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
                            int order, double* C, int64_t ldc, float* P,
                            int64_t ldp, void* state, size_t state_bytes,
-                           hipStream_t st, bool sym = false) {
+                           hipStream_t st, const int32_t* Asum, const int32_t* Bsum,
+                           bool sym = false) {
+  if (i8 && (!Asum || !Bsum)) {
+    set_error("int8 slice planes need their line sums");
+    return OZK_ERR_INVALID;
+  }
   const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, nhi, nlo, order);
   if (state_bytes < need || (need && !state)) {
     set_error("gemm workspace of %zu bytes < %zu needed", state_bytes, need);
@@ -1094,6 +1170,10 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.P = P;
   a.ldp = ldp;
   a.state = (char*)state;
+  a.fix.as = Asum;
+  a.fix.bs = Bsum;
+  a.fix.off = i8 ? (uint32_t)i8_offset(rho) : 0u;
+  a.fix.kpo2 = (uint32_t)((uint64_t)(a.nst * kChunkBytes) * a.fix.off * a.fix.off);
 #define OZK_AP_ALL(Op)                                                    \
   do {                                                                    \
     if (nhi == 4 && nlo == 1) launch_ap_order<Op, 4, 1>(order, a);        \
@@ -1124,22 +1204,23 @@ bool gram_sym_supported(int nhi, int nlo) { return nlo == 1 && (nhi == 4 || nhi 
 
 int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int nhi,
                     int nlo, double* G, int64_t ldg, void* ws, size_t ws_bytes,
-                    hipStream_t st, bool i8, int rho) {
+                    hipStream_t st, bool i8, int rho, const int32_t* Ssum) {
   if (!gram_sym_supported(nhi, nlo)) {
     set_error("symmetric gram needs the high or medium preset");
     return OZK_ERR_UNSUPPORTED;
   }
   return launch_allpairs(i8, S, E, S, E, n, n, K, rho, nhi, nlo, OZK_ORDER_2SUM, G, ldg,
-                         nullptr, 0, ws, ws_bytes, st, true);
+                         nullptr, 0, ws, ws_bytes, st, Ssum, Ssum, true);
 }
 
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
-                void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho) {
+                void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho,
+                const int32_t* Asum, const int32_t* Bsum) {
   if (allpairs_schedule(pipe, nhi, nlo) && allpairs_order(nhi, nlo, order))
     return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, order,
-                           C, ldc, nullptr, 0, ws, ws_bytes, st);
+                           C, ldc, nullptr, 0, ws, ws_bytes, st, Asum, Bsum);
   if (i8) {
     set_error("int8 slice planes need an all-pairs on-device schedule");
     return OZK_ERR_UNSUPPORTED;
@@ -1171,10 +1252,11 @@ int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
 int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
                      const int32_t* Be, int64_t N, int64_t M, int64_t K, int nhi,
                      int nlo, float* C_hi, float* C_lo, int64_t ldc, void* ws,
-                     size_t ws_bytes, hipStream_t st, bool i8, int rho) {
+                     size_t ws_bytes, hipStream_t st, bool i8, int rho,
+                     const int32_t* Asum, const int32_t* Bsum) {
   if (allpairs_schedule(OZK_PIPE_ONDEVICE, nhi, nlo))
     return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, kOrderPair,
-                           (double*)C_lo, ldc, C_hi, ldc, ws, ws_bytes, st);
+                           (double*)C_lo, ldc, C_hi, ldc, ws, ws_bytes, st, Asum, Bsum);
   if (i8) {
     set_error("int8 slice planes need an all-pairs on-device schedule");
     return OZK_ERR_UNSUPPORTED;
@@ -1194,10 +1276,11 @@ int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
 // the drivers use); other schedules (BF16 only) the pairwise kernel.
 int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
-                    int64_t ldp, hipStream_t st, bool i8, int rho) {
+                    int64_t ldp, hipStream_t st, bool i8, int rho, const int32_t* Asum,
+                    const int32_t* Bsum) {
   if (allpairs_schedule(pipe, nhi, nlo))
     return launch_allpairs(i8, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
-                           kOrderProducts, nullptr, 0, P, ldp, nullptr, 0, st);
+                           kOrderProducts, nullptr, 0, P, ldp, nullptr, 0, st, Asum, Bsum);
   if (i8) {
     set_error("int8 slice planes need an all-pairs on-device schedule");
     return OZK_ERR_UNSUPPORTED;

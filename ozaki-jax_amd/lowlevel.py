@@ -27,21 +27,36 @@ class Planes:
     """Slice planes of one operand on the device.
 
     s: (planes, lines_pad, ld) storage of int16 BF16 bit patterns, or of int8
-    grid counts q = slice * 2^(24 - rho) when `rho` is set (INT8 format).
+    grid counts q = slice * 2^(24 - rho) stored as q + offset (offset =
+    2^(25 - rho) - 1) when `rho` is set (INT8 format).
     The bytes of a plane are chunk-major (64-byte chunks of k, chunk c of
     every line together, the four 16-byte units of a line's chunk stored in
     the order u ^ unit_swizzle(line)); grid() returns the plain
     (planes, lines_pad, ld) arrangement.
-    e: int32 (planes, lines_pad) exponents; lines / length: logical sizes.
+    e: int32 (planes, lines_pad) exponents; sums: int32 (planes, lines_pad)
+    line sums of q (INT8 only); lines / length: logical sizes.
     """
 
-    def __init__(self, s, e, lines, length, flags, rho=None):
+    def __init__(self, s, e, lines, length, flags, rho=None, sums=None):
         self.s, self.e, self.lines, self.length, self.flags = s, e, lines, length, flags
         self.rho = rho
+        self.sums = sums
 
     @property
     def i8(self):
         return self.rho is not None
+
+    @property
+    def offset(self):
+        """The INT8 format's offset 2^(25 - rho) - 1."""
+        return (1 << (25 - self.rho)) - 1
+
+    def counts(self):
+        """INT8 grid counts q as int32 (planes, lines_pad, ld) (device)."""
+        return self.grid().to(D.torch.int32) - self.offset
+
+    def _sums_ptr(self):
+        return self.sums.data_ptr() if self.sums is not None else None
 
     def grid(self):
         """Plane elements as (planes, lines_pad, ld), line-major (device)."""
@@ -60,7 +75,7 @@ class Planes:
         """float32 (planes, lines, length) slice values (device)."""
         g = self.grid()
         if self.i8:
-            v = g.to(D.torch.float32) * 2.0 ** (self.rho - 24)
+            v = (g.to(D.torch.int32) - self.offset).to(D.torch.float32) * 2.0 ** (self.rho - 24)
         else:
             v = (g.to(D.torch.int32) << 16).view(D.torch.float32)
         return v[:, :self.lines, :self.length]
@@ -87,6 +102,7 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False, i8=False):
                       dtype=D.torch.int8 if i8 else D.torch.int16, device=dev)
     e = D.torch.zeros((planes, lib.ozk_slice_lines(max(lines, 1))),
                       dtype=D.torch.int32, device=dev)
+    sums = D.torch.zeros_like(e) if i8 else None
     flags = D.new_flags(dev)
     wsb = lib.ozk_extract_workspace_bytes(rows, cols, int(by_cols))
     ws = D.workspace(wsb, dev)
@@ -95,14 +111,18 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False, i8=False):
                                  int(by_cols), rho, n0, s.data_ptr(),
                                  e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
                                  wsb, D.stream_handle())
+    elif i8:
+        rc = lib.ozk_extract_f32_i8(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols),
+                                    rho, n0, n1, s.data_ptr(), e.data_ptr(),
+                                    sums.data_ptr(), flags.data_ptr(), ws.data_ptr(), wsb,
+                                    D.stream_handle())
     else:
-        fn = lib.ozk_extract_f32_i8 if i8 else lib.ozk_extract_f32
-        rc = fn(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols), rho, n0,
-                n1, s.data_ptr(), e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
-                wsb, D.stream_handle())
+        rc = lib.ozk_extract_f32(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols), rho,
+                                 n0, n1, s.data_ptr(), e.data_ptr(), flags.data_ptr(),
+                                 ws.data_ptr(), wsb, D.stream_handle())
     _lib.check(rc)
     _lib.check_flags(D.read_flags(flags))
-    return Planes(s, e, lines, length, flags, rho if i8 else None)
+    return Planes(s, e, lines, length, flags, rho if i8 else None, sums)
 
 
 def gemm(a, b, pipeline, n_hi, n_lo, order):
@@ -114,8 +134,8 @@ def gemm(a, b, pipeline, n_hi, n_lo, order):
     wsb = lib.ozk_gemm_workspace_bytes(N, M, pipeline, n_hi, n_lo, order)
     ws = D.workspace(wsb, dev)
     if a.i8:
-        rc = lib.ozk_gemm_i8(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
-                             b.e.data_ptr(), N, M, K, a.rho, n_hi, n_lo, order,
+        rc = lib.ozk_gemm_i8(a.s.data_ptr(), a.e.data_ptr(), a._sums_ptr(), b.s.data_ptr(),
+                             b.e.data_ptr(), b._sums_ptr(), N, M, K, a.rho, n_hi, n_lo, order,
                              C.data_ptr(), max(M, 1), ws.data_ptr(), wsb,
                              D.stream_handle())
     else:
@@ -136,8 +156,9 @@ def gemm_pair(a, b, n_hi, n_lo):
     C_lo = D.torch.empty((N, M), dtype=D.torch.float32, device=dev)
     wsb = lib.ozk_gemm_workspace_bytes(N, M, PIPE_ONDEVICE, n_hi, n_lo, ORDER_2SUM)
     ws = D.workspace(wsb, dev)
-    _lib.check(lib.ozk_gemm_2sum_pair(a.s.data_ptr(), a.e.data_ptr(), b.s.data_ptr(),
-                                      b.e.data_ptr(), N, M, K, 1 if a.i8 else 2,
+    _lib.check(lib.ozk_gemm_2sum_pair(a.s.data_ptr(), a.e.data_ptr(), a._sums_ptr(),
+                                      b.s.data_ptr(), b.e.data_ptr(), b._sums_ptr(),
+                                      N, M, K, 1 if a.i8 else 2,
                                       a.rho or 0, n_hi, n_lo, C_hi.data_ptr(),
                                       C_lo.data_ptr(), max(M, 1), ws.data_ptr(), wsb,
                                       D.stream_handle()))
@@ -152,7 +173,8 @@ def slice_products(a, b, pipeline, n_hi, n_lo):
     npairs = _lib.check(lib.ozk_pair_count(pipeline, n_hi, n_lo))
     P = D.torch.zeros((npairs, N, M), dtype=D.torch.float32, device=dev)
     if a.i8:
-        rc = lib.ozk_slice_products_i8(a.s.data_ptr(), b.s.data_ptr(), N, M, K,
+        rc = lib.ozk_slice_products_i8(a.s.data_ptr(), a._sums_ptr(), b.s.data_ptr(),
+                                       b._sums_ptr(), N, M, K,
                                        a.rho, n_hi, n_lo, P.data_ptr(),
                                        max(M, 1), D.stream_handle())
     else:

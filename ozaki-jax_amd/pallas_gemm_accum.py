@@ -108,9 +108,9 @@ def fused_gemm_accum(a_slices, b_slices, a_scales, b_scales, n_hi, n_lo, *,
                                            _lib.ORDER_2SUM)
         ws = fam.workspace(wsb)
         _lib.check(lib.ozk_gemm_2sum_pair(
-            A_dev.data_ptr(), Ae_dev.data_ptr(), B_dev.data_ptr(), Be_dev.data_ptr(),
-            N, M, max(K, 1), 2, 0, n_hi, n_lo, C_hi.data_ptr(), C_lo.data_ptr(), max(M, 1),
-            ws.data_ptr(), wsb, fam.stream()))
+            A_dev.data_ptr(), Ae_dev.data_ptr(), None, B_dev.data_ptr(), Be_dev.data_ptr(),
+            None, N, M, max(K, 1), 2, 0, n_hi, n_lo, C_hi.data_ptr(), C_lo.data_ptr(),
+            max(M, 1), ws.data_ptr(), wsb, fam.stream()))
     return fam.out(C_hi, want_torch), fam.out(C_lo, want_torch)
 
 

@@ -47,7 +47,7 @@ def test_header_compiles_as_c(tmp_path):
 
 
 def test_host_functions(lib):
-    assert lib.ozk_abi_version() == 2
+    assert lib.ozk_abi_version() == 3
     for K in [1, 2, 3, 64, 1040, 4096, 8192, 32768, 65536, 2 ** 22, 2 ** 22 + 1, 10 ** 9]:
         assert lib.ozk_rho_f32(K) == O.rho_f32(K)
         assert lib.ozk_rho_f64(K) == O.rho_f64(K)
@@ -60,44 +60,54 @@ def test_host_functions(lib):
     assert b"outside" in lib.ozk_last_error()
 
 
+def r256(b):
+    return -(-b // 256) * 256
+
+
 def gang_bytes(rows, cols):
-    """Column extraction of up to 65536 rows on the FP32 path: the ticket
+    """Column extraction of up to 8192 rows on the FP32 path: the ticket
     word and, per (16-column panel, slice) for up to 32 slices, one
-    128-byte exchange line per 512-row run of a column."""
+    128-byte exchange line per 512-row run of a column (256-byte aligned),
+    then the INT8 line sums of each run: 64 planes x runs x padded columns."""
     G = -(-(-(-rows // 64) * 64) // 512)
-    return 256 + (-(-cols // 64) * 64 // 16) * 32 * G * 128
+    lp = -(-cols // 64) * 64
+    return r256(256 + (lp // 16) * 32 * G * 128) + 64 * G * lp * 4
 
 
-def row_gang_bytes(lines):
+def row_gang_bytes(lines, length):
     """FP32 lines of 32769 to 262144 elements: the ticket word and, per
-    (line, slice) for up to 32 slices, one 128-byte exchange record."""
-    return 256 + -(-lines // 64) * 64 * 32 * 128
+    (line, slice) for up to 32 slices, one 128-byte exchange record
+    (256-byte aligned), then the INT8 line sums of each 16384-element run:
+    64 planes x runs x padded lines."""
+    G = -(-(-(-length // 64) * 64) // 16384)
+    lp = -(-lines // 64) * 64
+    return r256(256 + lp * 32 * 128) + 64 * G * lp * 4
 
 
 def test_workspace_sizes(lib):
-    # A and B slice planes + exponents + B's column-extraction exchange
-    # records; planes are INT8 when K > 4096 (rho >= 19) and the schedule is
-    # a preset, else BF16
+    # A and B slice planes + exponents (+ line sums on INT8 planes) + B's
+    # column-extraction exchange records; planes are INT8 when K > 4096
+    # (rho >= 19) and the schedule is a preset, else BF16
     for K, eb in [(8192, 1), (4096, 2)]:
         N = M = 8192
         for nh, nl in [(4, 1), (3, 1)]:
             ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, nh, nl)
             planes = 2 * (nh + nl) * 8192 * K * eb
-            extra = 2 * (nh + nl) * 8192 * 4 + 4096
+            extra = (2 if eb == 1 else 1) * 2 * (nh + nl) * 8192 * 4 + 4096
             assert planes + gang_bytes(K, M) <= ws <= planes + gang_bytes(K, M) + extra, (K, nh, nl)
     # max (5, 4): INT8 planes + exchange records + the 2Sum fold state
     # between its three sweeps (5 FP32 fields per output element)
     ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
     base = 2 * 9 * 8192 * 8192 + gang_bytes(8192, 8192) + 20 * 8192 * 8192
-    assert base <= ws <= base + 2 * 9 * 8192 * 4 + 8192
+    assert base <= ws <= base + 2 * 2 * 9 * 8192 * 4 + 8192
     # columns longer than 8192 rows, and the FP64 (host) pipeline, transpose B;
     # one extraction buffer serves A's rows and B's columns in turn
     ws = lib.ozk_matmul_workspace_bytes(64, 70000, 64, 0, 4, 1)
-    assert ws >= 8 * 70000 * 64 + row_gang_bytes(64)
+    assert ws >= 8 * 70000 * 64 + row_gang_bytes(64, 70000)
     N, K, M = 1024, 65536, 1024
     ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, 4, 1)
-    planes = 5 * (N + M) * K + 5 * (N + M) * 4
-    ex = max(row_gang_bytes(N), 8 * K * M + row_gang_bytes(M))
+    planes = 5 * (N + M) * K + 2 * 5 * (N + M) * 4
+    ex = max(row_gang_bytes(N, K), 8 * K * M + row_gang_bytes(M, K))
     assert planes + ex <= ws <= planes + ex + 4096
     ws = lib.ozk_matmul_workspace_bytes(64, 1000, 64, 1, 8, 0)
     assert ws >= 8 * 1000 * 64
@@ -114,8 +124,8 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
     assert lib.ozk_extract_workspace_bytes(100, 32768, 0) == 0
     # rows of 32769 to 262144 elements: row gangs; longer lines stream
-    assert lib.ozk_extract_workspace_bytes(3, 32769, 0) == row_gang_bytes(3)
-    assert lib.ozk_extract_workspace_bytes(100, 262144, 0) == row_gang_bytes(100)
+    assert lib.ozk_extract_workspace_bytes(3, 32769, 0) == row_gang_bytes(3, 32769)
+    assert lib.ozk_extract_workspace_bytes(100, 262144, 0) == row_gang_bytes(100, 262144)
     assert lib.ozk_extract_workspace_bytes(3, 262145, 0) == 0
     # the larger of the FP32 (exchange records) and FP64 (transpose, rounded
     # up to 256 bytes) needs
@@ -123,28 +133,38 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_extract_workspace_bytes(8, 5000, 1) == gang_bytes(8, 5000)
     # longer columns: the transposed copy (256-byte aligned), then the row
     # gangs' records while the transposed lines are within their reach
-    assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 1680128 + row_gang_bytes(3)
+    assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 1680128 + row_gang_bytes(3, 70000)
     assert lib.ozk_extract_workspace_bytes(300000, 3, 1) == 300000 * 3 * 8
 
 
 def test_int8_entry_points_reject_before_device_work(lib):
     from ozaki_jax_amd import _lib
-    # INT8 planes need rho >= 19 (|q| <= 64) and an all-pairs schedule: the
-    # presets and the custom schedules (1,1)-(1,4), (2,1)-(2,3), (3,2), (3,3)
-    # and (4,2); others, such as (5,1), (2,4) and (4,4), run on BF16 planes
-    rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, 18, 4, 1, None, None, None, None, 0, None)
-    assert rc == _lib.OZK_ERR_UNSUPPORTED and b"rho >= 19" in lib.ozk_last_error()
-    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 18, 4, 1, 0, None, 4,
-                         None, 0, None)
-    assert rc == _lib.OZK_ERR_UNSUPPORTED
-    for nh, nl in ((5, 1), (2, 4), (4, 4)):
-        rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, nh, nl, 0, None, 4,
-                             None, 0, None)
-        assert rc == _lib.OZK_ERR_UNSUPPORTED and b"all-pairs" in lib.ozk_last_error()
-        rc = lib.ozk_slice_products_i8(None, None, 4, 4, 8192, 19, nh, nl, None, 4, None)
+    # INT8 planes need 19 <= rho <= 24 (|q| <= 64, stored with an offset of
+    # at most 63) and an all-pairs schedule: the presets and the custom
+    # schedules (1,1)-(1,4), (2,1)-(2,3), (3,2), (3,3) and (4,2); others,
+    # such as (5,1), (2,4) and (4,4), run on BF16 planes
+    for rho in (18, 25):
+        rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, rho, 4, 1, None, None, None, None, None,
+                                    0, None)
+        assert rc == _lib.OZK_ERR_UNSUPPORTED and b"19 <= rho <= 24" in lib.ozk_last_error()
+        rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, rho, 4, 1, 0,
+                             None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED
-    rc = lib.ozk_gemm_i8(None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4,
+    for nh, nl in ((5, 1), (2, 4), (4, 4)):
+        rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, nh, nl, 0,
+                             None, 4, None, 0, None)
+        assert rc == _lib.OZK_ERR_UNSUPPORTED and b"all-pairs" in lib.ozk_last_error()
+        rc = lib.ozk_slice_products_i8(None, None, None, None, 4, 4, 8192, 19, nh, nl, None, 4,
+                                       None)
+        assert rc == _lib.OZK_ERR_UNSUPPORTED
+    rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4,
                          None, 0, None)
+    assert rc == _lib.OZK_ERR_INVALID
+    # the line sums are required
+    rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, 4, 1, 0, None, 4,
+                         None, 0, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"null pointer" in lib.ozk_last_error()
+    rc = lib.ozk_slice_products_i8(None, None, None, None, 4, 4, 8192, 19, 4, 1, None, 4, None)
     assert rc == _lib.OZK_ERR_INVALID
 
 

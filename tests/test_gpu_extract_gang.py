@@ -49,8 +49,11 @@ def to_np(t):
 
 
 def check_padding(pl, rows, cols):
-    g = to_np(pl.grid())
+    """Padding holds zero slices; INT8 line sums are those of the counts."""
+    g = to_np(pl.counts() if pl.i8 else pl.grid())
     assert not g[:, :, rows:].any() and not g[:, cols:, :].any(), "padding"
+    if pl.i8:
+        assert np.array_equal(to_np(pl.sums), g.astype(np.int64).sum(axis=2)), "line sums"
 
 
 LENGTHS = [1, 100, 511, 513, 1025, 2049, 4097, 5000, 8192, 8193]
@@ -88,8 +91,8 @@ def test_panel_f32_i8(ll, length, cols):
     sl, el = O.extract_cols_f32(lo, rho, 1)
     ref = np.concatenate([sh, sl]).transpose(0, 2, 1).astype(np.float64) * 2.0 ** (24 - rho)
     assert np.all(np.abs(ref) <= 64) and np.array_equal(ref, np.round(ref))
-    q = to_np(pl.grid())[:, :cols, :length]
-    assert np.array_equal(q, ref.astype(np.int8)), "int8 slices"
+    q = to_np(pl.counts())[:, :cols, :length]
+    assert np.array_equal(q, ref), "int8 slices"
     assert np.array_equal(to_np(pl.exponents()),
                           np.concatenate([eh, el]).astype(np.int32)), "exponents"
     check_padding(pl, length, cols)
@@ -132,6 +135,7 @@ def test_panel_nonfinite_columns(ll, length):
     sh, eh = O.extract_cols_f32(hi, rho, 4)
     sl, el = O.extract_cols_f32(lo, rho, 1)
     ref = np.concatenate([sh, sl]).transpose(0, 2, 1) * 2.0 ** (24 - rho)
-    q = to_np(pl.grid())[:, good, :length]
-    assert np.array_equal(q, ref.astype(np.int8)), "int8 slices"
+    q = to_np(pl.counts())[:, good, :length]
+    assert np.array_equal(q, ref), "int8 slices"
+    check_padding(pl, length, 20)
     assert np.array_equal(e[:, good], np.concatenate([eh, el]).astype(np.int32))

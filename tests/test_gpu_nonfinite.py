@@ -82,7 +82,7 @@ def test_extract_i8_nonfinite_lines(ll, length):
     for by_cols in (0, 1):
         case(f"ozk_extract_f32_i8 non-finite lines len={length} by_cols={by_cols}")
         pl = ll.extract(X.T.copy() if by_cols else X, by_cols, rho, n0, n1, i8=True)
-        q = pl.grid().cpu().numpy()[:, :10, :length].astype(np.float64)
+        q = pl.counts().cpu().numpy()[:, :10, :length].astype(np.float64)
         e = pl.exponents().cpu().numpy()
         for part, (s_ref, e_ref, p0, n) in enumerate([(sh, eh, 0, n0), (sl, el, n0, n1)]):
             for r in range(10):

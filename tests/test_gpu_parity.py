@@ -150,8 +150,10 @@ def test_extract_long_lines(ll, kind, shape, n0, n1, i8):
         assert np.array_equal(to_np(pl.values()), ref), "slices"
         assert np.array_equal(to_np(pl.exponents()),
                               np.concatenate([eh, el]).astype(np.int32)), "exponents"
-        g = to_np(pl.grid())
+        g = to_np(pl.counts() if i8 else pl.grid())
         assert not g[:, :, shape[1]:].any() and not g[:, shape[0]:, :].any(), "padding"
+        if i8:
+            assert np.array_equal(to_np(pl.sums), g.astype(np.int64).sum(axis=2)), "line sums"
 
 
 def test_extract_log2_edge_fixture(ll, golden_dir):
@@ -218,18 +220,19 @@ def test_extract_f32_i8_rows_and_cols(ll, kind, shape, rho_fixed):
         sl, el = O.extract_rows_f32(lo, rho, 1)
         ref = np.concatenate([sh, sl]).astype(np.float64) * 2.0 ** (24 - rho)
         assert np.all(np.abs(ref) <= 64) and np.array_equal(ref, np.round(ref))
-        q = to_np(pl.grid())[:, :shape[0], :shape[1]]
-        assert np.array_equal(q, ref.astype(np.int8)), "int8 slices"
+        g = to_np(pl.counts())
+        assert np.array_equal(g[:, :shape[0], :shape[1]], ref), "int8 slices"
         assert np.array_equal(to_np(pl.exponents()),
                               np.concatenate([eh, el]).astype(np.int32)), "exponents"
-        # padding stays zero (the GEMM reads it)
-        g = to_np(pl.grid())
+        # padding holds zero slices (the GEMM reads it); the line sums are
+        # those of the counts, padding lines included
         assert not g[:, :, shape[1]:].any() and not g[:, shape[0]:, :].any()
+        assert np.array_equal(to_np(pl.sums), g.astype(np.int64).sum(axis=2)), "line sums"
 
 
 def test_extract_i8_rejects_coarse_grid(ll):
     case("ozk_extract_f32_i8 rho=18 -> unsupported")
-    with pytest.raises(NotImplementedError, match="rho >= 19"):
+    with pytest.raises(NotImplementedError, match="19 <= rho"):
         ll.extract(np.ones((4, 4)), 0, 18, 4, 1, i8=True)
 
 
