@@ -171,7 +171,17 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
   static_assert((BLOCK * VEC) % kPer == 0, "BLOCK * VEC must hold whole chunks");
   const int64_t off0 = plane_offset<sizeof(T)>(line, (int64_t)t * VEC, eplane);
   const int64_t step = (int64_t)(BLOCK * VEC / kPer) * eplane * kPer;
-  W R[NP][EPT * VEC];
+  // 512-thread workgroups whose threads hold 32 elements keep the lo parts
+  // in LDS (64 KiB) and only the hi parts in registers, so that two of them
+  // fit on a CU rather than one.  (For 256 threads x 32 elements the
+  // registers alone were faster: 3 workgroups per CU, no LDS traffic.)
+  constexpr bool kLoLds = NP == 2 && BLOCK * LPB == 512 && EPT * VEC == 32;
+  __shared__ float lo[kLoLds ? EPT * VEC : 1][kLoLds ? BLOCK * LPB : 1];
+  W Rr[kLoLds ? 1 : NP][EPT * VEC];
+  auto R = [&](int q, int i) -> W& {
+    if constexpr (kLoLds) return q == 0 ? Rr[0][i] : lo[i][threadIdx.x];
+    else return Rr[q][i];
+  };
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
@@ -194,7 +204,7 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
       W p[NP];
       split<W>(v[u], p);
 #pragma unroll
-      for (int q = 0; q < NP; ++q) R[q][j * VEC + u] = p[q];
+      for (int q = 0; q < NP; ++q) R(q, j * VEC + u) = p[q];
     }
   }
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
@@ -206,7 +216,7 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
     for (int q = 0; q < NP; ++q) {
       m[q] = W(0);
 #pragma unroll
-      for (int j = 0; j < EPT * VEC; ++j) m[q] = max_w(m[q], fabs(R[q][j]));
+      for (int j = 0; j < EPT * VEC; ++j) m[q] = max_w(m[q], fabs(R(q, j)));
       m[q] = line_max_input<FMT>(m[q], bad);
     }
     block_max2<W, BLOCK, LPB, NP>(m, red);
@@ -227,10 +237,10 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
         } pk;
 #pragma unroll
         for (int u = 0; u < VEC; ++u) {
-          W r = R[q][j * VEC + u];
+          W r = R(q, j * VEC + u);
           W v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = W(0);
-          R[q][j * VEC + u] = r - v;
+          R(q, j * VEC + u) = r - v;
           const float sv = slice_value_f32(v, kc.inv);
           pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
         }
@@ -620,7 +630,11 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
   const int64_t step = (int64_t)(kRowThreads * V / kPer) * eplane * kPer;
   uint32_t* const my = rec + line * ns * kWords;
 
-  float R[NP][EPT * V];
+  // The run's hi parts stay in registers and its lo parts in LDS (64 KiB),
+  // so two workgroups fit on a CU.
+  __shared__ float lo[EPT * V][kRowThreads];
+  float hi[EPT * V];
+  auto R = [&](int q, int i) -> float& { return q == 0 ? hi[i] : lo[i][t]; };
   bool bad = false;
 #pragma unroll
   for (int j = 0; j < EPT; ++j) {
@@ -643,7 +657,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
       float p[NP];
       split<float>(v[u], p);
 #pragma unroll
-      for (int q = 0; q < NP; ++q) R[q][j * V + u] = p[q];
+      for (int q = 0; q < NP; ++q) R(q, j * V + u) = p[q];
     }
   }
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
@@ -655,7 +669,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
     for (int q = 0; q < NP; ++q) {
       m[q] = 0.0f;
 #pragma unroll
-      for (int j = 0; j < EPT * V; ++j) m[q] = max_w(m[q], fabsf(R[q][j]));
+      for (int j = 0; j < EPT * V; ++j) m[q] = max_w(m[q], fabsf(R(q, j)));
       m[q] = line_max_input<FMT>(m[q], bad);
     }
     block_max2<float, kRowThreads, 1, NP>(m, red);  // the run's maxima
@@ -694,10 +708,10 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
         } pk;
 #pragma unroll
         for (int u = 0; u < V; ++u) {
-          const float r = R[q][j * V + u];
+          const float r = R(q, j * V + u);
           float v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = 0.0f;
-          R[q][j * V + u] = r - v;
+          R(q, j * V + u) = r - v;
           const float sv = slice_value_f32(v, kc.inv);
           pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
         }
