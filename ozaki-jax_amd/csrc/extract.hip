@@ -240,7 +240,11 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
           W r = R(q, j * VEC + u);
           W v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = W(0);
-          R(q, j * VEC + u) = r - v;
+          W rn = r - v;
+          // pinned here: otherwise the residual updates sink below the
+          // stores and every v stays live meanwhile
+          asm volatile("" : "+v"(rn));
+          R(q, j * VEC + u) = rn;
           const float sv = slice_value_f32(v, kc.inv);
           pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
         }
@@ -399,8 +403,10 @@ __device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
 // column at part[(pl G + m) eplane + column] (added up by i8_sum_parts):
 // the packed bytes (q + offset) of all kGangRun rows, rows past the column's
 // end included (q = 0 there), less offset x kGangRun.
+// Bounded to 80 VGPRs (six waves per SIMD): three members per CU, which
+// cover each other's exchange waits, without spills.
 template <int FMT, bool VEC>
-__global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
+__global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6))) void extract_cols_gang(
     const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
@@ -543,7 +549,9 @@ __global__ __launch_bounds__(kGangThreads) void extract_cols_gang(
           const float r = Rg[q][c][i];
           float v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = 0.0f;
-          Rg[q][c][i] = r - v;
+          float rn = r - v;
+          asm volatile("" : "+v"(rn));  // as in extract_lines_reg
+          Rg[q][c][i] = rn;
           const float sv = slice_value_f32(v, kc.inv);
           out.e[i] = PlaneElem<FMT>::make(sv, qscale);
         }
@@ -711,7 +719,9 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
           const float r = R(q, j * V + u);
           float v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = 0.0f;
-          R(q, j * V + u) = r - v;
+          float rn = r - v;
+          asm volatile("" : "+v"(rn));  // as in extract_lines_reg
+          R(q, j * V + u) = rn;
           const float sv = slice_value_f32(v, kc.inv);
           pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
         }
