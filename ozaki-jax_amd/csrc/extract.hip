@@ -139,6 +139,8 @@ template <> struct PlaneVec<kFmtI8, 2> { typedef uint16_t type; };
 template <> struct PlaneVec<kFmtI8, 4> { typedef uint32_t type; };
 template <> struct PlaneVec<kFmtBf16, 2> { typedef uint32_t type; };
 template <> struct PlaneVec<kFmtBf16, 4> { typedef uint2 type; };
+template <> struct PlaneVec<kFmtI8, 8> { typedef uint2 type; };
+template <> struct PlaneVec<kFmtBf16, 8> { typedef uint4 type; };
 
 template <typename W, int BLOCK, int EPT, int LPB, int FMT, int VEC>
 __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
@@ -540,7 +542,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6)
         const int ce = plane_exponent<FMT>(kc, rho, flags, r0 == 0);
         const int64_t line = c0 + c;
         union {
-          typename std::conditional<FMT == kFmtI8, uint2, uint4>::type w;
+          typename PlaneVec<FMT, R>::type w;
           T e[R];
         } out;
         int qs = 0;
