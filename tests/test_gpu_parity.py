@@ -202,8 +202,8 @@ def test_extract_nonfinite_flag_long_lines(ll, length):
 # INT8 planes: q = slice * 2^(24 - rho), exact for rho >= 19.  Lines of
 # length > 4096 give rho >= 19 by themselves; shorter ones are run with an
 # explicit rho in [19, 24] (any rho is a valid extraction grid).
-I8_CASES = [((3, 5000), None), ((130, 4200), None), ((2, 9000), None),
-            ((64, 64), 19), ((77, 300), 21), ((5, 33), 24), ((1, 1), 19)]
+I8_CASES = [((3, 5000), None), ((130, 4200), None), ((2, 9000), None), ((3, 16384), None),
+            ((2, 20000), None), ((64, 64), 19), ((77, 300), 21), ((5, 33), 24), ((1, 1), 19)]
 
 
 @pytest.mark.parametrize("kind", ["randn", "wide", "zerorows"])
