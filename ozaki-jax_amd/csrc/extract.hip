@@ -43,7 +43,6 @@ template <> struct PlaneElem<kFmtI8> {
   }
 };
 
-// Sum over the 64 lanes of a wave.
 // acc + the sum of the signed bytes of w (one dot product with ones)
 __device__ __forceinline__ int byte_sum(uint32_t w, int acc) {
   return __builtin_amdgcn_sdot4((int)w, 0x01010101, acc, false);
@@ -51,6 +50,7 @@ __device__ __forceinline__ int byte_sum(uint32_t w, int acc) {
 __device__ __forceinline__ int byte_sum(uint16_t w, int acc) { return byte_sum((uint32_t)w, acc); }
 __device__ __forceinline__ int byte_sum(uint2 w, int acc) { return byte_sum(w.y, byte_sum(w.x, acc)); }
 
+// Sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_sum(int v) {
 #pragma unroll
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -405,10 +405,10 @@ __device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
 // column at part[(pl G + m) eplane + column] (added up by i8_sum_parts):
 // the packed bytes (q + offset) of all kGangRun rows, rows past the column's
 // end included (q = 0 there), less offset x kGangRun.
-// Bounded to 80 VGPRs (six waves per SIMD): three members per CU, which
-// cover each other's exchange waits, without spills.
+// Bounded to 64 VGPRs (eight waves per SIMD), with the lo parts in LDS:
+// four members per CU, which cover each other's exchange waits.
 template <int FMT, bool VEC>
-__global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6))) void extract_cols_gang(
+__global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8))) void extract_cols_gang(
     const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
@@ -444,7 +444,10 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6)
 
   // The one read.  The empty asm pins each part where it is made, so the
   // compiler does not hold the doubles until the non-finite check.
-  float Rg[NP][2][R];
+  // hi parts in registers, lo parts in LDS (32 KiB): four members per CU
+  float Rh[2][R];
+  __shared__ float lo_s[2 * R][kGangThreads];
+  auto Rg = [&](int q, int c, int i) -> float& { return q == 0 ? Rh[c][i] : lo_s[c * R + i][t]; };
   bool bad[2] = {false, false};
   const bool full = VEC && c0 + 1 < M;
 #pragma unroll
@@ -469,7 +472,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6)
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
         asm volatile("" : "+v"(p[q]));
-        Rg[q][c][i] = p[q];
+        Rg(q, c, i) = p[q];
       }
     }
   }
@@ -485,7 +488,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6)
       for (int c = 0; c < 2; ++c) {
         float mm = 0.0f;
 #pragma unroll
-        for (int i = 0; i < R; ++i) mm = max_w(mm, fabsf(Rg[q][c][i]));
+        for (int i = 0; i < R; ++i) mm = max_w(mm, fabsf(Rg(q, c, i)));
         mm = line_max_input<FMT>(mm, bad[c]);
 #pragma unroll
         for (int off = CP; off < 64; off <<= 1) mm = max_w(mm, __shfl_xor(mm, off));
@@ -548,12 +551,12 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(6)
         int qs = 0;
 #pragma unroll
         for (int i = 0; i < R; ++i) {
-          const float r = Rg[q][c][i];
+          const float r = Rg(q, c, i);
           float v = (r + kc.sigma) - kc.sigma;
           if (kc.zero) v = 0.0f;
           float rn = r - v;
           asm volatile("" : "+v"(rn));  // as in extract_lines_reg
-          Rg[q][c][i] = rn;
+          Rg(q, c, i) = rn;
           const float sv = slice_value_f32(v, kc.inv);
           out.e[i] = PlaneElem<FMT>::make(sv, qscale);
         }
