@@ -391,13 +391,17 @@ __device__ __forceinline__ void wait_stage(int64_t later) {
 // Fold state at a block boundary, kept in a workspace between the sweeps of
 // one product: 2Sum order (ct, cl, p0, p1, p2) as FP32 fields, the FP64
 // block order the running sum c.  Field f of element (row, col) lies at
-// state[f * N * M + row * M + col].
+// state[f * N * M + row * M + col].  DONE = the blocks folded before the
+// boundary: block lo parts p_DONE.. are still zero there, so they are
+// neither stored nor loaded.
 template <int ORDER> struct FoldState {  // the FP64 orders: the running sum
   static constexpr int kBytes = 8;
+  template <int DONE>
   static __device__ __forceinline__ void load(Fold64<ORDER>& f, const char* st, int64_t e,
                                               int64_t) {
     f.c = ((const double*)st)[e];
   }
+  template <int DONE>
   static __device__ __forceinline__ void store(const Fold64<ORDER>& f, char* st, int64_t e,
                                                int64_t) {
     ((double*)st)[e] = f.c;
@@ -406,23 +410,25 @@ template <int ORDER> struct FoldState {  // the FP64 orders: the running sum
 
 template <> struct FoldState<OZK_ORDER_2SUM> {
   static constexpr int kBytes = 5 * 4;
+  template <int DONE>
   static __device__ __forceinline__ void load(Fold2Sum& f, const char* st, int64_t e,
                                               int64_t nm) {
     const float* s = (const float*)st;
     f.ct = s[e];
     f.cl = s[nm + e];
-    f.p0 = s[2 * nm + e];
-    f.p1 = s[3 * nm + e];
-    f.p2 = s[4 * nm + e];
+    if constexpr (DONE > 0) f.p0 = s[2 * nm + e];
+    if constexpr (DONE > 1) f.p1 = s[3 * nm + e];
+    if constexpr (DONE > 2) f.p2 = s[4 * nm + e];
   }
+  template <int DONE>
   static __device__ __forceinline__ void store(const Fold2Sum& f, char* st, int64_t e,
                                                int64_t nm) {
     float* s = (float*)st;
     s[e] = f.ct;
     s[nm + e] = f.cl;
-    s[2 * nm + e] = f.p0;
-    s[3 * nm + e] = f.p1;
-    s[4 * nm + e] = f.p2;
+    if constexpr (DONE > 0) s[2 * nm + e] = f.p0;
+    if constexpr (DONE > 1) s[3 * nm + e] = f.p1;
+    if constexpr (DONE > 2) s[4 * nm + e] = f.p2;
   }
 };
 // ORDER value of the test hook that writes the per-pair products P.
@@ -520,7 +526,8 @@ __device__ __forceinline__ void tile_epilogue(
         fr[r].init();
         if constexpr (B0 > 0) {
           const int64_t row = rbase + 16 * h + r;
-          if (row < N && col < M) FoldState<ORDER>::load(fr[r], state, row * M + col, nm);
+          if (row < N && col < M)
+            FoldState<ORDER>::template load<B0>(fr[r], state, row * M + col, nm);
         }
       }
       // One wait for all of them here: the folds below sit in branches on
@@ -563,7 +570,7 @@ __device__ __forceinline__ void tile_epilogue(
             if (tm != tn) C[col * ldc + row] = out;
           }
         } else if constexpr (B1 < NBLK - 1) {
-          if (live) FoldState<ORDER>::store(f, state, row * M + col, nm);
+          if (live) FoldState<ORDER>::template store<B1 + 1>(f, state, row * M + col, nm);
         } else if constexpr (ORDER == kOrderPair) {
           float hi, lo;
           f.finish_pair(NBLK, hi, lo);
