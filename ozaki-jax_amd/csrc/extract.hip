@@ -175,8 +175,8 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
   const int64_t step = (int64_t)(BLOCK * VEC / kPer) * eplane * kPer;
   // 512-thread workgroups whose threads hold 32 elements keep the lo parts
   // in LDS (64 KiB) and only the hi parts in registers, so that two of them
-  // fit on a CU rather than one.  (For 256 threads x 32 elements the
-  // registers alone were faster: 3 workgroups per CU, no LDS traffic.)
+  // fit on a CU rather than one.  (256 threads x 32 elements fit four per
+  // CU in registers alone, which was faster than with the LDS traffic.)
   constexpr bool kLoLds = NP == 2 && BLOCK * LPB == 512 && EPT * VEC == 32;
   __shared__ float lo[kLoLds ? EPT * VEC : 1][kLoLds ? BLOCK * LPB : 1];
   W Rr[kLoLds ? 1 : NP][EPT * VEC];
