@@ -661,18 +661,27 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
         coords(bid + jj * nwg, tm, tn);
         const int64_t col = (int64_t)tn * kBN + 16 * mma.wc + (lane & 15);
         const int64_t rb = (int64_t)tm * kBM + 32 * mma.wr + 4 * (lane >> 4);
-        int sb[NB];
+        // per plane once: o sb + Kp o^2 and -o sa (modulo 2^32, as i8_start)
+        uint32_t tb[NB];
 #pragma unroll
-        for (int q = 0; q < NB; ++q) sb[q] = fix.bs[(SW::BB + q) * b_lines + col];
+        for (int q = 0; q < NB; ++q)
+          tb[q] = fix.off * (uint32_t)fix.bs[(SW::BB + q) * b_lines + col] + fix.kpo2;
 #pragma unroll
         for (int h = 0; h < 2; ++h) {
-          int32x4 sa[NA];
+          uint32_t na[NA][4];
 #pragma unroll
-          for (int q = 0; q < NA; ++q)
-            sa[q] = *(const int32x4*)(fix.as + (SW::A0 + q) * a_lines + rb + 16 * h);
+          for (int q = 0; q < NA; ++q) {
+            const int32x4 sa = *(const int32x4*)(fix.as + (SW::A0 + q) * a_lines + rb + 16 * h);
 #pragma unroll
-          for (int k = 0; k < NP; ++k)
-            mma.acc[k][h] = i8_start(fix, sa[SW::la(k)], sb[SW::lb(k)]);
+            for (int i = 0; i < 4; ++i) na[q][i] = 0u - fix.off * (uint32_t)sa[i];
+          }
+#pragma unroll
+          for (int k = 0; k < NP; ++k) {
+            int32x4 v;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) v[i] = (int32_t)(na[SW::la(k)][i] - tb[SW::lb(k)]);
+            mma.acc[k][h] = v;
+          }
         }
         return;
       }
