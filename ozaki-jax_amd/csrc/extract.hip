@@ -1,8 +1,9 @@
 // Split + sigma-trick slice extraction kernels (bandwidth-bound).
 //
 // One workgroup owns one line (a row of X, or a row of X^T for column
-// extraction) and keeps the whole line's residual in registers, so X is read
-// from HBM once and every slice plane is written once.  Per slice the line
+// extraction) and keeps the whole line's residual on chip (registers, and
+// for the longest lines the lo parts in LDS), so X is read from HBM once and
+// every slice plane is written once.  Per slice the line
 // maximum comes from a wavefront butterfly + an LDS combine across waves.
 // Lines too long for one workgroup, and columns read in place, are held by
 // gangs of workgroups that exchange their partial maxima through global
@@ -343,9 +344,9 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
 // Column extraction without a transposed copy of X.  The columns are cut
 // into panels of kGangPW = 16 (a 128-byte row segment of X) and each panel's
 // rows into runs of kGangRun; workgroup ("member") m of the panel's gang of
-// G = ceil(rows / kGangRun) holds run m of all 16 columns in registers
-// (thread t: columns 2 (t % 8) and 2 (t % 8) + 1, rows 8 (t / 8) .. +7 of
-// the run, read as 16-byte pairs), so X is read once, in whole 128-byte row
+// G = ceil(rows / kGangRun) holds run m of all 16 columns on chip (thread
+// t: columns 2 (t % 8) and 2 (t % 8) + 1, rows 8 (t / 8) .. +7 of the run,
+// read as 16-byte pairs; hi parts in registers, lo parts in LDS), so X is read once, in whole 128-byte row
 // segments, and every plane element is written once.  The arithmetic is
 // extract_lines_reg's; only the per-slice line maxima cross workgroups.
 //
@@ -585,9 +586,9 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
 // Row extraction of lines longer than one workgroup holds (FP32 path,
 // padded length 32769 .. kRowRun * kRowMaxMembers): each line is cut into
 // runs of kRowRun elements, one per workgroup ("member") of the line's gang
-// of G = ceil(ld / kRowRun), which holds its run in registers with
-// extract_lines_reg's layout (thread t: elements base + (512 j + t) * 4 + v)
-// and arithmetic.  Per slice the members exchange the run maxima of both
+// of G = ceil(ld / kRowRun), which holds its run on chip with
+// extract_lines_reg's layout (thread t: elements base + (512 j + t) * 4 + v;
+// hi parts in registers, lo parts in LDS) and arithmetic.  Per slice the members exchange the run maxima of both
 // parts, as extract_cols_gang does: member m stores its two order keys
 // into words 2 m, 2 m + 1 of the (line, slice) record (128 bytes, zeroed
 // before the launch), then every member waits for all 2 G words.  Places
