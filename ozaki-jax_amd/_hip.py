@@ -10,11 +10,17 @@ with the library's kernels, which this family launches there too.
 Device memory comes from a caching pool: blocks are rounded to size classes
 and kept for reuse after their arrays are garbage collected, so repeated
 calls of one shape allocate nothing after the first.
+
+Host copies of large arrays go through two pinned staging buffers: host
+threads copy one chunk between the NumPy array and a staging buffer while
+the DMA engine moves the other (a direct copy from pageable memory, and
+the page faults of a fresh output array, are otherwise serial).
 """
 
 import ctypes
 import os
 import threading
+from concurrent.futures import ThreadPoolExecutor
 
 import numpy as np
 
@@ -40,6 +46,11 @@ class _Runtime:
         vp, sz, i = ctypes.c_void_p, ctypes.c_size_t, ctypes.c_int
         for name, args in [("hipMalloc", [ctypes.POINTER(vp), sz]), ("hipFree", [vp]),
                            ("hipMemcpy", [vp, vp, sz, i]),
+                           ("hipMemcpyAsync", [vp, vp, sz, i, vp]),
+                           ("hipHostMalloc", [ctypes.POINTER(vp), sz, ctypes.c_uint]),
+                           ("hipEventCreate", [ctypes.POINTER(vp)]),
+                           ("hipEventRecord", [vp, vp]),
+                           ("hipEventSynchronize", [vp]),
                            ("hipStreamSynchronize", [vp]),
                            ("hipGetDeviceCount", [ctypes.POINTER(i)]),
                            ("hipGetLastError", [])]:
@@ -78,6 +89,85 @@ class _Runtime:
 
     def sync(self):
         self.check(self.h.hipStreamSynchronize(None), "hipStreamSynchronize")
+
+    def host_malloc(self, nbytes):
+        p = ctypes.c_void_p()
+        self.check(self.h.hipHostMalloc(ctypes.byref(p), nbytes, 0), f"hipHostMalloc({nbytes})")
+        return p.value
+
+    def copy_async(self, dst, src, nbytes, kind):
+        self.check(self.h.hipMemcpyAsync(dst, src, nbytes, kind, None), "hipMemcpyAsync")
+
+    def event(self):
+        e = ctypes.c_void_p()
+        self.check(self.h.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
+        return e.value
+
+    def record(self, e):
+        self.check(self.h.hipEventRecord(e, None), "hipEventRecord")
+
+    def wait(self, e):
+        self.check(self.h.hipEventSynchronize(e), "hipEventSynchronize")
+
+
+# Host copies of at least _STAGE_MIN bytes are staged in _STAGE_CHUNK pieces.
+_STAGE_MIN = 32 << 20
+_STAGE_CHUNK = 64 << 20
+
+
+class _Stager:
+    """Two pinned buffers of `chunk` bytes (allocated once, kept for the
+    process), an event per buffer on the null stream, and a thread pool for
+    the host-side copies.  One transfer at a time (a lock)."""
+
+    def __init__(self, rt, chunk=_STAGE_CHUNK):
+        self.rt, self.chunk = rt, int(chunk)
+        self.buf = [rt.host_malloc(self.chunk) for _ in range(2)]
+        self.ev = [rt.event() for _ in range(2)]
+        self.nthreads = max(1, min(8, os.cpu_count() or 1))
+        self.pool = ThreadPoolExecutor(self.nthreads)
+        self.lock = threading.Lock()
+
+    def _host_copy(self, dst, src):
+        """dst[:] = src for two flat uint8 arrays, split over the threads."""
+        n = dst.size
+        step = -(-n // self.nthreads)
+        parts = [(a, min(a + step, n)) for a in range(0, n, step)]
+        list(self.pool.map(lambda ab: np.copyto(dst[ab[0]:ab[1]], src[ab[0]:ab[1]]), parts))
+
+    def _staging(self, i, n):
+        return np.ctypeslib.as_array((ctypes.c_uint8 * n).from_address(self.buf[i]))
+
+    def to_device(self, dev_ptr, host):
+        """host: a C-contiguous array; its bytes to dev_ptr."""
+        src = host.reshape(-1).view(np.uint8)
+        with self.lock:
+            for k, a in enumerate(range(0, src.size, self.chunk)):
+                b = min(a + self.chunk, src.size)
+                i = k & 1
+                if k >= 2:
+                    self.rt.wait(self.ev[i])  # the DMA of chunk k - 2 has read buffer i
+                self._host_copy(self._staging(i, b - a), src[a:b])
+                self.rt.copy_async(dev_ptr + a, self.buf[i], b - a, _H2D)
+                self.rt.record(self.ev[i])
+            self.rt.sync()
+
+    def to_host(self, out, dev_ptr):
+        """out: a C-contiguous array; its bytes from dev_ptr."""
+        dst = out.reshape(-1).view(np.uint8)
+        with self.lock:
+            chunks = [(a, min(a + self.chunk, dst.size)) for a in range(0, dst.size, self.chunk)]
+            for k, (a, b) in enumerate(chunks[:2]):
+                self.rt.copy_async(self.buf[k], dev_ptr + a, b - a, _D2H)
+                self.rt.record(self.ev[k])
+            for k, (a, b) in enumerate(chunks):
+                i = k & 1
+                self.rt.wait(self.ev[i])
+                self._host_copy(dst[a:b], self._staging(i, b - a))
+                if k + 2 < len(chunks):  # buffer i is free again
+                    a2, b2 = chunks[k + 2]
+                    self.rt.copy_async(self.buf[i], dev_ptr + a2, b2 - a2, _D2H)
+                    self.rt.record(self.ev[i])
 
 
 class _Pool:
@@ -181,7 +271,10 @@ class DeviceArray:
         a = np.ascontiguousarray(a)
         d = cls(a.shape, a.dtype)
         assert d.nbytes == a.nbytes
-        _rt().copy(d.data_ptr(), a.ctypes.data, a.nbytes, _H2D)
+        if a.nbytes >= _STAGE_MIN:
+            _stager().to_device(d.data_ptr(), a)
+        else:
+            _rt().copy(d.data_ptr(), a.ctypes.data, a.nbytes, _H2D)
         return d
 
     def numpy(self):
@@ -193,6 +286,8 @@ class DeviceArray:
             full = np.empty((self.shape[0], self.ld), self.dtype)
             _rt().copy(full.ctypes.data, self.data_ptr(), self.nbytes, _D2H)
             out[:] = full[:, :self.shape[1]]
+        elif out.nbytes >= _STAGE_MIN:
+            _stager().to_host(out, self.data_ptr())
         else:
             _rt().copy(out.ctypes.data, self.data_ptr(), out.nbytes, _D2H)
         return out
@@ -287,6 +382,10 @@ def _rt():
 
 def _pool():
     return _get("pool", lambda: _Pool(_rt()))
+
+
+def _stager():
+    return _get("stager", lambda: _Stager(_rt()))
 
 
 def blas():

@@ -132,3 +132,34 @@ def test_device_pool_reuses_blocks(no_torch):
     finally:
         pool.rt.malloc = real
     assert calls["n"] == 0 and sum(len(v) for v in pool.free.values()) >= before
+
+
+@pytest.mark.parametrize("nbytes,chunk", [(5 * (1 << 20) + 24, 1 << 20), (2 << 20, 1 << 20),
+                                          (3 << 20, 1 << 20), (1 << 20, 1 << 20),
+                                          (4096 + 8, 1 << 20)])
+def test_staged_transfers_round_trip(no_torch, nbytes, chunk):
+    """Host copies through the pinned staging buffers: chunk boundaries,
+    a final partial chunk, one and two chunks."""
+    from ozaki_jax_amd import _hip
+    rng = np.random.RandomState(nbytes % 1000)
+    a = rng.randn(nbytes // 8)
+    st = _hip._Stager(_hip._rt(), chunk)
+    case(f"staged H2D / D2H of {a.nbytes} bytes in {chunk}-byte chunks")
+    d = _hip.DeviceArray(a.shape)
+    st.to_device(d.data_ptr(), a)
+    assert np.array_equal(d.numpy(), a), "H2D"
+    out = np.empty_like(a)
+    st.to_host(out, d.data_ptr())
+    assert np.array_equal(out, a), "D2H"
+
+
+def test_large_array_round_trip(no_torch):
+    """An array above the staging threshold goes through the default stager
+    both ways."""
+    from ozaki_jax_amd import _hip
+    rng = np.random.RandomState(11)
+    n = (_hip._STAGE_MIN + 2 * _hip._STAGE_CHUNK) // 8 + 1000
+    a = rng.randn(n // 1000, 1000)
+    case(f"DeviceArray round trip of {a.nbytes} bytes (staged)")
+    d = _hip.DeviceArray.from_numpy(a)
+    assert np.array_equal(d.numpy(), a)
