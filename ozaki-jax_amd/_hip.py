@@ -142,32 +142,38 @@ class _Stager:
         """host: a C-contiguous array; its bytes to dev_ptr."""
         src = host.reshape(-1).view(np.uint8)
         with self.lock:
-            for k, a in enumerate(range(0, src.size, self.chunk)):
-                b = min(a + self.chunk, src.size)
-                i = k & 1
-                if k >= 2:
-                    self.rt.wait(self.ev[i])  # the DMA of chunk k - 2 has read buffer i
-                self._host_copy(self._staging(i, b - a), src[a:b])
-                self.rt.copy_async(dev_ptr + a, self.buf[i], b - a, _H2D)
-                self.rt.record(self.ev[i])
-            self.rt.sync()
+            try:
+                for k, a in enumerate(range(0, src.size, self.chunk)):
+                    b = min(a + self.chunk, src.size)
+                    i = k & 1
+                    if k >= 2:
+                        self.rt.wait(self.ev[i])  # the DMA of chunk k - 2 has read buffer i
+                    self._host_copy(self._staging(i, b - a), src[a:b])
+                    self.rt.copy_async(dev_ptr + a, self.buf[i], b - a, _H2D)
+                    self.rt.record(self.ev[i])
+            finally:  # no copy may still read the buffers once the lock is free
+                self.rt.sync()
 
     def to_host(self, out, dev_ptr):
         """out: a C-contiguous array; its bytes from dev_ptr."""
         dst = out.reshape(-1).view(np.uint8)
         with self.lock:
             chunks = [(a, min(a + self.chunk, dst.size)) for a in range(0, dst.size, self.chunk)]
-            for k, (a, b) in enumerate(chunks[:2]):
-                self.rt.copy_async(self.buf[k], dev_ptr + a, b - a, _D2H)
-                self.rt.record(self.ev[k])
-            for k, (a, b) in enumerate(chunks):
-                i = k & 1
-                self.rt.wait(self.ev[i])
-                self._host_copy(dst[a:b], self._staging(i, b - a))
-                if k + 2 < len(chunks):  # buffer i is free again
-                    a2, b2 = chunks[k + 2]
-                    self.rt.copy_async(self.buf[i], dev_ptr + a2, b2 - a2, _D2H)
-                    self.rt.record(self.ev[i])
+            try:
+                for k, (a, b) in enumerate(chunks[:2]):
+                    self.rt.copy_async(self.buf[k], dev_ptr + a, b - a, _D2H)
+                    self.rt.record(self.ev[k])
+                for k, (a, b) in enumerate(chunks):
+                    i = k & 1
+                    self.rt.wait(self.ev[i])
+                    self._host_copy(dst[a:b], self._staging(i, b - a))
+                    if k + 2 < len(chunks):  # buffer i is free again
+                        a2, b2 = chunks[k + 2]
+                        self.rt.copy_async(self.buf[i], dev_ptr + a2, b2 - a2, _D2H)
+                        self.rt.record(self.ev[i])
+            except BaseException:
+                self.rt.sync()  # no copy may still write the buffers once the lock is free
+                raise
 
 
 class _Pool:
