@@ -38,6 +38,30 @@ _NO_GPU = ("ozaki_jax_amd needs a ROCm GPU; there is no CPU implementation "
            "(no HIP device found).")
 
 
+def _numpy_to_torch(a, dev):
+    """A contiguous NumPy array as a device tensor.  Large ones go through
+    the pinned staging buffers (_hip), after torch's current stream has
+    drained (the copy runs on the null stream)."""
+    if a.nbytes < _hip._STAGE_MIN:
+        return torch.from_numpy(a).to(dev)
+    t = torch.empty(a.shape, dtype=_TORCH_DTYPES[a.dtype], device=dev)
+    torch.cuda.current_stream(dev).synchronize()
+    _hip._stager().to_device(t.data_ptr(), a)
+    return t
+
+
+def _torch_to_numpy(t):
+    """A device tensor as a new NumPy array, large contiguous ones through the
+    pinned staging buffers."""
+    if (not t.is_cuda or not t.is_contiguous() or t.dtype not in _NUMPY_DTYPES
+            or t.numel() * t.element_size() < _hip._STAGE_MIN):
+        return t.cpu().numpy()
+    out = np.empty(tuple(t.shape), _NUMPY_DTYPES[t.dtype])
+    torch.cuda.current_stream(t.device).synchronize()
+    _hip._stager().to_host(out, t.data_ptr())
+    return out
+
+
 class _TorchFamily:
     """Torch tensors on torch's current device and stream."""
 
@@ -63,7 +87,7 @@ class _TorchFamily:
                 t = t.to(self.dev)
         else:
             a = np.ascontiguousarray(np.asarray(x, dtype=np.float64))
-            t = torch.from_numpy(a).to(self.dev)
+            t = _numpy_to_torch(a, self.dev)
         if t.dim() >= 1 and t.numel() > 0 and t.stride(-1) != 1:
             t = t.contiguous()
         if t.dim() == 2 and t.numel() > 0 and t.stride(0) < max(t.shape[1], 1):
@@ -94,7 +118,7 @@ class _TorchFamily:
         return v[:, 0]
 
     def out(self, t, want_torch):
-        return t if want_torch else t.cpu().numpy()
+        return t if want_torch else _torch_to_numpy(t)
 
     def matmul(self, A, B):
         """FP64 A @ B."""
@@ -165,9 +189,11 @@ class _HipFamily:
 
 
 _TORCH_DTYPES = {}
+_NUMPY_DTYPES = {}
 if torch is not None:
     _TORCH_DTYPES = {np.dtype(np.float64): torch.float64, np.dtype(np.float32): torch.float32,
                      np.dtype(np.int32): torch.int32, np.dtype(np.uint8): torch.uint8}
+    _NUMPY_DTYPES = {v: k for k, v in _TORCH_DTYPES.items()}
 
 
 def family(want_torch):
@@ -214,7 +240,7 @@ def to_family(t, want_torch):
     """Return device tensor `t` as a torch tensor or as a NumPy array."""
     if want_torch:
         return t
-    return t.cpu().numpy()
+    return _torch_to_numpy(t)
 
 
 def ptr(t):

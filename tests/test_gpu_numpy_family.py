@@ -163,3 +163,23 @@ def test_large_array_round_trip(no_torch):
     case(f"DeviceArray round trip of {a.nbytes} bytes (staged)")
     d = _hip.DeviceArray.from_numpy(a)
     assert np.array_equal(d.numpy(), a)
+
+
+def test_torch_staged_conversions(ozk):
+    """NumPy <-> torch device conversions above the staging threshold (the
+    torch family's inputs from NumPy and its NumPy outputs)."""
+    import torch
+    from ozaki_jax_amd import _device as D, _hip
+    rng = np.random.RandomState(12)
+    a = rng.randn(_hip._STAGE_MIN // 8 // 1000 + 700, 1000)
+    dev = torch.device("cuda", torch.cuda.current_device())
+    case(f"numpy -> torch -> numpy of {a.nbytes} bytes (staged)")
+    t = D._numpy_to_torch(a, dev)
+    assert t.device == dev and np.array_equal(t.cpu().numpy(), a)
+    assert np.array_equal(D._torch_to_numpy(t * 2.0), a * 2.0)
+    case("solve on NumPy input through the staged conversions")
+    n = 2100
+    A = rng.randn(n, n) + n * np.eye(n)
+    b = rng.randn(n)
+    x = ozk.solve(A, b)
+    assert isinstance(x, np.ndarray) and np.linalg.norm(A @ x - b) <= 1e-12 * np.linalg.norm(b) * n
