@@ -266,6 +266,22 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
                int pipeline, int n_hi, int n_lo, int order,
                void* workspace, size_t workspace_bytes, uint32_t* flags,
                void* stream);
+/* ozk_matmul, and also a copy of the call's final flag word to host_flags
+ * (pinned host memory, e.g. from hipHostMalloc), then `event` (a hipEvent_t)
+ * recorded on `stream`.  Both come as soon as the kernels that set flags
+ * (the extraction) are queued, ahead of the GEMM.  A caller that waits for
+ * `event` and reads *host_flags has the call's flags without waiting for
+ * the product, so it can raise or fall back as matmul.py:127-135 does while
+ * the GEMM still runs.  This serves callers whose result is ordered on the
+ * stream, as a JAX or torch array is (the reference's calls return JAX
+ * arrays, matmul.py:781-851).  It has no counterpart of its own in the
+ * reference. */
+int ozk_matmul_early_flags(const double* A, int64_t lda, const double* B,
+                           int64_t ldb, double* C, int64_t ldc, int64_t N,
+                           int64_t K, int64_t M, int pipeline, int n_hi,
+                           int n_lo, int order, void* workspace,
+                           size_t workspace_bytes, uint32_t* flags,
+                           uint32_t* host_flags, void* event, void* stream);
 
 /* ozk_matmul without a workspace argument, for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,

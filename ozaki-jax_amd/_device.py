@@ -10,6 +10,9 @@ libozaki_amd.so in both.  Arrays cross into the library as (device pointer,
 leading dimension) pairs.
 """
 
+import ctypes
+import threading
+
 import numpy as np
 
 from . import _hip
@@ -62,6 +65,9 @@ def _torch_to_numpy(t):
     return out
 
 
+_early = threading.local()
+
+
 class _TorchFamily:
     """Torch tensors on torch's current device and stream."""
 
@@ -106,6 +112,29 @@ class _TorchFamily:
 
     def zero_flags(self):
         return torch.zeros(1, dtype=torch.int32, device=self.dev)
+
+    def early_flags(self):
+        """(host word, event, read) for ozk_matmul_early_flags: a pinned
+        host word and a HIP event of this thread and device, kept for the
+        process, and read() waiting for the event and returning the word.
+        The product stays ordered on the current stream, as torch's own
+        results are."""
+        slots = getattr(_early, "slots", None)
+        if slots is None:
+            slots = _early.slots = {}
+        slot = slots.get(self.dev.index)
+        if slot is None:
+            rt = _hip._rt()
+            with torch.cuda.device(self.dev):
+                word, ev = rt.host_malloc(4), rt.event()
+            word_v = ctypes.c_uint32.from_address(word)
+
+            def read():
+                rt.wait(ev)
+                return int(word_v.value)
+
+            slot = slots[self.dev.index] = (word, ev, read)
+        return slot
 
     def read_flags(self, f):
         """Synchronising read of a device flag word."""

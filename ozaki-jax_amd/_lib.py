@@ -88,6 +88,10 @@ SIGNATURES = {
     "ozk_matmul": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
                             _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                             _c_vp, _c_size, _c_vp, _c_vp]),
+    "ozk_matmul_early_flags": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64,
+                                        _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int,
+                                        _c_int, _c_vp, _c_size, _c_vp, _c_vp, _c_vp,
+                                        _c_vp]),
     "ozk_matmul_noalloc": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_i64,
                                     _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                     _c_vp, _c_vp]),

@@ -469,10 +469,22 @@ int ozk_matmul_plane_bytes(int pipeline, int64_t K, int n_hi, int n_lo) {
   return i8 ? 1 : 2;
 }
 
-int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
-               double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
-               int pipeline, int n_hi, int n_lo, int order, void* workspace,
-               size_t workspace_bytes, uint32_t* flags, void* stream) {
+// After the kernels that set flags (the fill and the extraction), copy the
+// flag word to host_flags and record `event`, when given: the caller can
+// then read the flags without waiting for the GEMM queued behind.
+static int flags_to_host(const uint32_t* flags, uint32_t* host_flags, void* event,
+                         hipStream_t st) {
+  if (!host_flags) return OZK_OK;
+  OZK_HIP(hipMemcpyAsync(host_flags, flags, sizeof(uint32_t), hipMemcpyDeviceToHost, st));
+  OZK_HIP(hipEventRecord((hipEvent_t)event, st));
+  return OZK_OK;
+}
+
+static int matmul_call(const double* A, int64_t lda, const double* B, int64_t ldb,
+                       double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
+                       int pipeline, int n_hi, int n_lo, int order, void* workspace,
+                       size_t workspace_bytes, uint32_t* flags, uint32_t* host_flags,
+                       void* event, void* stream) {
   clear_error();
   hipStream_t st = (hipStream_t)stream;
   const int pipe_arg = pipeline;
@@ -488,7 +500,7 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
                 "leading dimension smaller than the row length");
   OZK_CHECK_ARG(flags, "null flags pointer");
   if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
-  if (N == 0 || M == 0) return OZK_OK;
+  if (N == 0 || M == 0) return flags_to_host(flags, host_flags, event, st);
   const size_t need = ozk_matmul_workspace_bytes(N, K, M, pipe_arg, n_hi, n_lo);
   if (!workspace || workspace_bytes < need) {
     set_error("matmul: workspace of %zu bytes needed, %zu given", need,
@@ -519,8 +531,28 @@ int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
                               tws, tbytes, st, false, nullptr)))
       return rc;
   }
+  if ((rc = flags_to_host(flags, host_flags, event, st))) return rc;
   return launch_gemm(sa.s, sa.e, sb.s, sb.e, N, M, K, pipeline, n_hi, n_lo,
                      order, C, ldc, gws, gwsb, st, i8, rho, sa.sum, sb.sum);
+}
+
+int ozk_matmul(const double* A, int64_t lda, const double* B, int64_t ldb,
+               double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
+               int pipeline, int n_hi, int n_lo, int order, void* workspace,
+               size_t workspace_bytes, uint32_t* flags, void* stream) {
+  return matmul_call(A, lda, B, ldb, C, ldc, N, K, M, pipeline, n_hi, n_lo, order,
+                     workspace, workspace_bytes, flags, nullptr, nullptr, stream);
+}
+
+int ozk_matmul_early_flags(const double* A, int64_t lda, const double* B, int64_t ldb,
+                           double* C, int64_t ldc, int64_t N, int64_t K, int64_t M,
+                           int pipeline, int n_hi, int n_lo, int order, void* workspace,
+                           size_t workspace_bytes, uint32_t* flags, uint32_t* host_flags,
+                           void* event, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(host_flags && event, "null host flag word or event");
+  return matmul_call(A, lda, B, ldb, C, ldc, N, K, M, pipeline, n_hi, n_lo, order,
+                     workspace, workspace_bytes, flags, host_flags, event, stream);
 }
 
 static size_t gram_ws(int64_t rows, int64_t cols, int nhi, int nlo, void* ws,

@@ -121,15 +121,22 @@ def _run_matmul(fam, At, Bt, pipeline, n_hi, n_lo, order):
     if N == 0 or M == 0:
         return C, 0
     flags = fam.flags()  # cleared by the call
+    early = getattr(fam, "early_flags", None)
 
     def run(pipe):
         wsb = lib.ozk_matmul_workspace_bytes(N, K, M, pipe, n_hi, n_lo)
         ws = fam.workspace(wsb)
-        _lib.check(lib.ozk_matmul(
-            At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
-            D.ld_of(C), N, K, M, pipe, n_hi, n_lo, order, ws.data_ptr(), wsb,
-            flags.data_ptr(), fam.stream()))
-        return _lib.check_flags(fam.read_flags(flags))
+        args = (At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
+                D.ld_of(C), N, K, M, pipe, n_hi, n_lo, order, ws.data_ptr(), wsb,
+                flags.data_ptr())
+        if early is None:
+            _lib.check(lib.ozk_matmul(*args, fam.stream()))
+            return _lib.check_flags(fam.read_flags(flags))
+        # torch tensors: the flags are read once the extraction has run, and
+        # C is returned while the GEMM is still queued on the current stream
+        word, ev, read = early()
+        _lib.check(lib.ozk_matmul_early_flags(*args, word, ev, fam.stream()))
+        return _lib.check_flags(read())
 
     fl = run(pipeline)
     if (fl & _lib.OZK_FLAG_INF_SLICE and order == _lib.ORDER_BLOCK64
