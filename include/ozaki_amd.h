@@ -309,6 +309,14 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
              int n_hi, int n_lo, double* G, int64_t ldg,
              void* workspace, size_t workspace_bytes, uint32_t* flags,
              void* stream);
+/* ozk_gram with the flag word copied to host_flags and `event` recorded
+ * once the column extraction is queued, as ozk_matmul_early_flags does
+ * (the reference's gram returns a JAX array, gram.py:47-99). */
+int ozk_gram_early_flags(const double* A, int64_t lda, int64_t rows,
+                         int64_t cols, int n_hi, int n_lo, double* G,
+                         int64_t ldg, void* workspace, size_t workspace_bytes,
+                         uint32_t* flags, uint32_t* host_flags, void* event,
+                         void* stream);
 
 /* residual(A, x, b, mode="ozaki"): r = b - Ozaki(A, x) in order 2SUM with
  * rho = ozk_rho_f32(K); x is K x ncols, b and r are N x ncols

@@ -98,6 +98,9 @@ SIGNATURES = {
     "ozk_gram_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_int, _c_int]),
     "ozk_gram": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp,
                           _c_i64, _c_vp, _c_size, _c_vp, _c_vp]),
+    "ozk_gram_early_flags": (_c_int, [_c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int,
+                                      _c_vp, _c_i64, _c_vp, _c_size, _c_vp, _c_vp, _c_vp,
+                                      _c_vp]),
     "ozk_residual_workspace_bytes": (_c_size, [_c_i64, _c_i64, _c_i64, _c_int,
                                                _c_int]),
     "ozk_residual": (_c_int, [_c_vp, _c_i64, _c_vp, _c_i64, _c_vp, _c_i64, _c_vp,

@@ -581,9 +581,10 @@ size_t ozk_gram_workspace_bytes(int64_t rows, int64_t cols, int n_hi,
   return gram_ws(rows, cols, n_hi, n_lo, nullptr, nullptr, nullptr);
 }
 
-int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
-             int n_hi, int n_lo, double* G, int64_t ldg, void* workspace,
-             size_t workspace_bytes, uint32_t* flags, void* stream) {
+static int gram_call(const double* A, int64_t lda, int64_t rows, int64_t cols, int n_hi,
+                     int n_lo, double* G, int64_t ldg, void* workspace,
+                     size_t workspace_bytes, uint32_t* flags, uint32_t* host_flags,
+                     void* event, void* stream) {
   clear_error();
   hipStream_t st = (hipStream_t)stream;
   int rc = check_counts(OZK_PIPE_ONDEVICE, n_hi, n_lo);
@@ -594,7 +595,7 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
                 "leading dimension too small");
   OZK_CHECK_ARG(flags, "null flags pointer");
   if ((rc = launch_fill_u32(flags, 0u, st))) return rc;
-  if (cols == 0) return OZK_OK;
+  if (cols == 0) return flags_to_host(flags, host_flags, event, st);
   const size_t need = ozk_gram_workspace_bytes(rows, cols, n_hi, n_lo);
   if (!workspace || workspace_bytes < need) {
     set_error("gram: workspace of %zu bytes needed, %zu given", need,
@@ -613,6 +614,7 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
                            flags, tws, extract_workspace_bytes(rows, cols, 1, false), st,
                            i8, s.sum)))
     return rc;
+  if ((rc = flags_to_host(flags, host_flags, event, st))) return rc;
   // high / medium: upper tiles only, the symmetrisation folded into the
   // epilogue.  max (three K sweeps): full product, then symmetrise.
   if (gram_sym_supported(n_hi, n_lo))
@@ -626,6 +628,23 @@ int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
                      0, st, G, cols, ldg);
   OZK_LAUNCH_CHECK();
   return OZK_OK;
+}
+
+int ozk_gram(const double* A, int64_t lda, int64_t rows, int64_t cols,
+             int n_hi, int n_lo, double* G, int64_t ldg, void* workspace,
+             size_t workspace_bytes, uint32_t* flags, void* stream) {
+  return gram_call(A, lda, rows, cols, n_hi, n_lo, G, ldg, workspace, workspace_bytes,
+                   flags, nullptr, nullptr, stream);
+}
+
+int ozk_gram_early_flags(const double* A, int64_t lda, int64_t rows, int64_t cols,
+                         int n_hi, int n_lo, double* G, int64_t ldg, void* workspace,
+                         size_t workspace_bytes, uint32_t* flags, uint32_t* host_flags,
+                         void* event, void* stream) {
+  clear_error();
+  OZK_CHECK_ARG(host_flags && event, "null host flag word or event");
+  return gram_call(A, lda, rows, cols, n_hi, n_lo, G, ldg, workspace, workspace_bytes,
+                   flags, host_flags, event, stream);
 }
 
 // Residual workspace.  Up to 4 right-hand sides with K <= 16384 (presets

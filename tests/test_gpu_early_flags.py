@@ -76,6 +76,41 @@ def test_early_flags_match_matmul(ozk, shape, nh, nl, order, kind):
     assert np.array_equal(C1.cpu().numpy(), C2.cpu().numpy(), equal_nan=True)
 
 
+@pytest.mark.parametrize("rows,cols,nh,nl,kind", [(9000, 200, 4, 1, None), (9000, 200, 4, 1, "nan"),
+                                                  (3000, 150, 5, 4, None), (300, 0, 4, 1, None)])
+def test_gram_early_flags_match_gram(ozk, rows, cols, nh, nl, kind):
+    import torch
+    from ozaki_jax_amd import _lib, _device as D
+    lib = _lib.load()
+    dev = torch.device("cuda", 0)
+    rng = np.random.RandomState(rows + cols)
+    A = rng.randn(rows, cols)
+    if kind == "nan":
+        A[rows // 2, cols // 3] = np.nan
+    At = torch.from_numpy(A).to(dev)
+    wsb = lib.ozk_gram_workspace_bytes(rows, cols, nh, nl)
+    ws = D.workspace(wsb, dev)
+
+    def run(fn, *extra):
+        G = torch.full((cols, cols), 7.0, dtype=torch.float64, device=dev)
+        f = torch.full((1,), -559038737, dtype=torch.int32, device=dev)
+        _lib.check(fn(At.data_ptr(), D.ld_of(At), rows, cols, nh, nl, G.data_ptr(),
+                      max(cols, 1), ws.data_ptr(), wsb, f.data_ptr(), *extra,
+                      D.stream_handle()))
+        return G, f
+
+    case(f"ozk_gram vs ozk_gram_early_flags ({rows},{cols}) ({nh},{nl}) {kind}")
+    G1, f1 = run(lib.ozk_gram)
+    fl1 = int(f1.item()) & 0xffffffff
+    word, ev, read = D._TorchFamily().early_flags()
+    G2, f2 = run(lib.ozk_gram_early_flags, word, ev)
+    early = read()
+    torch.cuda.synchronize()
+    assert early == int(f2.item()) & 0xffffffff == fl1
+    assert (fl1 & _lib.OZK_FLAG_NONFINITE) == (kind == "nan")
+    assert np.array_equal(G1.cpu().numpy(), G2.cpu().numpy(), equal_nan=True)
+
+
 def test_early_flags_rejects_null_host_word(ozk):
     import torch
     from ozaki_jax_amd import _lib, _device as D
@@ -84,12 +119,16 @@ def test_early_flags_rejects_null_host_word(ozk):
     A = torch.ones((8, 8), dtype=torch.float64, device=dev)
     C = torch.empty((8, 8), dtype=torch.float64, device=dev)
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
-    case("ozk_matmul_early_flags with a null host word")
+    case("ozk_matmul_early_flags / ozk_gram_early_flags with a null host word")
     with pytest.raises(ValueError, match="host flag word"):
         _lib.check(lib.ozk_matmul_early_flags(
             A.data_ptr(), 8, A.data_ptr(), 8, C.data_ptr(), 8, 8, 8, 8,
             _lib.PIPE_ONDEVICE, 4, 1, 0, None, 0, flags.data_ptr(), None, None,
             D.stream_handle()))
+    with pytest.raises(ValueError, match="host flag word"):
+        _lib.check(lib.ozk_gram_early_flags(
+            A.data_ptr(), 8, 8, 8, 4, 1, C.data_ptr(), 8, None, 0, flags.data_ptr(),
+            None, None, D.stream_handle()))
 
 
 def test_torch_matmul_returns_before_the_product_and_raises_on_nan(ozk):
