@@ -155,3 +155,23 @@ def test_torch_matmul_returns_before_the_product_and_raises_on_nan(ozk):
         ozk.matmul(A2t, Bt, pipeline="ondevice", precision="high")
     C = ozk.matmul(A2t, Bt, pipeline="ondevice", precision="high", safe_mode="fallback")
     assert np.array_equal(C.cpu().numpy(), torch.matmul(A2t, Bt).cpu().numpy(), equal_nan=True)
+
+
+def test_torch_matmul_and_gram_on_a_side_stream(ozk):
+    """Under `torch.cuda.stream(s)` the calls run, copy their flags and
+    record their events on s; results read after s has drained are exact."""
+    import torch
+    import oracle as O
+    dev = torch.device("cuda", 0)
+    rng = np.random.RandomState(6)
+    A, B = rng.randn(80, 6000), rng.randn(6000, 72)
+    At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    case("torch matmul and gram on a side stream")
+    with torch.cuda.stream(s):
+        C = ozk.matmul(At, Bt, pipeline="ondevice", accumulation="fused", precision="high")
+        G = ozk.gram(Bt, mode="ozaki", precision="high")
+    s.synchronize()
+    assert np.array_equal(C.cpu().numpy(), O.matmul_ondevice_a4(A, B, "raise", 4, 1))
+    assert np.array_equal(G.cpu().numpy(), ozk.gram(B, mode="ozaki", precision="high"))
