@@ -51,7 +51,9 @@ class _Runtime:
                            ("hipEventCreate", [ctypes.POINTER(vp)]),
                            ("hipEventRecord", [vp, vp]),
                            ("hipEventSynchronize", [vp]),
+                           ("hipEventDestroy", [vp]),
                            ("hipStreamSynchronize", [vp]),
+                           ("hipStreamCreateWithFlags", [ctypes.POINTER(vp), ctypes.c_uint]),
                            ("hipGetDeviceCount", [ctypes.POINTER(i)]),
                            ("hipGetLastError", [])]:
             fn = getattr(h, name)
@@ -87,8 +89,8 @@ class _Runtime:
         if nbytes:
             self.check(self.h.hipMemcpy(dst, src, nbytes, kind), "hipMemcpy")
 
-    def sync(self):
-        self.check(self.h.hipStreamSynchronize(None), "hipStreamSynchronize")
+    def sync(self, stream=None):
+        self.check(self.h.hipStreamSynchronize(stream), "hipStreamSynchronize")
 
     def host_malloc(self, nbytes):
         p = ctypes.c_void_p()
@@ -103,11 +105,22 @@ class _Runtime:
         self.check(self.h.hipEventCreate(ctypes.byref(e)), "hipEventCreate")
         return e.value
 
-    def record(self, e):
-        self.check(self.h.hipEventRecord(e, None), "hipEventRecord")
+    def record(self, e, stream=None):
+        self.check(self.h.hipEventRecord(e, stream), "hipEventRecord")
+
+    def nonblocking_stream(self):
+        """A stream that does not wait for the null stream's work, nor the
+        null stream for its (hipStreamNonBlocking), at the default priority."""
+        s = ctypes.c_void_p()
+        self.check(self.h.hipStreamCreateWithFlags(ctypes.byref(s), 1),
+                   "hipStreamCreateWithFlags")
+        return s.value
 
     def wait(self, e):
         self.check(self.h.hipEventSynchronize(e), "hipEventSynchronize")
+
+    def destroy_event(self, e):
+        self.check(self.h.hipEventDestroy(e), "hipEventDestroy")
 
 
 # Host copies of at least _STAGE_MIN bytes are staged in _STAGE_CHUNK pieces.
@@ -392,6 +405,12 @@ def _pool():
 
 def _stager():
     return _get("stager", lambda: _Stager(_rt()))
+
+
+def compute_stream():
+    """The NumPy family's stream for work that overlaps its null-stream
+    copies (kept for the process)."""
+    return _get("cstream", lambda: _rt().nonblocking_stream())
 
 
 def blas():

@@ -13,6 +13,7 @@ GPU) out for pipeline='ondevice'; the host pipeline always returns NumPy
 import numpy as np
 
 from . import _device as D
+from . import _hip
 from . import _lib
 from .extract import rho_f32, rho_f64
 
@@ -169,6 +170,77 @@ def _matmul_ondevice(fam, At, Bt, safe_mode, accumulation, n_hi, n_lo):
     return C
 
 
+def _numpy_halves_ok(A, B):
+    """NumPy operands for which the two-halves form pays: each half of A and
+    of C at least _hip._STAGE_MIN bytes (the staged copies)."""
+    if not (isinstance(A, np.ndarray) and isinstance(B, np.ndarray)
+            and A.ndim == 2 and B.ndim == 2 and A.shape[1] == B.shape[0]):
+        return False
+    N, K = A.shape
+    M = B.shape[1]
+    half = 8 * (N // 2)
+    return N >= 256 and half * K >= _hip._STAGE_MIN and half * M >= _hip._STAGE_MIN
+
+
+def _matmul_ondevice_numpy(fam, A, B, safe_mode, accumulation, n_hi, n_lo):
+    """_matmul_ondevice for large NumPy operands, as two ozk_matmul calls on
+    the row halves of A on a stream of their own.  The second half's upload
+    runs while the first half computes, and the first half's download while
+    the second computes; B is uploaded once.  A's slice lines are its rows,
+    so each half's slices, products and folds are those of the whole call,
+    bit for bit.  Calls that the preflight marks, or whose flags ask for a
+    rerun or a fallback, take the one-call path."""
+    A = np.ascontiguousarray(A, dtype=np.float64)
+    B = np.ascontiguousarray(B, dtype=np.float64)
+    _validate_accumulation_mode(accumulation)
+    _validate_shapes(A, B)
+    N, K = A.shape
+    M = B.shape[1]
+    _check_safe_mode(safe_mode)
+
+    def whole():
+        return _matmul_ondevice(fam, fam.f64(A), fam.f64(B), safe_mode, accumulation,
+                                n_hi, n_lo).numpy()
+
+    if _kbound_reasons(K, 24 - rho_f32(K), "large for FP32 extraction"):
+        return whole()
+    order = _lib.ORDER_BLOCK64 if accumulation == "host" else _lib.ORDER_2SUM
+    lib, rt, st = _lib.load(), _hip._rt(), _hip.compute_stream()
+    h = (N // 2 + 63) // 64 * 64
+    Bt = fam.f64(B)
+    held, done = [Bt], []
+    out = np.empty((N, M))
+    fl = 0
+    try:
+        for r0, r1 in ((0, h), (h, N)):
+            At = fam.f64(A[r0:r1])  # null stream: overlaps the previous half's kernels
+            C = fam.empty((r1 - r0, M))
+            flags = fam.flags()
+            wsb = lib.ozk_matmul_workspace_bytes(r1 - r0, K, M, _lib.PIPE_ONDEVICE, n_hi, n_lo)
+            ws = fam.workspace(wsb)
+            held += [At, C, flags, ws]
+            _lib.check(lib.ozk_matmul(
+                At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
+                D.ld_of(C), r1 - r0, K, M, _lib.PIPE_ONDEVICE, n_hi, n_lo, order,
+                ws.data_ptr(), wsb, flags.data_ptr(), st))
+            ev = rt.event()
+            done.append((r0, r1, C, flags, ev))
+            rt.record(ev, st)
+        for r0, r1, C, flags, ev in done:
+            rt.wait(ev)  # then the download (null stream) overlaps the next half
+            _hip._stager().to_host(out[r0:r1], C.data_ptr())
+            fl |= fam.read_flags(flags)
+    finally:
+        rt.sync(st)  # no kernel may still use a block once it is released
+        for *_, ev in done:
+            rt.destroy_event(ev)
+    _lib.check_flags(fl)
+    if fl & _lib.OZK_FLAG_NONFINITE or (fl & _lib.OZK_FLAG_INF_SLICE
+                                        and order == _lib.ORDER_BLOCK64):
+        return whole()
+    return out
+
+
 def _matmul_host(fam, At, Bt, n_slices, safe_mode, order):
     """matmul.py:826-851 / :866-900: FP64 extraction (rho from
     `_compute_rho`), triangular slice pairs i + j <= n_slices - 1, FP64
@@ -224,6 +296,8 @@ def matmul(A, B, n_slices=8, safe_mode="raise", pipeline="host",
     fam = D.family(want_torch)
     if pipeline == "ondevice":
         n_hi, n_lo = _resolve_precision(precision)
+        if not want_torch and _numpy_halves_ok(A, B):
+            return _matmul_ondevice_numpy(fam, A, B, safe_mode, accumulation, n_hi, n_lo)
         At, Bt = fam.f64(A), fam.f64(B)
         C = _matmul_ondevice(fam, At, Bt, safe_mode, accumulation, n_hi, n_lo)
         return fam.out(C, want_torch)
@@ -243,6 +317,9 @@ def matmul_numpy(A_f64, B_f64, n_slices=8, safe_mode="raise", pipeline="host",
     GPU kernels.  Accepts array-likes; returns NumPy."""
     want_torch = D.is_torch(A_f64) and D.is_torch(B_f64)
     fam = D.family(want_torch)
+    if pipeline == "ondevice" and not want_torch and _numpy_halves_ok(A_f64, B_f64):
+        n_hi, n_lo = _resolve_precision(precision)
+        return _matmul_ondevice_numpy(fam, A_f64, B_f64, safe_mode, "host", n_hi, n_lo)
     At, Bt = fam.f64(A_f64), fam.f64(B_f64)
     if pipeline == "ondevice":
         n_hi, n_lo = _resolve_precision(precision)

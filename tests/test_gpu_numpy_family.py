@@ -183,3 +183,50 @@ def test_torch_staged_conversions(ozk):
     b = rng.randn(n)
     x = ozk.solve(A, b)
     assert isinstance(x, np.ndarray) and np.linalg.norm(A @ x - b) <= 1e-12 * np.linalg.norm(b) * n
+
+
+@pytest.mark.parametrize("shape,prec,acc,kind", [((2048, 4096, 4096), "high", "fused", None),
+                                                 ((1100, 8192, 8192), "high", "fused", None),
+                                                 ((1100, 8192, 8192), "medium", "host", "big"),
+                                                 ((1100, 8192, 8192), "high", "fused", "nan")])
+def test_numpy_matmul_in_row_halves(no_torch, monkeypatch, shape, prec, acc, kind):
+    """Large NumPy products run as two calls on A's row halves, overlapping
+    the transfers with the kernels: the same bits as the one-call path, and
+    the same errors, fallbacks and reruns."""
+    ozk = no_torch
+    import importlib
+    MM = importlib.import_module("ozaki_jax_amd.matmul")
+    N, K, M = shape
+    rng = np.random.RandomState(N + K)
+    A, B = rng.randn(N, K), rng.randn(K, M)
+    if kind == "big":
+        A[7] *= 2.0 ** 110  # INF_SLICE in the FP64 block order: rerun on BF16 planes
+    if kind == "nan":
+        A[N - 3, 5] = np.nan
+    assert MM._numpy_halves_ok(A, B)
+    case(f"numpy matmul ondevice {prec} {acc} {shape} {kind}: halves vs one call")
+    if kind == "nan":
+        with pytest.raises(ValueError, match="NaN or Inf"):
+            ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=prec)
+        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=prec,
+                       safe_mode="fallback")
+        monkeypatch.setattr(MM, "_numpy_halves_ok", lambda *a: False)
+        C1 = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=prec,
+                        safe_mode="fallback")
+        assert np.array_equal(C, C1, equal_nan=True)
+        return
+    C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=prec)
+    Cn = ozk.matmul_numpy(A, B, pipeline="ondevice", precision=prec) if acc == "host" else None
+    monkeypatch.setattr(MM, "_numpy_halves_ok", lambda *a: False)
+    C1 = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=prec)
+    assert isinstance(C, np.ndarray) and np.array_equal(C, C1, equal_nan=True)
+    if Cn is not None:
+        assert np.array_equal(Cn, ozk.matmul_numpy(A, B, pipeline="ondevice", precision=prec),
+                              equal_nan=True)
+    rows = [0, 1, 575, 576, N - 1]
+    nh, nl = OP.resolve_precision(prec)
+    f = O.matmul_ondevice_a3 if acc == "host" else O.matmul_ondevice_a4
+    case("sampled rows against the oracle")
+    assert np.array_equal(C[rows[:4] if N > 576 else rows[:2]],
+                          f(A[rows[:4] if N > 576 else rows[:2]], B, "raise", nh, nl),
+                          equal_nan=True)
