@@ -186,6 +186,21 @@ def test_argument_errors_before_device_work(lib):
     assert rc == _lib.OZK_ERR_INVALID
     with pytest.raises(ValueError):
         _lib.check(rc)
+    # the early-flag variants check their host word and event first
+    rc = lib.ozk_matmul_early_flags(None, 4, None, 4, None, 4, 4, 4, 4, 0, 4, 1, 0, None, 0,
+                                    None, None, None, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"host flag word" in lib.ozk_last_error()
+    rc = lib.ozk_gram_early_flags(None, 4, 4, 4, 4, 1, None, 4, None, 0, None, None, None,
+                                  None)
+    assert rc == _lib.OZK_ERR_INVALID and b"host flag word" in lib.ozk_last_error()
+    # and then the same arguments as ozk_matmul / ozk_gram
+    word = (ctypes.c_uint32 * 1)()
+    rc = lib.ozk_matmul_early_flags(None, 4, None, 4, None, 4, 4, 0, 4, 0, 4, 1, 0, None, 0,
+                                    None, ctypes.addressof(word), 1, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"invalid shape" in lib.ozk_last_error()
+    rc = lib.ozk_gram_early_flags(None, 4, 0, 4, 4, 1, None, 4, None, 0, None,
+                                  ctypes.addressof(word), 1, None)
+    assert rc == _lib.OZK_ERR_INVALID and b"invalid shape" in lib.ozk_last_error()
 
 
 def test_pivots_to_perm(lib):
