@@ -171,10 +171,15 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * All-pairs schedules: the on-device presets high (4,1) and medium (3,1),
  * which run in one K sweep, max (5,4), which runs its hh, hl and lh blocks
  * (matmul.py:670-674) as three sweeps and keeps the fold state between them
- * in the workspace (ozk_gemm_workspace_bytes; 0 bytes for the other
- * schedules), and the custom schedules (1,2), (1,3), (1,4), (2,1), (2,2),
- * (2,3) and (3,2), which fit one sweep.  Other schedules, and the host
- * pipeline, run one pair at a time on BF16 planes. */
+ * in the workspace, and the custom schedules (1,2), (1,3), (1,4), (2,1),
+ * (2,2), (2,3) and (3,2), which fit one sweep.  Other schedules, and the host
+ * pipeline, run one pair at a time on BF16 planes.
+ * Workspace: ozk_gemm_workspace_bytes is the fold state (max and the
+ * two-sweep schedules only) plus 4352 bytes of tile counters, with which
+ * the last rounds of output tiles are handed out at run time to the
+ * workgroups that finish first.  Any workspace from the fold state up (none
+ * for one-sweep schedules) is accepted; below the full size the tiles run in
+ * a static order. */
 size_t ozk_gemm_workspace_bytes(int64_t N, int64_t M, int pipeline, int n_hi,
                                 int n_lo, int order);
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,

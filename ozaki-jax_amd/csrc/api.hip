@@ -60,6 +60,7 @@ int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Asum, const int32_t* Bsum);
 size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
                             int order);
+size_t gemm_state_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo, int order);
 int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
                      const int32_t* Be, int64_t N, int64_t M, int64_t K, int nhi,
                      int nlo, float* C_hi, float* C_lo, int64_t ldc, void* ws,
@@ -367,7 +368,7 @@ int ozk_gemm_2sum_pair(const void* a_slices, const int32_t* a_exps,
   if (N == 0 || M == 0) return OZK_OK;
   OZK_CHECK_ARG(a_slices && a_exps && b_slices && b_exps && C_hi && C_lo, "null pointer");
   OZK_CHECK_ARG(!i8 || (a_sums && b_sums), "null pointer");
-  const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, n_hi, n_lo, OZK_ORDER_2SUM);
+  const size_t need = gemm_state_bytes(N, M, OZK_PIPE_ONDEVICE, n_hi, n_lo, OZK_ORDER_2SUM);
   if (workspace_bytes < need || (need && !workspace)) {
     set_error("gemm_2sum_pair: workspace of %zu bytes needed, %zu given", need,
               workspace_bytes);

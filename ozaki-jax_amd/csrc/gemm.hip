@@ -198,6 +198,9 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 
 constexpr int kThreads16 = 512;
 constexpr int kRing = 4;       // stage buffers (kRing - 1 stages in flight)
+// Dynamic-tail words (gemm_allpairs): kXcds counters per sweep, then one
+// word per workgroup (at most kDynMaxGrid) that passes a claimed tile on.
+constexpr int kDynSlot0 = 64, kDynMaxGrid = 1024;
 
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef int int32x16 __attribute__((ext_vector_type(16)));
@@ -606,7 +609,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     int64_t N, int64_t M, int64_t nst, int64_t a_lines, int64_t b_lines,
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
     int64_t ldp, char* __restrict__ state, int tail_P, uint32_t* __restrict__ part,
-    I8Fix fix) {
+    I8Fix fix, uint32_t* __restrict__ dyn, int dyn_nstat) {
   typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
   constexpr int kBuf = SW::S * 4 * 64;  // uint4 per stage buffer
@@ -626,19 +629,37 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     if constexpr (SYM) tile_coords_sym(t, ntm, tm, tn);
     else tile_coords(t, ntm, ntn, tm, tn);
   };
-  // Work items of this workgroup: whole tiles bid + j nwg, j < nfull.  With
+  // Work items of this workgroup: whole tiles bid + j nwg, j < nstat.  With
   // tail_P > 1 (K-split tail) every workgroup runs the ntiles / nwg whole
   // rounds, and the ntiles % nwg tail tiles are split along K into tail_P
   // pieces of about nst / tail_P stages: workgroup bid < tail tiles * tail_P
   // runs piece bid % tail_P of tail tile bid / tail_P and stores its raw
   // sums in part (block bid) for gemm_tail_fixup.
-  const int nfull = tail_P ? ntiles / nwg : (ntiles - 1 - bid) / nwg + 1;
+  //
+  // With dyn (dynamic tail, never together with tail_P) every workgroup runs
+  // dyn_nstat whole rounds in the static order, and the tiles after them
+  // are handed out at run time, so that workgroups on faster XCDs take more
+  // of them: tile nstat nwg + d, d = x mod 8, comes from XCD x's counter
+  // dyn[x] (d = 8 dyn[x]++ + x, which the static order would also have put
+  // on XCD x), and a workgroup whose own counter is spent takes from the
+  // other XCDs'.  Item j + 1 is claimed when item j starts, so the stage
+  // ring's prefetch across the tile boundary is kept.  The LDS is all ring,
+  // so the claimed tile reaches the other waves through the workgroup's
+  // word dyn[kDynSlot0 + bid].
+  const int nstat = dyn ? dyn_nstat : (tail_P ? ntiles / nwg : (ntiles - 1 - bid) / nwg + 1);
+  const int ndyn = dyn ? ntiles - nstat * nwg : 0;  // dynamic tiles
   const bool has_piece = tail_P > 0 && bid < (ntiles % nwg) * tail_P;
-  const int piece_tile = has_piece ? nfull * nwg + bid / tail_P : 0;
+  const int piece_tile = has_piece ? nstat * nwg + bid / tail_P : 0;
   const int64_t ps0 = has_piece ? (int64_t)(bid % tail_P) * nst / tail_P : 0;
   const int64_t ps1 = has_piece ? (int64_t)(bid % tail_P + 1) * nst / tail_P : 0;
-  const int nitems = nfull + (has_piece ? 1 : 0);
-  const int64_t total = (int64_t)nfull * nst + (ps1 - ps0);  // stages of this workgroup
+  int nwhole = nstat;  // whole-tile items known so far (grows with claims)
+  int nitems = nstat + (has_piece ? 1 : 0);
+  int64_t total = (int64_t)nstat * nst + (ps1 - ps0);  // stages of this workgroup
+  int dt0 = 0, dt1 = 0;  // claimed tiles of the even / odd dynamic items
+  bool more = dyn != nullptr;
+  auto item_tile = [&](int jj) {
+    return jj < nstat ? bid + jj * nwg : (jj < nwhole ? ((jj & 1) ? dt1 : dt0) : piece_tile);
+  };
   const int64_t a_stage = a_lines * kChunkBytes, b_stage = b_lines * kChunkBytes;
   const int64_t aplane = a_stage * nst, bplane = b_stage * nst;
   const char* Ab = As + SW::A0 * aplane;
@@ -655,10 +676,39 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   // minus the offset's part (I8Fix); a K-split piece stores raw sums and
   // its fixup removes that part once.
   auto start_item = [&](int jj) {
+    // claim item jj + 1 (one workgroup-wide wait on the counter, per item)
+    if (more && jj < nwhole && jj + 1 >= nstat) {
+      if (threadIdx.x == 256) {  // a wave that issues no stage loads
+        int t = -1;
+        for (int i = 0; i < kXcds; ++i) {
+          const int y = (bid + i) & (kXcds - 1);
+          const int d = kXcds * (int)__hip_atomic_fetch_add(dyn + y, 1u, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT) + y;
+          if (d < ndyn) {
+            t = nstat * nwg + d;
+            break;
+          }
+        }
+        __hip_atomic_store(dyn + kDynSlot0 + bid, (uint32_t)t, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+      }
+      __syncthreads();
+      const int t = __builtin_amdgcn_readfirstlane((int)__hip_atomic_load(
+          dyn + kDynSlot0 + bid, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+      if (t >= 0) {
+        if ((jj + 1) & 1) dt1 = t;
+        else dt0 = t;
+        ++nwhole;
+        ++nitems;
+        total += nst;
+      } else {
+        more = false;
+      }
+    }
     if constexpr (std::is_same<Op, OpI8>::value) {
-      if (jj < nfull) {
+      if (jj < nwhole) {
         int tm, tn;
-        coords(bid + jj * nwg, tm, tn);
+        coords(item_tile(jj), tm, tn);
         const int64_t col = (int64_t)tn * kBN + 16 * mma.wc + (lane & 15);
         const int64_t rb = (int64_t)tm * kBM + 32 * mma.wr + 4 * (lane >> 4);
         // per plane once: o sb + Kp o^2 and -o sa (modulo 2^32, as i8_start)
@@ -703,11 +753,11 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   const char *fA = Ab, *fB = Bb;
   auto load_tile = [&](int j) {
     int tm, tn;
-    coords(j < nfull ? bid + j * nwg : piece_tile, tm, tn);
+    coords(item_tile(j), tm, tn);
     fA = Ab + (int64_t)tm * kBM * kChunkBytes;
     fB = Bb + (int64_t)tn * kBN * kChunkBytes;
-    fs = j < nfull ? 0 : ps0;
-    fe = j < nfull ? nst : ps1;
+    fs = j < nwhole ? 0 : ps0;
+    fe = j < nwhole ? nst : ps1;
   };
   // issue stage g of the sequence into ring buffer g % kRing
   auto fetch = [&](int64_t g) {
@@ -735,11 +785,11 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     __syncthreads();
     if (g + kRing - 1 < total) fetch(g + kRing - 1);
     mma(lds + (g & (kRing - 1)) * kBuf);
-    if (++s < (j < nfull ? nst : ps1 - ps0)) continue;
+    if (++s < (j < nwhole ? nst : ps1 - ps0)) continue;
     s = 0;
-    if (j < nfull) {
+    if (j < nwhole) {
       int tm, tn;
-      coords(bid + j * nwg, tm, tn);
+      coords(item_tile(j), tm, tn);
       tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(mma.acc, tm, tn, mma.wr, mma.wc, lane, Ae,
                                                 Be, N, M, a_lines, b_lines, unit2, C, ldc,
                                                 P, ldp, state);
@@ -949,6 +999,10 @@ __global__ void probe_mfma16_kernel(int32_t* out) {
 
 // ---------------------------------------------------------------- launch
 
+__global__ void zero_u32_kernel(uint32_t* __restrict__ p, int n) {
+  for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
+}
+
 // Schedules with an all-pairs instantiation: high (4,1) and medium (3,1)
 // in one sweep, max (5,4) in three (hh, hl, lh; at most 25 pairs and 10
 // planes each), the custom schedules that fit one sweep (at most 10 planes,
@@ -994,8 +1048,9 @@ static int fold_state_bytes(int order) {
                                  : FoldState<OZK_ORDER_BLOCK64>::kBytes;
 }
 
-size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
-                            int order) {
+// Workspace an all-pairs product cannot run without: the fold state kept
+// between the sweeps of a multi-sweep schedule (0 for one sweep).
+size_t gemm_state_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo, int order) {
   if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(nhi, nlo, order) ||
       allpairs_sweeps(nhi, nlo) == 1 || order < 0)
     return 0;
@@ -1030,6 +1085,31 @@ static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np) {
   return tp;
 }
 
+// Dynamic tail (gemm_allpairs): with R = ntiles / cus whole rounds, the
+// last ceil(R / kDynDiv) of them are handed out at run time from one counter
+// per XCD and sweep (kDynBytes, zeroed before the launch).  Needs at least
+// kDynMinRounds rounds and kDynMinStages stages per tile, so that a claim
+// made when a tile starts is known before the ring fetches the next tile.
+constexpr int kDynDiv = 8, kDynMinRounds = 4, kDynMinStages = 8;
+constexpr size_t kDynBytes = (kDynSlot0 + kDynMaxGrid) * sizeof(uint32_t);
+
+static int dyn_static_rounds(int64_t ntiles, int grid, int64_t nst) {
+  const int64_t R = ntiles / grid;
+  if (grid % kXcds != 0 || grid > kDynMaxGrid || R < kDynMinRounds || nst < kDynMinStages)
+    return 0;
+  return (int)(R - (R + kDynDiv - 1) / kDynDiv);
+}
+
+// Workspace of the fastest all-pairs launch: the fold state, then the
+// dynamic-tail words.  (The K-split tail's partial sums, gemm_tail_bytes,
+// follow them where a driver reserves those too.)
+size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
+                            int order) {
+  if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(nhi, nlo, order)) return 0;
+  return (size_t)round_up((int64_t)gemm_state_bytes(N, M, pipe, nhi, nlo, order), 256) +
+         kDynBytes;
+}
+
 static int64_t allpairs_ntiles(int64_t N, int64_t M, bool sym) {
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
   return sym ? (al / kBM) * (al / kBM + 1) / 2 : (al / kBM) * (bl / kBN);
@@ -1057,6 +1137,8 @@ struct ApArgs {
   int tile0;  // first tail tile
   int64_t tail_T;
   uint32_t* part;
+  uint32_t* dyn;  // dynamic-tail counters: kXcds per sweep, or null
+  int dyn_nstat;
   hipStream_t st;
   const char *As, *Bs;
   const int32_t *Ae, *Be;
@@ -1076,7 +1158,8 @@ static void launch_sweep(const ApArgs& a) {
   hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
                      a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
                      a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
-                     split ? a.tail_P : 0, a.part, a.fix);
+                     split ? a.tail_P : 0, a.part, a.fix,
+                     a.dyn ? a.dyn + kXcds * B0 : nullptr, a.dyn_nstat);
   if constexpr (B0 == 0 && B1 == 2) {
     if (split)
       hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
@@ -1127,9 +1210,10 @@ static void launch_ap_order(int order, const ApArgs& a) {
 }
 
 // All-pairs launch for an all-pairs schedule; `i8` selects the INT8 plane
-// format (rho >= 19).  order = kOrderProducts writes P.  `state` holds
-// gemm_workspace_bytes() for multi-sweep schedules; a single-sweep schedule
-// splits its tail along K when `state` also holds gemm_tail_bytes().
+// format (rho >= 19).  order = kOrderProducts writes P.  `state` holds at
+// least gemm_state_bytes(); with gemm_workspace_bytes() the last rounds of
+// tiles are handed out dynamically, and a single-sweep schedule splits its
+// tail along K instead when `state` also holds gemm_tail_bytes().
 static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
                            const void* Bs, const int32_t* Be, int64_t N,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
@@ -1141,7 +1225,7 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
     set_error("int8 slice planes need their line sums");
     return OZK_ERR_INVALID;
   }
-  const size_t need = gemm_workspace_bytes(N, M, OZK_PIPE_ONDEVICE, nhi, nlo, order);
+  const size_t need = gemm_state_bytes(N, M, OZK_PIPE_ONDEVICE, nhi, nlo, order);
   if (state_bytes < need || (need && !state)) {
     set_error("gemm workspace of %zu bytes < %zu needed", state_bytes, need);
     return OZK_ERR_WORKSPACE;
@@ -1157,16 +1241,27 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.tile0 = 0;
   a.tail_T = 0;
   a.part = nullptr;
+  a.dyn = nullptr;
+  a.dyn_nstat = 0;
+  // workspace: fold state | dynamic-tail words | K-split partial sums
+  const size_t off = round_up((int64_t)need, 256);
   if (allpairs_sweeps(nhi, nlo) == 1) {
     const TailPlan tp = plan_tail(ntiles, cus, allpairs_nst(K, i8),
                                   pair_count(OZK_PIPE_ONDEVICE, nhi, nlo));
-    const size_t off = round_up((int64_t)need, 256);
-    if (tp.P > 1 && state && state_bytes >= off + tp.bytes) {
+    if (tp.P > 1 && state && state_bytes >= off + kDynBytes + tp.bytes) {
       a.grid = dim3((unsigned)tp.grid);
       a.tail_P = tp.P;
       a.tail_T = tp.T;
       a.tile0 = (int)(ntiles - tp.T);
-      a.part = (uint32_t*)((char*)state + off);
+      a.part = (uint32_t*)((char*)state + off + kDynBytes);
+    }
+  }
+  if (!a.part && state && state_bytes >= off + kDynBytes) {
+    const int ns = dyn_static_rounds(ntiles, (int)a.grid.x, allpairs_nst(K, i8));
+    if (ns > 0) {
+      a.dyn = (uint32_t*)((char*)state + off);
+      a.dyn_nstat = ns;
+      hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, st, a.dyn, kDynSlot0);
     }
   }
   a.sym = sym;

@@ -60,6 +60,11 @@ def test_host_functions(lib):
     assert b"outside" in lib.ozk_last_error()
 
 
+# dynamic-tail words of an all-pairs product: 64 counters and one word per
+# workgroup (up to 1024)
+DYN = (64 + 1024) * 4
+
+
 def r256(b):
     return -(-b // 256) * 256
 
@@ -93,13 +98,13 @@ def test_workspace_sizes(lib):
         for nh, nl in [(4, 1), (3, 1)]:
             ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, nh, nl)
             planes = 2 * (nh + nl) * 8192 * K * eb
-            extra = (2 if eb == 1 else 1) * 2 * (nh + nl) * 8192 * 4 + 4096
+            extra = (2 if eb == 1 else 1) * 2 * (nh + nl) * 8192 * 4 + 4096 + DYN
             assert planes + gang_bytes(K, M) <= ws <= planes + gang_bytes(K, M) + extra, (K, nh, nl)
     # max (5, 4): INT8 planes + exchange records + the 2Sum fold state
     # between its three sweeps (5 FP32 fields per output element)
     ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
     base = 2 * 9 * 8192 * 8192 + gang_bytes(8192, 8192) + 20 * 8192 * 8192
-    assert base <= ws <= base + 2 * 2 * 9 * 8192 * 4 + 8192
+    assert base <= ws <= base + 2 * 2 * 9 * 8192 * 4 + 8192 + DYN
     # columns longer than 8192 rows, and the FP64 (host) pipeline, transpose B;
     # one extraction buffer serves A's rows and B's columns in turn
     ws = lib.ozk_matmul_workspace_bytes(64, 70000, 64, 0, 4, 1)
@@ -108,19 +113,26 @@ def test_workspace_sizes(lib):
     ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, 4, 1)
     planes = 5 * (N + M) * K + 2 * 5 * (N + M) * 4
     ex = max(row_gang_bytes(N, K), 8 * K * M + row_gang_bytes(M, K))
-    assert planes + ex <= ws <= planes + ex + 4096
+    assert planes + ex <= ws <= planes + ex + 4096 + DYN
     ws = lib.ozk_matmul_workspace_bytes(64, 1000, 64, 1, 8, 0)
     assert ws >= 8 * 1000 * 64
 
 
 def test_gemm_workspace_bytes(lib):
-    # only the three-sweep max schedule keeps state between launches
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 4, 1, 0) == 0
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 3, 1, 1) == 0
+    # all-pairs schedules: the fold state the three-sweep max schedule keeps
+    # between launches (rounded to 256 B), then the dynamic-tail words (64
+    # counters and one word for each of up to 1024 workgroups)
+    dyn = DYN
+
+    def up(x):
+        return (x + 255) // 256 * 256
+
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 4, 1, 0) == dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 3, 1, 1) == dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 8, 0, 3) == 0
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 0) == 100 * 70 * 20
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == 100 * 70 * 8
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == 0
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 0) == up(100 * 70 * 20) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == up(100 * 70 * 8) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == dyn
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
     assert lib.ozk_extract_workspace_bytes(100, 32768, 0) == 0
     # rows of 32769 to 262144 elements: row gangs; longer lines stream
