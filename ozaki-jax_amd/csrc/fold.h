@@ -15,6 +15,7 @@ struct PairInfo {
   bool ge;    // last pair of its group
   bool bs;    // first pair of its block
   bool be;    // last pair of its block
+  bool fg;    // in the first group of its block
 };
 
 __host__ __device__ constexpr int pair_count(int pipe, int nhi, int nlo) {
@@ -27,18 +28,18 @@ __host__ __device__ constexpr int pair_count(int pipe, int nhi, int nlo) {
 // Host: (i, j) with i + j <= n - 1, i-major (matmul.py:27-31).
 __host__ __device__ constexpr PairInfo pair_info(int pipe, int nhi, int nlo,
                                                  int p) {
-  PairInfo r{0, 0, 0, false, false, false, false};
+  PairInfo r{0, 0, 0, false, false, false, false, false};
   if (pipe == OZK_PIPE_ONDEVICE) {
     const int hh = nhi * nhi, hl = nhi * nlo;
     if (p < hh) {
       const int i = p / nhi, j = p % nhi;
-      r = PairInfo{i, j, 0, j == 0, j == nhi - 1, p == 0, p == hh - 1};
+      r = PairInfo{i, j, 0, j == 0, j == nhi - 1, p == 0, p == hh - 1, i == 0};
     } else if (p < hh + hl) {
       const int q = p - hh, i = q / nlo, j = q % nlo;
-      r = PairInfo{i, nhi + j, 1, j == 0, j == nlo - 1, q == 0, q == hl - 1};
+      r = PairInfo{i, nhi + j, 1, j == 0, j == nlo - 1, q == 0, q == hl - 1, i == 0};
     } else {
       const int q = p - hh - hl, i = q / nhi, j = q % nhi;
-      r = PairInfo{nhi + i, j, 2, j == 0, j == nhi - 1, q == 0, q == hl - 1};
+      r = PairInfo{nhi + i, j, 2, j == 0, j == nhi - 1, q == 0, q == hl - 1, i == 0};
     }
   } else {
     const int n = nhi;
@@ -48,7 +49,7 @@ __host__ __device__ constexpr PairInfo pair_info(int pipe, int nhi, int nlo,
       ++i;
     }
     const int np = n * (n + 1) / 2;
-    r = PairInfo{i, q, 0, q == 0, q == n - 1 - i, p == 0, p == np - 1};
+    r = PairInfo{i, q, 0, q == 0, q == n - 1 - i, p == 0, p == np - 1, i == 0};
   }
   return r;
 }
@@ -74,27 +75,45 @@ __device__ __forceinline__ void twosum(float& s, float& l, float x) {
   l = l + e;
 }
 
+// twosum(s, l, x) from s = l = +0: s = 0 + x, and l = 0 + ((0 - s) + x),
+// which is +0 for every finite x (also -0) and NaN for an infinite or NaN
+// x, as is x - x.  Two operations instead of four, the same bits.
+__device__ __forceinline__ void twosum_from_zero(float& s, float& l, float x) {
+  s = x + 0.0f;
+  l = x - x;
+}
+
 struct Fold2Sum {
   float it, il, bt, bl, ct, cl, p0, p1, p2;
   __device__ __forceinline__ void init() {
     it = il = bt = bl = ct = cl = p0 = p1 = p2 = 0.0f;
   }
-  __device__ __forceinline__ void pair(const PairInfo& q, float P, float cs32,
-                                       float rs32, double, double) {
-    if (q.bs) { bt = 0.0f; bl = 0.0f; }
-    if (q.gs) { it = 0.0f; il = 0.0f; }
-    twosum(it, il, P * cs32);
+  // Pair q's product at its column scale, x = P * 2^cb (pallas_ops.py:206-214).
+  // A group's first product, a block's first group sum and block 0's sum
+  // start from zeros (the reference's zero-initialised accumulators).
+  __device__ __forceinline__ void pair_x(const PairInfo& q, float x, float rs32) {
+    if (q.gs) twosum_from_zero(it, il, x);
+    else twosum(it, il, x);
     if (q.ge) {
       const float ht = it * rs32, hl = il * rs32;
-      twosum(bt, bl, ht);
+      if (q.fg) twosum_from_zero(bt, bl, ht);
+      else twosum(bt, bl, ht);
       twosum(bt, bl, hl);
       if (q.be) {
-        twosum(ct, cl, bt);
-        if (q.blk == 0) p0 = bl;
-        else if (q.blk == 1) p1 = bl;
-        else p2 = bl;
+        if (q.blk == 0) {
+          twosum_from_zero(ct, cl, bt);
+          p0 = bl;
+        } else {
+          twosum(ct, cl, bt);
+          if (q.blk == 1) p1 = bl;
+          else p2 = bl;
+        }
       }
     }
+  }
+  __device__ __forceinline__ void pair(const PairInfo& q, float P, float cs32,
+                                       float rs32, double, double) {
+    pair_x(q, P * cs32, rs32);
   }
   // The blocks' lo parts after their hi parts (pallas_ops.py:230-237): the
   // double-float pair (C_hi, C_lo) ...
