@@ -68,13 +68,26 @@ extern "C" {
  * product with it as NaN. */
 #define OZK_EXP_NONFINITE (-2147483647 - 1)
 
-/* Test hook, no counterpart in the reference: the poll limit of every
- * bounded wait between workgroups (column extraction, ozk_lu_solve_f32) for
- * the kernels launched after the call; 0 restores the built-in limits.  A
- * tiny limit makes those waits give up, so that a test can check
+/* Test hook, no counterpart in the reference: the limit of every bounded
+ * wait between workgroups for the kernels launched after the call (ticks of
+ * the 100 MHz real-time counter in the extraction gangs, polls in
+ * ozk_lu_solve_f32); 0 restores the built-in limits (0.2 s per wait in the
+ * gangs).  A tiny limit makes those waits give up, so that a test can check
  * OZK_FLAG_WAIT_TIMEOUT and the callers' handling of it while every kernel
  * still exits normally. */
 void ozk_set_wait_polls(uint32_t polls);
+
+/* No counterpart in the reference: the extraction strategy of the calling
+ * thread's later calls (thread-local).  1 (the default): columns of up to
+ * 8192 rows, and FP32 rows of 32769 to 262144 elements, are extracted by
+ * gangs of workgroups that exchange their partial maxima, with waits that
+ * give up after 0.2 s (OZK_FLAG_WAIT_TIMEOUT) when other work keeps the
+ * gang's members from running together.  0: no waits between workgroups;
+ * columns go through an FP64 transposed copy, long rows are streamed (a
+ * larger workspace for columns: query the *_workspace_bytes functions after
+ * the switch).  The Python layer repeats a call that reports
+ * OZK_FLAG_WAIT_TIMEOUT once with 0; the results are bit-identical. */
+void ozk_set_gangs(int enable);
 
 /* Accumulation orders (the four orders of the reference). */
 #define OZK_ORDER_2SUM 0     /* A4: pallas_ops.py:178-239 == matmul.py:382-488 */

@@ -381,7 +381,9 @@ class _Blas:
 
 
 _state = {}
-_state_lock = threading.Lock()
+# Re-entrant: a maker may create another singleton (the stager's and the
+# pool's makers take the runtime), and any of them may be the first created.
+_state_lock = threading.RLock()
 
 
 def _get(name, make):

@@ -41,6 +41,30 @@ def check_flags(fl):
                            "(OZK_FLAG_WAIT_TIMEOUT); the result is not valid")
     return fl
 
+
+# Calls repeated without extraction gangs after OZK_FLAG_WAIT_TIMEOUT.
+gang_retries = 0
+
+
+def with_gang_retry(call):
+    """Run call() -> flag word.  When the extraction gangs' waits gave up
+    (other work held the CUs that a gang needed), run it once more with the
+    gangs switched off for this thread (ozk_set_gangs(0): transposed columns
+    and streamed rows, no waits between workgroups; the same bits), then
+    raise on the flag as check_flags does.  call() must query its workspace
+    size itself, since the gang-free path needs a larger one."""
+    global gang_retries
+    fl = call()
+    if fl & OZK_FLAG_WAIT_TIMEOUT:
+        lib = load()
+        gang_retries += 1
+        lib.ozk_set_gangs(0)
+        try:
+            fl = call()
+        finally:
+            lib.ozk_set_gangs(1)
+    return check_flags(fl)
+
 _c_i64 = ctypes.c_int64
 _c_int = ctypes.c_int
 _c_size = ctypes.c_size_t
@@ -51,6 +75,7 @@ SIGNATURES = {
     "ozk_last_error": (ctypes.c_char_p, []),
     "ozk_abi_version": (_c_int, []),
     "ozk_set_wait_polls": (None, [ctypes.c_uint32]),
+    "ozk_set_gangs": (None, [_c_int]),
     "ozk_device_info": (_c_int, [ctypes.c_char_p, _c_size, ctypes.POINTER(_c_int)]),
     "ozk_rho_f64": (_c_int, [_c_i64]),
     "ozk_rho_f32": (_c_int, [_c_i64]),

@@ -42,6 +42,10 @@ uint32_t wait_polls(uint32_t dflt) {
   return v ? v : dflt;
 }
 
+// Gang extraction on (1) or off (0) for the calling thread's calls.
+static thread_local int t_gangs = 1;
+bool gangs_enabled() { return t_gangs != 0; }
+
 // Implemented in extract.hip / gemm.hip.
 template <typename W>
 int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
@@ -206,6 +210,8 @@ int ozk_abi_version(void) { return 3; }
 void ozk_set_wait_polls(uint32_t polls) {
   ozk::g_wait_polls.store(polls, std::memory_order_relaxed);
 }
+
+void ozk_set_gangs(int enable) { ozk::t_gangs = enable ? 1 : 0; }
 
 int ozk_device_info(char* buf, size_t len, int* cu_count) {
   clear_error();

@@ -56,9 +56,14 @@ void clear_error();
 // query fails).  Persistent kernels size their grids with it.
 int cu_count();
 
-// Poll limit of the kernels' bounded waits between workgroups: `dflt`, or
-// the limit a test set with ozk_set_wait_polls.
+// Limit of the kernels' bounded waits between workgroups: `dflt`, or the
+// limit a test set with ozk_set_wait_polls.
 uint32_t wait_polls(uint32_t dflt);
+
+// Whether the calling thread's extractions may use gangs of workgroups
+// (ozk_set_gangs); without them, columns go through a transposed copy and
+// long rows are streamed, with no waits between workgroups.
+bool gangs_enabled();
 
 // ---------------------------------------------------------------- layout
 // Slice planes hold BF16 bit patterns or INT8 grid counts with lines padded
@@ -122,7 +127,11 @@ __device__ __forceinline__ float bf16_bits_to_f32(uint16_t h) {
 // lane's byte offset from `gbase`, which must be 16-byte aligned.  Written as
 // inline assembly so that the compiler does not order LDS reads behind these
 // loads: the kernels wait for them themselves (wait_vm).  M0 carries the LDS
-// address; nothing else in the kernels that use it touches M0.
+// address and is declared clobbered, so the compiler keeps no value of its
+// own in M0 across the load.  (Clang warns that M0 is a reserved register
+// whose value it will not save for the statement, which is not wanted here.)
+#pragma clang diagnostic push
+#pragma clang diagnostic ignored "-Winline-asm"
 __device__ __forceinline__ void dma16(uint32_t lds_addr, const void* gbase,
                                       uint32_t voff) {
   asm volatile(
@@ -131,8 +140,9 @@ __device__ __forceinline__ void dma16(uint32_t lds_addr, const void* gbase,
       "global_load_lds_dwordx4 %1, %2"
       :
       : "s"(lds_addr), "v"(voff), "s"(gbase)
-      : "memory");
+      : "memory", "m0");
 }
+#pragma clang diagnostic pop
 
 // Wait until at most N of this wave's vector-memory operations are
 // outstanding.

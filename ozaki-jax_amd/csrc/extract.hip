@@ -362,16 +362,19 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
 // starts, so all members of the gangs before the first incomplete one have
 // started, and those gangs finish; the incomplete gang's remaining members
 // then need only free slots (G <= kGangMaxMembers workgroups resident at
-// once).  Every wait is bounded all the same: after kGangSpin polls (or the
-// limit a test set with ozk_set_wait_polls) it sets OZK_FLAG_WAIT_TIMEOUT
-// (the slices are then not valid) and the member waits no more in later
-// slices.
+// once).  Every wait is bounded all the same: after kGangWaitTicks ticks of
+// the 100 MHz real-time counter (0.2 s, or the limit a test set with
+// ozk_set_wait_polls) it sets OZK_FLAG_WAIT_TIMEOUT (the slices are then not
+// valid) and the member waits no more in later slices.  Other work that
+// holds the CUs for longer (another process, or a persistent GEMM on
+// another stream) can keep a gang's members apart that long; the caller
+// then repeats the extraction without gangs (ozk_set_gangs).
 constexpr int kGangPW = 16;
 constexpr int kGangRowsPT = 8;
 constexpr int kGangThreads = 512;
 constexpr int kGangRun = kGangThreads / (kGangPW / 2) * kGangRowsPT;  // 512 rows
 constexpr int kGangMaxMembers = 16;
-constexpr uint32_t kGangSpin = 1u << 18;
+constexpr uint32_t kGangWaitTicks = 20000000u;
 constexpr int kGangKeys = 2 * kGangPW;  // keys per record line
 constexpr int64_t kGangLine = 128;      // bytes per record line
 constexpr int64_t kGangHeader = 256;    // the ticket word, padded
@@ -390,12 +393,15 @@ __device__ __forceinline__ float key_max(uint32_t k) {
   return k == 1u ? __builtin_nanf("") : __uint_as_float(k - 2u);
 }
 
-// Bounded wait for a nonzero word; 0 after `polls` polls (and the flag).
+// Bounded wait for a nonzero word; 0 (and the flag) once `ticks` ticks of
+// the 100 MHz real-time counter have passed without it.
 __device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
-                                             uint32_t polls) {
-  for (uint32_t spin = 0; spin < polls; ++spin) {
+                                             uint32_t ticks) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
     const uint32_t k = __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (k) return k;
+    if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
     __builtin_amdgcn_s_sleep(1);
   }
   atomicOr(flags, OZK_FLAG_WAIT_TIMEOUT);
@@ -413,7 +419,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
     const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
-    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls,
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t wait_ticks,
     int32_t* __restrict__ part) {
   typedef typename PlaneElem<FMT>::type T;
   constexpr int NP = 2, CP = kGangPW / 2, NW = kGangThreads / 64, R = kGangRowsPT;
@@ -520,7 +526,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
       uint32_t k = 0u;
       if (!gave_up) {
         for (int mb = t / kGangKeys; mb < G; mb += NG) {
-          const uint32_t km = wait_key(rs + mb * kWords + t % kGangKeys, flags, polls);
+          const uint32_t km = wait_key(rs + mb * kWords + t % kGangKeys, flags, wait_ticks);
           if (!km) gave_up = 1;
           k = max(k, km);
         }
@@ -607,7 +613,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
     int n1,
     typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
-    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t polls,
+    uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t wait_ticks,
     int32_t* __restrict__ part) {
   typedef typename PlaneElem<FMT>::type T;
   typedef typename PlaneVec<FMT, kRowVEC>::type TV;
@@ -693,7 +699,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
     if (t < 2 * G) {  // every member's maxima
       uint32_t k = 0u;
       if (!gave_up) {
-        k = wait_key(rs + t, flags, polls);
+        k = wait_key(rs + t, flags, wait_ticks);
         if (!k) gave_up = 1;
       }
       comb[t] = k;
@@ -869,7 +875,7 @@ static int launch_sum_parts(const int32_t* part, int G, int planes, int64_t epla
 // kRowRun * kRowMaxMembers long run on row gangs.
 static bool gang_rows(int64_t len) {
   const int64_t ld = round_up(len, kKPad);
-  return ld > 32768 && ld <= (int64_t)kRowRun * kRowMaxMembers;
+  return ld > 32768 && ld <= (int64_t)kRowRun * kRowMaxMembers && gangs_enabled();
 }
 
 // Ticket and exchange records (zeroed per launch), then the INT8 partial
@@ -908,15 +914,15 @@ static int launch_rows_gang(const double* X, int64_t lines, int64_t len, int64_t
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
   int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(lp * G));
-  const uint32_t polls = wait_polls(kGangSpin);
+  const uint32_t wait_ticks = wait_polls(kGangWaitTicks);
   if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
     hipLaunchKernelGGL((extract_lines_gang<FMT, true>), grid, dim3(kRowThreads), 0, st, X,
                        lines, len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, polls, part);
+                       ticket, G, wait_ticks, part);
   else
     hipLaunchKernelGGL((extract_lines_gang<FMT, false>), grid, dim3(kRowThreads), 0, st, X,
                        lines, len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, polls, part);
+                       ticket, G, wait_ticks, part);
   OZK_LAUNCH_CHECK();
   if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;
@@ -992,7 +998,7 @@ int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st) {
 // runs on gangs; FP64 column extraction, and longer columns, go through an
 // FP64 transpose of X into the workspace.
 static bool gang_columns(int64_t rows) {
-  return round_up(rows, kKPad) <= (int64_t)kGangRun * kGangMaxMembers;
+  return round_up(rows, kKPad) <= (int64_t)kGangRun * kGangMaxMembers && gangs_enabled();
 }
 
 // Ticket and exchange records (zeroed per launch), then the INT8 partial
@@ -1045,15 +1051,15 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
   int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(npanels * G));
-  const uint32_t polls = wait_polls(kGangSpin);
+  const uint32_t wait_ticks = wait_polls(kGangWaitTicks);
   if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
     hipLaunchKernelGGL((extract_cols_gang<FMT, true>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, polls, part);
+                       ticket, G, wait_ticks, part);
   else
     hipLaunchKernelGGL((extract_cols_gang<FMT, false>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, polls, part);
+                       ticket, G, wait_ticks, part);
   OZK_LAUNCH_CHECK();
   if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;

@@ -45,20 +45,23 @@ def gram(A, precision="high", accumulation="bf16_interleaved", mode="f64"):
     # which runs no preflight here; the flag word is read only for
     # OZK_FLAG_WAIT_TIMEOUT.
     flags = fam.flags()
-    wsb = lib.ozk_gram_workspace_bytes(rows, cols, n_hi, n_lo)
-    ws = fam.workspace(wsb)
-    args = (At.data_ptr(), D.ld_of(At), rows, cols, n_hi, n_lo, G.data_ptr(),
-            D.ld_of(G), ws.data_ptr(), wsb, flags.data_ptr())
     early = getattr(fam, "early_flags", None)
-    if early is None:
-        _lib.check(lib.ozk_gram(*args, fam.stream()))
-        _lib.check_flags(fam.read_flags(flags))
-    else:
+
+    def once():
+        wsb = lib.ozk_gram_workspace_bytes(rows, cols, n_hi, n_lo)
+        ws = fam.workspace(wsb)
+        args = (At.data_ptr(), D.ld_of(At), rows, cols, n_hi, n_lo, G.data_ptr(),
+                D.ld_of(G), ws.data_ptr(), wsb, flags.data_ptr())
+        if early is None:
+            _lib.check(lib.ozk_gram(*args, fam.stream()))
+            return fam.read_flags(flags)
         # torch tensors: the flags are read once the extraction has run; G is
         # returned while the GEMM is still queued on the current stream
         word, ev, read = early()
         _lib.check(lib.ozk_gram_early_flags(*args, word, ev, fam.stream()))
-        _lib.check_flags(read())
+        return read()
+
+    _lib.with_gang_retry(once)
     return fam.out(G, want_torch)
 
 

@@ -103,25 +103,31 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False, i8=False):
     e = D.torch.zeros((planes, lib.ozk_slice_lines(max(lines, 1))),
                       dtype=D.torch.int32, device=dev)
     sums = D.torch.zeros_like(e) if i8 else None
-    flags = D.new_flags(dev)
-    wsb = lib.ozk_extract_workspace_bytes(rows, cols, int(by_cols))
-    ws = D.workspace(wsb, dev)
-    if f64:
-        rc = lib.ozk_extract_f64(Xt.data_ptr(), rows, cols, D.ld_of(Xt),
-                                 int(by_cols), rho, n0, s.data_ptr(),
-                                 e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
-                                 wsb, D.stream_handle())
-    elif i8:
-        rc = lib.ozk_extract_f32_i8(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols),
-                                    rho, n0, n1, s.data_ptr(), e.data_ptr(),
-                                    sums.data_ptr(), flags.data_ptr(), ws.data_ptr(), wsb,
-                                    D.stream_handle())
-    else:
-        rc = lib.ozk_extract_f32(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols), rho,
-                                 n0, n1, s.data_ptr(), e.data_ptr(), flags.data_ptr(),
-                                 ws.data_ptr(), wsb, D.stream_handle())
-    _lib.check(rc)
-    _lib.check_flags(D.read_flags(flags))
+    flags = None
+
+    def once():
+        nonlocal flags
+        flags = D.new_flags(dev)  # the extraction entry points OR into the word
+        wsb = lib.ozk_extract_workspace_bytes(rows, cols, int(by_cols))
+        ws = D.workspace(wsb, dev)
+        if f64:
+            rc = lib.ozk_extract_f64(Xt.data_ptr(), rows, cols, D.ld_of(Xt),
+                                     int(by_cols), rho, n0, s.data_ptr(),
+                                     e.data_ptr(), flags.data_ptr(), ws.data_ptr(),
+                                     wsb, D.stream_handle())
+        elif i8:
+            rc = lib.ozk_extract_f32_i8(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols),
+                                        rho, n0, n1, s.data_ptr(), e.data_ptr(),
+                                        sums.data_ptr(), flags.data_ptr(), ws.data_ptr(),
+                                        wsb, D.stream_handle())
+        else:
+            rc = lib.ozk_extract_f32(Xt.data_ptr(), rows, cols, D.ld_of(Xt), int(by_cols),
+                                     rho, n0, n1, s.data_ptr(), e.data_ptr(),
+                                     flags.data_ptr(), ws.data_ptr(), wsb, D.stream_handle())
+        _lib.check(rc)
+        return D.read_flags(flags)
+
+    _lib.with_gang_retry(once)
     return Planes(s, e, lines, length, flags, rho if i8 else None, sums)
 
 

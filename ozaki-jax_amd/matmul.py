@@ -124,7 +124,7 @@ def _run_matmul(fam, At, Bt, pipeline, n_hi, n_lo, order):
     flags = fam.flags()  # cleared by the call
     early = getattr(fam, "early_flags", None)
 
-    def run(pipe):
+    def once(pipe):
         wsb = lib.ozk_matmul_workspace_bytes(N, K, M, pipe, n_hi, n_lo)
         ws = fam.workspace(wsb)
         args = (At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
@@ -132,12 +132,15 @@ def _run_matmul(fam, At, Bt, pipeline, n_hi, n_lo, order):
                 flags.data_ptr())
         if early is None:
             _lib.check(lib.ozk_matmul(*args, fam.stream()))
-            return _lib.check_flags(fam.read_flags(flags))
+            return fam.read_flags(flags)
         # torch tensors: the flags are read once the extraction has run, and
         # C is returned while the GEMM is still queued on the current stream
         word, ev, read = early()
         _lib.check(lib.ozk_matmul_early_flags(*args, word, ev, fam.stream()))
-        return _lib.check_flags(read())
+        return read()
+
+    def run(pipe):
+        return _lib.with_gang_retry(lambda: once(pipe))
 
     fl = run(pipeline)
     if (fl & _lib.OZK_FLAG_INF_SLICE and order == _lib.ORDER_BLOCK64
@@ -189,7 +192,8 @@ def _matmul_ondevice_numpy(fam, A, B, safe_mode, accumulation, n_hi, n_lo):
     the second computes; B is uploaded once.  A's slice lines are its rows,
     so each half's slices, products and folds are those of the whole call,
     bit for bit.  Calls that the preflight marks, or whose flags ask for a
-    rerun or a fallback, take the one-call path."""
+    rerun or a fallback (or whose extraction gangs gave up), take the
+    one-call path."""
     A = np.ascontiguousarray(A, dtype=np.float64)
     B = np.ascontiguousarray(B, dtype=np.float64)
     _validate_accumulation_mode(accumulation)
@@ -234,10 +238,9 @@ def _matmul_ondevice_numpy(fam, A, B, safe_mode, accumulation, n_hi, n_lo):
         rt.sync(st)  # no kernel may still use a block once it is released
         for *_, ev in done:
             rt.destroy_event(ev)
-    _lib.check_flags(fl)
-    if fl & _lib.OZK_FLAG_NONFINITE or (fl & _lib.OZK_FLAG_INF_SLICE
-                                        and order == _lib.ORDER_BLOCK64):
-        return whole()
+    if fl & _lib.OZK_FLAG_WAIT_TIMEOUT or fl & _lib.OZK_FLAG_NONFINITE or (
+            fl & _lib.OZK_FLAG_INF_SLICE and order == _lib.ORDER_BLOCK64):
+        return whole()  # repeats a call whose gangs gave up without them
     return out
 
 

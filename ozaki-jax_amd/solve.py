@@ -88,19 +88,28 @@ def ozaki_residual_device(fam, At, xt, bt, n_hi, n_lo):
         raise ValueError("zero-size array to reduction operation maximum "
                          "which has no identity")
     flags = fam.flags()  # ozk_residual clears the flag word itself
-    wsb = lib.ozk_residual_workspace_bytes(N, K, nc, n_hi, n_lo)
-    ws = fam.workspace(wsb)
-    _lib.check(lib.ozk_residual(
-        At.data_ptr(), D.ld_of(At), xt.data_ptr(), D.ld_of(xt), bt.data_ptr(),
-        D.ld_of(bt), r.data_ptr(), D.ld_of(r), N, K, nc, n_hi, n_lo,
-        ws.data_ptr(), wsb, flags.data_ptr(), fam.stream()))
-    if wsb == 0 and getattr(fam, "early_flags", None) is not None:
+    fused = lib.ozk_residual_workspace_bytes(N, K, nc, n_hi, n_lo) == 0
+
+    def once():
+        wsb = lib.ozk_residual_workspace_bytes(N, K, nc, n_hi, n_lo)
+        ws = fam.workspace(wsb)
+        _lib.check(lib.ozk_residual(
+            At.data_ptr(), D.ld_of(At), xt.data_ptr(), D.ld_of(xt), bt.data_ptr(),
+            D.ld_of(bt), r.data_ptr(), D.ld_of(r), N, K, nc, n_hi, n_lo,
+            ws.data_ptr(), wsb, flags.data_ptr(), fam.stream()))
+        return fam.read_flags(flags)
+
+    if fused and getattr(fam, "early_flags", None) is not None:
         # The fused row kernels (no workspace) have no bounded waits, so the
         # word can hold no OZK_FLAG_WAIT_TIMEOUT, and NaN / Inf are left to
         # propagate as in the reference: a torch result is returned ordered
         # on the current stream, without waiting for the kernel.
+        _lib.check(lib.ozk_residual(
+            At.data_ptr(), D.ld_of(At), xt.data_ptr(), D.ld_of(xt), bt.data_ptr(),
+            D.ld_of(bt), r.data_ptr(), D.ld_of(r), N, K, nc, n_hi, n_lo,
+            0, 0, flags.data_ptr(), fam.stream()))
         return r
-    _lib.check_flags(fam.read_flags(flags))
+    _lib.with_gang_retry(once)
     return r
 
 
