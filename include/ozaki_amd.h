@@ -82,11 +82,13 @@ void ozk_set_wait_polls(uint32_t polls);
  * 8192 rows, and FP32 rows of 32769 to 262144 elements, are extracted by
  * gangs of workgroups that exchange their partial maxima, with waits that
  * give up after 0.2 s (OZK_FLAG_WAIT_TIMEOUT) when other work keeps the
- * gang's members from running together.  0: no waits between workgroups;
- * columns go through an FP64 transposed copy, long rows are streamed (a
- * larger workspace for columns: query the *_workspace_bytes functions after
- * the switch).  The Python layer repeats a call that reports
- * OZK_FLAG_WAIT_TIMEOUT once with 0; the results are bit-identical. */
+ * gang's members from running together; ozk_lu_solve_f32 spreads each
+ * column's row blocks over several workgroups.  0: no waits between
+ * workgroups; columns go through an FP64 transposed copy, long rows are
+ * streamed (a larger workspace for columns: query the *_workspace_bytes
+ * functions after the switch), and one workgroup solves each column.  The
+ * Python layer repeats a call that reports OZK_FLAG_WAIT_TIMEOUT once with
+ * 0; the results are bit-identical. */
 void ozk_set_gangs(int enable);
 
 /* Accumulation orders (the four orders of the reference). */

@@ -5,10 +5,14 @@ Drop-in for the hot path of ozaki_jax (``ozaki_jax/__init__.py:5-25``):
 ``lstsq``, ``norm``, the ``*extract_split_*`` helpers and
 ``accumulate_2sum`` / ``validate_accumulation_2sum``, same signatures and
 defaults.  Every
-computation runs in hand-written HIP kernels for gfx950 (libozaki_amd.so,
-C ABI in include/ozaki_amd.h), bound with ctypes; PyTorch-ROCm provides
-device memory and the current stream.  NumPy in -> NumPy out; torch tensors
-play the role of the reference's JAX arrays.
+Ozaki computation runs in hand-written HIP kernels for gfx950
+(libozaki_amd.so, C ABI in include/ozaki_amd.h), bound with ctypes.  NumPy
+in -> NumPy out: NumPy inputs take device memory from the HIP runtime and
+FP64 products from rocBLAS, both through ctypes, so matmul, matmul_numpy,
+gram, residual, the extraction helpers, solve and inv (n up to
+ozk_lu_factor_max_n()) and norm need no PyTorch.  Torch tensors (PyTorch-ROCm
+memory and current stream) play the role of the reference's JAX arrays;
+lstsq and larger solves use torch.linalg for their FP32 factorisations.
 """
 
 __version__ = "0.7.0"

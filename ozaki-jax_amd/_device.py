@@ -11,6 +11,7 @@ leading dimension) pairs.
 """
 
 import ctypes
+import sys
 import threading
 
 import numpy as np
@@ -25,9 +26,10 @@ except ImportError:  # pragma: no cover - torch is optional
 
 
 def is_torch(x):
-    """A torch tensor?  Decided from the type alone: NumPy inputs never
-    touch the torch module."""
-    return type(x).__module__.split(".")[0] == "torch"
+    """A torch tensor (or a subclass of one)?  Checked against the torch
+    module the program has imported, if any; this never imports it."""
+    t = sys.modules.get("torch")
+    return t is not None and isinstance(x, t.Tensor)
 
 
 def ld_of(t):
@@ -65,7 +67,11 @@ def _torch_to_numpy(t):
     return out
 
 
-_early = threading.local()
+# Pinned host words and HIP events of the early flag reads, per device: a
+# call takes one pair for the time of its read and gives it back, so the
+# pairs are shared by all threads and never leak.
+_early_free = {}
+_early_lock = threading.Lock()
 
 
 class _TorchFamily:
@@ -113,28 +119,34 @@ class _TorchFamily:
     def zero_flags(self):
         return torch.zeros(1, dtype=torch.int32, device=self.dev)
 
+    def zeros(self, shape, dtype):
+        return torch.zeros(shape, dtype=_TORCH_DTYPES[np.dtype(dtype)], device=self.dev)
+
     def early_flags(self):
         """(host word, event, read) for ozk_matmul_early_flags: a pinned
-        host word and a HIP event of this thread and device, kept for the
-        process, and read() waiting for the event and returning the word.
-        The product stays ordered on the current stream, as torch's own
-        results are."""
-        slots = getattr(_early, "slots", None)
-        if slots is None:
-            slots = _early.slots = {}
-        slot = slots.get(self.dev.index)
-        if slot is None:
-            rt = _hip._rt()
+        host word and a HIP event of this device, taken from a shared free
+        list, and read() waiting for the event, returning the word and giving
+        the pair back.  The product stays ordered on the current stream, as
+        torch's own results are."""
+        rt = _hip._rt()
+        with _early_lock:
+            free = _early_free.setdefault(self.dev.index, [])
+            pair = free.pop() if free else None
+        if pair is None:
             with torch.cuda.device(self.dev):
-                word, ev = rt.host_malloc(4), rt.event()
-            word_v = ctypes.c_uint32.from_address(word)
+                pair = (rt.host_malloc(4), rt.event())
+        word, ev = pair
+        word_v = ctypes.c_uint32.from_address(word)
 
-            def read():
+        def read():
+            try:
                 rt.wait(ev)
                 return int(word_v.value)
+            finally:
+                with _early_lock:
+                    _early_free[self.dev.index].append(pair)
 
-            slot = slots[self.dev.index] = (word, ev, read)
-        return slot
+        return word, ev, read
 
     def read_flags(self, f):
         """Synchronising read of a device flag word."""
@@ -186,7 +198,10 @@ class _HipFamily:
         return _hip.DeviceArray((1,), np.int32)
 
     def zero_flags(self):
-        return _hip.DeviceArray.from_numpy(np.zeros(1, np.int32))
+        return _hip.DeviceArray.zeros((1,), np.int32)
+
+    def zeros(self, shape, dtype):
+        return _hip.DeviceArray.zeros(shape, dtype)
 
     def read_flags(self, f):
         return int(f.numpy()[0]) & 0xffffffff
@@ -221,7 +236,8 @@ _TORCH_DTYPES = {}
 _NUMPY_DTYPES = {}
 if torch is not None:
     _TORCH_DTYPES = {np.dtype(np.float64): torch.float64, np.dtype(np.float32): torch.float32,
-                     np.dtype(np.int32): torch.int32, np.dtype(np.uint8): torch.uint8}
+                     np.dtype(np.int32): torch.int32, np.dtype(np.int16): torch.int16,
+                     np.dtype(np.int8): torch.int8, np.dtype(np.uint8): torch.uint8}
     _NUMPY_DTYPES = {v: k for k, v in _TORCH_DTYPES.items()}
 
 

@@ -47,6 +47,7 @@ class _Runtime:
         for name, args in [("hipMalloc", [ctypes.POINTER(vp), sz]), ("hipFree", [vp]),
                            ("hipMemcpy", [vp, vp, sz, i]),
                            ("hipMemcpyAsync", [vp, vp, sz, i, vp]),
+                           ("hipMemset", [vp, i, sz]),
                            ("hipHostMalloc", [ctypes.POINTER(vp), sz, ctypes.c_uint]),
                            ("hipEventCreate", [ctypes.POINTER(vp)]),
                            ("hipEventRecord", [vp, vp]),
@@ -88,6 +89,10 @@ class _Runtime:
     def copy(self, dst, src, nbytes, kind):
         if nbytes:
             self.check(self.h.hipMemcpy(dst, src, nbytes, kind), "hipMemcpy")
+
+    def memset(self, dst, value, nbytes):
+        if nbytes:
+            self.check(self.h.hipMemset(dst, value, nbytes), "hipMemset")
 
     def sync(self, stream=None):
         self.check(self.h.hipStreamSynchronize(stream), "hipStreamSynchronize")
@@ -226,7 +231,9 @@ class _Pool:
 class _Block:
     """One pool block, returned to the pool when the last array using it is
     collected.  Work that still reads it was queued on the null stream
-    before any later use of the block, so reuse stays in order."""
+    before any later use of the block, so reuse on the null stream stays in
+    order; a user that writes a block on another stream first synchronizes
+    the null stream (matmul's two-halves path does)."""
     __slots__ = ("ptr", "cls", "__weakref__")
 
     def __init__(self, nbytes):
@@ -311,6 +318,12 @@ class DeviceArray:
             _rt().copy(out.ctypes.data, self.data_ptr(), out.nbytes, _D2H)
         return out
 
+    @classmethod
+    def zeros(cls, shape, dtype=np.float64):
+        d = cls(shape, dtype)
+        _rt().memset(d.data_ptr(), 0, d.nbytes)
+        return d
+
     def copy_from(self, other):
         """Device-to-device copy of an array of the same shape and layout."""
         if other.shape != self.shape or other.nbytes != self.nbytes:
@@ -369,6 +382,16 @@ class _Blas:
                                        A.data_ptr(), A.ld, A.data_ptr(), A.ld, self._c(0.0),
                                        G.data_ptr(), G.ld), "rocblas_dgemm")
         return G
+
+    def add(self, A, B, out):
+        """out = A + B (row-major matrices of one shape; one rounding per
+        element, as an FP64 add)."""
+        n, m = A.shape
+        if n and m:
+            self._chk(self.b.rocblas_dgeam(self.h, _OP_N, _OP_N, m, n, self._c(1.0),
+                                           A.data_ptr(), A.ld, self._c(1.0), B.data_ptr(),
+                                           B.ld, out.data_ptr(), out.ld), "rocblas_dgeam")
+        return out
 
     def half_sum_transpose(self, G, out):
         """out = G * 0.5 + G^T * 0.5, which equals (G + G^T) * 0.5 exactly

@@ -227,13 +227,18 @@ int launch_lu_solve(const float* LU, int64_t lda, const int32_t* perm, int64_t n
   const int64_t chunk = ts_chunk(ncols);
   const int vec = ((uintptr_t)LU % 16 == 0) && (lda % 4 == 0);
   const int64_t per = cu_count() / chunk;
-  const unsigned G = (unsigned)(nb < per ? nb : (per > 0 ? per : 1));
+  // Without gangs (ozk_set_gangs(0)) one workgroup solves all blocks of its
+  // column: its waits are then only for words that its own wave 0 stored
+  // before the barrier ending the previous block, and they take the
+  // built-in limit.
+  const bool one = !gangs_enabled();
+  const unsigned G = one ? 1u : (unsigned)(nb < per ? nb : (per > 0 ? per : 1));
   const int64_t words = 2 * n * ncols;
   const int64_t fb = (words + 255) / 256;
   hipLaunchKernelGGL(fill_u64_array_kernel, dim3((unsigned)(fb < 4096 ? fb : 4096)), dim3(256), 0,
                      st, wf, words, (uint64_t)0);
   OZK_LAUNCH_CHECK();
-  const uint32_t spin_limit = wait_polls(kTsSpinLimit);
+  const uint32_t spin_limit = one ? kTsSpinLimit : wait_polls(kTsSpinLimit);
   for (int64_t c0 = 0; c0 < ncols; c0 += chunk) {
     const int64_t nc = ncols - c0 < chunk ? ncols - c0 : chunk;
     hipLaunchKernelGGL(lu_trsv_kernel<false>, dim3(G, (unsigned)nc), dim3(kTsThreads), 0, st,

@@ -223,6 +223,11 @@ def _matmul_ondevice_numpy(fam, A, B, safe_mode, accumulation, n_hi, n_lo):
             wsb = lib.ozk_matmul_workspace_bytes(r1 - r0, K, M, _lib.PIPE_ONDEVICE, n_hi, n_lo)
             ws = fam.workspace(wsb)
             held += [At, C, flags, ws]
+            # Pool blocks are reused in null-stream order; work queued there
+            # before these blocks were taken (another thread's product that
+            # still reads a block it released) must end before the compute
+            # stream writes them.
+            rt.sync()
             _lib.check(lib.ozk_matmul(
                 At.data_ptr(), D.ld_of(At), Bt.data_ptr(), D.ld_of(Bt), C.data_ptr(),
                 D.ld_of(C), r1 - r0, K, M, _lib.PIPE_ONDEVICE, n_hi, n_lo, order,

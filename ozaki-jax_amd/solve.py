@@ -9,8 +9,9 @@ an FP32 LU with partial pivoting, factored once and reused (the reference
 re-solves with the same matrix each iteration, which yields the same
 factors): ozk_lu_factor_f32 up to n = ozk_lu_factor_max_n() (torch.linalg's
 getrf above), then the library's triangular solves (ozk_lu_solve_f32) on that
-factor.  mode='f64' paths are plain FP64 products (rocBLAS DGEMM through
-torch).
+factor.  mode='f64' paths are plain FP64 products (rocBLAS DGEMM).  NumPy
+operands up to n = ozk_lu_factor_max_n() need no PyTorch (device arrays of
+the HIP runtime, rocBLAS through ctypes), as in the reference's NumPy use.
 """
 
 from . import _device as D
@@ -146,6 +147,8 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
     A, b = _asarray(A), _asarray(b)
     want_torch = D.is_torch(A)
     _validate_solve_inputs(A, b)
+    if not want_torch and not D.is_torch(b) and A.shape[0] <= _lib.load().ozk_lu_factor_max_n():
+        return _solve_numpy(A, b, precision, max_iterations, residual_mode)
     dev = D.require_gpu()
     fam = D.family(True)
     torch = D.torch
@@ -183,6 +186,67 @@ def solve(A, b, precision="high", accumulation="bf16_interleaved",
     if vec:
         x = x[:, 0]
     return D.to_family(x, want_torch)
+
+
+def _solve_numpy(A, b, precision, max_iterations, residual_mode):
+    """solve() for NumPy operands of n <= ozk_lu_factor_max_n(), with no
+    PyTorch: device arrays of the HIP runtime, the library's FP32 LU and
+    triangular solves, rocBLAS for the FP64 residual and the update."""
+    import numpy as np
+    from . import _hip
+    lib = _lib.load()
+    fam = D.family(False)
+    A = np.ascontiguousarray(A, dtype=np.float64)
+    b = np.asarray(b, dtype=np.float64)
+    vec = b.ndim == 1
+    n = A.shape[0]
+    At = fam.f64(A)
+    bt = fam.f64(b[:, None] if vec else b)
+    nc = bt.shape[1]
+    if n == 0 or nc == 0:
+        return np.zeros(b.shape)
+    # A32 = RN32(A) with 16-byte rows, as the torch path's LU.copy_(At)
+    lda = max(-(-n // 4) * 4, 4)
+    a32 = np.zeros((n, lda), np.float32)
+    a32[:, :n] = A
+    LU = _hip.DeviceArray.from_numpy(a32)
+    perm = fam.empty((n,), np.int32)
+    wsb = lib.ozk_lu_factor_workspace_bytes(n)
+    ws = fam.workspace(wsb)
+    _lib.check(lib.ozk_lu_factor_f32(LU.data_ptr(), lda, n, perm.data_ptr(), ws.data_ptr(),
+                                     wsb, fam.flags().data_ptr(), None))
+
+    def solve32(rhs):
+        # A row block that gave up waiting (the GPU shared with other work
+        # long enough to stall the chain) leaves d invalid: with_gang_retry
+        # solves again with one workgroup per column, which waits for no
+        # other workgroup.
+        d = fam.empty((n, nc))
+
+        def once():
+            flags = fam.flags()  # cleared by the call
+            wsb = lib.ozk_lu_solve_workspace_bytes(n, nc)
+            ws = fam.workspace(wsb)
+            _lib.check(lib.ozk_lu_solve_f32(
+                LU.data_ptr(), lda, perm.data_ptr(), n, rhs.data_ptr(), D.ld_of(rhs),
+                d.data_ptr(), D.ld_of(d), nc, ws.data_ptr(), wsb, flags.data_ptr(), None))
+            return fam.read_flags(flags)
+
+        _lib.with_gang_retry(once)
+        return d
+
+    blas = _hip.blas()
+    x = solve32(bt)
+    if residual_mode == "ozaki":
+        n_hi, n_lo = _resolve_precision(precision)
+    for _ in range(max_iterations):
+        if residual_mode == "f64":
+            r = fam.residual_f64(At, x, bt)
+        else:
+            r = ozaki_residual_device(fam, At, x, bt, n_hi, n_lo)
+        x = blas.add(x, solve32(r), fam.empty((n, nc)))
+    out = x.numpy()
+    return out[:, 0] if vec else out
 
 
 # ozk_lu_solve_f32 solves each right-hand side as its own chain of row

@@ -230,3 +230,80 @@ def test_numpy_matmul_in_row_halves(no_torch, monkeypatch, shape, prec, acc, kin
     assert np.array_equal(C[rows[:4] if N > 576 else rows[:2]],
                           f(A[rows[:4] if N > 576 else rows[:2]], B, "raise", nh, nl),
                           equal_nan=True)
+
+
+def test_extract_helpers_without_torch(no_torch):
+    """extract_split_*, f32_extract_split_* and jax_extract_split_* on NumPy
+    input (extract.py:21-286) with the planes unpacked on the host, bit for
+    bit against the oracle; shapes cover the row kernels, the column gangs
+    (8192 rows) and the transposed long columns."""
+    ozk = no_torch
+    rng = np.random.RandomState(21)
+    for shape in [(20, 33), (96, 5000), (8192, 40), (9000, 24)]:
+        X = (rng.rand(*shape) - 0.5) * np.exp(2.0 * rng.randn(*shape))
+        X32 = X.astype(np.float32)
+        r64, c64 = O.rho_f64(shape[1]), O.rho_f64(shape[0])
+        r32, c32 = O.rho_f32(shape[1]), O.rho_f32(shape[0])
+        case(f"extract helpers {shape} without torch")
+        for got, ref in [
+                (ozk.extract_split_rows(X, r64, 8), O.extract_rows_f64(X, r64, 8)),
+                (ozk.extract_split_cols(X, c64, 8), O.extract_cols_f64(X, c64, 8)),
+                (ozk.f32_extract_split_rows(X32, r32, 5), O.extract_rows_f32(X32, r32, 5)),
+                (ozk.f32_extract_split_cols(X32, c32, 5), O.extract_cols_f32(X32, c32, 5))]:
+            s, e = got
+            assert isinstance(s[0], np.ndarray) and s[0].dtype == np.float32
+            assert np.array_equal(np.stack(s), ref[0]) and np.array_equal(np.stack(e), ref[1])
+            assert np.stack(e).dtype == ref[1].dtype
+        st, et = ozk.jax_extract_split_rows(X32, r32, 4)
+        rs, re_ = O.extract_rows_f32(X32, r32, 4)
+        assert np.array_equal(st, rs) and np.array_equal(et, re_) and et.dtype == np.float32
+        st, et = ozk.jax_extract_split_cols(X32, c32, 4)
+        rs, re_ = O.extract_cols_f32(X32, c32, 4)
+        assert np.array_equal(st, rs) and np.array_equal(et, re_)
+
+
+def test_solve_inv_norm_without_torch(no_torch):
+    """solve (FP32 LU and triangular solves of the library, FP64 or Ozaki
+    residuals), inv and norm on NumPy input.  solve at n = 1024, cond 1e6,
+    is within 2x of the oracle's refinement (NumPy's FP32 LAPACK solve, the
+    oracle's Ozaki residuals) and 10x below the unrefined FP32 solve."""
+    ozk = no_torch
+    rng = np.random.RandomState(22)
+    n = 1024
+    Q1, _ = np.linalg.qr(rng.randn(n, n))
+    Q2, _ = np.linalg.qr(rng.randn(n, n))
+    A = (Q1 * np.logspace(0, 6, n)) @ Q2.T
+    b = rng.randn(n)
+    xr = np.linalg.solve(A, b)
+
+    def err(x):
+        return np.linalg.norm(x - xr) / np.linalg.norm(xr)
+
+    case("solve ozaki n=1024 cond 1e6 without torch")
+    x = ozk.solve(A, b, residual_mode="ozaki")
+    assert isinstance(x, np.ndarray) and x.shape == (n,)
+    e_ref = err(O.solve_ozaki(A, b))
+    assert err(x) <= 2.0 * e_ref
+    assert e_ref < err(O.solve_ozaki(A, b, max_iterations=0)) / 10.0
+    case("solve f64 residuals, 3 right-hand sides, well conditioned, without torch")
+    W = rng.randn(n, n) + n * np.eye(n)
+    B = rng.randn(n, 3)
+    Xs = ozk.solve(W, B)
+    assert Xs.shape == (n, 3)
+    assert np.linalg.norm(Xs - np.linalg.solve(W, B)) / np.linalg.norm(Xs) < 1e-13
+    case("inv n=200 without torch (FP64 and Ozaki residuals)")
+    M = rng.randn(200, 200) + 200 * np.eye(200)
+    assert np.abs(ozk.inv(M) @ M - np.eye(200)).max() < 1e-13
+    Mr = np.linalg.inv(M)
+    Mi = ozk.inv(M, residual_mode="ozaki")
+    assert np.linalg.norm(Mi - Mr) / np.linalg.norm(Mr) <= 1e-6  # the Tier-1 bound
+    case("norms without torch")
+    v = rng.randn(300)
+    for o in (None, 2, 1, np.inf, -np.inf, 0, 3):
+        assert np.isclose(ozk.norm(v, o), np.linalg.norm(v, o), rtol=1e-14)
+    G = rng.randn(400, 60)
+    for o in (None, "fro", 1, -1, np.inf, -np.inf):
+        assert np.isclose(ozk.norm(G, o), np.linalg.norm(G, o), rtol=1e-14)
+    s2 = ozk.norm(G, 2, mode="ozaki")
+    assert isinstance(s2, np.float64)
+    assert np.isclose(s2, np.linalg.norm(G, 2), rtol=1e-12)

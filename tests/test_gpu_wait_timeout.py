@@ -7,9 +7,11 @@ kernel still exits) and the row-block chains of the LU triangular solves.
 On the flag after an extraction, the package repeats the call once with the
 gangs switched off for the thread (ozk_set_gangs(0): transposed columns and
 streamed rows, no waits between workgroups), so matmul, gram, residual and
-lowlevel.extract still return the exact result; solve() redoes a triangular
-solve that gave up on torch.linalg's path.  After ozk_set_wait_polls(0) the
-same calls run on the gangs again, with no repeat.
+lowlevel.extract still return the exact result.  solve() redoes a
+triangular solve that gave up: on torch.linalg's path for torch input, and
+with one workgroup per column (no waits between workgroups) for NumPy input.
+After ozk_set_wait_polls(0) the same calls run on the gangs again, with no
+repeat.
 """
 
 import sys
@@ -135,12 +137,16 @@ def test_lu_solve_gives_up_and_solve_falls_back(ozk, set_polls):
     assert D.read_flags(flags) & _lib.OZK_FLAG_WAIT_TIMEOUT
     # the bounds of the solve tests: FP64 residuals reach FP64 accuracy, the
     # Ozaki residual (high, K = 2100) bounds the refinement near 1e-8
-    case(f"solve n={n} with the triangular solves giving up")
+    case(f"solve n={n} with the triangular solves giving up (NumPy and torch input)")
     xr = np.linalg.solve(A, b)
+    n0 = retries()
     x = ozk.solve(A, b)
+    assert retries() > n0  # the NumPy path repeated its solves
     assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-12
     x = ozk.solve(A, b, residual_mode="ozaki")
     assert np.linalg.norm(x - xr) / np.linalg.norm(xr) <= 1e-5
+    xt = ozk.solve(At, torch.from_numpy(b).to(dev)).cpu().numpy()
+    assert np.linalg.norm(xt - xr) / np.linalg.norm(xr) <= 1e-12
     set_polls(0)
     case(f"ozk_lu_solve_f32 n={n}, built-in limit")
     d, flags = S.lu_solve_f32(LU, perm, rhs, dev)
