@@ -17,6 +17,7 @@ the DMA engine moves the other (a direct copy from pageable memory, and
 the page faults of a fresh output array, are otherwise serial).
 """
 
+import atexit
 import ctypes
 import os
 import threading
@@ -48,6 +49,9 @@ class _Runtime:
                            ("hipMemcpy", [vp, vp, sz, i]),
                            ("hipMemcpyAsync", [vp, vp, sz, i, vp]),
                            ("hipMemset", [vp, i, sz]),
+                           ("hipHostFree", [vp]),
+                           ("hipStreamDestroy", [vp]),
+                           ("hipDeviceSynchronize", []),
                            ("hipHostMalloc", [ctypes.POINTER(vp), sz, ctypes.c_uint]),
                            ("hipEventCreate", [ctypes.POINTER(vp)]),
                            ("hipEventRecord", [vp, vp]),
@@ -348,6 +352,8 @@ class _Blas:
         b.rocblas_dgemm.argtypes = [vp, i, i, i, i, i, dp, vp, i, vp, i, dp, vp, i]
         b.rocblas_dgeam.restype = i
         b.rocblas_dgeam.argtypes = [vp, i, i, i, i, dp, vp, i, dp, vp, i, vp, i]
+        b.rocblas_destroy_handle.restype = i
+        b.rocblas_destroy_handle.argtypes = [vp]
         h = vp()
         self._chk(b.rocblas_create_handle(ctypes.byref(h)), "rocblas_create_handle")
         self._chk(b.rocblas_set_stream(h, None), "rocblas_set_stream")
@@ -422,6 +428,53 @@ def _get(name, make):
 
 def _rt():
     return _get("rt", _Runtime)
+
+
+def _release_at_exit():
+    """At interpreter exit, before the runtime's own teardown: let queued
+    work end, then release what this module holds in the runtime (the
+    staging buffers and their events, the rocBLAS handle, the compute stream,
+    the pool's cached blocks), so that none of it is left for the runtime's
+    static destructors.  The runtime and the pool stay: blocks that arrays
+    release later are freed at once.  Errors are ignored: the runtime may be
+    unusable by then."""
+    with _state_lock:
+        st = dict(_state)
+        for k in ("stager", "blas", "cstream"):
+            _state.pop(k, None)
+    rt = st.get("rt")
+    if rt is None:
+        return
+    h = rt.h
+    try:
+        h.hipDeviceSynchronize()
+        stager = st.get("stager")
+        if stager is not None:
+            stager.pool.shutdown(wait=True)
+            for b in stager.buf:
+                h.hipHostFree(b)
+            for e in stager.ev:
+                h.hipEventDestroy(e)
+        blas_ = st.get("blas")
+        if blas_ is not None:
+            blas_.b.rocblas_destroy_handle(blas_.h)
+        if st.get("cstream") is not None:
+            h.hipStreamDestroy(st["cstream"])
+        pool = st.get("pool")
+        if pool is not None:
+            with pool.lock:
+                for ptrs in pool.free.values():
+                    for ptr in ptrs:
+                        h.hipFree(ptr)
+                pool.free.clear()
+                pool.cached = 0
+                pool.keep = 0  # blocks released later are freed, not kept
+        h.hipGetLastError()
+    except Exception:
+        pass
+
+
+atexit.register(_release_at_exit)
 
 
 def _pool():

@@ -411,7 +411,14 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
 // wave 0 adds and folds.  Every partial sum of a slice product lies on one
 // grid below 2^24 units, so the sum over the waves is exact in any order.
 // x's slices are extracted the same way, once.
-template <int EPL, bool FULL, int W, int NHI, int NLO>
+//
+// D > 0: the rows reach the waves through an LDS ring of D row buffers
+// instead of a one-row register prefetch, so that D rows are in flight per
+// workgroup while one is worked on.  Each wave copies its own KW elements of
+// a row (global_load_lds_dwordx4, EPL / 2 loads of 1 KiB) and reads only
+// those, so its own vmcnt orders the copy before the reads.  Needs 16-byte
+// aligned rows and even K.
+template <int EPL, bool FULL, int W, int NHI, int NLO, int D = 0>
 __global__ __launch_bounds__(64 * W) void residual_split_kernel(
     const double* __restrict__ A, int64_t N, int64_t K, int64_t lda,
     const double* __restrict__ x, int64_t ldx, const double* __restrict__ b,
@@ -456,6 +463,31 @@ __global__ __launch_bounds__(64 * W) void residual_split_kernel(
     row_max2(u, v);
     return u;
   };
+
+  // LDS ring (D > 0): buffer trow % D of this wave holds its elements of
+  // the workgroup's row trow (rows cur = blockIdx.x + trow G).
+  constexpr int kDmaPerRow = D > 0 ? KW * 8 / 1024 : 0;
+  static_assert(D == 0 || KW % 128 == 0, "whole 1 KiB copies per wave");
+  __shared__ double ring[D > 0 ? D : 1][D > 0 ? W : 1][D > 0 ? KW : 1];
+  auto dma_row = [&](int64_t row, int slot) {
+    // lane l copies elements e, e + 1 (e = 2 l + 128 i) of the wave's part;
+    // past the end of a short row it copies the row's last pair instead
+    const char* a = (const char*)(A + row * lda);
+    const uint32_t base = lds_offset(&ring[slot][wave][0]);
+#pragma unroll
+    for (int i = 0; i < kDmaPerRow; ++i) {
+      int e = kw0 + 128 * i + 2 * lane;
+      if constexpr (!FULL) e = e < Ki ? e : Ki - 2;
+      dma16(base + i * 1024, a, 8u * (uint32_t)e);
+    }
+  };
+  int trow = 0;  // this workgroup's row counter
+  if constexpr (D > 0) {  // the first D rows load while x is extracted
+#pragma unroll
+    for (int i = 0; i < D; ++i)
+      if ((int64_t)blockIdx.x + i * (int64_t)gridDim.x < N)
+        dma_row((int64_t)blockIdx.x + i * (int64_t)gridDim.x, i);
+  }
 
   uint32_t xp[NT][H];  // x's slices, BF16 pairs (elements j, j + 1)
   float cs[NT];        // their scales 2^c
@@ -513,7 +545,7 @@ __global__ __launch_bounds__(64 * W) void residual_split_kernel(
       }
     }
   };
-  constexpr bool PF = EPL <= 16;  // the next row's prefetch fits in registers
+  constexpr bool PF = EPL <= 16 && D == 0;  // the next row's prefetch fits in registers
   const int64_t G = gridDim.x;
   int64_t cur = blockIdx.x;
   if (PF && cur < N) load_row(cur);
@@ -521,8 +553,31 @@ __global__ __launch_bounds__(64 * W) void residual_split_kernel(
 
   while (cur < N) {  // uniform over the workgroup
     const int64_t nxt = cur + G;
-    if constexpr (!PF) load_row(cur);
-    const double bv = (wave == 0 && lane == 0) ? b[cur * ldb] : 0.0;
+    if constexpr (D > 0) {
+      // rows copied after this one: min(D - 1, rows left after it); every
+      // other vector memory operation of the wave only adds to the count
+      static_assert(D <= 3, "waits for up to two later rows");
+      const int64_t later = (N - 1 - cur) / G;
+      const int slot = trow % D;
+      if (later >= D - 1) wait_vm<(D - 1) * kDmaPerRow>();
+      else if (later == 1) wait_vm<kDmaPerRow>();
+      else wait_vm<0>();
+#pragma unroll
+      for (int j = 0; j < EPL; ++j) {
+        const int k = kw0 + j * 64 + lane;
+        const double v = ring[slot][wave][j * 64 + lane];
+        nx[j] = (FULL || k < Ki) ? v : 0.0;
+      }
+      // the reads complete before the buffer is refilled with row trow + D
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (cur + (int64_t)D * G < N) dma_row(cur + (int64_t)D * G, slot);
+      ++trow;
+    } else if constexpr (!PF) {
+      load_row(cur);
+    }
+    // a wave-uniform (scalar) load: a vector load would make the compiler
+    // wait for every outstanding copy of the ring before its use
+    const double bv = b[cur * ldb];
     float Rh[EPL], Rl[EPL];
     bool bad = false;
     float mh = 0.0f, ml = 0.0f;
@@ -723,27 +778,38 @@ static void launch_rows_1(const double* A, int64_t N, int64_t K, int64_t lda,
 
 // One right-hand side on the split-row kernel (2048 < K <= kResMaxK): W = 4
 // waves of 1024 elements up to K = 4096, else 8 waves of 1024 or 2048.
+// Rows longer than 4096 elements come through an LDS ring (D = 2 rows of
+// 8192, one of 16384 elements: 128 KiB) when they are 16-byte aligned and K
+// is even, else through the register prefetch.
 static void launch_rows_split(const double* A, int64_t N, int64_t K, int64_t lda,
                               const double* x, int64_t ldx, const double* b, int64_t ldb,
                               double* r, int64_t ldr, int rho, int nhi, uint32_t* flags,
                               hipStream_t st) {
   // persistent grid: 8 / W workgroups per CU
   const int64_t cus = cu_count();
-#define OZK_SPLIT(E, W, H)                                                           \
+  const bool ring = (uintptr_t)A % 16 == 0 && lda % 2 == 0 && K % 2 == 0;
+#define OZK_SPLIT_D(E, W, H, D)                                                      \
   do {                                                                               \
     const int64_t g = cus * (8 / (W));                                               \
     const dim3 grid((unsigned)(N < g ? N : g));                                      \
     if (K == 64 * (E) * (W))                                                         \
-      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, 1>), grid, dim3(64 * (W)), \
-                         0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, rho, flags);   \
+      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, 1, D>), grid,         \
+                         dim3(64 * (W)), 0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, \
+                         rho, flags);                                                \
     else                                                                             \
-      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, 1>), grid, dim3(64 * (W)), \
-                         0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, rho, flags);   \
+      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, 1, D>), grid,        \
+                         dim3(64 * (W)), 0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, \
+                         rho, flags);                                                \
   } while (0)
-#define OZK_SPLIT_K(H)                          \
-  if (K <= 64 * 16 * 4) OZK_SPLIT(16, 4, H);    \
-  else if (K <= 64 * 16 * 8) OZK_SPLIT(16, 8, H); \
-  else OZK_SPLIT(32, 8, H);
+#define OZK_SPLIT(E, W, H, D)          \
+  do {                                 \
+    if (ring) OZK_SPLIT_D(E, W, H, D); \
+    else OZK_SPLIT_D(E, W, H, 0);      \
+  } while (0)
+#define OZK_SPLIT_K(H)                                 \
+  if (K <= 64 * 16 * 4) OZK_SPLIT_D(16, 4, H, 0);      \
+  else if (K <= 64 * 16 * 8) OZK_SPLIT(16, 8, H, 2);   \
+  else OZK_SPLIT(32, 8, H, 1);
   if (nhi == 4) {
     OZK_SPLIT_K(4);
   } else {
@@ -751,6 +817,7 @@ static void launch_rows_split(const double* A, int64_t N, int64_t K, int64_t lda
   }
 #undef OZK_SPLIT_K
 #undef OZK_SPLIT
+#undef OZK_SPLIT_D
 }
 
 // r = b - Ozaki(A, x) for up to kResMaxCols right-hand sides (column j of x,

@@ -11,7 +11,8 @@ units), so the FP32 products the reference forms are order-independent.
   gram     gram(A, mode='ozaki', precision='high') on 32768 x 2048 N(0,1)
            (rho from A.shape[0] = 32768: 20; K-split tail of 16 tiles)
   wide     matmul medium / max at K = 8192, a_ij = (U - 0.5) exp(phi N)
-           with phi_A, phi_B in {0.5, 4}
+           with phi_A, phi_B in {0.5, 4}: 48 x 8192 x 40 in full, and
+           8192^3 on 3 rows for each of the four (phi_A, phi_B) pairs
   C2       matmul high 4096^3 N(0,1) (rho 18, BF16 planes)
   metric   matmul high 8192^3 N(0,1) (rho 19, INT8 planes)
   solve    solve(A, b, residual_mode='ozaki'), n = 4096,
@@ -128,19 +129,67 @@ def test_wide_range_k8192(ozk, precision, phi_a, phi_b):
         assert np.array_equal(C, ref, equal_nan=True)
 
 
+# 8192^3 wide-range operands, each drawn on its own generator as the
+# configuration states, and the oracle's column extraction of each B with
+# the max preset's slices (5 hi, 4 lo), whose leading slices are those of
+# the medium preset: the extraction is sequential.
+_WIDE = {}
+
+
+def _wide_operand(phi, which):
+    key = (phi, which)
+    if key not in _WIDE:
+        n = 8192
+        rs = np.random.RandomState({"A": 40, "B": 41}[which] + int(10 * phi))
+        _WIDE[key] = (rs.rand(n, n) - 0.5) * np.exp(phi * rs.randn(n, n))
+    return _WIDE[key]
+
+
+def _wide_b_slices(phi):
+    key = (phi, "Bsl")
+    if key not in _WIDE:
+        B = _wide_operand(phi, "B")
+        rho = O.rho_f32(B.shape[0])
+        hi, lo = OP.split_hi_lo(B)
+        bh, bhe = O.extract_cols_f32(hi, rho, 5)
+        bl, ble = O.extract_cols_f32(lo, rho, 4)
+        _WIDE[key] = (bh, bhe, bl, ble)
+    return _WIDE[key]
+
+
+def _oracle_rows_b(A_rows, bsl, rho, nh, nl):
+    """Order A4 on rows of A against B's precomputed slices."""
+    bh, bhe, bl, ble = bsl
+    hi, lo = OP.split_hi_lo(A_rows)
+    ah, ahe = O.extract_rows_f32(hi, rho, nh)
+    al, ale = O.extract_rows_f32(lo, rho, nl)
+    a, ae = np.concatenate([ah, al]), np.concatenate([ahe, ale])
+    b, be = np.concatenate([bh[:nh], bl[:nl]]), np.concatenate([bhe[:nh], ble[:nl]])
+    sched = OP.ondevice_schedule(nh, nl)
+    with warnings.catch_warnings(), np.errstate(all="ignore"):
+        warnings.simplefilter("ignore")
+        P = OP.slice_products(a, b, sched)
+        return OP.combine_f64(*OP.accumulate_a4(P, sched, ae, be))
+
+
+@pytest.mark.parametrize("phi_a,phi_b", [(0.5, 0.5), (0.5, 4.0), (4.0, 0.5), (4.0, 4.0)])
 @pytest.mark.parametrize("precision", ["medium", "max"])
-def test_wide_range_8192_cubed(ozk, precision):
-    rng = np.random.RandomState(4)
+def test_wide_range_8192_cubed(ozk, precision, phi_a, phi_b):
     n = 8192
-    A, B = wide(rng, (n, n), 4.0), wide(rng, (n, n), 0.5)
+    A, B = _wide_operand(phi_a, "A"), _wide_operand(phi_b, "B")
     nh, nl = OP.resolve_precision(precision)
-    case(f"matmul {precision} fused 8192^3 phi=(4, 0.5) on device")
+    case(f"matmul {precision} fused 8192^3 phi=({phi_a}, {phi_b}) on device")
     At, Bt = torch_inputs(A, B)
     C = ozk.matmul(At, Bt, pipeline="ondevice", precision=precision).cpu().numpy()
     del At, Bt
     rows = np.r_[0, 4097, n - 1]
-    case(f"matmul {precision} oracle on 3 rows")
-    assert np.array_equal(C[rows], O.matmul_ondevice_a4(A[rows], B, "raise", nh, nl))
+    case(f"matmul {precision} oracle on 3 rows, phi=({phi_a}, {phi_b})")
+    ref = _oracle_rows_b(A[rows], _wide_b_slices(phi_b), O.rho_f32(n), nh, nl)
+    assert np.array_equal(C[rows], ref, equal_nan=True)
+    if (phi_a, phi_b) == (4.0, 0.5) and precision == "max":
+        # the whole pipeline's oracle on one row pins the helper above
+        assert np.array_equal(C[rows[:1]], O.matmul_ondevice_a4(A[rows[:1]], B, "raise", nh, nl),
+                              equal_nan=True)
 
 
 @pytest.mark.parametrize("n,kind", [(4096, "C2 BF16 planes"), (8192, "metric INT8 planes")])
@@ -151,8 +200,8 @@ def test_high_square(ozk, n, kind):
     At, Bt = torch_inputs(A, B)
     C = ozk.matmul(At, Bt, pipeline="ondevice", precision="high").cpu().numpy()
     del At, Bt
-    rows = np.r_[0, 1, n // 2, n - 1]
-    case(f"matmul high oracle on 4 rows of {n}^3")
+    rows = np.r_[0, 1, n // 3, n // 2, n // 2 + 1, 2 * n // 3, n - 2, n - 1]
+    case(f"matmul high oracle on 8 rows of {n}^3")
     ref, cert = oracle_a4(A[rows], B, O.rho_f32(n), 4, 1)
     assert cert
     assert np.array_equal(C[rows], ref)

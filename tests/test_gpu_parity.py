@@ -586,13 +586,15 @@ def test_residual_bit_exact(ozk, shape):
 
 
 @pytest.mark.parametrize("N,K", [(37, 1), (37, 1100), (129, 4096), (5, 513), (70, 2049),
-                                 (33, 3000), (40, 8192), (9, 12000), (17, 16384),
-                                 (6, 16385)])
+                                 (33, 3000), (40, 8192), (300, 8192), (11, 5001), (9, 12000),
+                                 (7, 9999), (17, 16384), (6, 16385)])
 @pytest.mark.parametrize("precision", ["high", "medium", "max"])
 def test_residual_fused_rows_bit_exact(ozk, N, K, precision):
     # high / medium: K <= 2048 runs the one-wave-per-row kernel, K <= 16384
     # the split-row kernel (4 waves of 1024 elements up to K = 4096, then 8
-    # waves of 1024 or 2048); K = 16385 and max take the slice-GEMM route
+    # waves of 1024 or 2048, their rows through an LDS ring when K is even,
+    # else the register prefetch: 5001, 9999); K = 16385 and max take the
+    # slice-GEMM route
     rng = np.random.RandomState(N + K)
     A = (rng.rand(N, K) - 0.5) * np.exp(2.0 * rng.randn(N, K))
     x, b = rng.randn(K), rng.randn(N)
