@@ -18,6 +18,8 @@
 
 #include "sigma.h"
 
+#include <type_traits>
+
 namespace ozk {
 
 // Slice plane formats.  BF16: the FP32 slice value's BF16 bits.  I8: the
@@ -50,6 +52,17 @@ __device__ __forceinline__ int byte_sum(uint32_t w, int acc) {
 }
 __device__ __forceinline__ int byte_sum(uint16_t w, int acc) { return byte_sum((uint32_t)w, acc); }
 __device__ __forceinline__ int byte_sum(uint2 w, int acc) { return byte_sum(w.y, byte_sum(w.x, acc)); }
+
+// A value that every lane of the wave holds, as a scalar.
+__device__ __forceinline__ float wave_uniform(float x) {
+  return __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(x)));
+}
+__device__ __forceinline__ double wave_uniform(double x) {
+  const uint64_t u = (uint64_t)__double_as_longlong(x);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)u);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(u >> 32));
+  return __longlong_as_double((long long)(((uint64_t)hi << 32) | lo));
+}
 
 // Sum over the 64 lanes of a wave.
 __device__ __forceinline__ int wave_sum(int v) {
@@ -132,7 +145,8 @@ __device__ __forceinline__ int64_t xcd_line(int64_t bid, int64_t n) {
 // BLOCK threads each; thread t of a line owns the VEC consecutive elements
 // k = (j * BLOCK + t) * VEC + v, j < EPT, v < VEC, which must cover the
 // padded line (EPT * BLOCK * VEC >= ld).  With `vec_ok` (line starts 16-byte
-// aligned) a thread reads its VEC doubles with 16-byte loads; it writes its
+// aligned, len a multiple of VEC) a thread reads its VEC doubles with 16-byte
+// loads; it writes its
 // VEC plane elements, which are adjacent in the plane, with one store.
 // Planes: part 0 -> [0, n0), part 1 -> [n0, n0 + n1).
 template <int FMT, int VEC> struct PlaneVec;
@@ -142,6 +156,44 @@ template <> struct PlaneVec<kFmtBf16, 2> { typedef uint32_t type; };
 template <> struct PlaneVec<kFmtBf16, 4> { typedef uint2 type; };
 template <> struct PlaneVec<kFmtI8, 8> { typedef uint2 type; };
 template <> struct PlaneVec<kFmtBf16, 8> { typedef uint4 type; };
+
+// Short-form plane words (fast_step): the carriers c[u] of the VEC
+// elements (INT8: q + i8_magic(offset), whose low byte is the element; BF16:
+// q * 2^(rho - 24), exact in BF16, whose high half is the element) packed
+// as the elements' word.
+template <int FMT, int VEC>
+__device__ __forceinline__ typename PlaneVec<FMT, VEC>::type pack_fast(const float (&c)[VEC]) {
+  typedef typename PlaneVec<FMT, VEC>::type TV;
+  if constexpr (FMT == kFmtI8 && VEC == 2) {
+    return (TV)pack_low_bytes(c[0], c[1], c[1], c[1]);
+  } else {
+    union {
+      TV v;
+      uint32_t w[sizeof(TV) / 4];
+    } o;
+    if constexpr (FMT == kFmtI8) {
+#pragma unroll
+      for (int i = 0; i < VEC / 4; ++i)
+        o.w[i] = pack_low_bytes(c[4 * i], c[4 * i + 1], c[4 * i + 2], c[4 * i + 3]);
+    } else {
+#pragma unroll
+      for (int i = 0; i < VEC / 2; ++i) o.w[i] = pack_high_halves(c[2 * i], c[2 * i + 1]);
+    }
+    return o.v;
+  }
+}
+
+// The carrier constant of pack_fast for a slice of grid count q.
+template <int FMT>
+__device__ __forceinline__ float fast_carrier(int rho) {
+  return FMT == kFmtI8 ? i8_magic(i8_offset(rho)) : ldexpf(1.0f, rho - 24);
+}
+// BF16: q * 2^(rho - 24) + 0, so that q = -0 (rint of a small negative
+// number) gives +0, as the plain form's (R + sigma) - sigma does.
+template <int FMT>
+__device__ __forceinline__ float fast_carry(float q, float k) {
+  return FMT == kFmtI8 ? q + k : __builtin_fmaf(q, k, 0.0f);
+}
 
 template <typename W, int BLOCK, int EPT, int LPB, int FMT, int VEC>
 __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
@@ -164,7 +216,6 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
   const int64_t grp = xcd_line(blockIdx.x, gridDim.x);
   const int64_t line = grp * LPB + threadIdx.x / BLOCK;
   const bool live = line < lines;
-  const double* x = X + line * ldx;
   // Plane offset of the thread's first element: BLOCK * VEC is a multiple of
   // the elements per chunk, so the in-chunk position (and its swizzle) is
   // fixed per thread and j only advances the chunk by BLOCK * VEC / kPer.
@@ -186,30 +237,48 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
     else return Rr[q][i];
   };
   bool bad = false;
+  // Every load reads an address inside X (an element past the line's end
+  // reads the line's first element, a line past the last reads line 0) and
+  // its value is replaced by zero afterwards, so no branch separates the
+  // chunks' loads and several are in flight at once.  vec_ok (16-byte
+  // aligned lines, len a multiple of VEC): 16-byte loads, whole chunks.
+  const double* xl = X + (live ? line : 0) * ldx;
+  auto read_split = [&](auto vec) {
 #pragma unroll
-  for (int j = 0; j < EPT; ++j) {
-    const int64_t k0 = ((int64_t)j * BLOCK + t) * VEC;
-    double v[VEC];
-    if (vec_ok && live && k0 + VEC <= len) {
+    for (int j = 0; j < EPT; ++j) {
+      const int64_t k0 = ((int64_t)j * BLOCK + t) * VEC;
+      double v[VEC];
+      if constexpr (decltype(vec)::value) {
+        const bool ok = live && k0 < len;
+        const double* p = xl + (ok ? k0 : 0);
 #pragma unroll
-      for (int u = 0; u < VEC; u += 2) {
-        const double2 d = *(const double2*)(x + k0 + u);
-        v[u] = d.x;
-        v[u + 1] = d.y;
+        for (int u = 0; u < VEC; u += 2) {
+          const double2 d = *(const double2*)(p + u);
+          v[u] = ok ? d.x : 0.0;
+          v[u + 1] = ok ? d.y : 0.0;
+        }
+      } else {
+#pragma unroll
+        for (int u = 0; u < VEC; ++u) {
+          const bool ok = live && k0 + u < len;
+          const double d = xl[ok ? k0 + u : 0];
+          v[u] = ok ? d : 0.0;
+        }
       }
-    } else {
 #pragma unroll
-      for (int u = 0; u < VEC; ++u) v[u] = (live && k0 + u < len) ? x[k0 + u] : 0.0;
+      for (int u = 0; u < VEC; ++u) {
+        bad |= !isfinite(v[u]);
+        W p[NP];
+        split<W>(v[u], p);
+#pragma unroll
+        for (int q = 0; q < NP; ++q) R(q, j * VEC + u) = p[q];
+      }
     }
-#pragma unroll
-    for (int u = 0; u < VEC; ++u) {
-      bad |= !isfinite(v[u]);
-      W p[NP];
-      split<W>(v[u], p);
-#pragma unroll
-      for (int q = 0; q < NP; ++q) R(q, j * VEC + u) = p[q];
-    }
-  }
+  };
+  if (vec_ok)
+    read_split(std::true_type());
+  else
+    read_split(std::false_type());
   if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 
   const int ns = NP == 2 ? max(n0, n1) : n0;
@@ -227,32 +296,61 @@ __global__ __launch_bounds__(BLOCK * LPB) void extract_lines_reg(
     for (int q = 0; q < NP; ++q) {
       const int nq = q == 0 ? n0 : n1;
       if (s >= nq) continue;  // uniform
-      SliceConst<W> kc = slice_const<W>(m[q], rho);
+      // the line maximum is the same in every lane of a wave: the slice
+      // constants are computed once, by scalar instructions
+      SliceConst<W> kc = slice_const<W>(wave_uniform(m[q]), rho);
       const int ce = plane_exponent<FMT>(kc, rho, flags, t == 0);
       const int pl = (q == 0 ? 0 : n0) + s;
       T* out = S + pl * plane + off0;
       int qs = 0;
+      auto emit = [&](auto fastc) {
+        constexpr bool FAST = decltype(fastc)::value;
 #pragma unroll
-      for (int j = 0; j < EPT; ++j) {
-        union {
-          TV w;
-          T e[VEC];
-        } pk;
+        for (int j = 0; j < EPT; ++j) {
+          union {
+            TV w;
+            T e[VEC];
+          } pk;
+          if constexpr (FAST) {
+            const FastSlice fs = fast_slice(kc, rho);
+            const float carrier = fast_carrier<FMT>(rho);
+            float c[VEC];
 #pragma unroll
-        for (int u = 0; u < VEC; ++u) {
-          W r = R(q, j * VEC + u);
-          W v = (r + kc.sigma) - kc.sigma;
-          if (kc.zero) v = W(0);
-          W rn = r - v;
-          // pinned here: otherwise the residual updates sink below the
-          // stores and every v stays live meanwhile
-          asm volatile("" : "+v"(rn));
-          R(q, j * VEC + u) = rn;
-          const float sv = slice_value_f32(v, kc.inv);
-          pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
+            for (int u = 0; u < VEC; ++u) {
+              float r = R(q, j * VEC + u);
+              const float qv = fast_step(r, fs);
+              asm volatile("" : "+v"(r));
+              R(q, j * VEC + u) = r;
+              c[u] = fast_carry<FMT>(qv, carrier);
+            }
+            pk.w = pack_fast<FMT, VEC>(c);
+          } else {
+#pragma unroll
+            for (int u = 0; u < VEC; ++u) {
+              W r = R(q, j * VEC + u);
+              W v = (r + kc.sigma) - kc.sigma;
+              if (kc.zero) v = W(0);
+              W rn = r - v;
+              // pinned here: otherwise the residual updates sink below the
+              // stores and every v stays live meanwhile
+              asm volatile("" : "+v"(rn));
+              R(q, j * VEC + u) = rn;
+              const float sv = slice_value_f32(v, kc.inv);
+              pk.e[u] = PlaneElem<FMT>::make(sv, qscale);
+            }
+          }
+          if constexpr (FMT == kFmtI8) qs = byte_sum(pk.w, qs);
+          if (((int64_t)j * BLOCK + t) * VEC < ld) *(TV*)(out + j * step) = pk.w;
         }
-        if constexpr (FMT == kFmtI8) qs = byte_sum(pk.w, qs);
-        if (((int64_t)j * BLOCK + t) * VEC < ld) *(TV*)(out + j * step) = pk.w;
+      };
+      if constexpr (sizeof(W) == 4) {
+        // uniform per wave: a wave's lanes hold one line
+        if (__builtin_amdgcn_readfirstlane((int)fast_slice(kc, rho).ok))
+          emit(std::true_type());
+        else
+          emit(std::false_type());
+      } else {
+        emit(std::false_type());
       }
       if constexpr (FMT == kFmtI8) {
         qs = wave_sum(qs);
@@ -427,7 +525,11 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
   constexpr int64_t kWords = kGangLine / 4;
   const float qscale = ldexpf(1.0f, 24 - rho);
   __shared__ float red[NW][NP][kGangPW];
-  __shared__ float fin[NP][kGangPW];
+  // per (part, column): the slice constants of the slice at hand, computed
+  // once per workgroup (short form: s, u; plain form: sigma, inv, zero)
+  __shared__ float cst_s[NP][kGangPW], cst_u[NP][kGangPW];
+  __shared__ float cst_sig[NP][kGangPW], cst_inv[NP][kGangPW];
+  __shared__ int cst_mode[NP][kGangPW];  // 1: short form; 2: zero slice
   __shared__ uint32_t comb[NG][kGangKeys];
   __shared__ uint32_t place;
   __shared__ int gave_up;
@@ -456,23 +558,35 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
   __shared__ float lo_s[2 * R][kGangThreads];
   auto Rg = [&](int q, int c, int i) -> float& { return q == 0 ? Rh[c][i] : lo_s[c * R + i][t]; };
   bool bad[2] = {false, false};
-  const bool full = VEC && c0 + 1 < M;
+  // Every load reads an address inside X (a row past the last reads row 0, a
+  // column past the last reads column 0 or M - 1) and its value is replaced
+  // by zero afterwards, so no branch separates the R rows' loads: all of
+  // them are in flight at once.  VEC (X 16-byte aligned, ldx and M even):
+  // one 16-byte load per row for both columns.
+  double v[R][2];
 #pragma unroll
   for (int i = 0; i < R; ++i) {
     const int64_t row = r0 + i;
-    const double* x = X + (row < K ? row : 0) * ldx + c0;
-    double v[2];
-    if (full) {
-      const double2 d = *(const double2*)x;
-      v[0] = d.x;
-      v[1] = d.y;
+    const double* xr = X + (row < K ? row : 0) * ldx;
+    if constexpr (VEC) {
+      const bool ok = row < K && c0 < M;
+      const double2 d = *(const double2*)(xr + (ok ? c0 : 0));
+      v[i][0] = ok ? d.x : 0.0;
+      v[i][1] = ok ? d.y : 0.0;
     } else {
-      v[0] = c0 < M ? x[0] : 0.0;
-      v[1] = c0 + 1 < M ? x[1] : 0.0;
+#pragma unroll
+      for (int c = 0; c < 2; ++c) {
+        const bool ok = row < K && c0 + c < M;
+        const double d = xr[c0 + c < M ? c0 + c : M - 1];
+        v[i][c] = ok ? d : 0.0;
+      }
     }
+  }
+#pragma unroll
+  for (int i = 0; i < R; ++i) {
 #pragma unroll
     for (int c = 0; c < 2; ++c) {
-      const double xv = row < K ? v[c] : 0.0;
+      const double xv = v[i][c];
       bad[c] |= !isfinite(xv);
       float p[NP];
       split<float>(xv, p);
@@ -502,7 +616,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
         m[q][c] = mm;
       }
     }
-    __syncthreads();  // the previous slice's readers of fin are done
+    __syncthreads();  // the previous slice's readers of the constants are done
     if (lane < CP) {
 #pragma unroll
       for (int q = 0; q < NP; ++q) {
@@ -538,7 +652,18 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
       uint32_t kk = comb[0][t];
 #pragma unroll
       for (int g = 1; g < NG; ++g) kk = max(kk, comb[g][t]);
-      fin[t / kGangPW][t % kGangPW] = key_max(kk);
+      const int q = t / kGangPW, col = t % kGangPW;
+      SliceConst<float> kc = slice_const<float>(key_max(kk), rho);
+      if (s < (q == 0 ? n0 : n1)) {
+        const int ce = plane_exponent<FMT>(kc, rho, flags, member == 0);
+        if (member == 0) E[((q == 0 ? 0 : n0) + s) * eplane + panel * kGangPW + col] = ce;
+      }
+      const FastSlice fs = fast_slice(kc, rho);
+      cst_s[q][col] = fs.s;
+      cst_u[q][col] = fs.u;
+      cst_sig[q][col] = kc.sigma;
+      cst_inv[q][col] = kc.inv;
+      cst_mode[q][col] = fs.ok ? 1 : (kc.zero ? 2 : 0);
     }
     __syncthreads();
 #pragma unroll
@@ -548,36 +673,55 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
       const int pl = (q == 0 ? 0 : n0) + s;
 #pragma unroll
       for (int c = 0; c < 2; ++c) {
-        SliceConst<float> kc = slice_const<float>(fin[q][2 * cp + c], rho);
-        const int ce = plane_exponent<FMT>(kc, rho, flags, r0 == 0);
+        const int col = 2 * cp + c;
+        const int mode = cst_mode[q][col];
         const int64_t line = c0 + c;
-        union {
-          typename PlaneVec<FMT, R>::type w;
-          T e[R];
-        } out;
+        typedef typename PlaneVec<FMT, R>::type TV;
+        TV out;  // merged as a whole word (byte-wise merges cost more)
         int qs = 0;
+        if (mode == 1) {  // every lane, but for exceptional lines
+          const FastSlice fs = {cst_s[q][col], cst_u[q][col], true};
+          const float carrier = fast_carrier<FMT>(rho);
+          float cv[R];
 #pragma unroll
-        for (int i = 0; i < R; ++i) {
-          const float r = Rg(q, c, i);
-          float v = (r + kc.sigma) - kc.sigma;
-          if (kc.zero) v = 0.0f;
-          float rn = r - v;
-          asm volatile("" : "+v"(rn));  // as in extract_lines_reg
-          Rg(q, c, i) = rn;
-          const float sv = slice_value_f32(v, kc.inv);
-          out.e[i] = PlaneElem<FMT>::make(sv, qscale);
+          for (int i = 0; i < R; ++i) {
+            float r = Rg(q, c, i);
+            const float qv = fast_step(r, fs);
+            asm volatile("" : "+v"(r));  // as in extract_lines_reg
+            Rg(q, c, i) = r;
+            cv[i] = fast_carry<FMT>(qv, carrier);
+          }
+          out = pack_fast<FMT, R>(cv);
+        } else {
+          const float sig = cst_sig[q][col], inv = cst_inv[q][col];
+          const bool zero = mode == 2;
+          union {
+            TV w;
+            T e[R];
+          } pk;
+#pragma unroll
+          for (int i = 0; i < R; ++i) {
+            const float r = Rg(q, c, i);
+            float v = (r + sig) - sig;
+            if (zero) v = 0.0f;
+            float rn = r - v;
+            asm volatile("" : "+v"(rn));  // as in extract_lines_reg
+            Rg(q, c, i) = rn;
+            const float sv = slice_value_f32(v, inv);
+            pk.e[i] = PlaneElem<FMT>::make(sv, qscale);
+          }
+          out = pk.w;
         }
-        if constexpr (FMT == kFmtI8) qs = byte_sum(out.w, qs);
+        if constexpr (FMT == kFmtI8) qs = byte_sum(out, qs);
         if (store)
-          *(decltype(out.w)*)(S + pl * plane + plane_offset<sizeof(T)>(line, r0, eplane)) =
-              out.w;
+          *(TV*)(S + pl * plane + plane_offset<sizeof(T)>(line, r0, eplane)) =
+              out;
         if constexpr (FMT == kFmtI8) {
           // the wave's lanes of this column pair: lane % CP
 #pragma unroll
           for (int off = CP; off < 64; off <<= 1) qs += __shfl_xor(qs, off);
           if (lane < CP) atomicAdd(&ssum[pl * kGangPW + 2 * cp + c], qs);
         }
-        if (r0 == 0) E[pl * eplane + line] = ce;
       }
     }
   }
@@ -949,7 +1093,7 @@ static int launch_lines(const double* X, int64_t lines, int64_t len,
 #define OZK_REG(B, EPT, LPB, V)                                                        \
   hipLaunchKernelGGL((extract_lines_reg<W, B, EPT, LPB, FMT, V>),                      \
                      dim3((unsigned)(lp / LPB)), dim3(B * LPB), 0, st, X, lines, len, ldx, \
-                     vec_ok, rho, n0, n1, S, ld, plane, E, lp, flags, Sg)
+                     vec_ok && len % V == 0, rho, n0, n1, S, ld, plane, E, lp, flags, Sg)
   // Shapes measured per line-length bucket (one or two lines per workgroup
   // so that several workgroups share a CU and overlap loads with stores).
   if (ld <= 256) {
@@ -1052,7 +1196,7 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
   int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(npanels * G));
   const uint32_t wait_ticks = wait_polls(kGangWaitTicks);
-  if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
+  if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0) && (cols % 2 == 0))
     hipLaunchKernelGGL((extract_cols_gang<FMT, true>), grid, dim3(kGangThreads), 0, st, X,
                        rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
                        ticket, G, wait_ticks, part);

@@ -98,7 +98,10 @@ def test_extract_f32_rows_and_cols(ll, kind, shape):
         else:
             sh, eh = O.extract_rows_f32(hi, rho, 4)
             sl, el = O.extract_rows_f32(lo, rho, 1)
-        assert np.array_equal(v, np.concatenate([sh, sl])), "slices"
+        ref = np.concatenate([sh, sl])
+        assert np.array_equal(v, ref), "slices"
+        # bit patterns too: the oracle's zero slices are +0, and so are the planes'
+        assert np.array_equal(v.view(np.uint32), ref.astype(np.float32).view(np.uint32)), "bits"
         assert np.array_equal(e, np.concatenate([eh, el]).astype(np.int32)), "exponents"
         assert not pl.nonfinite()
 
