@@ -78,7 +78,7 @@ extern "C" {
 void ozk_set_wait_polls(uint32_t polls);
 
 /* No counterpart in the reference: the extraction strategy of the calling
- * thread's later calls (thread-local).  1 (the default): columns of up to
+ * thread's later calls (thread-local).  1 (the default): columns of 4097 to
  * 8192 rows, and FP32 rows of 32769 to 262144 elements, are extracted by
  * gangs of workgroups that exchange their partial maxima, with waits that
  * give up after 0.2 s (OZK_FLAG_WAIT_TIMEOUT) when other work keeps the
@@ -126,9 +126,10 @@ int64_t ozk_slice_lines(int64_t lines);
  * sigma-trick extraction: n_hi slices of hi then n_lo slices of lo
  * (extract.py:197-286; NumPy twin extract.py:116-191).  by_cols = 0 extracts
  * per row of X (rows x cols), by_cols = 1 per column; in both cases a line
- * is stored contiguously.  Columns of up to 8192 rows are extracted in place
- * by groups of workgroups that exchange their per-slice column maxima through
- * the workspace (a bounded wait that gives up sets OZK_FLAG_WAIT_TIMEOUT in
+ * is stored contiguously.  Columns of up to 4096 rows are extracted in place,
+ * each by one workgroup (no workspace); columns of 4097 to 8192 rows in place
+ * by groups of workgroups that exchange their column maxima through the
+ * workspace (a bounded wait that gives up sets OZK_FLAG_WAIT_TIMEOUT in
  * flags: the planes are then not valid); longer columns are transposed
  * through the workspace.  Lines of 32769 to 262144 elements (rows, or the
  * transposed columns) are likewise held by groups of workgroups exchanging

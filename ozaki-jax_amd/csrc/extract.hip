@@ -443,18 +443,39 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
 // into panels of kGangPW = 16 (a 128-byte row segment of X) and each panel's
 // rows into runs of kGangRun; workgroup ("member") m of the panel's gang of
 // G = ceil(rows / kGangRun) holds run m of all 16 columns on chip (thread
-// t: columns 2 (t % 8) and 2 (t % 8) + 1, rows 8 (t / 8) .. +7 of the run,
-// read as 16-byte pairs; hi parts in registers, lo parts in LDS), so X is read once, in whole 128-byte row
-// segments, and every plane element is written once.  The arithmetic is
-// extract_lines_reg's; only the per-slice line maxima cross workgroups.
+// t: column t % 16, rows 32 (t / 16) .. +31 of the run; hi parts in
+// registers, lo parts in LDS), so X is read once, in whole 128-byte row
+// segments, and every plane element is written once.  The arithmetic is extract_lines_reg's; only line maxima
+// cross workgroups.
 //
-// Exchange, per (panel, slice): a record of G lines of 128 bytes, zeroed
-// before the launch.  Member m stores its 32 partial maxima (2 parts x 16
-// columns) as order keys, which are never 0, into line m, then waits until
-// every line is complete and combines them.  Every word is written once per
-// launch, so a reader that sees a nonzero word sees its final value: relaxed
-// agent-scope atomic loads and stores suffice (no fences, and no
-// read-modify-write on shared words).
+// Rounds.  A slice's exponent needs the maximum of the residual over the
+// whole column, so each slice costs an exchange between the members.
+// Round 0 settles slice 0 of both parts.  Round 1 settles up to three
+// slices of a part at once: besides max |R| (slice j), each member sends the
+// maxima of the next two residuals under the exponents they can have.  The
+// residual after a slice with grid u is at most u / 2 in magnitude, so the
+// next exponent is c' = rho + c - 25 unless the column's largest residual
+// falls below 2^(rho + c - 25) (then c' <= rho + c - 26): the members send
+// max |R_{j+1}| for c_j in {a, a - 1}, a = rho + c_{j-1} - 25, and
+// max |R_{j+2}| for the four (c_j, c_{j+1}) pairs that follow (keys
+// 0, 1..2, 3..6).  The combined maxima settle slice j exactly; slice j + 1
+// when c_j is one of its two candidates, and slice j + 2 likewise.  The
+// candidates' residuals are the short-form steps (fast_step) that the
+// emission then takes, so a settled slice is the one the slice-by-slice
+// procedure gives.  Candidates are taken only where the short form holds
+// for them; other columns, and later rounds, settle one slice per part.
+// For normally distributed columns the exponents step by -6 or -7
+// (rho = 19), so the four hi slices of the high preset take two rounds.
+//
+// Exchange, per (panel, round): a record of G lines, zeroed before the
+// launch (2 parts x 16 columns words a line; 7 times that in round 1).
+// Member m stores its partial maxima as order keys, which are never 0,
+// into line m, then waits until every line is complete and combines them.
+// Every word is written once per launch, so a reader that sees a nonzero
+// word sees its final value: relaxed agent-scope atomic loads and stores
+// suffice (no fences, and no read-modify-write on shared words).  Every
+// member settles the same slices (the same combined keys, the same rules),
+// so all agree on the next round's record.
 //
 // Progress: a member's place (panel, m) comes from a ticket taken when it
 // starts, so all members of the gangs before the first incomplete one have
@@ -463,22 +484,33 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
 // once).  Every wait is bounded all the same: after kGangWaitTicks ticks of
 // the 100 MHz real-time counter (0.2 s, or the limit a test set with
 // ozk_set_wait_polls) it sets OZK_FLAG_WAIT_TIMEOUT (the slices are then not
-// valid) and the member waits no more in later slices.  Other work that
+// valid) and the member waits no more in later rounds.  Other work that
 // holds the CUs for longer (another process, or a persistent GEMM on
 // another stream) can keep a gang's members apart that long; the caller
 // then repeats the extraction without gangs (ozk_set_gangs).
 constexpr int kGangPW = 16;
-constexpr int kGangRowsPT = 8;
-constexpr int kGangThreads = 512;
-constexpr int kGangRun = kGangThreads / (kGangPW / 2) * kGangRowsPT;  // 512 rows
+constexpr int kGangRowsPT = 32;
+constexpr int kGangThreads = 256;
+constexpr int kGangRun = kGangThreads / kGangPW * kGangRowsPT;  // 512 rows
 constexpr int kGangMaxMembers = 16;
 constexpr uint32_t kGangWaitTicks = 20000000u;
-constexpr int kGangKeys = 2 * kGangPW;  // keys per record line
-constexpr int64_t kGangLine = 128;      // bytes per record line
+constexpr int kGangSpecKeys = 7;        // keys per (part, column) in round 1
+constexpr int kGangWords = 2 * kGangPW;  // words per record line (round 1: x 7)
 constexpr int64_t kGangHeader = 256;    // the ticket word, padded
 
 __host__ __device__ constexpr int gang_members(int64_t ld) {
   return (int)((ld + kGangRun - 1) / kGangRun);
+}
+// Words per member line in round r, and the word offset of round r's
+// records in a panel's (rounds 0 .. r - 1 before it).
+__host__ __device__ constexpr int gang_round_words(int r) {
+  return r == 1 ? kGangSpecKeys * kGangWords : kGangWords;
+}
+__host__ __device__ constexpr int64_t gang_round_offset(int r, int G) {
+  return r == 0 ? 0
+                : (int64_t)G * (kGangWords + (r >= 2 ? kGangSpecKeys * kGangWords +
+                                                           (int64_t)(r - 2) * kGangWords
+                                                     : 0));
 }
 
 // Order key of a partial maximum (a non-negative float or NaN): the key of
@@ -506,37 +538,81 @@ __device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
   return 0u;
 }
 
+// Bounded wait for the n <= N nonzero words base[off + i * stride] at once
+// (their loads in flight together); false (and the flag) on time-out.
+template <int N>
+__device__ __forceinline__ bool wait_keys(const uint32_t* base, uint32_t off, uint32_t stride,
+                                          uint32_t (&k)[N], int n, uint32_t* flags,
+                                          uint32_t ticks) {
+  const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+  for (;;) {
+    bool all = true;
+#pragma unroll
+    for (int i = 0; i < N; ++i) {
+      if (i < n && !k[i])
+        k[i] = __hip_atomic_load(base + off + i * stride, __ATOMIC_RELAXED,
+                                 __HIP_MEMORY_SCOPE_AGENT);
+    }
+#pragma unroll
+    for (int i = 0; i < N; ++i) all &= i >= n || k[i] != 0u;
+    if (all) return true;
+    if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
+    __builtin_amdgcn_s_sleep(1);
+  }
+  atomicOr(flags, OZK_FLAG_WAIT_TIMEOUT);
+  return false;
+}
+
+// The short-form constants of exponent c (fast_slice for a known c).
+__device__ __forceinline__ FastSlice fast_slice_c(int c, int rho) {
+  SliceConst<float> k;
+  k.zero = false;
+  k.c = c;
+  return fast_slice(k, rho);
+}
+
 // INT8: `part` receives member m's sums of q over its rows, per plane pl and
 // column at part[(pl G + m) eplane + column] (added up by i8_sum_parts):
 // the packed bytes (q + offset) of all kGangRun rows, rows past the column's
 // end included (q = 0 there), less offset x kGangRun.
-// Bounded to 64 VGPRs (eight waves per SIMD), with the lo parts in LDS:
-// four members per CU, which cover each other's exchange waits.
-template <int FMT, bool VEC>
-__global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8))) void extract_cols_gang(
+// Four waves, up to 128 VGPRs each (four waves per SIMD), with the lo parts
+// in LDS: four members per CU, which cover each other's exchange waits.
+template <int FMT>
+__global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(4))) void extract_cols_gang(
     const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0,
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
     uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t wait_ticks,
     int32_t* __restrict__ part) {
   typedef typename PlaneElem<FMT>::type T;
-  constexpr int NP = 2, CP = kGangPW / 2, NW = kGangThreads / 64, R = kGangRowsPT;
-  constexpr int NG = kGangThreads / kGangKeys;  // key groups of a workgroup
-  constexpr int64_t kWords = kGangLine / 4;
+  constexpr int NP = 2, R = kGangRowsPT, NKS = kGangSpecKeys;
+  constexpr int NWORD = R * (int)sizeof(T) / 4;  // plane words of a thread's rows
+  constexpr int kMaxWords = NKS * kGangWords;    // 224
   const float qscale = ldexpf(1.0f, 24 - rho);
-  __shared__ float red[NW][NP][kGangPW];
-  // per (part, column): the slice constants of the slice at hand, computed
-  // once per workgroup (short form: s, u; plain form: sigma, inv, zero)
-  __shared__ float cst_s[NP][kGangPW], cst_u[NP][kGangPW];
-  __shared__ float cst_sig[NP][kGangPW], cst_inv[NP][kGangPW];
-  __shared__ int cst_mode[NP][kGangPW];  // 1: short form; 2: zero slice
-  __shared__ uint32_t comb[NG][kGangKeys];
+  // per-workgroup key maxima of the round, then all members' (order keys,
+  // LDS atomic max)
+  __shared__ uint32_t wkey[kMaxWords], wall[kMaxWords];
+  // per (part, column): slices settled so far, the last settled exponent,
+  // whether round 1 may take candidates after it, this round's count, and
+  // per slice settled in the round its constants (short form: s, u; plain
+  // form: sigma, inv) and form (1: short form; 2: zero slice; 0: plain)
+  struct GangCol {
+    int done, c, spec, d;
+    float a[3], b[3];
+    int mode[3], pad;
+  };
+  __shared__ GangCol gc[NP][kGangPW];
   __shared__ uint32_t place;
-  __shared__ int gave_up;
+  __shared__ int gave_up, more;
   __shared__ int ssum[FMT == kFmtI8 ? kMaxPlanes * kGangPW : 1];
-  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  const int t = threadIdx.x, lane = t & 63;
   if constexpr (FMT == kFmtI8) {
     for (int i = t; i < kMaxPlanes * kGangPW; i += kGangThreads) ssum[i] = 0;
+  }
+  for (int i = t; i < kMaxWords; i += kGangThreads) wkey[i] = wall[i] = 0u;
+  if (t < NP * kGangPW) {
+    gc[t / kGangPW][t % kGangPW].done = 0;
+    gc[t / kGangPW][t % kGangPW].spec = 0;
   }
   if (t == 0) {
     place = __hip_atomic_fetch_add(ticket, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -546,190 +622,413 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(8)
   const int64_t panel = place / (uint32_t)G;
   const int member = (int)(place % (uint32_t)G);
   const int ns = max(n0, n1);
-  uint32_t* const my = rec + panel * ns * G * kWords;
-  const int cp = t % CP;
-  const int64_t r0 = (int64_t)member * kGangRun + R * (t / CP);
-  const int64_t c0 = panel * kGangPW + 2 * cp;  // the thread's first line (column)
+  uint32_t* const my = rec + panel * gang_round_offset(ns, G);
+  const int col = t % kGangPW;
+  const int64_t r0 = (int64_t)member * kGangRun + R * (t / kGangPW);
+  const int64_t line = panel * kGangPW + col;  // the thread's column
 
-  // The one read.  The empty asm pins each part where it is made, so the
-  // compiler does not hold the doubles until the non-finite check.
-  // hi parts in registers, lo parts in LDS (32 KiB): four members per CU
-  float Rh[2][R];
-  __shared__ float lo_s[2 * R][kGangThreads];
-  auto Rg = [&](int q, int c, int i) -> float& { return q == 0 ? Rh[c][i] : lo_s[c * R + i][t]; };
-  bool bad[2] = {false, false};
-  // Every load reads an address inside X (a row past the last reads row 0, a
-  // column past the last reads column 0 or M - 1) and its value is replaced
-  // by zero afterwards, so no branch separates the R rows' loads: all of
-  // them are in flight at once.  VEC (X 16-byte aligned, ldx and M even):
-  // one 16-byte load per row for both columns.
-  double v[R][2];
+  // The one read: hi parts in registers, lo parts in LDS (32 KiB): four
+  // members per CU.  Every load reads an address inside X (a row past the
+  // last reads row 0, a column past the last column 0) and its value is
+  // replaced by zero afterwards, so no branch separates the R loads: all
+  // of them are in flight at once.
+  float Rh[R];
+  __shared__ float lo_s[R][kGangThreads];
+  bool bad = false;
+  {
+    double v[R];
+    const bool cok = line < M;
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-    const int64_t row = r0 + i;
-    const double* xr = X + (row < K ? row : 0) * ldx;
-    if constexpr (VEC) {
-      const bool ok = row < K && c0 < M;
-      const double2 d = *(const double2*)(xr + (ok ? c0 : 0));
-      v[i][0] = ok ? d.x : 0.0;
-      v[i][1] = ok ? d.y : 0.0;
-    } else {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const bool ok = row < K && c0 + c < M;
-        const double d = xr[c0 + c < M ? c0 + c : M - 1];
-        v[i][c] = ok ? d : 0.0;
-      }
+    for (int i = 0; i < R; ++i) {
+      const int64_t row = r0 + i;
+      const bool ok = cok && row < K;
+      const double d = X[(ok ? row : 0) * ldx + (ok ? line : 0)];
+      v[i] = ok ? d : 0.0;
     }
-  }
 #pragma unroll
-  for (int i = 0; i < R; ++i) {
-#pragma unroll
-    for (int c = 0; c < 2; ++c) {
-      const double xv = v[i][c];
-      bad[c] |= !isfinite(xv);
+    for (int i = 0; i < R; ++i) {
+      bad |= !isfinite(v[i]);
       float p[NP];
-      split<float>(xv, p);
-#pragma unroll
-      for (int q = 0; q < NP; ++q) {
-        asm volatile("" : "+v"(p[q]));
-        Rg(q, c, i) = p[q];
-      }
+      split<float>(v[i], p);
+      // pinned where made, so the doubles are not held until the check
+      asm volatile("" : "+v"(p[0]), "+v"(p[1]));
+      Rh[i] = p[0];
+      lo_s[i][t] = p[1];
     }
   }
-  if (bad[0] || bad[1]) atomicOr(flags, OZK_FLAG_NONFINITE);
+  if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 
+  // Lanes col, col + 16, col + 32, col + 48 of a wave hold the same column.
+  auto wave_col_max = [&](float m) {
+    m = max_w(m, __shfl_xor(m, 16));
+    return max_w(m, __shfl_xor(m, 32));
+  };
   const bool store = r0 < ld;  // the R rows lie in one padded unit
-  for (int s = 0; s < ns; ++s) {
-    uint32_t* const rs = my + s * G * kWords;  // this slice's record
-    float m[NP][2];
-#pragma unroll
-    for (int q = 0; q < NP; ++q) {
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        float mm = 0.0f;
-#pragma unroll
-        for (int i = 0; i < R; ++i) mm = max_w(mm, fabsf(Rg(q, c, i)));
-        mm = line_max_input<FMT>(mm, bad[c]);
-#pragma unroll
-        for (int off = CP; off < 64; off <<= 1) mm = max_w(mm, __shfl_xor(mm, off));
-        m[q][c] = mm;
-      }
-    }
-    __syncthreads();  // the previous slice's readers of the constants are done
-    if (lane < CP) {
-#pragma unroll
-      for (int q = 0; q < NP; ++q) {
-        red[wave][q][2 * lane] = m[q][0];
-        red[wave][q][2 * lane + 1] = m[q][1];
-      }
-    }
-    __syncthreads();
-    // Publish: wave 0, one lane per key (part t / 16, column t % 16).
-    if (t < kGangKeys) {
-      const int q = t / kGangPW, col = t % kGangPW;
-      float mm = red[0][q][col];
-#pragma unroll
-      for (int w = 1; w < NW; ++w) mm = max_w(mm, red[w][q][col]);
-      __hip_atomic_store(rs + member * kWords + t, max_key(mm), __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    }
-    // Combine: thread t waits for key t % 32 of members t / 32, t / 32 +
-    // NG, ..., then the groups' maxima meet in LDS.
+  for (int r = 0;; ++r) {
+    const int words = gang_round_words(r);
+    const int nk = r == 1 ? NKS : 1;  // keys per (part, column)
+    uint32_t* const rs = my + gang_round_offset(r, G);  // this round's record
+    // 1. The thread's partial maxima, reduced over the wave's lanes of the
+    // column, then over the waves by LDS atomic max.  Candidates for the
+    // hi part only (the lo part has one slice in the presets).
+    auto publish_local = [&](int q, int k, float m) {
+      m = wave_col_max(m);
+      if (lane < kGangPW) atomicMax(&wkey[(q * nk + k) * kGangPW + col], max_key(m));
+    };
     {
-      uint32_t k = 0u;
-      if (!gave_up) {
-        for (int mb = t / kGangKeys; mb < G; mb += NG) {
-          const uint32_t km = wait_key(rs + mb * kWords + t % kGangKeys, flags, wait_ticks);
-          if (!km) gave_up = 1;
-          k = max(k, km);
+      const int left = n0 - gc[0][col].done;
+      if (left > 0) {
+        const int depth = (r == 1 && gc[0][col].spec) ? min(left, 3) : 1;
+        float m0 = 0.0f;
+#pragma unroll
+        for (int i = 0; i < R; ++i) m0 = max_w(m0, fabsf(Rh[i]));
+        publish_local(0, 0, line_max_input<FMT>(m0, bad));
+        if (depth > 1) {
+          // c_j in {a, a - 1}; then c_{j+1} in {rho + c_j - 25, that - 1}
+          const int a = rho + gc[0][col].c - 25;
+#pragma unroll 1
+          for (int x = 0; x < 2; ++x) {
+            const FastSlice f1 = fast_slice_c(a - x, rho);
+            const FastSlice f2a = fast_slice_c(rho + a - x - 25, rho);
+            const FastSlice f2b = fast_slice_c(rho + a - x - 26, rho);
+            float m1 = 0.0f, m2a = 0.0f, m2b = 0.0f;
+#pragma unroll
+            for (int i = 0; i < R; ++i) {
+              float r1 = Rh[i];
+              fast_step(r1, f1);
+              m1 = max_w(m1, fabsf(r1));
+              float r2 = r1, r3 = r1;
+              fast_step(r2, f2a);
+              fast_step(r3, f2b);
+              m2a = max_w(m2a, fabsf(r2));
+              m2b = max_w(m2b, fabsf(r3));
+            }
+            publish_local(0, 1 + x, m1);
+            if (depth > 2) {
+              publish_local(0, 3 + 2 * x, m2a);
+              publish_local(0, 4 + 2 * x, m2b);
+            }
+          }
         }
       }
-      comb[t / kGangKeys][t % kGangKeys] = k;
-    }
-    __syncthreads();
-    if (t < kGangKeys) {
-      uint32_t kk = comb[0][t];
+      if (n1 - gc[1][col].done > 0) {
+        float m0 = 0.0f;
 #pragma unroll
-      for (int g = 1; g < NG; ++g) kk = max(kk, comb[g][t]);
-      const int q = t / kGangPW, col = t % kGangPW;
-      SliceConst<float> kc = slice_const<float>(key_max(kk), rho);
-      if (s < (q == 0 ? n0 : n1)) {
-        const int ce = plane_exponent<FMT>(kc, rho, flags, member == 0);
-        if (member == 0) E[((q == 0 ? 0 : n0) + s) * eplane + panel * kGangPW + col] = ce;
+        for (int i = 0; i < R; ++i) m0 = max_w(m0, fabsf(lo_s[i][t]));
+        publish_local(1, 0, line_max_input<FMT>(m0, bad));
       }
-      const FastSlice fs = fast_slice(kc, rho);
-      cst_s[q][col] = fs.s;
-      cst_u[q][col] = fs.u;
-      cst_sig[q][col] = kc.sigma;
-      cst_inv[q][col] = kc.inv;
-      cst_mode[q][col] = fs.ok ? 1 : (kc.zero ? 2 : 0);
     }
     __syncthreads();
+    // 2. Publish (words never 0: keys unused this round are max_key(0)).
+    if (t < words) {
+      const uint32_t k = wkey[t];
+      __hip_atomic_store(rs + member * words + t, k ? k : max_key(0.0f), __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    }
+    // 3. Combine: thread t waits for word t % words of members
+    // t / words, t / words + ng, ... (all loads in flight together), then
+    // the maxima meet in LDS.
+    {
+      const int ng = kGangThreads / words;  // 8 groups, or 1 in round 1
+      const int grp = t / words, w = t % words;
+      if (grp < ng && grp < G) {
+        uint32_t kk[kGangMaxMembers];
+#pragma unroll
+        for (int i = 0; i < kGangMaxMembers; ++i) kk[i] = 0u;
+        const int n = (G - 1 - grp) / ng + 1;  // members grp, grp + ng, ... < G
+        if (!gave_up && !wait_keys(rs, (uint32_t)(grp * words + w), (uint32_t)(ng * words), kk,
+                                   n, flags, wait_ticks))
+          gave_up = 1;
+        uint32_t k = 0u;
+#pragma unroll
+        for (int i = 0; i < kGangMaxMembers; ++i) k = max(k, kk[i]);
+        atomicMax(&wall[w], k);
+      }
+    }
+    __syncthreads();
+    if (t == 0) more = 0;
+    // 4. Settle: one thread per (part, column).
+    if (t < NP * kGangPW) {
+      const int q = t / kGangPW, cl = t % kGangPW;
+      GangCol& g = gc[q][cl];
+      auto key = [&](int k) { return key_max(wall[(q * nk + k) * kGangPW + cl]); };
+      const int nq = q == 0 ? n0 : n1;
+      const int done = g.done;
+      const int left = nq - done;
+      int d = 0;
+      if (left > 0) {
+        const int depth = (r == 1 && q == 0 && g.spec) ? min(left, 3) : 1;
+        const int a = rho + g.c - 25;
+        int kidx = 0;   // key of the slice at hand
+        int cnext = a;  // largest candidate exponent of the next slice
+        for (int j = 0; j < depth; ++j) {
+          SliceConst<float> kc = slice_const<float>(key(kidx), rho);
+          const int cexact = kc.c;
+          const int ce = plane_exponent<FMT>(kc, rho, flags, member == 0);
+          const int pl = (q == 0 ? 0 : n0) + done + j;
+          if (member == 0) E[pl * eplane + panel * kGangPW + cl] = ce;
+          const FastSlice fs = fast_slice(kc, rho);
+          g.a[j] = fs.ok ? fs.s : kc.sigma;
+          g.b[j] = fs.ok ? fs.u : kc.inv;
+          g.mode[j] = fs.ok ? 1 : (kc.zero ? 2 : 0);
+          g.c = cexact;
+          g.spec = fs.ok;
+          ++d;
+          if (j + 1 >= depth || !fs.ok) break;
+          // the next slice's key, if this exponent is one of its candidates
+          const int x = cnext - cexact;
+          if (x != 0 && x != 1) break;
+          kidx = j == 0 ? 1 + x : 3 + 2 * (kidx - 1) + x;
+          cnext = rho + cexact - 25;
+        }
+        if (done + d < nq) more = 1;
+      }
+      g.d = d;
+    }
+    __syncthreads();
+    // 5. Emit the settled slices.
 #pragma unroll
     for (int q = 0; q < NP; ++q) {
-      const int nq = q == 0 ? n0 : n1;
-      if (s >= nq) continue;  // uniform
-      const int pl = (q == 0 ? 0 : n0) + s;
-#pragma unroll
-      for (int c = 0; c < 2; ++c) {
-        const int col = 2 * cp + c;
-        const int mode = cst_mode[q][col];
-        const int64_t line = c0 + c;
-        typedef typename PlaneVec<FMT, R>::type TV;
-        TV out;  // merged as a whole word (byte-wise merges cost more)
-        int qs = 0;
-        if (mode == 1) {  // every lane, but for exceptional lines
-          const FastSlice fs = {cst_s[q][col], cst_u[q][col], true};
+      const GangCol& g = gc[q][col];
+      const int d = g.d, done = g.done;
+      for (int j = 0; j < d; ++j) {
+        const int pl = (q == 0 ? 0 : n0) + done + j;
+        const int mode = g.mode[j];
+        const float ka = g.a[j], kb = g.b[j];
+        uint32_t w[NWORD];
+        if (mode == 1) {  // every lane, but for exceptional columns
+          const FastSlice fs = {ka, kb, true};
           const float carrier = fast_carrier<FMT>(rho);
           float cv[R];
 #pragma unroll
           for (int i = 0; i < R; ++i) {
-            float r = Rg(q, c, i);
-            const float qv = fast_step(r, fs);
-            asm volatile("" : "+v"(r));  // as in extract_lines_reg
-            Rg(q, c, i) = r;
+            float rv = q == 0 ? Rh[i] : lo_s[i][t];
+            const float qv = fast_step(rv, fs);
+            asm volatile("" : "+v"(rv));  // as in extract_lines_reg
+            if (q == 0) Rh[i] = rv; else lo_s[i][t] = rv;
             cv[i] = fast_carry<FMT>(qv, carrier);
           }
-          out = pack_fast<FMT, R>(cv);
+          if constexpr (FMT == kFmtI8) {
+#pragma unroll
+            for (int u = 0; u < NWORD; ++u)
+              w[u] = pack_low_bytes(cv[4 * u], cv[4 * u + 1], cv[4 * u + 2], cv[4 * u + 3]);
+          } else {
+#pragma unroll
+            for (int u = 0; u < NWORD; ++u) w[u] = pack_high_halves(cv[2 * u], cv[2 * u + 1]);
+          }
         } else {
-          const float sig = cst_sig[q][col], inv = cst_inv[q][col];
           const bool zero = mode == 2;
           union {
-            TV w;
+            uint32_t w[NWORD];
             T e[R];
           } pk;
 #pragma unroll
           for (int i = 0; i < R; ++i) {
-            const float r = Rg(q, c, i);
-            float v = (r + sig) - sig;
-            if (zero) v = 0.0f;
-            float rn = r - v;
+            const float rv = q == 0 ? Rh[i] : lo_s[i][t];
+            float vv = (rv + ka) - ka;
+            if (zero) vv = 0.0f;
+            float rn = rv - vv;
             asm volatile("" : "+v"(rn));  // as in extract_lines_reg
-            Rg(q, c, i) = rn;
-            const float sv = slice_value_f32(v, inv);
+            if (q == 0) Rh[i] = rn; else lo_s[i][t] = rn;
+            const float sv = slice_value_f32(vv, kb);
             pk.e[i] = PlaneElem<FMT>::make(sv, qscale);
           }
-          out = pk.w;
-        }
-        if constexpr (FMT == kFmtI8) qs = byte_sum(out, qs);
-        if (store)
-          *(TV*)(S + pl * plane + plane_offset<sizeof(T)>(line, r0, eplane)) =
-              out;
-        if constexpr (FMT == kFmtI8) {
-          // the wave's lanes of this column pair: lane % CP
 #pragma unroll
-          for (int off = CP; off < 64; off <<= 1) qs += __shfl_xor(qs, off);
-          if (lane < CP) atomicAdd(&ssum[pl * kGangPW + 2 * cp + c], qs);
+          for (int u = 0; u < NWORD; ++u) w[u] = pk.w[u];
+        }
+        if (store) {
+          // 16-byte units of the chunk-major layout (8 or 16 rows each)
+          constexpr int UR = 16 / (int)sizeof(T);
+#pragma unroll
+          for (int u = 0; u < NWORD / 4; ++u)
+            *(uint4*)(S + pl * plane + plane_offset<sizeof(T)>(line, r0 + u * UR, eplane)) =
+                make_uint4(w[4 * u], w[4 * u + 1], w[4 * u + 2], w[4 * u + 3]);
+        }
+        if constexpr (FMT == kFmtI8) {
+          int qs = 0;
+#pragma unroll
+          for (int u = 0; u < NWORD; ++u) qs = byte_sum(w[u], qs);
+          qs += __shfl_xor(qs, 16);
+          qs += __shfl_xor(qs, 32);
+          if (lane < kGangPW) atomicAdd(&ssum[pl * kGangPW + col], qs);
         }
       }
     }
+    const int again = more;
+    __syncthreads();  // the settled counts and constants are read; reset for the next round
+    if (t < NP * kGangPW) gc[t / kGangPW][t % kGangPW].done += gc[t / kGangPW][t % kGangPW].d;
+    for (int i = t; i < kMaxWords; i += kGangThreads) wkey[i] = wall[i] = 0u;
+    if (!again) break;
+    __syncthreads();
   }
   if constexpr (FMT == kFmtI8) {
     __syncthreads();
     for (int i = t; i < (n0 + n1) * kGangPW; i += kGangThreads)
       part[((int64_t)(i / kGangPW) * G + member) * eplane + panel * kGangPW + i % kGangPW] =
           ssum[i] - i8_offset(rho) * kGangRun;
+  }
+}
+
+// Column extraction without a transposed copy of X and without exchanges
+// between workgroups, for columns of up to 4096 rows: workgroup b holds a
+// panel of kPanelCols = 2 whole columns of up to 256 RPT rows on chip
+// (thread t: column t % 2, rows RPT (t / 2) .. + RPT - 1, hi and lo parts
+// in registers), so every line maximum is a reduction inside the
+// workgroup, X is read once and every plane element is written once.  Lanes 2 k and 2 k + 1 of a load read one
+// 16-byte row segment; the panels that share X's 128-byte lines run on one
+// XCD (xcd_line), whose L2 serves the segments of a line to all of them.
+// The arithmetic is extract_lines_reg's (the short form of the slice step
+// where it holds).  INT8: the line sums are complete in the workgroup.
+constexpr int kPanelCols = 2;
+constexpr int kPanelThreads = 512;
+constexpr int kPanelGroups = kPanelThreads / kPanelCols;  // 256 row groups
+
+template <int FMT, int RPT>
+__global__ __launch_bounds__(kPanelThreads) __attribute__((amdgpu_waves_per_eu(4))) void extract_cols_panel(
+    const double* __restrict__ X, int64_t K, int64_t M, int64_t ldx, int rho, int n0, int n1,
+    typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
+    int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
+    int32_t* __restrict__ Sg) {
+  typedef typename PlaneElem<FMT>::type T;
+  constexpr int NP = 2, NW = kPanelThreads / 64;
+  constexpr int BYTES = RPT * (int)sizeof(T);  // plane bytes of a thread's rows
+  constexpr int NWORD = (BYTES + 3) / 4;
+  const float qscale = ldexpf(1.0f, 24 - rho);
+  __shared__ float red[NW][NP][kPanelCols];
+  __shared__ int ssum[FMT == kFmtI8 ? kMaxPlanes * kPanelCols : 1];
+  const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+  if constexpr (FMT == kFmtI8) {
+    for (int i = t; i < kMaxPlanes * kPanelCols; i += kPanelThreads) ssum[i] = 0;
+  }
+  const int64_t panel = xcd_line(blockIdx.x, gridDim.x);
+  const int cl = t % kPanelCols;
+  const int64_t line = panel * kPanelCols + cl;  // the thread's column
+  const int64_t r0 = (int64_t)RPT * (t / kPanelCols);
+
+  // The one read.  Every load reads an address inside X (a row past the
+  // last reads row 0, a column past the last column 0) and its value is
+  // replaced by zero afterwards, so no branch separates the RPT loads.
+  float Rr[NP][RPT];
+  bool bad = false;
+  {
+    const bool cok = line < M;
+#pragma unroll
+    for (int i = 0; i < RPT; ++i) {
+      const int64_t row = r0 + i;
+      const bool ok = cok && row < K;
+      const double d = X[(ok ? row : 0) * ldx + (ok ? line : 0)];
+      const double v = ok ? d : 0.0;
+      bad |= !isfinite(v);
+      float p[NP];
+      split<float>(v, p);
+      Rr[0][i] = p[0];
+      Rr[1][i] = p[1];
+    }
+  }
+  if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
+
+  const bool store = r0 < ld;
+  const int ns = max(n0, n1);
+  for (int s = 0; s < ns; ++s) {
+    // line maxima: the thread, the wave's lanes of the column, the waves
+    float m[NP];
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      m[q] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < RPT; ++i) m[q] = max_w(m[q], fabsf(Rr[q][i]));
+      m[q] = line_max_input<FMT>(m[q], bad);
+#pragma unroll
+      for (int off = kPanelCols; off < 64; off <<= 1) m[q] = max_w(m[q], __shfl_xor(m[q], off));
+    }
+    __syncthreads();  // the previous slice's readers of red are done
+    if (lane < kPanelCols) {
+      red[wave][0][lane] = m[0];
+      red[wave][1][lane] = m[1];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int q = 0; q < NP; ++q) {
+      const int nq = q == 0 ? n0 : n1;
+      if (s >= nq) continue;  // uniform
+      float mm = red[0][q][cl];
+#pragma unroll
+      for (int w = 1; w < NW; ++w) mm = max_w(mm, red[w][q][cl]);
+      SliceConst<float> kc = slice_const<float>(mm, rho);
+      const int ce = plane_exponent<FMT>(kc, rho, flags, t < kPanelCols);
+      const int pl = (q == 0 ? 0 : n0) + s;
+      uint32_t w[NWORD];
+      const FastSlice fs = fast_slice(kc, rho);
+      if (fs.ok) {  // every lane, but for exceptional columns
+        const float carrier = fast_carrier<FMT>(rho);
+        float cv[RPT];
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          float rv = Rr[q][i];
+          const float qv = fast_step(rv, fs);
+          asm volatile("" : "+v"(rv));  // as in extract_lines_reg
+          Rr[q][i] = rv;
+          cv[i] = fast_carry<FMT>(qv, carrier);
+        }
+        if constexpr (FMT == kFmtI8) {
+#pragma unroll
+          for (int u = 0; u < NWORD; ++u)
+            w[u] = pack_low_bytes(cv[4 * u], cv[(4 * u + 1) % RPT], cv[(4 * u + 2) % RPT],
+                                  cv[(4 * u + 3) % RPT]);
+        } else {
+#pragma unroll
+          for (int u = 0; u < NWORD; ++u) w[u] = pack_high_halves(cv[2 * u], cv[2 * u + 1]);
+        }
+      } else {
+        union {
+          uint32_t w[NWORD];
+          T e[NWORD * 4 / sizeof(T)];
+        } pk;
+#pragma unroll
+        for (int i = 0; i < RPT; ++i) {
+          const float rv = Rr[q][i];
+          float vv = (rv + kc.sigma) - kc.sigma;
+          if (kc.zero) vv = 0.0f;
+          float rn = rv - vv;
+          asm volatile("" : "+v"(rn));  // as in extract_lines_reg
+          Rr[q][i] = rn;
+          const float sv = slice_value_f32(vv, kc.inv);
+          pk.e[i] = PlaneElem<FMT>::make(sv, qscale);
+        }
+#pragma unroll
+        for (int u = 0; u < NWORD; ++u) w[u] = pk.w[u];
+      }
+      if (store) {
+        T* out = S + pl * plane;
+        if constexpr (BYTES >= 16) {
+          // whole 16-byte units of the chunk-major layout
+#pragma unroll
+          for (int u = 0; u < BYTES / 16; ++u)
+            *(uint4*)(out + plane_offset<sizeof(T)>(line, r0 + u * (16 / (int)sizeof(T)),
+                                                    eplane)) =
+                make_uint4(w[4 * u], w[4 * u + 1], w[4 * u + 2], w[4 * u + 3]);
+        } else if constexpr (BYTES == 8) {
+          *(uint2*)(out + plane_offset<sizeof(T)>(line, r0, eplane)) = make_uint2(w[0], w[1]);
+        } else {
+          *(uint32_t*)(out + plane_offset<sizeof(T)>(line, r0, eplane)) = w[0];
+        }
+      }
+      if constexpr (FMT == kFmtI8) {
+        int qs = 0;
+#pragma unroll
+        for (int u = 0; u < NWORD; ++u) qs = byte_sum(w[u], qs);
+#pragma unroll
+        for (int off = kPanelCols; off < 64; off <<= 1) qs += __shfl_xor(qs, off);
+        if (lane < kPanelCols) atomicAdd(&ssum[pl * kPanelCols + cl], qs);
+      }
+      if (t < kPanelCols) E[pl * eplane + line] = ce;
+    }
+  }
+  if constexpr (FMT == kFmtI8) {
+    __syncthreads();
+    for (int i = t; i < (n0 + n1) * kPanelCols; i += kPanelThreads)
+      Sg[(i / kPanelCols) * eplane + panel * kPanelCols + i % kPanelCols] =
+          ssum[i] - i8_offset(rho) * (kPanelGroups * RPT);
   }
 }
 
@@ -1145,12 +1444,46 @@ static bool gang_columns(int64_t rows) {
   return round_up(rows, kKPad) <= (int64_t)kGangRun * kGangMaxMembers && gangs_enabled();
 }
 
+// FP32 columns of up to 256 x 16 rows: one panel per workgroup
+// (extract_cols_panel).  Longer ones go to the gangs, whose members read
+// whole 128-byte lines of X: a panel's 16-byte row segments cost as many
+// L2 requests as whole lines do, which bounds it below the gangs there
+// (8192 x 8192: 0.34 ms, the gangs 0.30 ms; 4096 x 4096: 0.095 ms, the
+// gangs 0.104 ms).
+static bool panel_columns(int64_t rows) {
+  return round_up(rows, kKPad) <= (int64_t)kPanelGroups * 16;
+}
+
+template <int FMT>
+static int launch_cols_panel(const double* X, int64_t rows, int64_t cols, int64_t ldx,
+                             int rho, int n0, int n1, void* Sv, int32_t* E, uint32_t* flags,
+                             hipStream_t st, int32_t* Sg) {
+  typedef typename PlaneElem<FMT>::type T;
+  if (rows <= 0 || cols <= 0) return OZK_OK;
+  const int64_t ld = round_up(rows, kKPad), lp = round_up(cols, kLinePad);
+  const int64_t plane = lp * ld;
+  const dim3 grid((unsigned)(lp / kPanelCols));
+#define OZK_PANEL_LAUNCH(RPT)                                                              \
+  hipLaunchKernelGGL((extract_cols_panel<FMT, RPT>), grid, dim3(kPanelThreads), 0, st, X,  \
+                     rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, Sg)
+  if (ld <= kPanelGroups * 4)
+    OZK_PANEL_LAUNCH(4);
+  else if (ld <= kPanelGroups * 8)
+    OZK_PANEL_LAUNCH(8);
+  else
+    OZK_PANEL_LAUNCH(16);
+#undef OZK_PANEL_LAUNCH
+  OZK_LAUNCH_CHECK();
+  return OZK_OK;
+}
+
 // Ticket and exchange records (zeroed per launch), then the INT8 partial
 // line sums (2 nslices planes x G members x padded columns).
 static size_t gang_records(int64_t rows, int64_t cols, int nslices) {
-  const int64_t G = gang_members(round_up(rows, kKPad));
-  return (size_t)round_up(
-      kGangHeader + (round_up(cols, kLinePad) / kGangPW) * nslices * G * kGangLine, 256);
+  const int G = gang_members(round_up(rows, kKPad));
+  return (size_t)round_up(kGangHeader + (round_up(cols, kLinePad) / kGangPW) *
+                                            gang_round_offset(nslices, G) * 4,
+                          256);
 }
 static size_t gang_workspace_bytes(int64_t rows, int64_t cols, int nslices) {
   const int64_t G = gang_members(round_up(rows, kKPad));
@@ -1165,6 +1498,7 @@ static size_t transpose_bytes(int64_t rows, int64_t cols) {
 
 size_t extract_workspace_bytes(int64_t rows, int64_t cols, int by_cols, bool f64) {
   if (!by_cols) return !f64 && gang_rows(cols) ? row_gang_bytes(rows, cols, kMaxSlices) : 0;
+  if (!f64 && panel_columns(rows)) return 0;
   if (!f64 && gang_columns(rows)) return gang_workspace_bytes(rows, cols, kMaxSlices);
   return transpose_bytes(rows, cols) +
          (!f64 && gang_rows(rows) ? row_gang_bytes(cols, rows, kMaxSlices) : 0);
@@ -1196,14 +1530,9 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
   int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(npanels * G));
   const uint32_t wait_ticks = wait_polls(kGangWaitTicks);
-  if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0) && (cols % 2 == 0))
-    hipLaunchKernelGGL((extract_cols_gang<FMT, true>), grid, dim3(kGangThreads), 0, st, X,
-                       rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, wait_ticks, part);
-  else
-    hipLaunchKernelGGL((extract_cols_gang<FMT, false>), grid, dim3(kGangThreads), 0, st, X,
-                       rows, cols, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, wait_ticks, part);
+  hipLaunchKernelGGL((extract_cols_gang<FMT>), grid, dim3(kGangThreads), 0, st, X, rows, cols,
+                     ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec, ticket, G,
+                     wait_ticks, part);
   OZK_LAUNCH_CHECK();
   if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;
@@ -1229,6 +1558,13 @@ int extract(const double* X, int64_t rows, int64_t cols, int64_t ldx,
   const double* src = X;
   int64_t lines = rows, len = cols, lds = ldx;
   if constexpr (sizeof(W) == 4) {
+    if (by_cols && panel_columns(rows)) {
+      if (i8)
+        return launch_cols_panel<kFmtI8>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, st,
+                                         sums);
+      return launch_cols_panel<kFmtBf16>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, st,
+                                         nullptr);
+    }
     if (by_cols && gang_columns(rows)) {
       if (i8)
         return launch_cols_gang<kFmtI8>(X, rows, cols, ldx, rho, n0, n1, S, E, flags, ws,

@@ -70,13 +70,17 @@ def r256(b):
 
 
 def gang_bytes(rows, cols):
-    """Column extraction of up to 8192 rows on the FP32 path: the ticket
-    word and, per (16-column panel, slice) for up to 32 slices, one
-    128-byte exchange line per 512-row run of a column (256-byte aligned),
-    then the INT8 line sums of each run: 64 planes x runs x padded columns."""
-    G = -(-(-(-rows // 64) * 64) // 512)
+    """Column extraction of 4097 to 8192 rows on the FP32 path: the ticket
+    word and, per 16-column panel, the exchange records of up to 32 rounds
+    for each 512-row run of a column (32 words a round, 224 in round 1;
+    256-byte aligned), then the INT8 line sums of each run: 64 planes x
+    runs x padded columns.  Columns of up to 4096 rows need no workspace."""
+    ld = -(-rows // 64) * 64
+    if ld <= 4096:
+        return 0
+    G = -(-ld // 512)
     lp = -(-cols // 64) * 64
-    return r256(256 + (lp // 16) * 32 * G * 128) + 64 * G * lp * 4
+    return r256(256 + (lp // 16) * G * (32 + 224 + 30 * 32) * 4) + 64 * G * lp * 4
 
 
 def row_gang_bytes(lines, length):
@@ -139,10 +143,12 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_extract_workspace_bytes(3, 32769, 0) == row_gang_bytes(3, 32769)
     assert lib.ozk_extract_workspace_bytes(100, 262144, 0) == row_gang_bytes(100, 262144)
     assert lib.ozk_extract_workspace_bytes(3, 262145, 0) == 0
-    # the larger of the FP32 (exchange records) and FP64 (transpose, rounded
-    # up to 256 bytes) needs
-    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == max(40192, gang_bytes(100, 50))
-    assert lib.ozk_extract_workspace_bytes(8, 5000, 1) == gang_bytes(8, 5000)
+    # the larger of the FP32 (none for columns of up to 4096 rows, else the
+    # exchange records) and FP64 (transpose, rounded up to 256 bytes) needs
+    assert lib.ozk_extract_workspace_bytes(100, 50, 1) == 40192
+    assert lib.ozk_extract_workspace_bytes(8, 5000, 1) == 320000
+    assert lib.ozk_extract_workspace_bytes(5000, 8, 1) == max(320000, gang_bytes(5000, 8))
+    assert gang_bytes(5000, 8) > 320000
     # longer columns: the transposed copy (256-byte aligned), then the row
     # gangs' records while the transposed lines are within their reach
     assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 1680128 + row_gang_bytes(3, 70000)
