@@ -405,8 +405,8 @@ def main():
     log(f"gemm kernel {gemm_s * 1e3:.2f} ms, {achieved:.1f} T(FL)OP/s "
         f"{'INT8' if i8 else 'BF16'} of {peak}")
 
-    # Extraction phase (split + A rows + B columns, B through its transpose)
-    # on the plane buffers allocated above: the C entry point alone.
+    # Extraction phase (split + A by rows + B by columns, in place) on the
+    # plane buffers allocated above: the C entry point alone.
     lib = _lib.load()
     ext_fn = lib.ozk_extract_f32_i8 if i8 else lib.ozk_extract_f32
     flags = torch.zeros(1, dtype=torch.int32, device=dev)
