@@ -1004,13 +1004,16 @@ __global__ void zero_u32_kernel(uint32_t* __restrict__ p, int n) {
 }
 
 // Schedules with an all-pairs instantiation: high (4,1) and medium (3,1)
-// in one sweep, max (5,4) in three (hh, hl, lh; at most 25 pairs and 10
-// planes each), the custom schedules that fit one sweep (at most 10 planes,
-// n_hi + n_lo <= 5, and 21 pairs), and (4,2) and (3,3) in two (hh + hl,
-// then lh).  Custom schedules take the on-device orders only (2Sum, FP64
-// block, and the pair and per-product forms).
+// in one sweep, max (5,4) and (4,4) in three (hh, hl, lh; at most 25 pairs
+// and 10 planes each), the custom schedules that fit one sweep (at most 10
+// planes, n_hi + n_lo <= 5, and 21 pairs), and (4,2), (3,3) and (2,4) in
+// two (hh + hl, then lh).  Custom schedules take the on-device orders only
+// (2Sum, FP64 block, and the pair and per-product forms).
 constexpr bool allpairs_two_sweeps(int nhi, int nlo) {
-  return (nhi == 4 && nlo == 2) || (nhi == 3 && nlo == 3);
+  return (nhi == 4 && nlo == 2) || (nhi == 3 && nlo == 3) || (nhi == 2 && nlo == 4);
+}
+constexpr bool allpairs_three_sweeps(int nhi, int nlo) {
+  return (nhi == 5 && nlo == 4) || (nhi == 4 && nlo == 4);
 }
 
 constexpr bool allpairs_preset(int nhi, int nlo) {
@@ -1026,7 +1029,8 @@ static bool allpairs_order(int nhi, int nlo, int order) {
 
 static bool allpairs_custom(int nhi, int nlo) {
   return (nhi == 1 && nlo >= 1 && nlo <= 4) || (nhi == 2 && nlo >= 1 && nlo <= 3) ||
-         (nhi == 3 && nlo == 2) || allpairs_two_sweeps(nhi, nlo);
+         (nhi == 3 && nlo == 2) || allpairs_two_sweeps(nhi, nlo) ||
+         (nhi == 4 && nlo == 4);
 }
 
 static bool allpairs_schedule(int pipe, int nhi, int nlo) {
@@ -1040,7 +1044,7 @@ bool allpairs_supported(int pipe, int nhi, int nlo) {
 }
 
 static int allpairs_sweeps(int nhi, int nlo) {
-  return nhi == 5 && nlo == 4 ? 3 : (allpairs_two_sweeps(nhi, nlo) ? 2 : 1);
+  return allpairs_three_sweeps(nhi, nlo) ? 3 : (allpairs_two_sweeps(nhi, nlo) ? 2 : 1);
 }
 
 static int fold_state_bytes(int order) {
@@ -1171,7 +1175,7 @@ static void launch_sweep(const ApArgs& a) {
 
 template <class Op, int NHI, int NLO, int ORDER>
 static void launch_schedule(const ApArgs& a) {
-  if constexpr (NHI == 5 && NLO == 4) {
+  if constexpr (allpairs_three_sweeps(NHI, NLO)) {
     launch_sweep<Op, NHI, NLO, ORDER, 0, 0>(a);
     launch_sweep<Op, NHI, NLO, ORDER, 1, 1>(a);
     launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
@@ -1299,6 +1303,8 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
     else if (nhi == 2 && nlo == 3) launch_ap_order<Op, 2, 3>(order, a);   \
     else if (nhi == 3 && nlo == 2) launch_ap_order<Op, 3, 2>(order, a);   \
     else if (nhi == 4 && nlo == 2) launch_ap_order<Op, 4, 2>(order, a);   \
+    else if (nhi == 2 && nlo == 4) launch_ap_order<Op, 2, 4>(order, a);   \
+    else if (nhi == 4 && nlo == 4) launch_ap_order<Op, 4, 4>(order, a);   \
     else launch_ap_order<Op, 3, 3>(order, a);                             \
   } while (0)
   if (i8) OZK_AP_ALL(OpI8);

@@ -168,7 +168,7 @@ def test_int8_entry_points_reject_before_device_work(lib):
         rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, rho, 4, 1, 0,
                              None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED
-    for nh, nl in ((5, 1), (2, 4), (4, 4)):
+    for nh, nl in ((5, 1), (6, 1), (1, 5)):
         rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, nh, nl, 0,
                              None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED and b"all-pairs" in lib.ozk_last_error()

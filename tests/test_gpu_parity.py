@@ -350,7 +350,8 @@ def test_gemm_orders_bit_exact(ll, pipe, nh, nl, shape):
 # ---------------------------------------------------------------- public API
 
 @pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (2, 2), (1, 1), (1, 2),
-                                       (1, 4), (2, 1), (2, 3), (3, 2), (3, 3), (5, 1)])
+                                       (1, 4), (2, 1), (2, 3), (3, 2), (3, 3), (2, 4), (4, 4),
+                                       (5, 1)])
 @pytest.mark.parametrize("accumulation", ["fused", "bf16_interleaved", "ondevice", "host"])
 def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
     A, B = gen("randn", (150, 300), 21), gen("randn", (300, 90), 22)
@@ -368,11 +369,12 @@ def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
 
 
 @pytest.mark.parametrize("precision", ["high", "medium", "max", (1, 1), (1, 2), (1, 3), (2, 1),
-                                       (2, 2), (2, 3), (3, 2), (3, 3), (4, 2), (5, 1)])
+                                       (2, 2), (2, 3), (3, 2), (3, 3), (4, 2), (2, 4), (4, 4),
+                                       (5, 1)])
 def test_matmul_long_contraction_bit_exact(ozk, precision):
     # K > 4096: rho >= 19, the presets and the custom schedules of the
-    # all-pairs kernel run on INT8 planes ((4, 2) and (3, 3) in two sweeps);
-    # (5, 1) on BF16 planes in the pairwise kernel
+    # all-pairs kernel run on INT8 planes ((4, 2), (3, 3) and (2, 4) in two
+    # sweeps, (4, 4) in three); (5, 1) on BF16 planes in the pairwise kernel
     A, B = gen("randn", (40, 6000), 23), gen("wide2", (6000, 70), 24)
     nh, nl = OP.resolve_precision(precision)
     for acc, ref in [("fused", lambda: O.matmul_ondevice_a4(A, B, "raise", nh, nl)),
