@@ -238,7 +238,22 @@ __device__ __forceinline__ int frag_lane(int lane) {
 // hh uses the hi planes of A and B, hl the hi planes of A and the lo planes
 // of B, lh the lo planes of A and the hi planes of B; a sweep stages exactly
 // the planes its blocks use.
-template <int PIPE, int NHI, int NLO, int B0, int B1>
+// Row blocks of 16 lines per wave of an all-pairs tile: a workgroup's 8
+// waves hold 2 x RB blocks of rows and 4 of columns, so its tile is
+// 32 RB x 64.  RB = 3 (96-row tiles) where the sweep's pairs fit three
+// blocks of accumulators (at most 16 pairs) and its stage buffer (2 RB
+// fragments of 1 KiB per A plane, 4 per B plane) the 40 KiB slot of the
+// four-stage ring: fewer staged bytes per MFMA.  Square 64-row tiles for the
+// symmetric (gram) form and the multi-sweep schedules.
+constexpr int ap_rb(int nhi, int nlo, int b0, int b1, bool sym) {
+  const int na = (b1 == 2 ? nhi + nlo : nhi) - (b0 == 2 ? nhi : 0);
+  const int bb = (b0 == 1 && b1 == 1) ? nhi : 0;
+  const int nb = ((b0 <= 1 && b1 >= 1) ? nhi + nlo : nhi) - bb;
+  const int np = nhi * nhi + 2 * nhi * nlo;
+  return (!sym && b0 == 0 && b1 == 2 && np <= 16 && 6 * na + 4 * nb <= 40) ? 3 : 2;
+}
+
+template <int PIPE, int NHI, int NLO, int B0, int B1, bool SYM = false>
 struct Sweep {
   static_assert(PIPE == OZK_PIPE_ONDEVICE, "sweeps cover the on-device schedule");
   static constexpr int A0 = B0 == 2 ? NHI : 0;                    // first A plane
@@ -251,6 +266,10 @@ struct Sweep {
                                                : NHI * NHI + 2 * NHI * NLO);
   static constexpr int NP = P1 - P0;  // pairs of the sweep
   static constexpr int S = NA + NB;   // LDS slots per stage
+  static constexpr int RB = ap_rb(NHI, NLO, B0, B1, SYM);  // row blocks per wave
+  static constexpr int TM = 32 * RB;                     // tile rows
+  static constexpr int FA = 2 * RB;                      // fragments per A slot
+  static constexpr int NFRAG = NA * FA + NB * 4;         // fragments per stage
   static constexpr PairInfo pair(int k) { return pair_info(PIPE, NHI, NLO, P0 + k); }
   static constexpr int la(int k) { return pair(k).a - A0; }  // local A slot
   static constexpr int lb(int k) { return pair(k).b - BB; }  // local B slot
@@ -264,8 +283,8 @@ struct Sweep {
 
 template <class Op, class SW>
 struct AllPairsMMA {
-  static constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
-  typename Op::acc_t acc[NP][2];
+  static constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP, RB = SW::RB;
+  typename Op::acc_t acc[NP][RB];
   int fl, wr, wc;  // fl = frag_lane(lane)
 
   // MFMAs of one (A slot, row block) for every pair of that A slot.
@@ -276,18 +295,18 @@ struct AllPairsMMA {
       if (SW::la(k) == SA) acc[k][H] = Op::mma(af, bf[SW::lb(k)], acc[k][H]);
   }
 
-  // The 2 NA blocks of a stage (A slot j >> 1, row block j & 1), A fragments
-  // software-pipelined through kDepth + 1 registers: the read of block
-  // j + kDepth is issued before the MFMAs of block j.  Scheduling barriers
-  // keep the reads where they are.
-  static constexpr int kBlocks = NA * 2, kDepth = 3;
-  static_assert(kBlocks >= kDepth + 1, "the opening fills blocks 2, 3 (and 4 when there)");
+  // The RB NA blocks of a stage (A slot j / RB, row block j % RB), A
+  // fragments software-pipelined through kDepth + 1 = RB + 2 registers: the
+  // read of block j + kDepth is issued before the MFMAs of block j.
+  // Scheduling barriers keep the reads where they are.
+  static constexpr int kBlocks = NA * RB, kDepth = RB + 1;
+  static_assert(kBlocks >= kDepth + 1, "the opening fills blocks RB .. 2 RB");
 
   __device__ __forceinline__ uint4 read_a(const uint4* buf, int j) const {
-    return buf[((j >> 1) * 4 + 2 * wr + (j & 1)) * 64 + fl];
+    return buf[((j / RB) * SW::FA + RB * wr + (j % RB)) * 64 + fl];
   }
   __device__ __forceinline__ uint4 read_b(const uint4* buf, int s) const {
-    return buf[((NA + s) * 4 + wc) * 64 + fl];
+    return buf[(NA * SW::FA + s * 4 + wc) * 64 + fl];
   }
 
   template <int J>
@@ -297,16 +316,17 @@ struct AllPairsMMA {
     if constexpr (J < kBlocks) {
       if constexpr (J + kDepth < kBlocks)
         af[(J + kDepth) % (kDepth + 1)] = read_a(buf, J + kDepth);
-      block<J / 2, J % 2>(af[J % (kDepth + 1)], bf);
+      block<J / RB, J % RB>(af[J % (kDepth + 1)], bf);
       __builtin_amdgcn_sched_barrier(0);
       pipe_step<J + 1>(buf, af, bf);
     }
   }
 
-  // Opening of a stage: the pairs of A slot 0 walk the B slots (both row
-  // blocks per B slot), so the first MFMA needs only one B and A slot 0's two
+  // Opening of a stage: the pairs of A slot 0 walk the B slots (all RB row
+  // blocks per B slot), so the first MFMA needs only one B and A slot 0's RB
   // fragments; later B fragments are read two pairs ahead and the A ring for
-  // blocks 2.. is filled on the way.
+  // blocks RB .. 2 RB is filled on the way (blocks RB + 2 .. into the
+  // registers of blocks 0 .. as the last pair leaves them).
   static constexpr int count_a0() {
     int n = 0;
     for (int k = 0; k < NP; ++k) n += SW::la(k) == 0;
@@ -330,55 +350,76 @@ struct AllPairsMMA {
         constexpr int b2 = SW::lb(a0_pair(K + 2));
         bf[b2] = read_b(buf, b2);
       }
-      if constexpr (K == kA0 - 2) af[2] = read_a(buf, 2);
-      if constexpr (K == kA0 - 1) af[3] = read_a(buf, 3);
-      acc[k][0] = Op::mma(af[0], bf[b], acc[k][0]);
-      if constexpr (K == kA0 - 1 && kBlocks > 4) af[0] = read_a(buf, 4);
-      acc[k][1] = Op::mma(af[1], bf[b], acc[k][1]);
+      if constexpr (K == kA0 - 2) af[RB] = read_a(buf, RB);
+      if constexpr (K == kA0 - 1) af[RB + 1] = read_a(buf, RB + 1);
+#pragma unroll
+      for (int h = 0; h < RB; ++h) {
+        acc[k][h] = Op::mma(af[h], bf[b], acc[k][h]);
+        if (K == kA0 - 1 && h + 1 < RB && RB + 2 + h < kBlocks) af[h] = read_a(buf, RB + 2 + h);
+      }
       __builtin_amdgcn_sched_barrier(0);
       opening<K + 1>(buf, af, bf);
     }
   }
 
   __device__ __forceinline__ void operator()(const uint4* buf) {
-    static_assert(kDepth == 3, "the opening fills ring slots 2, 3, 0");
     uint4 bf[NB];
     uint4 af[kDepth + 1];
     constexpr int b0 = SW::lb(a0_pair(0));
     constexpr int b1 = SW::lb(a0_pair(1));
     bf[b0] = read_b(buf, b0);
-    af[0] = read_a(buf, 0);
-    af[1] = read_a(buf, 1);
+#pragma unroll
+    for (int h = 0; h < RB; ++h) af[h] = read_a(buf, h);
     bf[b1] = read_b(buf, b1);
     __builtin_amdgcn_sched_barrier(0);
     opening<0>(buf, af, bf);
-    pipe_step<2>(buf, af, bf);
+    pipe_step<RB>(buf, af, bf);
   }
 };
 
 // Fetch stage `st` (chunk st of every line of the tile) into the LDS buffer
 // at byte offset `buf_lds`.  Waves 0..3 move the whole stage: wave w moves
-// line group w of every slot, a contiguous 1 KiB of the slot's plane, into
-// fragment 4 slot + w of the buffer.  Waves 4..7 move nothing, so on every
-// SIMD one wave issues MFMAs while the other waits on the texture
-// addresser, which takes a stage's 40 loads one by one.  At, Bt point at the
-// tile's first line of the sweep's first A / B plane in chunk 0; chunk st
-// lies st * a_stage / st * b_stage bytes further.  All addresses lie inside
-// the zero-padded slice planes.
-template <int NA, int NB>
+// line groups w and w + 4 (16 lines, a contiguous 1 KiB of the slot's
+// plane) of every A slot, of FA groups, into its fragments FA slot + group,
+// and line group w of every B slot into fragment NA FA + 4 slot + w.
+// Waves 4..7 move nothing, so on every SIMD one wave issues MFMAs while the
+// other waits on the texture addresser, which takes a stage's 40 loads one
+// by one.  At, Bt point at the tile's first line of the sweep's first A / B
+// plane in chunk 0; chunk st lies st * a_stage / st * b_stage bytes
+// further.  A tile of 96 rows at the end of the lines has `agroups` < FA
+// groups inside the planes: its later groups read the last of them again
+// (their rows are never stored), so all addresses lie inside the
+// zero-padded slice planes.
+template <int NA, int NB, int FA>
 __device__ __forceinline__ void stage_dma(const char* At, int64_t aplane,
                                           int64_t a_stage, const char* Bt,
                                           int64_t bplane, int64_t b_stage,
                                           int64_t st, uint32_t buf_lds,
-                                          int wave, uint32_t lane_bytes) {
-  const int64_t g = (int64_t)wave * 1024;
-  const int64_t qa = st * a_stage + g, qb = st * b_stage + g;
+                                          int wave, uint32_t lane_bytes, int agroups) {
+  const int64_t qa = st * a_stage, qb = st * b_stage + (int64_t)wave * 1024;
 #pragma unroll
-  for (int slot = 0; slot < NA + NB; ++slot) {
-    const char* base = slot < NA ? At + slot * aplane + qa : Bt + (slot - NA) * bplane + qb;
-    dma16(__builtin_amdgcn_readfirstlane(buf_lds + (4 * slot + wave) * 1024),
-          (const void*)base, lane_bytes);
+  for (int slot = 0; slot < NA; ++slot) {
+#pragma unroll
+    for (int gg = 0; gg < (FA + 3) / 4; ++gg) {
+      const int g = wave + 4 * gg;
+      if (gg == 0 || g < FA) {  // uniform
+        const int gs = g < agroups ? g : agroups - 1;
+        dma16(__builtin_amdgcn_readfirstlane(buf_lds + (FA * slot + g) * 1024),
+              (const void*)(At + slot * aplane + qa + (int64_t)gs * 1024), lane_bytes);
+      }
+    }
   }
+#pragma unroll
+  for (int slot = 0; slot < NB; ++slot)
+    dma16(__builtin_amdgcn_readfirstlane(buf_lds + (NA * FA + 4 * slot + wave) * 1024),
+          (const void*)(Bt + slot * bplane + qb), lane_bytes);
+}
+
+// Loads a DMA wave issues per stage: one per B slot and one or two per A
+// slot (waves 0 .. FA - 5 take two A groups).
+template <int NA, int NB, int FA>
+__host__ __device__ constexpr int stage_loads(int wave) {
+  return NB + NA * (wave + 4 < FA ? 2 : 1);
 }
 
 // vmcnt wait before consuming a stage: the loads of the `later` stages
@@ -472,30 +513,30 @@ __device__ __forceinline__ int32x4 i8_start(const I8Fix& fix, int32x4 sa, int sb
 }
 
 // Fold and store one output tile (tm, tn) from one wave's accumulators:
-// wave (wr, wc) owns rows 32 wr .. +31 and columns 16 wc .. +15 of the tile
-// as two 16x16 blocks h.  Shared by the all-pairs kernel and the fixup of
-// its K-split tail tiles.
+// wave (wr, wc) owns rows 16 RB wr .. + 16 RB - 1 and columns 16 wc .. +15
+// of the tile as RB 16x16 blocks h.  Shared by the all-pairs kernel and the
+// fixup of its K-split tail tiles.
 
 template <class Op, class SW, int ORDER, int B0, int B1, bool SYM>
 __device__ __forceinline__ void tile_epilogue(
-    const typename Op::acc_t (&acc)[SW::NP][2], int tm, int tn, int wr, int wc,
+    const typename Op::acc_t (&acc)[SW::NP][SW::RB], int tm, int tn, int wr, int wc,
     int lane, const int32_t* __restrict__ Ae, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t a_lines, int64_t b_lines, float unit2,
     double* __restrict__ C, int64_t ldc, float* __restrict__ P, int64_t ldp,
     char* __restrict__ state) {
-  constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
+  constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP, RB = SW::RB;
   constexpr int NBLK = 3;
-  const int64_t row0 = (int64_t)tm * kBM, col0 = (int64_t)tn * kBN;
+  const int64_t row0 = (int64_t)tm * SW::TM, col0 = (int64_t)tn * kBN;
 
   // Accumulator register r of lane l of a 16x16 block holds row
   // 4 * (l / 16) + r, column l % 16.
   const int64_t col = col0 + 16 * wc + (lane & 15);
   if constexpr (ORDER == kOrderProducts) {
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < RB; ++h) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int64_t row = row0 + 32 * wr + 16 * h + 4 * (lane >> 4) + r;
+        const int64_t row = row0 + 16 * RB * wr + 16 * h + 4 * (lane >> 4) + r;
         if (row < N && col < M) {
 #pragma unroll
           for (int k = 0; k < NP; ++k)
@@ -509,18 +550,20 @@ __device__ __forceinline__ void tile_epilogue(
     // The exponents of the lane's column, and per 16-row block those of its
     // 4 consecutive rows (one 16-byte load per A plane), are loaded
     // together, so the epilogue waits for memory twice.  Rows and columns
-    // up to the padded line counts lie inside Ae / Be.
-    const int64_t rbase = row0 + 32 * wr + 4 * (lane >> 4);
+    // up to the padded line counts lie inside Ae / Be; the blocks of a
+    // 96-row tile past them read the last 4 rows again (never stored).
+    const int64_t rbase = row0 + 16 * RB * wr + 4 * (lane >> 4);
     int eb[NB];
 #pragma unroll
     for (int q = 0; q < NB; ++q) eb[q] = Be[(SW::BB + q) * b_lines + col];
     const int64_t nm = N * M;
 #pragma unroll
-    for (int h = 0; h < 2; ++h) {
+    for (int h = 0; h < RB; ++h) {
       int32x4 ea4[NA];
+      const int64_t rh = rbase + 16 * h < a_lines ? rbase + 16 * h : a_lines - 4;
 #pragma unroll
       for (int q = 0; q < NA; ++q)
-        ea4[q] = *(const int32x4*)(Ae + (SW::A0 + q) * a_lines + rbase + 16 * h);
+        ea4[q] = *(const int32x4*)(Ae + (SW::A0 + q) * a_lines + rh);
       // A sweep that continues the schedule loads the fold state of the
       // block's 4 rows here too.
       typename FoldOf<ORDER>::type fr[4];
@@ -610,15 +653,15 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
     int64_t ldp, char* __restrict__ state, int tail_P, uint32_t* __restrict__ part,
     I8Fix fix, uint32_t* __restrict__ dyn, int dyn_nstat) {
-  typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
-  constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP;
-  constexpr int kBuf = SW::S * 4 * 64;  // uint4 per stage buffer
+  typedef Sweep<PIPE, NHI, NLO, B0, B1, SYM> SW;
+  constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP, RB = SW::RB, FA = SW::FA;
+  constexpr int kBuf = SW::NFRAG * 64;  // uint4 per stage buffer
   static_assert(kRing == 4, "wait_stage assumes 4 stage buffers");
-  static_assert(SW::S <= 10, "a stage holds at most 10 planes (160 KiB ring)");
-  // S = 10: 4 x 40 KiB, the whole 160 KiB LDS of a gfx950 CU.
+  static_assert(SW::NFRAG <= 40, "a stage holds at most 40 fragments (160 KiB ring)");
+  // 40 fragments: 4 x 40 KiB, the whole 160 KiB LDS of a gfx950 CU.
   __shared__ uint4 lds[kRing * kBuf];
 
-  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
+  const int ntm = (int)((a_lines + SW::TM - 1) / SW::TM), ntn = (int)(b_lines / kBN);
   const int bid = (int)blockIdx.x, nwg = (int)gridDim.x;
   // SYM: B's planes are A's (a gram matrix); only tiles tm <= tn are run
   // and each element folds both C[i][j] and C[j][i] (see the epilogue).
@@ -710,18 +753,20 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
         int tm, tn;
         coords(item_tile(jj), tm, tn);
         const int64_t col = (int64_t)tn * kBN + 16 * mma.wc + (lane & 15);
-        const int64_t rb = (int64_t)tm * kBM + 32 * mma.wr + 4 * (lane >> 4);
+        const int64_t rb = (int64_t)tm * SW::TM + 16 * RB * mma.wr + 4 * (lane >> 4);
         // per plane once: o sb + Kp o^2 and -o sa (modulo 2^32, as i8_start)
         uint32_t tb[NB];
 #pragma unroll
         for (int q = 0; q < NB; ++q)
           tb[q] = fix.off * (uint32_t)fix.bs[(SW::BB + q) * b_lines + col] + fix.kpo2;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
+        for (int h = 0; h < RB; ++h) {
           uint32_t na[NA][4];
+          // rows past the lines (a 96-row tile's last blocks) read the last 4
+          const int64_t rh = rb + 16 * h < a_lines ? rb + 16 * h : a_lines - 4;
 #pragma unroll
           for (int q = 0; q < NA; ++q) {
-            const int32x4 sa = *(const int32x4*)(fix.as + (SW::A0 + q) * a_lines + rb + 16 * h);
+            const int32x4 sa = *(const int32x4*)(fix.as + (SW::A0 + q) * a_lines + rh);
 #pragma unroll
             for (int i = 0; i < 4; ++i) na[q][i] = 0u - fix.off * (uint32_t)sa[i];
           }
@@ -738,8 +783,8 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     }
 #pragma unroll
     for (int k = 0; k < NP; ++k) {
-      mma.acc[k][0] = typename Op::acc_t{};
-      mma.acc[k][1] = typename Op::acc_t{};
+#pragma unroll
+      for (int h = 0; h < RB; ++h) mma.acc[k][h] = typename Op::acc_t{};
     }
   };
   start_item(0);
@@ -751,20 +796,23 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   int fj = 0;
   int64_t fs = 0, fe = 0;
   const char *fA = Ab, *fB = Bb;
+  int fg = FA;  // line groups of the fetched tile inside the A planes
   auto load_tile = [&](int j) {
     int tm, tn;
     coords(item_tile(j), tm, tn);
-    fA = Ab + (int64_t)tm * kBM * kChunkBytes;
+    fA = Ab + (int64_t)tm * SW::TM * kChunkBytes;
     fB = Bb + (int64_t)tn * kBN * kChunkBytes;
+    const int64_t left = (a_lines - (int64_t)tm * SW::TM) / 16;
+    fg = left < FA ? (int)left : FA;
     fs = j < nwhole ? 0 : ps0;
     fe = j < nwhole ? nst : ps1;
   };
   // issue stage g of the sequence into ring buffer g % kRing
   auto fetch = [&](int64_t g) {
     if (dma_wave)
-      stage_dma<NA, NB>(fA, aplane, a_stage, fB, bplane, b_stage, fs,
-                        lds0 + (uint32_t)((g & (kRing - 1)) * kBuf * 16), wave,
-                        lane_bytes);
+      stage_dma<NA, NB, FA>(fA, aplane, a_stage, fB, bplane, b_stage, fs,
+                            lds0 + (uint32_t)((g & (kRing - 1)) * kBuf * 16), wave,
+                            lane_bytes, fg);
     if (++fs == fe) {
       if (++fj < nitems) load_tile(fj);
     }
@@ -781,7 +829,10 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
   int64_t s = 0;
   for (int64_t g = 0; g < total; ++g) {
     const int64_t later = total - 1 - g < kRing - 2 ? total - 1 - g : kRing - 2;
-    if (dma_wave) wait_stage<SW::S>(later);
+    if (dma_wave) {
+      if (wave + 4 < FA) wait_stage<stage_loads<NA, NB, FA>(0)>(later);
+      else wait_stage<stage_loads<NA, NB, FA>(3)>(later);
+    }
     __syncthreads();
     if (g + kRing - 1 < total) fetch(g + kRing - 1);
     mma(lds + (g & (kRing - 1)) * kBuf);
@@ -797,11 +848,11 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
       // part[bid][thread][k][h]: each thread's sums are contiguous, so the
       // 16-byte stores take immediate offsets
       typename Op::acc_t* dst =
-          (typename Op::acc_t*)part + ((int64_t)bid * kThreads16 + threadIdx.x) * NP * 2;
+          (typename Op::acc_t*)part + ((int64_t)bid * kThreads16 + threadIdx.x) * NP * RB;
 #pragma unroll
       for (int k = 0; k < NP; ++k) {
-        dst[2 * k] = mma.acc[k][0];
-        dst[2 * k + 1] = mma.acc[k][1];
+#pragma unroll
+        for (int h = 0; h < RB; ++h) dst[RB * k + h] = mma.acc[k][h];
       }
     }
     ++j;
@@ -822,17 +873,17 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     const int32_t* __restrict__ Ae, const int32_t* __restrict__ Be, int64_t N,
     int64_t M, int64_t a_lines, int64_t b_lines, float unit2, double* __restrict__ C,
     int64_t ldc, float* __restrict__ P, int64_t ldp, char* __restrict__ state, I8Fix fix) {
-  typedef Sweep<PIPE, NHI, NLO, B0, B1> SW;
+  typedef Sweep<PIPE, NHI, NLO, B0, B1, SYM> SW;
   typedef typename Op::acc_t V;
-  constexpr int NP = SW::NP, NV = 2 * NP;  // accumulator vectors per lane
-  constexpr int PER = (NV + 7) / 8;        // vectors per wave
+  constexpr int NP = SW::NP, RB = SW::RB, NV = RB * NP;  // accumulator vectors per lane
+  constexpr int PER = (NV + 7) / 8;                      // vectors per wave
   __shared__ V sum[NV][64];
   const int tl = blockIdx.x >> 3, w = blockIdx.x & 7;
   const int v = threadIdx.x >> 6, lane = threadIdx.x & 63;
   V s[PER];
 #pragma unroll
   for (int i = 0; i < PER; ++i) s[i] = V{};
-  // part[slot][thread][2 NP] with slot = tail tile * tail_P + piece and
+  // part[slot][thread][RB NP] with slot = tail tile * tail_P + piece and
   // thread = 64 w + lane of the all-pairs workgroup
   const V* src = (const V*)part + ((int64_t)tl * tail_P * kThreads16 + w * 64 + lane) * NV;
   const int64_t piece_stride = (int64_t)kThreads16 * NV;
@@ -842,21 +893,21 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     for (int i = 0; i < PER; ++i)
       if (v * PER + i < NV) s[i] += src[q * piece_stride + v * PER + i];
   }
-  const int ntm = (int)(a_lines / kBM), ntn = (int)(b_lines / kBN);
+  const int ntm = (int)((a_lines + SW::TM - 1) / SW::TM), ntn = (int)(b_lines / kBN);
   int tm, tn;
   if constexpr (SYM) tile_coords_sym(tile0 + tl, ntm, tm, tn);
   else tile_coords(tile0 + tl, ntm, ntn, tm, tn);
   if constexpr (std::is_same<Op, OpI8>::value) {
     // the offset's part (I8Fix) out of the pieces' raw sums
     const int64_t col = (int64_t)tn * kBN + 16 * (w & 3) + (lane & 15);
-    const int64_t rb = (int64_t)tm * kBM + 32 * (w >> 2) + 4 * (lane >> 4);
+    const int64_t rb = (int64_t)tm * SW::TM + 16 * RB * (w >> 2) + 4 * (lane >> 4);
 #pragma unroll
     for (int i = 0; i < PER; ++i) {
-      const int idx = v * PER + i;  // vector idx = 2 k + h
+      const int idx = v * PER + i;  // vector idx = RB k + h
       if (idx < NV) {
-        const int k = idx >> 1, h = idx & 1;
-        const int32x4 sa = *(const int32x4*)(fix.as + (SW::A0 + SW::la(k)) * a_lines + rb +
-                                              16 * h);
+        const int k = idx / RB, h = idx % RB;
+        const int64_t rh = rb + 16 * h < a_lines ? rb + 16 * h : a_lines - 4;
+        const int32x4 sa = *(const int32x4*)(fix.as + (SW::A0 + SW::la(k)) * a_lines + rh);
         const int sb = fix.bs[(SW::BB + SW::lb(k)) * b_lines + col];
         s[i] += i8_start(fix, sa, sb);
       }
@@ -867,11 +918,11 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     if (v * PER + i < NV) sum[v * PER + i][lane] = s[i];
   __syncthreads();
   if (v != 0) return;
-  V acc[NP][2];
+  V acc[NP][RB];
 #pragma unroll
   for (int k = 0; k < NP; ++k) {
-    acc[k][0] = sum[2 * k][lane];
-    acc[k][1] = sum[2 * k + 1][lane];
+#pragma unroll
+    for (int h = 0; h < RB; ++h) acc[k][h] = sum[RB * k + h][lane];
   }
   tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(acc, tm, tn, w >> 2, w & 3, lane, Ae, Be, N, M,
                                             a_lines, b_lines, unit2, C, ldc, P, ldp, state);
@@ -1076,7 +1127,7 @@ struct TailPlan {
   size_t bytes = 0; // partial sums
 };
 
-static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np) {
+static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np, int rb) {
   TailPlan tp;
   const int64_t R = ntiles / cus, T = ntiles % cus;
   if (T == 0) return tp;
@@ -1085,7 +1136,7 @@ static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np) {
   tp.P = (int)P;
   tp.T = T;
   tp.grid = R > 0 ? cus : (int)(T * P);
-  tp.bytes = (size_t)(T * P) * (size_t)np * 8 * kThreads16 * sizeof(uint32_t);
+  tp.bytes = (size_t)(T * P) * (size_t)np * 4 * rb * kThreads16 * sizeof(uint32_t);
   return tp;
 }
 
@@ -1114,9 +1165,14 @@ size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
          kDynBytes;
 }
 
-static int64_t allpairs_ntiles(int64_t N, int64_t M, bool sym) {
+// Tile rows of a single-sweep all-pairs launch of schedule (nhi, nlo).
+static int allpairs_tm(int nhi, int nlo, bool sym) {
+  return 32 * (allpairs_sweeps(nhi, nlo) == 1 ? ap_rb(nhi, nlo, 0, 2, sym) : 2);
+}
+
+static int64_t allpairs_ntiles(int64_t N, int64_t M, bool sym, int tm) {
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
-  return sym ? (al / kBM) * (al / kBM + 1) / 2 : (al / kBM) * (bl / kBN);
+  return sym ? (al / kBM) * (al / kBM + 1) / 2 : ((al + tm - 1) / tm) * (bl / kBN);
 }
 
 static int64_t allpairs_nst(int64_t K, bool i8) {
@@ -1129,8 +1185,9 @@ static int64_t allpairs_nst(int64_t K, bool i8) {
 size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int nlo,
                        bool sym, bool i8) {
   if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(nhi, nlo) != 1) return 0;
-  return plan_tail(allpairs_ntiles(N, M, sym), cu_count(), allpairs_nst(K, i8),
-                   pair_count(pipe, nhi, nlo))
+  const int tm = allpairs_tm(nhi, nlo, sym);
+  return plan_tail(allpairs_ntiles(N, M, sym, tm), cu_count(), allpairs_nst(K, i8),
+                   pair_count(pipe, nhi, nlo), tm / 32)
       .bytes;
 }
 
@@ -1236,7 +1293,8 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   }
   ApArgs a;
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
-  const int64_t ntiles = allpairs_ntiles(N, M, sym);
+  const int tmr = allpairs_tm(nhi, nlo, sym);
+  const int64_t ntiles = allpairs_ntiles(N, M, sym, tmr);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
   // persistent: one workgroup per CU (the 160 KiB ring fills its LDS)
   const int cus = cu_count();
@@ -1251,7 +1309,7 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   const size_t off = round_up((int64_t)need, 256);
   if (allpairs_sweeps(nhi, nlo) == 1) {
     const TailPlan tp = plan_tail(ntiles, cus, allpairs_nst(K, i8),
-                                  pair_count(OZK_PIPE_ONDEVICE, nhi, nlo));
+                                  pair_count(OZK_PIPE_ONDEVICE, nhi, nlo), tmr / 32);
     if (tp.P > 1 && state && state_bytes >= off + kDynBytes + tp.bytes) {
       a.grid = dim3((unsigned)tp.grid);
       a.tail_P = tp.P;

@@ -1,7 +1,8 @@
-"""FP32 column extraction without a transposed copy (columns of up to 8192
-rows, cut into 512-row runs held by the workgroups of a gang, which combine
-their per-slice column maxima through the workspace), against the oracle's
-column extraction (extract.py:157-191, :21-103 for FP64).
+"""FP32 column extraction without a transposed copy (columns of up to 4096
+rows held whole by one workgroup; 4097 to 8192 rows cut into 512-row runs
+held by the workgroups of a gang, which combine their column maxima through
+the workspace), against the oracle's column extraction (extract.py:157-191,
+:21-103 for FP64).
 
 Lengths straddle the runs (gangs of 2 to 16 workgroups) and the 8192-row
 limit (8193 rows go through the FP64 transpose, as FP64 extraction always
@@ -96,6 +97,35 @@ def test_panel_f32_i8(ll, length, cols):
     assert np.array_equal(to_np(pl.exponents()),
                           np.concatenate([eh, el]).astype(np.int32)), "exponents"
     check_padding(pl, length, cols)
+
+
+@pytest.mark.parametrize("length", [4097, 8192])
+@pytest.mark.parametrize("kind", ["integers", "spiky", "binade"])
+def test_panel_f32_candidates_missed(ll, length, kind):
+    """Columns whose later exponents are not the two candidates the gangs'
+    second round sends keys for (residuals that vanish, or that fall more
+    than one binade below the bound): those columns settle their slices one
+    round at a time, bit-exact, on both plane formats."""
+    rng = np.random.RandomState(length + len(kind))
+    if kind == "integers":      # few significant bits: residuals reach zero
+        X = rng.randint(-300, 300, size=(length, 40)).astype(np.float64)
+    elif kind == "spiky":       # one large element per column, the rest tiny
+        X = rng.randn(length, 40) * 1e-6
+        X[rng.randint(0, length, 40), np.arange(40)] = 1e3
+    else:                       # every element in [1, 2): exponent steps of the bound
+        X = 1.0 + rng.rand(length, 40)
+    hi, lo = O.split_hi_lo(X)
+    for i8 in (False, True):
+        rho = max(19, O.rho_f32(length)) if i8 else O.rho_f32(length)
+        case(f"ozk_extract_f32 gang {kind} ({length}, 40) i8={i8} rho={rho}")
+        pl = ll.extract(X, 1, rho, 4, 1, i8=i8)
+        sh, eh = O.extract_cols_f32(hi, rho, 4)
+        sl, el = O.extract_cols_f32(lo, rho, 1)
+        ref = np.concatenate([sh, sl]).transpose(0, 2, 1)
+        assert np.array_equal(to_np(pl.values()), ref), "slices"
+        assert np.array_equal(to_np(pl.exponents()),
+                              np.concatenate([eh, el]).astype(np.int32)), "exponents"
+        check_padding(pl, length, 40)
 
 
 @pytest.mark.parametrize("length", [1024, 2049, 4097, 8192])
