@@ -79,7 +79,7 @@ void ozk_set_wait_polls(uint32_t polls);
 
 /* No counterpart in the reference: the extraction strategy of the calling
  * thread's later calls (thread-local).  1 (the default): columns of 4097 to
- * 8192 rows, and FP32 rows of 32769 to 262144 elements, are extracted by
+ * 65536 rows, and FP32 rows of 32769 to 262144 elements, are extracted by
  * gangs of workgroups that exchange their partial maxima, with waits that
  * give up after 0.2 s (OZK_FLAG_WAIT_TIMEOUT) when other work keeps the
  * gang's members from running together; ozk_lu_solve_f32 spreads each
@@ -127,7 +127,7 @@ int64_t ozk_slice_lines(int64_t lines);
  * (extract.py:197-286; NumPy twin extract.py:116-191).  by_cols = 0 extracts
  * per row of X (rows x cols), by_cols = 1 per column; in both cases a line
  * is stored contiguously.  Columns of up to 4096 rows are extracted in place,
- * each by one workgroup (no workspace); columns of 4097 to 8192 rows in place
+ * each by one workgroup (no workspace); columns of 4097 to 65536 rows in place
  * by groups of workgroups that exchange their column maxima through the
  * workspace (a bounded wait that gives up sets OZK_FLAG_WAIT_TIMEOUT in
  * flags: the planes are then not valid); longer columns are transposed

@@ -468,7 +468,8 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
 // (rho = 19), so the four hi slices of the high preset take two rounds.
 //
 // Exchange, per (panel, round): a record of G lines, zeroed before the
-// launch (2 parts x 16 columns words a line; 7 times that in round 1).
+// launch (2 parts x 16 columns words a line; in round 1 the hi part sends
+// 7 keys a column: 8 x 16 words).
 // Member m stores its partial maxima as order keys, which are never 0,
 // into line m, then waits until every line is complete and combines them.
 // Every word is written once per launch, so a reader that sees a nonzero
@@ -480,8 +481,8 @@ __global__ __launch_bounds__(BLOCK) void extract_lines_stream(
 // Progress: a member's place (panel, m) comes from a ticket taken when it
 // starts, so all members of the gangs before the first incomplete one have
 // started, and those gangs finish; the incomplete gang's remaining members
-// then need only free slots (G <= kGangMaxMembers workgroups resident at
-// once).  Every wait is bounded all the same: after kGangWaitTicks ticks of
+// then need only free slots (G <= kGangMaxMembers = 128 workgroups resident
+// at once, of the 1024 that 256 CUs hold).  Every wait is bounded all the same: after kGangWaitTicks ticks of
 // the 100 MHz real-time counter (0.2 s, or the limit a test set with
 // ozk_set_wait_polls) it sets OZK_FLAG_WAIT_TIMEOUT (the slices are then not
 // valid) and the member waits no more in later rounds.  Other work that
@@ -492,10 +493,12 @@ constexpr int kGangPW = 16;
 constexpr int kGangRowsPT = 32;
 constexpr int kGangThreads = 256;
 constexpr int kGangRun = kGangThreads / kGangPW * kGangRowsPT;  // 512 rows
-constexpr int kGangMaxMembers = 16;
+constexpr int kGangMaxMembers = 128;
+constexpr int kGangBatch = 8;  // exchange words a combining thread loads at once
 constexpr uint32_t kGangWaitTicks = 20000000u;
-constexpr int kGangSpecKeys = 7;        // keys per (part, column) in round 1
-constexpr int kGangWords = 2 * kGangPW;  // words per record line (round 1: x 7)
+constexpr int kGangSpecKeys = 7;        // keys per hi column in round 1
+constexpr int kGangWords = 2 * kGangPW;  // words per record line (round 1: x 4)
+constexpr int kGangSpecWords = (kGangSpecKeys + 1) * kGangPW;  // 128
 constexpr int64_t kGangHeader = 256;    // the ticket word, padded
 
 __host__ __device__ constexpr int gang_members(int64_t ld) {
@@ -504,13 +507,18 @@ __host__ __device__ constexpr int gang_members(int64_t ld) {
 // Words per member line in round r, and the word offset of round r's
 // records in a panel's (rounds 0 .. r - 1 before it).
 __host__ __device__ constexpr int gang_round_words(int r) {
-  return r == 1 ? kGangSpecKeys * kGangWords : kGangWords;
+  return r == 1 ? kGangSpecWords : kGangWords;
 }
 __host__ __device__ constexpr int64_t gang_round_offset(int r, int G) {
   return r == 0 ? 0
-                : (int64_t)G * (kGangWords + (r >= 2 ? kGangSpecKeys * kGangWords +
+                : (int64_t)G * (kGangWords + (r >= 2 ? kGangSpecWords +
                                                            (int64_t)(r - 2) * kGangWords
                                                      : 0));
+}
+// Word of key k of part q, column col, in a record line of a round whose
+// hi part sends nk keys a column (the lo part sends one).
+__device__ __forceinline__ int gang_word(int q, int k, int nk, int col) {
+  return (q == 0 ? k : nk) * kGangPW + col;
 }
 
 // Order key of a partial maximum (a non-negative float or NaN): the key of
@@ -538,23 +546,25 @@ __device__ __forceinline__ uint32_t wait_key(const uint32_t* p, uint32_t* flags,
   return 0u;
 }
 
-// Bounded wait for the n <= N nonzero words base[off + i * stride] at once
-// (their loads in flight together); false (and the flag) on time-out.
+// Bounded wait for the n <= N word pairs base[off + i * stride] (8-byte
+// aligned), both words nonzero, with their loads in flight together; false
+// (and the flag) on time-out.
 template <int N>
-__device__ __forceinline__ bool wait_keys(const uint32_t* base, uint32_t off, uint32_t stride,
-                                          uint32_t (&k)[N], int n, uint32_t* flags,
-                                          uint32_t ticks) {
+__device__ __forceinline__ bool wait_pairs(const uint64_t* base, uint32_t off, uint32_t stride,
+                                           uint64_t (&k)[N], int n, uint32_t* flags,
+                                           uint32_t ticks) {
+  auto whole = [](uint64_t v) { return (uint32_t)v != 0u && (uint32_t)(v >> 32) != 0u; };
   const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
   for (;;) {
     bool all = true;
 #pragma unroll
     for (int i = 0; i < N; ++i) {
-      if (i < n && !k[i])
+      if (i < n && !whole(k[i]))
         k[i] = __hip_atomic_load(base + off + i * stride, __ATOMIC_RELAXED,
                                  __HIP_MEMORY_SCOPE_AGENT);
     }
 #pragma unroll
-    for (int i = 0; i < N; ++i) all &= i >= n || k[i] != 0u;
+    for (int i = 0; i < N; ++i) all &= i >= n || whole(k[i]);
     if (all) return true;
     if (__builtin_amdgcn_s_memrealtime() - t0 >= ticks) break;
     __builtin_amdgcn_s_sleep(1);
@@ -571,10 +581,11 @@ __device__ __forceinline__ FastSlice fast_slice_c(int c, int rho) {
   return fast_slice(k, rho);
 }
 
-// INT8: `part` receives member m's sums of q over its rows, per plane pl and
-// column at part[(pl G + m) eplane + column] (added up by i8_sum_parts):
-// the packed bytes (q + offset) of all kGangRun rows, rows past the column's
-// end included (q = 0 there), less offset x kGangRun.
+// INT8: every member adds its sums of q over its rows, per plane pl and
+// column, into sums[pl eplane + column] (zeroed before the launch): the
+// packed bytes (q + offset) of all kGangRun rows, rows past the column's
+// end included (q = 0 there), less offset x kGangRun.  Integer sums, so
+// the order of the members' atomic adds does not matter.
 // Four waves, up to 128 VGPRs each (four waves per SIMD), with the lo parts
 // in LDS: four members per CU, which cover each other's exchange waits.
 template <int FMT>
@@ -583,11 +594,11 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(4)
     int n1, typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
     uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t wait_ticks,
-    int32_t* __restrict__ part) {
+    int32_t* __restrict__ sums) {
   typedef typename PlaneElem<FMT>::type T;
   constexpr int NP = 2, R = kGangRowsPT, NKS = kGangSpecKeys;
   constexpr int NWORD = R * (int)sizeof(T) / 4;  // plane words of a thread's rows
-  constexpr int kMaxWords = NKS * kGangWords;    // 224
+  constexpr int kMaxWords = kGangSpecWords;      // 128
   const float qscale = ldexpf(1.0f, 24 - rho);
   // per-workgroup key maxima of the round, then all members' (order keys,
   // LDS atomic max)
@@ -666,14 +677,14 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(4)
   const bool store = r0 < ld;  // the R rows lie in one padded unit
   for (int r = 0;; ++r) {
     const int words = gang_round_words(r);
-    const int nk = r == 1 ? NKS : 1;  // keys per (part, column)
+    const int nk = r == 1 ? NKS : 1;  // keys per hi column
     uint32_t* const rs = my + gang_round_offset(r, G);  // this round's record
     // 1. The thread's partial maxima, reduced over the wave's lanes of the
     // column, then over the waves by LDS atomic max.  Candidates for the
     // hi part only (the lo part has one slice in the presets).
     auto publish_local = [&](int q, int k, float m) {
       m = wave_col_max(m);
-      if (lane < kGangPW) atomicMax(&wkey[(q * nk + k) * kGangPW + col], max_key(m));
+      if (lane < kGangPW) atomicMax(&wkey[gang_word(q, k, nk, col)], max_key(m));
     };
     {
       const int left = n0 - gc[0][col].done;
@@ -725,24 +736,33 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(4)
       __hip_atomic_store(rs + member * words + t, k ? k : max_key(0.0f), __ATOMIC_RELAXED,
                          __HIP_MEMORY_SCOPE_AGENT);
     }
-    // 3. Combine: thread t waits for word t % words of members
-    // t / words, t / words + ng, ... (all loads in flight together), then
-    // the maxima meet in LDS.
+    // 3. Combine: thread t waits for word pair w = t % (words / 2) of
+    // members t / (words / 2), that + ng, ... (kGangBatch 8-byte loads in
+    // flight together), then the maxima meet in LDS.
     {
-      const int ng = kGangThreads / words;  // 8 groups, or 1 in round 1
-      const int grp = t / words, w = t % words;
-      if (grp < ng && grp < G) {
-        uint32_t kk[kGangMaxMembers];
-#pragma unroll
-        for (int i = 0; i < kGangMaxMembers; ++i) kk[i] = 0u;
+      const int pairs = words / 2;
+      const int ng = kGangThreads / pairs;  // 16 groups, or 4 in round 1
+      const int grp = t / pairs, w = t % pairs;
+      if (grp < G) {
         const int n = (G - 1 - grp) / ng + 1;  // members grp, grp + ng, ... < G
-        if (!gave_up && !wait_keys(rs, (uint32_t)(grp * words + w), (uint32_t)(ng * words), kk,
-                                   n, flags, wait_ticks))
-          gave_up = 1;
-        uint32_t k = 0u;
+        uint32_t k0 = 0u, k1 = 0u;
+        for (int b = 0; b < n; b += kGangBatch) {
+          uint64_t kk[kGangBatch];
 #pragma unroll
-        for (int i = 0; i < kGangMaxMembers; ++i) k = max(k, kk[i]);
-        atomicMax(&wall[w], k);
+          for (int i = 0; i < kGangBatch; ++i) kk[i] = 0u;
+          if (!gave_up &&
+              !wait_pairs((const uint64_t*)rs, (uint32_t)((grp + b * ng) * pairs + w),
+                          (uint32_t)(ng * pairs), kk, min(n - b, kGangBatch), flags,
+                          wait_ticks))
+            gave_up = 1;
+#pragma unroll
+          for (int i = 0; i < kGangBatch; ++i) {
+            k0 = max(k0, (uint32_t)kk[i]);
+            k1 = max(k1, (uint32_t)(kk[i] >> 32));
+          }
+        }
+        atomicMax(&wall[2 * w], k0);
+        atomicMax(&wall[2 * w + 1], k1);
       }
     }
     __syncthreads();
@@ -751,7 +771,7 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(4)
     if (t < NP * kGangPW) {
       const int q = t / kGangPW, cl = t % kGangPW;
       GangCol& g = gc[q][cl];
-      auto key = [&](int k) { return key_max(wall[(q * nk + k) * kGangPW + cl]); };
+      auto key = [&](int k) { return key_max(wall[gang_word(q, k, nk, cl)]); };
       const int nq = q == 0 ? n0 : n1;
       const int done = g.done;
       const int left = nq - done;
@@ -863,9 +883,10 @@ __global__ __launch_bounds__(kGangThreads) __attribute__((amdgpu_waves_per_eu(4)
   }
   if constexpr (FMT == kFmtI8) {
     __syncthreads();
-    for (int i = t; i < (n0 + n1) * kGangPW; i += kGangThreads)
-      part[((int64_t)(i / kGangPW) * G + member) * eplane + panel * kGangPW + i % kGangPW] =
-          ssum[i] - i8_offset(rho) * kGangRun;
+    for (int i = t; i < (n0 + n1) * kGangPW; i += kGangThreads) {
+      const int64_t c = panel * kGangPW + i % kGangPW;
+      if (c < M) atomicAdd(&sums[(i / kGangPW) * eplane + c], ssum[i] - i8_offset(rho) * kGangRun);
+    }
   }
 }
 
@@ -1197,6 +1218,12 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
   }
 }
 
+__global__ void zero_i32_kernel(int32_t* __restrict__ p, int64_t n) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+       i += (int64_t)gridDim.x * blockDim.x)
+    p[i] = 0;
+}
+
 __global__ void zero_u32x4_kernel(uint4* __restrict__ p, int64_t n) {
   for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
        i += (int64_t)gridDim.x * blockDim.x)
@@ -1437,9 +1464,9 @@ int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st) {
   return OZK_OK;
 }
 
-// FP32 column extraction of columns up to kGangRun * kGangMaxMembers rows
-// runs on gangs; FP64 column extraction, and longer columns, go through an
-// FP64 transpose of X into the workspace.
+// FP32 column extraction of columns up to kGangRun * kGangMaxMembers =
+// 65536 rows runs on gangs; FP64 column extraction, and longer columns, go
+// through an FP64 transpose of X into the workspace.
 static bool gang_columns(int64_t rows) {
   return round_up(rows, kKPad) <= (int64_t)kGangRun * kGangMaxMembers && gangs_enabled();
 }
@@ -1477,18 +1504,12 @@ static int launch_cols_panel(const double* X, int64_t rows, int64_t cols, int64_
   return OZK_OK;
 }
 
-// Ticket and exchange records (zeroed per launch), then the INT8 partial
-// line sums (2 nslices planes x G members x padded columns).
-static size_t gang_records(int64_t rows, int64_t cols, int nslices) {
+// Ticket and exchange records (zeroed per launch).
+static size_t gang_workspace_bytes(int64_t rows, int64_t cols, int nslices) {
   const int G = gang_members(round_up(rows, kKPad));
   return (size_t)round_up(kGangHeader + (round_up(cols, kLinePad) / kGangPW) *
                                             gang_round_offset(nslices, G) * 4,
                           256);
-}
-static size_t gang_workspace_bytes(int64_t rows, int64_t cols, int nslices) {
-  const int64_t G = gang_members(round_up(rows, kKPad));
-  return gang_records(rows, cols, nslices) +
-         (size_t)(2 * nslices * G * round_up(cols, kLinePad)) * sizeof(int32_t);
 }
 
 // Offset of the row-gang records after the transposed copy.
@@ -1519,22 +1540,25 @@ static int launch_cols_gang(const double* X, int64_t rows, int64_t cols, int64_t
   const int64_t ld = round_up(rows, kKPad), lp = round_up(cols, kLinePad);
   const int64_t plane = lp * ld, npanels = lp / kGangPW;
   const int G = gang_members(ld);
-  // the ticket and the exchange records start at zero
-  const size_t recb = gang_records(rows, cols, ns);
-  const int64_t n16 = (int64_t)recb / 16;
+  // the ticket, the exchange records and the INT8 line sums start at zero
+  const int64_t n16 = (int64_t)need / 16;
   hipLaunchKernelGGL(zero_u32x4_kernel, dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)),
                      dim3(256), 0, st, (uint4*)ws, n16);
   OZK_LAUNCH_CHECK();
+  if constexpr (FMT == kFmtI8) {
+    const int64_t ns32 = (int64_t)(n0 + n1) * lp;
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)((ns32 + 255) / 256 < 1024 ? (ns32 + 255) / 256 : 1024)),
+                       dim3(256), 0, st, Sg, ns32);
+    OZK_LAUNCH_CHECK();
+  }
   uint32_t* ticket = (uint32_t*)ws;
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
-  int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(npanels * G));
   const uint32_t wait_ticks = wait_polls(kGangWaitTicks);
   hipLaunchKernelGGL((extract_cols_gang<FMT>), grid, dim3(kGangThreads), 0, st, X, rows, cols,
                      ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec, ticket, G,
-                     wait_ticks, part);
+                     wait_ticks, Sg);
   OZK_LAUNCH_CHECK();
-  if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;
 }
 

@@ -70,17 +70,17 @@ def r256(b):
 
 
 def gang_bytes(rows, cols):
-    """Column extraction of 4097 to 8192 rows on the FP32 path: the ticket
+    """Column extraction of 4097 to 65536 rows on the FP32 path: the ticket
     word and, per 16-column panel, the exchange records of up to 32 rounds
-    for each 512-row run of a column (32 words a round, 224 in round 1;
-    256-byte aligned), then the INT8 line sums of each run: 64 planes x
-    runs x padded columns.  Columns of up to 4096 rows need no workspace."""
+    for each 512-row run of a column (32 words a round, 128 in round 1;
+    256-byte aligned).  The members add their INT8 line sums into the
+    plane sums directly.  Columns of up to 4096 rows need no workspace."""
     ld = -(-rows // 64) * 64
     if ld <= 4096:
         return 0
     G = -(-ld // 512)
     lp = -(-cols // 64) * 64
-    return r256(256 + (lp // 16) * G * (32 + 224 + 30 * 32) * 4) + 64 * G * lp * 4
+    return r256(256 + (lp // 16) * G * (32 + 128 + 30 * 32) * 4)
 
 
 def row_gang_bytes(lines, length):
@@ -109,15 +109,16 @@ def test_workspace_sizes(lib):
     ws = lib.ozk_matmul_workspace_bytes(8192, 8192, 8192, 0, 5, 4)
     base = 2 * 9 * 8192 * 8192 + gang_bytes(8192, 8192) + 20 * 8192 * 8192
     assert base <= ws <= base + 2 * 2 * 9 * 8192 * 4 + 8192 + DYN
-    # columns longer than 8192 rows, and the FP64 (host) pipeline, transpose B;
-    # one extraction buffer serves A's rows and B's columns in turn
+    # columns longer than 65536 rows, and the FP64 (host) pipeline, transpose
+    # B; one extraction buffer serves A's rows and B's columns in turn
     ws = lib.ozk_matmul_workspace_bytes(64, 70000, 64, 0, 4, 1)
     assert ws >= 8 * 70000 * 64 + row_gang_bytes(64, 70000)
     N, K, M = 1024, 65536, 1024
     ws = lib.ozk_matmul_workspace_bytes(N, K, M, 0, 4, 1)
     planes = 5 * (N + M) * K + 2 * 5 * (N + M) * 4
-    ex = max(row_gang_bytes(N, K), 8 * K * M + row_gang_bytes(M, K))
+    ex = max(row_gang_bytes(N, K), gang_bytes(K, M))
     assert planes + ex <= ws <= planes + ex + 4096 + DYN
+    assert ws - planes < 8 * K * M  # no transposed copy of B
     ws = lib.ozk_matmul_workspace_bytes(64, 1000, 64, 1, 8, 0)
     assert ws >= 8 * 1000 * 64
 
@@ -148,7 +149,7 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_extract_workspace_bytes(100, 50, 1) == 40192
     assert lib.ozk_extract_workspace_bytes(8, 5000, 1) == 320000
     assert lib.ozk_extract_workspace_bytes(5000, 8, 1) == max(320000, gang_bytes(5000, 8))
-    assert gang_bytes(5000, 8) > 320000
+    assert lib.ozk_extract_workspace_bytes(5000, 1, 1) == gang_bytes(5000, 1) > 40000
     # longer columns: the transposed copy (256-byte aligned), then the row
     # gangs' records while the transposed lines are within their reach
     assert lib.ozk_extract_workspace_bytes(70000, 3, 1) == 1680128 + row_gang_bytes(3, 70000)

@@ -1,11 +1,11 @@
 """FP32 column extraction without a transposed copy (columns of up to 4096
-rows held whole by one workgroup; 4097 to 8192 rows cut into 512-row runs
+rows held whole by one workgroup; 4097 to 65536 rows cut into 512-row runs
 held by the workgroups of a gang, which combine their column maxima through
 the workspace), against the oracle's column extraction (extract.py:157-191,
 :21-103 for FP64).
 
-Lengths straddle the runs (gangs of 2 to 16 workgroups) and the 8192-row
-limit (8193 rows go through the FP64 transpose, as FP64 extraction always
+Lengths straddle the runs (gangs of 2 to 128 workgroups) and the 65536-row
+limit (65537 rows go through the FP64 transpose, as FP64 extraction always
 does); column counts that are not a multiple of the 16-column panel, and
 odd counts (an odd leading dimension takes the element-wise loads), leave
 partial panels.  Bar: bit-exact slices and exponents, zero padding.
@@ -99,7 +99,32 @@ def test_panel_f32_i8(ll, length, cols):
     check_padding(pl, length, cols)
 
 
-@pytest.mark.parametrize("length", [4097, 8192])
+LONG = [8193, 16385, 32768, 40000, 65536, 65537]
+
+
+@pytest.mark.parametrize("length", LONG)
+def test_gang_long_columns(ll, length):
+    """Columns of 16 to 128 runs (gangs whose members combine their keys in
+    batches) and, past 65536 rows, the transposed copy: both plane formats,
+    33 columns (a partial panel), wide-range and zero columns."""
+    X = gen("wide", (length, 33), 5 * length)
+    X[:, 7] = 0.0
+    hi, lo = O.split_hi_lo(X)
+    for i8 in (False, True):
+        rho = max(19, O.rho_f32(length)) if i8 else O.rho_f32(length)
+        case(f"ozk_extract_f32 gang ({length}, 33) i8={i8} rho={rho}")
+        pl = ll.extract(X, 1, rho, 4, 1, i8=i8)
+        sh, eh = O.extract_cols_f32(hi, rho, 4)
+        sl, el = O.extract_cols_f32(lo, rho, 1)
+        ref = np.concatenate([sh, sl]).transpose(0, 2, 1)
+        assert np.array_equal(to_np(pl.values()), ref), "slices"
+        assert np.array_equal(to_np(pl.exponents()),
+                              np.concatenate([eh, el]).astype(np.int32)), "exponents"
+        assert not pl.nonfinite()
+        check_padding(pl, length, 33)
+
+
+@pytest.mark.parametrize("length", [4097, 8192, 32768])
 @pytest.mark.parametrize("kind", ["integers", "spiky", "binade"])
 def test_panel_f32_candidates_missed(ll, length, kind):
     """Columns whose later exponents are not the two candidates the gangs'
@@ -140,7 +165,7 @@ def test_panel_f64(ll, length):
     check_padding(pl, length, 35)
 
 
-@pytest.mark.parametrize("length", [2000, 8192])
+@pytest.mark.parametrize("length", [2000, 8192, 40000])
 def test_panel_nonfinite_columns(ll, length):
     """A NaN, an Inf and a 2^110-scaled column: the flag word reports the
     non-finite input; on INT8 planes the NaN and Inf columns carry the

@@ -236,7 +236,7 @@ def test_extract_helpers_without_torch(no_torch):
     """extract_split_*, f32_extract_split_* and jax_extract_split_* on NumPy
     input (extract.py:21-286) with the planes unpacked on the host, bit for
     bit against the oracle; shapes cover the row kernels, the column gangs
-    (8192 rows) and the transposed long columns."""
+    (8192 and 9000 rows) and the FP64 path's transposed columns."""
     ozk = no_torch
     rng = np.random.RandomState(21)
     for shape in [(20, 33), (96, 5000), (8192, 40), (9000, 24)]:
