@@ -300,7 +300,6 @@ struct AllPairsMMA {
   // read of block j + kDepth is issued before the MFMAs of block j.
   // Scheduling barriers keep the reads where they are.
   static constexpr int kBlocks = NA * RB, kDepth = RB + 1;
-  static_assert(kBlocks >= kDepth + 1, "the opening fills blocks RB .. 2 RB");
 
   __device__ __forceinline__ uint4 read_a(const uint4* buf, int j) const {
     return buf[((j / RB) * SW::FA + RB * wr + (j % RB)) * 64 + fl];
@@ -338,7 +337,8 @@ struct AllPairsMMA {
     return -1;
   }
   static constexpr int kA0 = count_a0();
-  static_assert(kA0 >= 2, "A slot 0 pairs with at least two B slots");
+  // the B fragments are read by the pairs of A slot 0
+  static_assert(kA0 == NB, "A slot 0 pairs with every B slot");
 
   template <int K>
   __device__ __forceinline__ void opening(const uint4* buf, uint4 (&af)[kDepth + 1],
@@ -350,8 +350,10 @@ struct AllPairsMMA {
         constexpr int b2 = SW::lb(a0_pair(K + 2));
         bf[b2] = read_b(buf, b2);
       }
-      if constexpr (K == kA0 - 2) af[RB] = read_a(buf, RB);
-      if constexpr (K == kA0 - 1) af[RB + 1] = read_a(buf, RB + 1);
+      // blocks RB and RB + 1 of the ring (both in the first pair when A
+      // slot 0 has only one; none past the stage's last block)
+      if constexpr (K == (kA0 >= 2 ? kA0 - 2 : 0) && RB < kBlocks) af[RB] = read_a(buf, RB);
+      if constexpr (K == kA0 - 1 && RB + 1 < kBlocks) af[RB + 1] = read_a(buf, RB + 1);
 #pragma unroll
       for (int h = 0; h < RB; ++h) {
         acc[k][h] = Op::mma(af[h], bf[b], acc[k][h]);
@@ -366,11 +368,13 @@ struct AllPairsMMA {
     uint4 bf[NB];
     uint4 af[kDepth + 1];
     constexpr int b0 = SW::lb(a0_pair(0));
-    constexpr int b1 = SW::lb(a0_pair(1));
     bf[b0] = read_b(buf, b0);
 #pragma unroll
     for (int h = 0; h < RB; ++h) af[h] = read_a(buf, h);
-    bf[b1] = read_b(buf, b1);
+    if constexpr (kA0 >= 2) {
+      constexpr int b1 = SW::lb(a0_pair(1));
+      bf[b1] = read_b(buf, b1);
+    }
     __builtin_amdgcn_sched_barrier(0);
     opening<0>(buf, af, bf);
     pipe_step<RB>(buf, af, bf);
@@ -1012,6 +1016,7 @@ __global__ __launch_bounds__(kThreads) void gemm_pairwise(
   }
 }
 
+#ifndef OZK_GEMM_PART
 // One MFMA on a pattern that encodes (row, col) in the result:
 // A[i][0] = i, A[i][1] = 1, B[0][j] = 1, B[1][j] = 64 j, all other k zero,
 // under the operand layout lane l -> (row l % 32, k 8 * (l / 32) + e).
@@ -1053,23 +1058,131 @@ __global__ void probe_mfma16_kernel(int32_t* out) {
 __global__ void zero_u32_kernel(uint32_t* __restrict__ p, int n) {
   for (int i = threadIdx.x; i < n; i += blockDim.x) p[i] = 0u;
 }
+#endif  // OZK_GEMM_PART
 
-// Schedules with an all-pairs instantiation: high (4,1) and medium (3,1)
-// in one sweep, max (5,4) and (4,4) in three (hh, hl, lh; at most 25 pairs
-// and 10 planes each), the custom schedules that fit one sweep (at most 10
-// planes, n_hi + n_lo <= 5, and 21 pairs), and (4,2), (3,3) and (2,4) in
-// two (hh + hl, then lh).  Custom schedules take the on-device orders only
-// (2Sum, FP64 block, and the pair and per-product forms).
-constexpr bool allpairs_two_sweeps(int nhi, int nlo) {
-  return (nhi == 4 && nlo == 2) || (nhi == 3 && nlo == 3) || (nhi == 2 && nlo == 4);
+// Schedules with an all-pairs instantiation: every (n_hi, n_lo) with both
+// counts in 1 .. 5, in as few sweeps as fit the kernel (a sweep holds at
+// most 25 pairs, the accumulators, and 10 planes, the 160 KiB ring).  One
+// sweep when n_hi + n_lo <= 5 (high (4,1), medium (3,1)); else two (hh +
+// hl, then lh) when hh + hl fit; else three (hh, hl, lh; max (5,4)).
+// Custom schedules take the on-device orders only (2Sum, FP64 block, and
+// the pair and per-product forms).
+constexpr int allpairs_nsweeps(int nhi, int nlo) {
+  return (nhi < 1 || nlo < 1 || nhi > 5 || nlo > 5) ? 0
+         : nhi + nlo <= 5                            ? 1
+         : (2 * nhi + nlo <= 10 && nhi * (nhi + nlo) <= 25) ? 2
+                                                              : 3;
 }
+constexpr bool allpairs_two_sweeps(int nhi, int nlo) { return allpairs_nsweeps(nhi, nlo) == 2; }
 constexpr bool allpairs_three_sweeps(int nhi, int nlo) {
-  return (nhi == 5 && nlo == 4) || (nhi == 4 && nlo == 4);
+  return allpairs_nsweeps(nhi, nlo) == 3;
 }
 
 constexpr bool allpairs_preset(int nhi, int nlo) {
   return (nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1) || (nhi == 5 && nlo == 4);
 }
+
+
+struct ApArgs {
+  dim3 grid;
+  bool sym;
+  int tail_P;
+  int tile0;  // first tail tile
+  int64_t tail_T;
+  uint32_t* part;
+  uint32_t* dyn;  // dynamic-tail counters: kXcds per sweep, or null
+  int dyn_nstat;
+  hipStream_t st;
+  const char *As, *Bs;
+  const int32_t *Ae, *Be;
+  int64_t N, M, nst, al, bl;
+  float unit2;
+  double* C;
+  int64_t ldc;
+  float* P;
+  int64_t ldp;
+  char* state;
+  I8Fix fix;
+};
+
+template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
+static void launch_sweep(const ApArgs& a) {
+  const bool split = a.tail_P > 1 && B0 == 0 && B1 == 2;
+  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
+                     a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
+                     a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
+                     split ? a.tail_P : 0, a.part, a.fix,
+                     a.dyn ? a.dyn + kXcds * B0 : nullptr, a.dyn_nstat);
+  if constexpr (B0 == 0 && B1 == 2) {
+    if (split)
+      hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
+                         dim3((unsigned)(a.tail_T * 8)), dim3(kThreads16), 0, a.st, a.part, a.tail_P,
+                         a.tile0, a.Ae, a.Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P,
+                         a.ldp, a.state, a.fix);
+  }
+}
+
+template <class Op, int NHI, int NLO, int ORDER>
+static void launch_schedule(const ApArgs& a) {
+  if constexpr (allpairs_three_sweeps(NHI, NLO)) {
+    launch_sweep<Op, NHI, NLO, ORDER, 0, 0>(a);
+    launch_sweep<Op, NHI, NLO, ORDER, 1, 1>(a);
+    launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
+  } else if constexpr (allpairs_two_sweeps(NHI, NLO)) {
+    launch_sweep<Op, NHI, NLO, ORDER, 0, 1>(a);
+    launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
+  } else {
+    launch_sweep<Op, NHI, NLO, ORDER, 0, 2>(a);
+  }
+}
+
+template <class Op, int NHI, int NLO>
+static void launch_ap_order(int order, const ApArgs& a) {
+  switch (order) {
+    case OZK_ORDER_2SUM:
+      if constexpr (NLO == 1 && (NHI == 3 || NHI == 4)) {  // high, medium: symmetric form
+        if (a.sym) {
+          launch_sweep<Op, NHI, NLO, OZK_ORDER_2SUM, 0, 2, true>(a);
+          break;
+        }
+      }
+      launch_schedule<Op, NHI, NLO, OZK_ORDER_2SUM>(a);
+      break;
+    case OZK_ORDER_BLOCK64: launch_schedule<Op, NHI, NLO, OZK_ORDER_BLOCK64>(a); break;
+    case OZK_ORDER_HOST_JAX:  // presets only (allpairs_order)
+      if constexpr (allpairs_preset(NHI, NLO))
+        launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a);
+      break;
+    case OZK_ORDER_HOST_NP:
+      if constexpr (allpairs_preset(NHI, NLO))
+        launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a);
+      break;
+    case kOrderPair: launch_schedule<Op, NHI, NLO, kOrderPair>(a); break;
+    default: launch_schedule<Op, NHI, NLO, kOrderProducts>(a); break;
+  }
+}
+
+
+#ifdef OZK_GEMM_PART
+// A part of the schedules' instantiations, compiled as a translation unit
+// of its own so that the parts build in parallel: OZK_GEMM_PART_TUPLES(X)
+// names its (n_hi, n_lo).  Returns false for a schedule of another part.
+bool OZK_GEMM_PART_FN(bool i8, int nhi, int nlo, int order, const ApArgs& a) {
+#define OZK_PART_CASE(H, L)                                   \
+  if (nhi == H && nlo == L) {                                 \
+    if (i8) launch_ap_order<OpI8, H, L>(order, a);            \
+    else launch_ap_order<OpBf16, H, L>(order, a);             \
+    return true;                                              \
+  }
+  OZK_GEMM_PART_TUPLES(OZK_PART_CASE)
+#undef OZK_PART_CASE
+  return false;
+}
+#else
+bool launch_ap_part1(bool i8, int nhi, int nlo, int order, const ApArgs& a);
+bool launch_ap_part2(bool i8, int nhi, int nlo, int order, const ApArgs& a);
+bool launch_ap_part3(bool i8, int nhi, int nlo, int order, const ApArgs& a);
+bool launch_ap_part4(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 
 // Orders the all-pairs kernel runs for schedule (nhi, nlo): every order for
 // the presets, the on-device ones for the custom schedules.
@@ -1078,24 +1191,14 @@ static bool allpairs_order(int nhi, int nlo, int order) {
          (order != OZK_ORDER_HOST_JAX && order != OZK_ORDER_HOST_NP);
 }
 
-static bool allpairs_custom(int nhi, int nlo) {
-  return (nhi == 1 && nlo >= 1 && nlo <= 4) || (nhi == 2 && nlo >= 1 && nlo <= 3) ||
-         (nhi == 3 && nlo == 2) || allpairs_two_sweeps(nhi, nlo) ||
-         (nhi == 4 && nlo == 4);
+static bool allpairs_schedule(int pipe, int nhi, int nlo) {
+  return pipe == OZK_PIPE_ONDEVICE && allpairs_nsweeps(nhi, nlo) > 0;
 }
 
-static bool allpairs_schedule(int pipe, int nhi, int nlo) {
-  return pipe == OZK_PIPE_ONDEVICE &&
-         ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1) || (nhi == 5 && nlo == 4) ||
-          allpairs_custom(nhi, nlo));
-}
+static int allpairs_sweeps(int nhi, int nlo) { return allpairs_nsweeps(nhi, nlo); }
 
 bool allpairs_supported(int pipe, int nhi, int nlo) {
   return allpairs_schedule(pipe, nhi, nlo);
-}
-
-static int allpairs_sweeps(int nhi, int nlo) {
-  return allpairs_three_sweeps(nhi, nlo) ? 3 : (allpairs_two_sweeps(nhi, nlo) ? 2 : 1);
 }
 
 static int fold_state_bytes(int order) {
@@ -1191,85 +1294,6 @@ size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int n
       .bytes;
 }
 
-struct ApArgs {
-  dim3 grid;
-  bool sym;
-  int tail_P;
-  int tile0;  // first tail tile
-  int64_t tail_T;
-  uint32_t* part;
-  uint32_t* dyn;  // dynamic-tail counters: kXcds per sweep, or null
-  int dyn_nstat;
-  hipStream_t st;
-  const char *As, *Bs;
-  const int32_t *Ae, *Be;
-  int64_t N, M, nst, al, bl;
-  float unit2;
-  double* C;
-  int64_t ldc;
-  float* P;
-  int64_t ldp;
-  char* state;
-  I8Fix fix;
-};
-
-template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
-static void launch_sweep(const ApArgs& a) {
-  const bool split = a.tail_P > 1 && B0 == 0 && B1 == 2;
-  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
-                     a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
-                     a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
-                     split ? a.tail_P : 0, a.part, a.fix,
-                     a.dyn ? a.dyn + kXcds * B0 : nullptr, a.dyn_nstat);
-  if constexpr (B0 == 0 && B1 == 2) {
-    if (split)
-      hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
-                         dim3((unsigned)(a.tail_T * 8)), dim3(kThreads16), 0, a.st, a.part, a.tail_P,
-                         a.tile0, a.Ae, a.Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P,
-                         a.ldp, a.state, a.fix);
-  }
-}
-
-template <class Op, int NHI, int NLO, int ORDER>
-static void launch_schedule(const ApArgs& a) {
-  if constexpr (allpairs_three_sweeps(NHI, NLO)) {
-    launch_sweep<Op, NHI, NLO, ORDER, 0, 0>(a);
-    launch_sweep<Op, NHI, NLO, ORDER, 1, 1>(a);
-    launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
-  } else if constexpr (allpairs_two_sweeps(NHI, NLO)) {
-    launch_sweep<Op, NHI, NLO, ORDER, 0, 1>(a);
-    launch_sweep<Op, NHI, NLO, ORDER, 2, 2>(a);
-  } else {
-    launch_sweep<Op, NHI, NLO, ORDER, 0, 2>(a);
-  }
-}
-
-template <class Op, int NHI, int NLO>
-static void launch_ap_order(int order, const ApArgs& a) {
-  switch (order) {
-    case OZK_ORDER_2SUM:
-      if constexpr (NLO == 1 && NHI >= 3) {  // high, medium: symmetric form available
-        if (a.sym) {
-          launch_sweep<Op, NHI, NLO, OZK_ORDER_2SUM, 0, 2, true>(a);
-          break;
-        }
-      }
-      launch_schedule<Op, NHI, NLO, OZK_ORDER_2SUM>(a);
-      break;
-    case OZK_ORDER_BLOCK64: launch_schedule<Op, NHI, NLO, OZK_ORDER_BLOCK64>(a); break;
-    case OZK_ORDER_HOST_JAX:  // presets only (allpairs_order)
-      if constexpr (allpairs_preset(NHI, NLO))
-        launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_JAX>(a);
-      break;
-    case OZK_ORDER_HOST_NP:
-      if constexpr (allpairs_preset(NHI, NLO))
-        launch_schedule<Op, NHI, NLO, OZK_ORDER_HOST_NP>(a);
-      break;
-    case kOrderPair: launch_schedule<Op, NHI, NLO, kOrderPair>(a); break;
-    default: launch_schedule<Op, NHI, NLO, kOrderProducts>(a); break;
-  }
-}
-
 // All-pairs launch for an all-pairs schedule; `i8` selects the INT8 plane
 // format (rho >= 19).  order = kOrderProducts writes P.  `state` holds at
 // least gemm_state_bytes(); with gemm_workspace_bytes() the last rounds of
@@ -1347,27 +1371,28 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.fix.bs = Bsum;
   a.fix.off = i8 ? (uint32_t)i8_offset(rho) : 0u;
   a.fix.kpo2 = (uint32_t)((uint64_t)(a.nst * kChunkBytes) * a.fix.off * a.fix.off);
-#define OZK_AP_ALL(Op)                                                    \
+  // the presets and the smallest custom schedules here, the others in the
+  // parts (gemm_parts.h)
+  bool done = true;
+#define OZK_AP_MAIN(Op)                                                   \
   do {                                                                    \
     if (nhi == 4 && nlo == 1) launch_ap_order<Op, 4, 1>(order, a);        \
     else if (nhi == 3 && nlo == 1) launch_ap_order<Op, 3, 1>(order, a);   \
     else if (nhi == 5 && nlo == 4) launch_ap_order<Op, 5, 4>(order, a);   \
     else if (nhi == 1 && nlo == 1) launch_ap_order<Op, 1, 1>(order, a);   \
-    else if (nhi == 1 && nlo == 2) launch_ap_order<Op, 1, 2>(order, a);   \
-    else if (nhi == 1 && nlo == 3) launch_ap_order<Op, 1, 3>(order, a);   \
-    else if (nhi == 1 && nlo == 4) launch_ap_order<Op, 1, 4>(order, a);   \
     else if (nhi == 2 && nlo == 1) launch_ap_order<Op, 2, 1>(order, a);   \
     else if (nhi == 2 && nlo == 2) launch_ap_order<Op, 2, 2>(order, a);   \
-    else if (nhi == 2 && nlo == 3) launch_ap_order<Op, 2, 3>(order, a);   \
-    else if (nhi == 3 && nlo == 2) launch_ap_order<Op, 3, 2>(order, a);   \
-    else if (nhi == 4 && nlo == 2) launch_ap_order<Op, 4, 2>(order, a);   \
-    else if (nhi == 2 && nlo == 4) launch_ap_order<Op, 2, 4>(order, a);   \
-    else if (nhi == 4 && nlo == 4) launch_ap_order<Op, 4, 4>(order, a);   \
-    else launch_ap_order<Op, 3, 3>(order, a);                             \
+    else done = false;                                                    \
   } while (0)
-  if (i8) OZK_AP_ALL(OpI8);
-  else OZK_AP_ALL(OpBf16);
-#undef OZK_AP_ALL
+  if (i8) OZK_AP_MAIN(OpI8);
+  else OZK_AP_MAIN(OpBf16);
+#undef OZK_AP_MAIN
+  if (!done && !launch_ap_part1(i8, nhi, nlo, order, a) &&
+      !launch_ap_part2(i8, nhi, nlo, order, a) && !launch_ap_part3(i8, nhi, nlo, order, a) &&
+      !launch_ap_part4(i8, nhi, nlo, order, a)) {
+    set_error("all-pairs schedule (%d, %d) has no instantiation", nhi, nlo);
+    return OZK_ERR_UNSUPPORTED;
+  }
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }
@@ -1516,5 +1541,7 @@ int launch_probe_mfma(int32_t* out, hipStream_t st) {
   OZK_LAUNCH_CHECK();
   return OZK_OK;
 }
+
+#endif  // OZK_GEMM_PART
 
 }  // namespace ozk

@@ -159,9 +159,9 @@ def test_gemm_workspace_bytes(lib):
 def test_int8_entry_points_reject_before_device_work(lib):
     from ozaki_jax_amd import _lib
     # INT8 planes need 19 <= rho <= 24 (|q| <= 64, stored with an offset of
-    # at most 63) and an all-pairs schedule: the presets and the custom
-    # schedules (1,1)-(1,4), (2,1)-(2,3), (3,2), (3,3) and (4,2); others,
-    # such as (5,1), (2,4) and (4,4), run on BF16 planes
+    # at most 63) and an all-pairs schedule: every (n_hi, n_lo) with both
+    # counts in 1 .. 5; others, such as (6,1), (1,6) and (6,6), run on BF16
+    # planes
     for rho in (18, 25):
         rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, rho, 4, 1, None, None, None, None, None,
                                     0, None)
@@ -169,7 +169,7 @@ def test_int8_entry_points_reject_before_device_work(lib):
         rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, rho, 4, 1, 0,
                              None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED
-    for nh, nl in ((5, 1), (6, 1), (1, 5)):
+    for nh, nl in ((6, 1), (1, 6), (6, 6)):
         rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, nh, nl, 0,
                              None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED and b"all-pairs" in lib.ozk_last_error()

@@ -242,10 +242,12 @@ def test_extract_i8_rejects_coarse_grid(ll):
 # ---------------------------------------------------------------- products
 
 # (2, 3), (1, 2), (2, 1), (1, 1): one-sweep custom schedules on the
-# all-pairs kernel; (4, 2): two sweeps of it; (5, 1): the pairwise kernel
+# all-pairs kernel; (4, 2), (1, 5): two sweeps of it; (5, 1): three;
+# (6, 1) and the host schedule: the pairwise kernel
 SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
              ("ondevice", 2, 3), ("ondevice", 1, 2), ("ondevice", 2, 1),
-             ("ondevice", 1, 1), ("ondevice", 4, 2), ("ondevice", 5, 1), ("host", 8, 0)]
+             ("ondevice", 1, 1), ("ondevice", 4, 2), ("ondevice", 5, 1), ("ondevice", 1, 5),
+             ("ondevice", 6, 1), ("host", 8, 0)]
 
 
 def _slices(ll, A, B, pipe, nh, nl):
@@ -296,7 +298,7 @@ def _slices_i8(ll, A, B, nh, nl, rho_fixed):
 
 
 @pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 2), (1, 4), (3, 2), (1, 1), (4, 2),
-                                   (3, 3)])
+                                   (3, 3), (5, 1), (1, 5), (5, 5), (3, 4)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
@@ -310,7 +312,7 @@ def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
 
 
 @pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 2), (1, 4), (3, 2), (1, 1), (4, 2),
-                                   (3, 3)])
+                                   (3, 3), (5, 1), (1, 5), (5, 5), (3, 4)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_gemm_i8_orders_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
@@ -351,7 +353,8 @@ def test_gemm_orders_bit_exact(ll, pipe, nh, nl, shape):
 
 @pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (2, 2), (1, 1), (1, 2),
                                        (1, 4), (2, 1), (2, 3), (3, 2), (3, 3), (2, 4), (4, 4),
-                                       (5, 1)])
+                                       (5, 1), (5, 2), (5, 3), (5, 5), (4, 3), (4, 5), (3, 4),
+                                       (3, 5), (2, 5), (1, 5), (6, 1)])
 @pytest.mark.parametrize("accumulation", ["fused", "bf16_interleaved", "ondevice", "host"])
 def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
     A, B = gen("randn", (150, 300), 21), gen("randn", (300, 90), 22)
@@ -370,11 +373,12 @@ def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
 
 @pytest.mark.parametrize("precision", ["high", "medium", "max", (1, 1), (1, 2), (1, 3), (2, 1),
                                        (2, 2), (2, 3), (3, 2), (3, 3), (4, 2), (2, 4), (4, 4),
-                                       (5, 1)])
+                                       (5, 1), (5, 2), (5, 3), (5, 5), (4, 3), (4, 5), (3, 4),
+                                       (3, 5), (2, 5), (1, 5), (6, 1)])
 def test_matmul_long_contraction_bit_exact(ozk, precision):
-    # K > 4096: rho >= 19, the presets and the custom schedules of the
-    # all-pairs kernel run on INT8 planes ((4, 2), (3, 3) and (2, 4) in two
-    # sweeps, (4, 4) in three); (5, 1) on BF16 planes in the pairwise kernel
+    # K > 4096: rho >= 19, every schedule with both counts in 1 .. 5 runs on
+    # INT8 planes in the all-pairs kernel (one, two or three sweeps); (6, 1)
+    # on BF16 planes in the pairwise kernel
     A, B = gen("randn", (40, 6000), 23), gen("wide2", (6000, 70), 24)
     nh, nl = OP.resolve_precision(precision)
     for acc, ref in [("fused", lambda: O.matmul_ondevice_a4(A, B, "raise", nh, nl)),
@@ -400,7 +404,7 @@ def test_matmul_operand_strides_bit_exact(ozk, K, aligned):
     o = 0 if aligned else 1
     At, Bt = Abig[:, o:o + K], Bbig[:, o:o + M]
     A, B = At.cpu().numpy(), Bt.cpu().numpy()
-    for precision in ("high", "medium", (5, 1)):
+    for precision in ("high", "medium", (5, 1), (6, 1)):
         nh, nl = OP.resolve_precision(precision)
         case(f"matmul strided views ({N},{K},{M}) aligned={aligned} {precision}")
         C = ozk.matmul(At, Bt, pipeline="ondevice", precision=precision)
