@@ -244,13 +244,16 @@ __device__ __forceinline__ int frag_lane(int lane) {
 // blocks of accumulators (at most 16 pairs) and its stage buffer (2 RB
 // fragments of 1 KiB per A plane, 4 per B plane) the 40 KiB slot of the
 // four-stage ring: fewer staged bytes per MFMA.  Square 64-row tiles for the
-// symmetric (gram) form and the multi-sweep schedules.
+// symmetric (gram) form.  The sweeps of one schedule may differ (the fold
+// state between them is kept per element, whatever the tiles).
 constexpr int ap_rb(int nhi, int nlo, int b0, int b1, bool sym) {
   const int na = (b1 == 2 ? nhi + nlo : nhi) - (b0 == 2 ? nhi : 0);
   const int bb = (b0 == 1 && b1 == 1) ? nhi : 0;
   const int nb = ((b0 <= 1 && b1 >= 1) ? nhi + nlo : nhi) - bb;
-  const int np = nhi * nhi + 2 * nhi * nlo;
-  return (!sym && b0 == 0 && b1 == 2 && np <= 16 && 6 * na + 4 * nb <= 40) ? 3 : 2;
+  const int p0 = b0 == 0 ? 0 : (b0 == 1 ? nhi * nhi : nhi * nhi + nhi * nlo);
+  const int p1 = b1 == 0 ? nhi * nhi
+                         : (b1 == 1 ? nhi * nhi + nhi * nlo : nhi * nhi + 2 * nhi * nlo);
+  return (!sym && p1 - p0 <= 16 && 6 * na + 4 * nb <= 40) ? 3 : 2;
 }
 
 template <int PIPE, int NHI, int NLO, int B0, int B1, bool SYM = false>
@@ -1083,6 +1086,27 @@ constexpr bool allpairs_preset(int nhi, int nlo) {
 }
 
 
+// Dynamic tail (gemm_allpairs): with R = ntiles / cus whole rounds, the
+// last ceil(R / kDynDiv) of them are handed out at run time from one counter
+// per XCD and sweep (kDynBytes, zeroed before the launch).  Needs at least
+// kDynMinRounds rounds and kDynMinStages stages per tile, so that a claim
+// made when a tile starts is known before the ring fetches the next tile.
+constexpr int kDynDiv = 8, kDynMinRounds = 4, kDynMinStages = 8;
+constexpr size_t kDynBytes = (kDynSlot0 + kDynMaxGrid) * sizeof(uint32_t);
+
+static int dyn_static_rounds(int64_t ntiles, int grid, int64_t nst) {
+  const int64_t R = ntiles / grid;
+  if (grid % kXcds != 0 || grid > kDynMaxGrid || R < kDynMinRounds || nst < kDynMinStages)
+    return 0;
+  return (int)(R - (R + kDynDiv - 1) / kDynDiv);
+}
+
+// Tiles of an all-pairs sweep with tm-row tiles.
+static int64_t allpairs_ntiles(int64_t N, int64_t M, bool sym, int tm) {
+  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
+  return sym ? (al / kBM) * (al / kBM + 1) / 2 : ((al + tm - 1) / tm) * (bl / kBN);
+}
+
 struct ApArgs {
   dim3 grid;
   bool sym;
@@ -1091,7 +1115,7 @@ struct ApArgs {
   int64_t tail_T;
   uint32_t* part;
   uint32_t* dyn;  // dynamic-tail counters: kXcds per sweep, or null
-  int dyn_nstat;
+  int cus;        // the GPU's compute units
   hipStream_t st;
   const char *As, *Bs;
   const int32_t *Ae, *Be;
@@ -1105,14 +1129,26 @@ struct ApArgs {
   I8Fix fix;
 };
 
+// One sweep.  Its grid (one workgroup per CU, at most one per tile) and
+// dynamic tail follow its own tile rows; a K-split tail (single sweeps
+// only) keeps the grid the tail plan chose.
 template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
 static void launch_sweep(const ApArgs& a) {
+  typedef Sweep<OZK_PIPE_ONDEVICE, NHI, NLO, B0, B1, SYM> SW;
   const bool split = a.tail_P > 1 && B0 == 0 && B1 == 2;
+  dim3 grid = a.grid;
+  uint32_t* dyn = nullptr;
+  int nstat = 0;
+  if (!split) {
+    const int64_t nt = allpairs_ntiles(a.N, a.M, SYM, SW::TM);
+    grid = dim3((unsigned)(nt < a.cus ? nt : a.cus));
+    nstat = a.dyn ? dyn_static_rounds(nt, (int)grid.x, a.nst) : 0;
+    if (nstat > 0) dyn = a.dyn + kXcds * B0;
+  }
   hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
-                     a.grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
+                     grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
                      a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
-                     split ? a.tail_P : 0, a.part, a.fix,
-                     a.dyn ? a.dyn + kXcds * B0 : nullptr, a.dyn_nstat);
+                     split ? a.tail_P : 0, a.part, a.fix, dyn, nstat);
   if constexpr (B0 == 0 && B1 == 2) {
     if (split)
       hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
@@ -1243,21 +1279,6 @@ static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np, int rb) 
   return tp;
 }
 
-// Dynamic tail (gemm_allpairs): with R = ntiles / cus whole rounds, the
-// last ceil(R / kDynDiv) of them are handed out at run time from one counter
-// per XCD and sweep (kDynBytes, zeroed before the launch).  Needs at least
-// kDynMinRounds rounds and kDynMinStages stages per tile, so that a claim
-// made when a tile starts is known before the ring fetches the next tile.
-constexpr int kDynDiv = 8, kDynMinRounds = 4, kDynMinStages = 8;
-constexpr size_t kDynBytes = (kDynSlot0 + kDynMaxGrid) * sizeof(uint32_t);
-
-static int dyn_static_rounds(int64_t ntiles, int grid, int64_t nst) {
-  const int64_t R = ntiles / grid;
-  if (grid % kXcds != 0 || grid > kDynMaxGrid || R < kDynMinRounds || nst < kDynMinStages)
-    return 0;
-  return (int)(R - (R + kDynDiv - 1) / kDynDiv);
-}
-
 // Workspace of the fastest all-pairs launch: the fold state, then the
 // dynamic-tail words.  (The K-split tail's partial sums, gemm_tail_bytes,
 // follow them where a driver reserves those too.)
@@ -1268,14 +1289,11 @@ size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
          kDynBytes;
 }
 
-// Tile rows of a single-sweep all-pairs launch of schedule (nhi, nlo).
+// Tile rows of the all-pairs launch of schedule (nhi, nlo): those of its
+// single sweep; 64 for a multi-sweep schedule, whose sweeps size their own
+// grids (64-row tiles give the most tiles, the bound the launch checks).
 static int allpairs_tm(int nhi, int nlo, bool sym) {
   return 32 * (allpairs_sweeps(nhi, nlo) == 1 ? ap_rb(nhi, nlo, 0, 2, sym) : 2);
-}
-
-static int64_t allpairs_ntiles(int64_t N, int64_t M, bool sym, int tm) {
-  const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
-  return sym ? (al / kBM) * (al / kBM + 1) / 2 : ((al + tm - 1) / tm) * (bl / kBN);
 }
 
 static int64_t allpairs_nst(int64_t K, bool i8) {
@@ -1328,7 +1346,7 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.tail_T = 0;
   a.part = nullptr;
   a.dyn = nullptr;
-  a.dyn_nstat = 0;
+  a.cus = cus;
   // workspace: fold state | dynamic-tail words | K-split partial sums
   const size_t off = round_up((int64_t)need, 256);
   if (allpairs_sweeps(nhi, nlo) == 1) {
@@ -1342,13 +1360,13 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
       a.part = (uint32_t*)((char*)state + off + kDynBytes);
     }
   }
-  if (!a.part && state && state_bytes >= off + kDynBytes) {
-    const int ns = dyn_static_rounds(ntiles, (int)a.grid.x, allpairs_nst(K, i8));
-    if (ns > 0) {
-      a.dyn = (uint32_t*)((char*)state + off);
-      a.dyn_nstat = ns;
-      hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, st, a.dyn, kDynSlot0);
-    }
+  // the dynamic tail's counters, when some sweep will use them (each sweep
+  // decides for its own tiles in launch_sweep)
+  if (!a.part && state && state_bytes >= off + kDynBytes &&
+      (allpairs_sweeps(nhi, nlo) > 1 ||
+       dyn_static_rounds(ntiles, (int)a.grid.x, allpairs_nst(K, i8)) > 0)) {
+    a.dyn = (uint32_t*)((char*)state + off);
+    hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, st, a.dyn, kDynSlot0);
   }
   a.sym = sym;
   a.st = st;
