@@ -1068,9 +1068,9 @@ constexpr int kRowRun = kRowThreads * kRowEPT * kRowVEC;  // 16384 elements
 constexpr int kRowMaxMembers = 16;
 constexpr int64_t kRowRecBytes = 8 * kRowMaxMembers;  // two keys per member
 
-// INT8: `part` receives member m's sum of q per plane pl at
-// part[(pl G + m) eplane + line] (added up by i8_sum_parts): the packed bytes
-// of its run, less offset x kRowRun, as in extract_lines_reg.
+// INT8: every member adds its run's sums of q per plane into
+// sums[pl eplane + line] (zeroed before the launch): the packed bytes of its
+// run, less offset x kRowRun, as in extract_lines_reg.
 template <int FMT, bool VEC>
 __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
     const double* __restrict__ X, int64_t lines, int64_t len, int64_t ldx, int rho, int n0,
@@ -1078,7 +1078,7 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
     typename PlaneElem<FMT>::type* __restrict__ S, int64_t ld, int64_t plane,
     int32_t* __restrict__ E, int64_t eplane, uint32_t* __restrict__ flags,
     uint32_t* __restrict__ rec, uint32_t* __restrict__ ticket, int G, uint32_t wait_ticks,
-    int32_t* __restrict__ part) {
+    int32_t* __restrict__ sums) {
   typedef typename PlaneElem<FMT>::type T;
   typedef typename PlaneVec<FMT, kRowVEC>::type TV;
   constexpr int NP = 2, EPT = kRowEPT, V = kRowVEC;
@@ -1213,8 +1213,8 @@ __global__ __launch_bounds__(kRowThreads) void extract_lines_gang(
   }
   if constexpr (FMT == kFmtI8) {
     __syncthreads();
-    if (t < n0 + n1)
-      part[((int64_t)t * G + member) * eplane + line] = ssum[t] - i8_offset(rho) * kRowRun;
+    if (t < n0 + n1 && live)
+      atomicAdd(&sums[(int64_t)t * eplane + line], ssum[t] - i8_offset(rho) * kRowRun);
   }
 }
 
@@ -1293,20 +1293,6 @@ __global__ void check_finite_kernel(const double* __restrict__ X, int64_t rows,
 
 __global__ void fill_u32_kernel(uint32_t* p, uint32_t v) { *p = v; }
 
-// INT8 line sums from the gangs' partial sums: sums[pl eplane + l] =
-// sum over members m of part[(pl G + m) eplane + l] for lines l < valid
-// (0 for the padding lines, which a row gang does not visit).
-__global__ void i8_sum_parts_kernel(const int32_t* __restrict__ part, int G, int planes,
-                                    int64_t eplane, int64_t valid, int32_t* __restrict__ sums) {
-  const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (i >= planes * eplane) return;
-  const int64_t pl = i / eplane, l = i - pl * eplane;
-  int v = 0;
-  if (l < valid)
-    for (int m = 0; m < G; ++m) v += part[(pl * G + m) * eplane + l];
-  sums[i] = v;
-}
-
 // INT8 line sums read back from stored planes (the streaming path): 64
 // lines per workgroup, four threads per line, each summing one 16-byte unit
 // of every chunk; the stored values are q + off.
@@ -1330,15 +1316,6 @@ __global__ __launch_bounds__(256) void i8_plane_sums_kernel(const int8_t* __rest
   if (t % 4 == 0) sums[pl * lp + line] = v - (int)ld * off;
 }
 
-static int launch_sum_parts(const int32_t* part, int G, int planes, int64_t eplane,
-                            int64_t valid, int32_t* sums, hipStream_t st) {
-  const int64_t n = planes * eplane;
-  hipLaunchKernelGGL(i8_sum_parts_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), 0, st,
-                     part, G, planes, eplane, valid, sums);
-  OZK_LAUNCH_CHECK();
-  return OZK_OK;
-}
-
 // ---------------------------------------------------------------- launchers
 
 // FP32 lines longer than one workgroup holds and at most
@@ -1348,15 +1325,9 @@ static bool gang_rows(int64_t len) {
   return ld > 32768 && ld <= (int64_t)kRowRun * kRowMaxMembers && gangs_enabled();
 }
 
-// Ticket and exchange records (zeroed per launch), then the INT8 partial
-// line sums (2 nslices planes x G members x padded lines).
-static size_t row_gang_records(int64_t lines, int nslices) {
+// Ticket and exchange records (zeroed per launch).
+static size_t row_gang_bytes(int64_t lines, int64_t, int nslices) {
   return (size_t)round_up(kGangHeader + round_up(lines, kLinePad) * nslices * kRowRecBytes, 256);
-}
-static size_t row_gang_bytes(int64_t lines, int64_t len, int nslices) {
-  const int64_t G = (round_up(len, kKPad) + kRowRun - 1) / kRowRun;
-  return row_gang_records(lines, nslices) +
-         (size_t)(2 * nslices * G * round_up(lines, kLinePad)) * sizeof(int32_t);
 }
 
 template <int FMT>
@@ -1373,28 +1344,31 @@ static int launch_rows_gang(const double* X, int64_t lines, int64_t len, int64_t
   const int64_t ld = round_up(len, kKPad), lp = round_up(lines, kLinePad);
   const int64_t plane = lp * ld;
   const int G = (int)((ld + kRowRun - 1) / kRowRun);
-  // the ticket and the exchange records start at zero
-  const size_t recb = row_gang_records(lines, ns);
-  const int64_t n16 = (int64_t)recb / 16;
+  // the ticket, the exchange records and the INT8 line sums start at zero
+  const int64_t n16 = (int64_t)need / 16;
   hipLaunchKernelGGL(zero_u32x4_kernel,
                      dim3((unsigned)((n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024)),
                      dim3(256), 0, st, (uint4*)ws, n16);
   OZK_LAUNCH_CHECK();
+  if constexpr (FMT == kFmtI8) {
+    const int64_t ns32 = (int64_t)(n0 + n1) * lp;
+    hipLaunchKernelGGL(zero_i32_kernel, dim3((unsigned)((ns32 + 255) / 256 < 1024 ? (ns32 + 255) / 256 : 1024)),
+                       dim3(256), 0, st, Sg, ns32);
+    OZK_LAUNCH_CHECK();
+  }
   uint32_t* ticket = (uint32_t*)ws;
   uint32_t* rec = (uint32_t*)((char*)ws + kGangHeader);
-  int32_t* part = (int32_t*)((char*)ws + recb);
   const dim3 grid((unsigned)(lp * G));
   const uint32_t wait_ticks = wait_polls(kGangWaitTicks);
   if (((uintptr_t)X % 16 == 0) && (ldx % 2 == 0))
     hipLaunchKernelGGL((extract_lines_gang<FMT, true>), grid, dim3(kRowThreads), 0, st, X,
                        lines, len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, wait_ticks, part);
+                       ticket, G, wait_ticks, Sg);
   else
     hipLaunchKernelGGL((extract_lines_gang<FMT, false>), grid, dim3(kRowThreads), 0, st, X,
                        lines, len, ldx, rho, n0, n1, (T*)Sv, ld, plane, E, lp, flags, rec,
-                       ticket, G, wait_ticks, part);
+                       ticket, G, wait_ticks, Sg);
   OZK_LAUNCH_CHECK();
-  if constexpr (FMT == kFmtI8) return launch_sum_parts(part, G, n0 + n1, lp, lp, Sg, st);
   return OZK_OK;
 }
 

@@ -86,11 +86,10 @@ def gang_bytes(rows, cols):
 def row_gang_bytes(lines, length):
     """FP32 lines of 32769 to 262144 elements: the ticket word and, per
     (line, slice) for up to 32 slices, one 128-byte exchange record
-    (256-byte aligned), then the INT8 line sums of each 16384-element run:
-    64 planes x runs x padded lines."""
-    G = -(-(-(-length // 64) * 64) // 16384)
+    (256-byte aligned).  The members add their INT8 line sums into the plane
+    sums directly."""
     lp = -(-lines // 64) * 64
-    return r256(256 + lp * 32 * 128) + 64 * G * lp * 4
+    return r256(256 + lp * 32 * 128)
 
 
 def test_workspace_sizes(lib):

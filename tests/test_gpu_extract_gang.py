@@ -153,6 +153,39 @@ def test_panel_f32_candidates_missed(ll, length, kind):
         check_padding(pl, length, 40)
 
 
+@pytest.mark.parametrize("length", [40000, 65536])
+@pytest.mark.parametrize("kind", ["wide", "integers", "spiky", "binade"])
+def test_row_gang_rounds(ll, length, kind):
+    """Rows of 32769 to 262144 elements, held by gangs of 16384-element runs
+    that settle one slice per exchange round: wide-range rows, rows whose
+    residuals vanish (integers), one large element among tiny ones (spiky),
+    every element in [1, 2) (binade), and a zero row; both plane formats,
+    bit-exact, with the members' INT8 line sums added up."""
+    rng = np.random.RandomState(length + 7 * len(kind))
+    shape = (13, length)
+    if kind == "wide":
+        X = gen("wide", shape, length)
+    elif kind == "integers":
+        X = rng.randint(-300, 300, size=shape).astype(np.float64)
+    elif kind == "spiky":
+        X = rng.randn(*shape) * 1e-6
+        X[np.arange(13), rng.randint(0, length, 13)] = 1e3
+    else:
+        X = 1.0 + rng.rand(*shape)
+    X[4] = 0.0
+    hi, lo = O.split_hi_lo(X)
+    for i8 in (False, True):
+        rho = max(19, O.rho_f32(length)) if i8 else O.rho_f32(length)
+        case(f"ozk_extract_f32 row gang {kind} (13, {length}) i8={i8} rho={rho}")
+        pl = ll.extract(X, 0, rho, 4, 1, i8=i8)
+        sh, eh = O.extract_rows_f32(hi, rho, 4)
+        sl, el = O.extract_rows_f32(lo, rho, 1)
+        assert np.array_equal(to_np(pl.values()), np.concatenate([sh, sl])), "slices"
+        assert np.array_equal(to_np(pl.exponents()),
+                              np.concatenate([eh, el]).astype(np.int32)), "exponents"
+        check_padding(pl, length, 13)
+
+
 @pytest.mark.parametrize("length", [1024, 2049, 4097, 8192])
 def test_panel_f64(ll, length):
     X = gen("wide", (length, 35), 11 + length)
