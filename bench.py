@@ -58,7 +58,8 @@ def parse_args():
                          "kernel) to calibrate HBM byte counters")
     ap.add_argument("--suite", action="store_true",
                     help="instead of the metric line, time every workload "
-                         "configuration (host 256, 4096 high, 8192 medium/max "
+                         "configuration (host 256 and 4096x1024x4096, 4096 high, "
+                         "8192 medium/max "
                          "wide range, custom schedules 8192, gram / residual "
                          "32768x2048, residual 8192^2 and 4096^2 x 4, long K, "
                          "solve) and print one JSON line each")
@@ -225,6 +226,39 @@ def suite(args):
         del At, Bt, C
         return d
 
+    # the host pipeline (FP64 extraction, 8 slices, 36 pairs on BF16 planes,
+    # order A2) on device tensors: 4096 x 1024 x 4096, N(0,1)
+    if want("host"):
+        rs = np.random.RandomState(0)
+        A, B = rs.randn(4096, 1024), rs.randn(1024, 4096)
+        At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
+        name = "matmul host n_slices=8 4096x1024x4096 N(0,1)"
+        log(f"suite: {name}")
+        # the call returns NumPy (as the reference's host pipeline does), so
+        # it includes C's copy to the host; the device part is timed from the
+        # extractions and the GEMM of the library's entry points
+        from ozaki_jax_amd import lowlevel as ll
+        t = _timeit(lambda: ozk.matmul(At, Bt, n_slices=8), 5, sync)
+        rho = ozk.rho_f64(1024)
+
+        def device_part():
+            pa = ll.extract(At, 0, rho, 8, f64=True)
+            pb = ll.extract(Bt, 1, rho, 8, f64=True)
+            return ll.gemm(pa, pb, ll.PIPE_HOST, 8, 0, ll.ORDER_HOST_JAX)
+        t_dev = _timeit(device_part, 5, sync)
+        rows = np.array([0, 2047, 4095])
+        Cr = ozk.matmul(At, Bt, n_slices=8)[rows]
+        ref = OP.matmul_host_a2(A[rows], B, n_slices=8)
+        t_dg = _timeit(lambda: torch.matmul(At, Bt), 3, sync)
+        flops = 2.0 * 4096 * 1024 * 4096
+        emit({"config": name, "ms": t * 1e3, "device_ms": t_dev * 1e3,
+              "fp64_eq_tflops_device": flops / t_dev / 1e12, "slice_format": "bf16",
+              "pair_rate_frac_of_mfma_peak": 36 * flops / t_dev / 1e12 / PEAK_BF16_TFLOPS,
+              "rocblas_dgemm_ms": t_dg * 1e3,
+              "max_scaled_err_vs_oracle": scaled_err(Cr, ref, A[rows], B),
+              "max_scaled_err_vs_fp64": scaled_err(Cr, A[rows] @ B, A[rows], B),
+              "rows_checked": len(rows)})
+        del At, Bt
     # 1: 4096^3 high, N(0,1)
     if want("4096"):
         rs = np.random.RandomState(0)

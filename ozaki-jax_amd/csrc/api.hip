@@ -447,9 +447,13 @@ static size_t matmul_ws(int64_t N, int64_t K, int64_t M, int pipeline, int nhi,
   SliceSet sa = carve_slices(c, planes, N, K, eb);
   SliceSet sb = carve_slices(c, planes, M, K, eb);
   void* t = c.take(extract_pair_bytes(N, K, M, pipeline != OZK_PIPE_ONDEVICE));
-  // fold state between sweeps (the 2Sum state bounds every order's), then
-  // the partial sums of a K-split tail
-  const size_t gb = round_up(gemm_workspace_bytes(N, M, pipeline, nhi, nlo, OZK_ORDER_2SUM),
+  // fold state between sweeps (on device the 2Sum state bounds every
+  // order's; the host pipeline's FP64 orders keep one running sum), then the
+  // partial sums of a K-split tail
+  const size_t gb = round_up(gemm_workspace_bytes(N, M, pipeline, nhi, nlo,
+                                                  pipeline == OZK_PIPE_ONDEVICE
+                                                      ? OZK_ORDER_2SUM
+                                                      : OZK_ORDER_HOST_JAX),
                              256) +
                     gemm_tail_bytes(N, M, K, pipeline, nhi, nlo, false, eb == 1);
   void* g = c.take(gb);

@@ -42,12 +42,13 @@ __host__ __device__ constexpr PairInfo pair_info(int pipe, int nhi, int nlo,
       r = PairInfo{nhi + i, j, 2, j == 0, j == nhi - 1, q == 0, q == hl - 1, i == 0};
     }
   } else {
+    // group i holds the pairs from i n - i (i - 1) / 2 on: count the group
+    // starts at or below p (a loop of n - 1 steps, which folds away when n
+    // and p are known at compile time)
     const int n = nhi;
-    int q = p, i = 0;
-    while (q >= n - i) {
-      q -= n - i;
-      ++i;
-    }
+    int i = 0;
+    for (int t = 1; t < n; ++t) i += p >= t * n - t * (t - 1) / 2 ? 1 : 0;
+    const int q = p - (i * n - i * (i - 1) / 2);
     const int np = n * (n + 1) / 2;
     r = PairInfo{i, q, 0, q == 0, q == n - 1 - i, p == 0, p == np - 1, i == 0};
   }

@@ -246,6 +246,9 @@ __device__ __forceinline__ int frag_lane(int lane) {
 // four-stage ring: fewer staged bytes per MFMA.  Square 64-row tiles for the
 // symmetric (gram) form.  The sweeps of one schedule may differ (the fold
 // state between them is kept per element, whatever the tiles).
+constexpr int ap_rb_of(int np, int na, int nb, bool sym) {
+  return (!sym && np <= 16 && 6 * na + 4 * nb <= 40) ? 3 : 2;
+}
 constexpr int ap_rb(int nhi, int nlo, int b0, int b1, bool sym) {
   const int na = (b1 == 2 ? nhi + nlo : nhi) - (b0 == 2 ? nhi : 0);
   const int bb = (b0 == 1 && b1 == 1) ? nhi : 0;
@@ -253,12 +256,18 @@ constexpr int ap_rb(int nhi, int nlo, int b0, int b1, bool sym) {
   const int p0 = b0 == 0 ? 0 : (b0 == 1 ? nhi * nhi : nhi * nhi + nhi * nlo);
   const int p1 = b1 == 0 ? nhi * nhi
                          : (b1 == 1 ? nhi * nhi + nhi * nlo : nhi * nhi + 2 * nhi * nlo);
-  return (!sym && p1 - p0 <= 16 && 6 * na + 4 * nb <= 40) ? 3 : 2;
+  return ap_rb_of(p1 - p0, na, nb, sym);
 }
 
+// Besides the planes and pairs, a sweep says whether it starts the schedule
+// (kFirst: no fold state to load) and ends it (kLast: C is written, not the
+// state), how many blocks the schedule folds (kNBlk) and, for the 2Sum
+// state, the blocks folded before and after it (kDone0, kDone1).
 template <int PIPE, int NHI, int NLO, int B0, int B1, bool SYM = false>
 struct Sweep {
   static_assert(PIPE == OZK_PIPE_ONDEVICE, "sweeps cover the on-device schedule");
+  static constexpr bool kFirst = B0 == 0, kLast = B1 == 2;
+  static constexpr int kNBlk = 3, kDone0 = B0, kDone1 = B1 + 1;
   static constexpr int A0 = B0 == 2 ? NHI : 0;                    // first A plane
   static constexpr int NA = (B1 == 2 ? NHI + NLO : NHI) - A0;     // A planes
   static constexpr int BB = (B0 == 1 && B1 == 1) ? NHI : 0;       // first B plane
@@ -283,6 +292,45 @@ struct Sweep {
     return -1;
   }
 };
+
+// A sweep of the host schedule (pairs (i, j), i + j <= N - 1, i-major) over
+// its groups G0..G1 (A planes G0..G1): B planes 0 .. N - 1 - G0, the planes
+// of the first group's pairs.  The FP64 orders fold the products of a group
+// into one running sum, so the sweeps, which cut between groups, carry that
+// sum alone.
+template <int N, int G0, int G1>
+struct Sweep<OZK_PIPE_HOST, N, 0, G0, G1, false> {
+  static constexpr bool kFirst = G0 == 0, kLast = G1 == N - 1;
+  static constexpr int kNBlk = 1, kDone0 = 0, kDone1 = 0;
+  static constexpr int A0 = G0, NA = G1 - G0 + 1, BB = 0, NB = N - G0;
+  static constexpr int P0 = G0 * N - G0 * (G0 - 1) / 2;
+  static constexpr int P1 = (G1 + 1) * N - G1 * (G1 + 1) / 2;
+  static constexpr int NP = P1 - P0;
+  static constexpr int S = NA + NB;
+  static constexpr int RB = ap_rb_of(NP, NA, NB, false);
+  static constexpr int TM = 32 * RB;
+  static constexpr int FA = 2 * RB;
+  static constexpr int NFRAG = NA * FA + NB * 4;
+  static constexpr PairInfo pair(int k) { return pair_info(OZK_PIPE_HOST, N, 0, P0 + k); }
+  static constexpr int la(int k) { return pair(k).a - A0; }
+  static constexpr int lb(int k) { return pair(k).b - BB; }
+  static constexpr int tpair(int) { return -1; }
+};
+
+// Last group of the host sweep that starts at group g0: as many groups as
+// keep the sweep within 10 planes and 25 pairs.
+constexpr int host_sweep_end(int n, int g0) {
+  int g1 = g0;
+  while (g1 + 1 < n && (g1 + 2 - g0) + (n - g0) <= 10 &&
+         ((g1 + 2) * n - (g1 + 1) * (g1 + 2) / 2) - (g0 * n - g0 * (g0 - 1) / 2) <= 25)
+    ++g1;
+  return g1;
+}
+constexpr int host_nsweeps(int n) {
+  int k = 0;
+  for (int g = 0; g < n; g = host_sweep_end(n, g) + 1) ++k;
+  return k;
+}
 
 template <class Op, class SW>
 struct AllPairsMMA {
@@ -532,7 +580,7 @@ __device__ __forceinline__ void tile_epilogue(
     double* __restrict__ C, int64_t ldc, float* __restrict__ P, int64_t ldp,
     char* __restrict__ state) {
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP, RB = SW::RB;
-  constexpr int NBLK = 3;
+  constexpr int NBLK = SW::kNBlk;
   const int64_t row0 = (int64_t)tm * SW::TM, col0 = (int64_t)tn * kBN;
 
   // Accumulator register r of lane l of a 16x16 block holds row
@@ -577,10 +625,10 @@ __device__ __forceinline__ void tile_epilogue(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         fr[r].init();
-        if constexpr (B0 > 0) {
+        if constexpr (!SW::kFirst) {
           const int64_t row = rbase + 16 * h + r;
           if (row < N && col < M)
-            FoldState<ORDER>::template load<B0>(fr[r], state, row * M + col, nm);
+            FoldState<ORDER>::template load<SW::kDone0>(fr[r], state, row * M + col, nm);
         }
       }
       // One wait for all of them here: the folds below sit in branches on
@@ -622,8 +670,8 @@ __device__ __forceinline__ void tile_epilogue(
             C[row * ldc + col] = out;
             if (tm != tn) C[col * ldc + row] = out;
           }
-        } else if constexpr (B1 < NBLK - 1) {
-          if (live) FoldState<ORDER>::template store<B1 + 1>(f, state, row * M + col, nm);
+        } else if constexpr (!SW::kLast) {
+          if (live) FoldState<ORDER>::template store<SW::kDone1>(f, state, row * M + col, nm);
         } else if constexpr (ORDER == kOrderPair) {
           float hi, lo;
           f.finish_pair(NBLK, hi, lo);
@@ -1132,10 +1180,10 @@ struct ApArgs {
 // One sweep.  Its grid (one workgroup per CU, at most one per tile) and
 // dynamic tail follow its own tile rows; a K-split tail (single sweeps
 // only) keeps the grid the tail plan chose.
-template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
-static void launch_sweep(const ApArgs& a) {
-  typedef Sweep<OZK_PIPE_ONDEVICE, NHI, NLO, B0, B1, SYM> SW;
-  const bool split = a.tail_P > 1 && B0 == 0 && B1 == 2;
+template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
+static void launch_sweep_of(const ApArgs& a) {
+  typedef Sweep<PIPE, NHI, NLO, B0, B1, SYM> SW;
+  const bool split = a.tail_P > 1 && SW::kFirst && SW::kLast;
   dim3 grid = a.grid;
   uint32_t* dyn = nullptr;
   int nstat = 0;
@@ -1145,16 +1193,43 @@ static void launch_sweep(const ApArgs& a) {
     nstat = a.dyn ? dyn_static_rounds(nt, (int)grid.x, a.nst) : 0;
     if (nstat > 0) dyn = a.dyn + kXcds * B0;
   }
-  hipLaunchKernelGGL((gemm_allpairs<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
+  hipLaunchKernelGGL((gemm_allpairs<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>),
                      grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
                      a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
                      split ? a.tail_P : 0, a.part, a.fix, dyn, nstat);
-  if constexpr (B0 == 0 && B1 == 2) {
+  if constexpr (SW::kFirst && SW::kLast) {
     if (split)
-      hipLaunchKernelGGL((gemm_tail_fixup<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>),
+      hipLaunchKernelGGL((gemm_tail_fixup<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>),
                          dim3((unsigned)(a.tail_T * 8)), dim3(kThreads16), 0, a.st, a.part, a.tail_P,
                          a.tile0, a.Ae, a.Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P,
                          a.ldp, a.state, a.fix);
+  }
+}
+
+template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
+static void launch_sweep(const ApArgs& a) {
+  launch_sweep_of<Op, OZK_PIPE_ONDEVICE, NHI, NLO, ORDER, B0, B1, SYM>(a);
+}
+
+// The host schedule's sweeps from group G0 on (host_sweep_end).
+template <int N, int ORDER, int G0>
+static void launch_host_sweeps(const ApArgs& a) {
+  if constexpr (G0 < N) {
+    constexpr int G1 = host_sweep_end(N, G0);
+    launch_sweep_of<OpBf16, OZK_PIPE_HOST, N, 0, ORDER, G0, G1>(a);
+    launch_host_sweeps<N, ORDER, G1 + 1>(a);
+  }
+}
+
+// The host schedule on BF16 planes in the FP64 orders (and the per-product
+// form of the test hook).
+template <int N>
+static void launch_host_order(int order, const ApArgs& a) {
+  switch (order) {
+    case OZK_ORDER_BLOCK64: launch_host_sweeps<N, OZK_ORDER_BLOCK64, 0>(a); break;
+    case OZK_ORDER_HOST_JAX: launch_host_sweeps<N, OZK_ORDER_HOST_JAX, 0>(a); break;
+    case OZK_ORDER_HOST_NP: launch_host_sweeps<N, OZK_ORDER_HOST_NP, 0>(a); break;
+    default: launch_host_sweeps<N, kOrderProducts, 0>(a); break;
   }
 }
 
@@ -1199,7 +1274,23 @@ static void launch_ap_order(int order, const ApArgs& a) {
 }
 
 
-#ifdef OZK_GEMM_PART
+#if defined(OZK_GEMM_PART_HOST)
+// The host schedules with 1 .. 8 slices (BF16 planes): false for any
+// other count.
+bool launch_ap_host(int n, int order, const ApArgs& a) {
+  switch (n) {
+    case 1: launch_host_order<1>(order, a); return true;
+    case 2: launch_host_order<2>(order, a); return true;
+    case 3: launch_host_order<3>(order, a); return true;
+    case 4: launch_host_order<4>(order, a); return true;
+    case 5: launch_host_order<5>(order, a); return true;
+    case 6: launch_host_order<6>(order, a); return true;
+    case 7: launch_host_order<7>(order, a); return true;
+    case 8: launch_host_order<8>(order, a); return true;
+    default: return false;
+  }
+}
+#elif defined(OZK_GEMM_PART)
 // A part of the schedules' instantiations, compiled as a translation unit
 // of its own so that the parts build in parallel: OZK_GEMM_PART_TUPLES(X)
 // names its (n_hi, n_lo).  Returns false for a schedule of another part.
@@ -1219,19 +1310,31 @@ bool launch_ap_part1(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 bool launch_ap_part2(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 bool launch_ap_part3(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 bool launch_ap_part4(bool i8, int nhi, int nlo, int order, const ApArgs& a);
+bool launch_ap_host(int n, int order, const ApArgs& a);
+
+// Host schedules (FP64 extraction, BF16 planes) of up to this many slices
+// run on the all-pairs kernel, in sweeps over groups of A planes.
+constexpr int kHostMaxSlices = 8;
 
 // Orders the all-pairs kernel runs for schedule (nhi, nlo): every order for
-// the presets, the on-device ones for the custom schedules.
-static bool allpairs_order(int nhi, int nlo, int order) {
+// the on-device presets, the on-device ones for the custom schedules, the
+// FP64 ones (and the per-product form) for the host schedules.
+static bool allpairs_order(int pipe, int nhi, int nlo, int order) {
+  if (pipe == OZK_PIPE_HOST)
+    return order == OZK_ORDER_BLOCK64 || order == OZK_ORDER_HOST_JAX ||
+           order == OZK_ORDER_HOST_NP || order == kOrderProducts;
   return allpairs_preset(nhi, nlo) ||
          (order != OZK_ORDER_HOST_JAX && order != OZK_ORDER_HOST_NP);
 }
 
 static bool allpairs_schedule(int pipe, int nhi, int nlo) {
+  if (pipe == OZK_PIPE_HOST) return nlo == 0 && nhi >= 1 && nhi <= kHostMaxSlices;
   return pipe == OZK_PIPE_ONDEVICE && allpairs_nsweeps(nhi, nlo) > 0;
 }
 
-static int allpairs_sweeps(int nhi, int nlo) { return allpairs_nsweeps(nhi, nlo); }
+static int allpairs_sweeps(int pipe, int nhi, int nlo) {
+  return pipe == OZK_PIPE_HOST ? host_nsweeps(nhi) : allpairs_nsweeps(nhi, nlo);
+}
 
 bool allpairs_supported(int pipe, int nhi, int nlo) {
   return allpairs_schedule(pipe, nhi, nlo);
@@ -1245,8 +1348,8 @@ static int fold_state_bytes(int order) {
 // Workspace an all-pairs product cannot run without: the fold state kept
 // between the sweeps of a multi-sweep schedule (0 for one sweep).
 size_t gemm_state_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo, int order) {
-  if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(nhi, nlo, order) ||
-      allpairs_sweeps(nhi, nlo) == 1 || order < 0)
+  if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(pipe, nhi, nlo, order) ||
+      allpairs_sweeps(pipe, nhi, nlo) == 1 || order < 0)
     return 0;
   return (size_t)N * (size_t)M * (size_t)fold_state_bytes(order);
 }
@@ -1284,7 +1387,7 @@ static TailPlan plan_tail(int64_t ntiles, int cus, int64_t nst, int np, int rb) 
 // follow them where a driver reserves those too.)
 size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
                             int order) {
-  if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(nhi, nlo, order)) return 0;
+  if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(pipe, nhi, nlo, order)) return 0;
   return (size_t)round_up((int64_t)gemm_state_bytes(N, M, pipe, nhi, nlo, order), 256) +
          kDynBytes;
 }
@@ -1292,8 +1395,10 @@ size_t gemm_workspace_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo,
 // Tile rows of the all-pairs launch of schedule (nhi, nlo): those of its
 // single sweep; 64 for a multi-sweep schedule, whose sweeps size their own
 // grids (64-row tiles give the most tiles, the bound the launch checks).
-static int allpairs_tm(int nhi, int nlo, bool sym) {
-  return 32 * (allpairs_sweeps(nhi, nlo) == 1 ? ap_rb(nhi, nlo, 0, 2, sym) : 2);
+static int allpairs_tm(int pipe, int nhi, int nlo, bool sym) {
+  if (allpairs_sweeps(pipe, nhi, nlo) != 1) return 64;
+  return 32 * (pipe == OZK_PIPE_HOST ? ap_rb_of(pair_count(pipe, nhi, 0), nhi, nhi, false)
+                                     : ap_rb(nhi, nlo, 0, 2, sym));
 }
 
 static int64_t allpairs_nst(int64_t K, bool i8) {
@@ -1305,8 +1410,8 @@ static int64_t allpairs_nst(int64_t K, bool i8) {
 // when the product does not split.
 size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int nlo,
                        bool sym, bool i8) {
-  if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(nhi, nlo) != 1) return 0;
-  const int tm = allpairs_tm(nhi, nlo, sym);
+  if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(pipe, nhi, nlo) != 1) return 0;
+  const int tm = allpairs_tm(pipe, nhi, nlo, sym);
   return plan_tail(allpairs_ntiles(N, M, sym, tm), cu_count(), allpairs_nst(K, i8),
                    pair_count(pipe, nhi, nlo), tm / 32)
       .bytes;
@@ -1317,7 +1422,7 @@ size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int n
 // least gemm_state_bytes(); with gemm_workspace_bytes() the last rounds of
 // tiles are handed out dynamically, and a single-sweep schedule splits its
 // tail along K instead when `state` also holds gemm_tail_bytes().
-static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
+static int launch_allpairs(bool i8, int pipe, const void* As, const int32_t* Ae,
                            const void* Bs, const int32_t* Be, int64_t N,
                            int64_t M, int64_t K, int rho, int nhi, int nlo,
                            int order, double* C, int64_t ldc, float* P,
@@ -1328,14 +1433,14 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
     set_error("int8 slice planes need their line sums");
     return OZK_ERR_INVALID;
   }
-  const size_t need = gemm_state_bytes(N, M, OZK_PIPE_ONDEVICE, nhi, nlo, order);
+  const size_t need = gemm_state_bytes(N, M, pipe, nhi, nlo, order);
   if (state_bytes < need || (need && !state)) {
     set_error("gemm workspace of %zu bytes < %zu needed", state_bytes, need);
     return OZK_ERR_WORKSPACE;
   }
   ApArgs a;
   const int64_t al = round_up(N, kLinePad), bl = round_up(M, kLinePad);
-  const int tmr = allpairs_tm(nhi, nlo, sym);
+  const int tmr = allpairs_tm(pipe, nhi, nlo, sym);
   const int64_t ntiles = allpairs_ntiles(N, M, sym, tmr);
   OZK_CHECK_ARG(ntiles < (1ll << 31), "problem too large for one launch");
   // persistent: one workgroup per CU (the 160 KiB ring fills its LDS)
@@ -1349,9 +1454,9 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.cus = cus;
   // workspace: fold state | dynamic-tail words | K-split partial sums
   const size_t off = round_up((int64_t)need, 256);
-  if (allpairs_sweeps(nhi, nlo) == 1) {
+  if (allpairs_sweeps(pipe, nhi, nlo) == 1) {
     const TailPlan tp = plan_tail(ntiles, cus, allpairs_nst(K, i8),
-                                  pair_count(OZK_PIPE_ONDEVICE, nhi, nlo), tmr / 32);
+                                  pair_count(pipe, nhi, nlo), tmr / 32);
     if (tp.P > 1 && state && state_bytes >= off + kDynBytes + tp.bytes) {
       a.grid = dim3((unsigned)tp.grid);
       a.tail_P = tp.P;
@@ -1363,7 +1468,7 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   // the dynamic tail's counters, when some sweep will use them (each sweep
   // decides for its own tiles in launch_sweep)
   if (!a.part && state && state_bytes >= off + kDynBytes &&
-      (allpairs_sweeps(nhi, nlo) > 1 ||
+      (allpairs_sweeps(pipe, nhi, nlo) > 1 ||
        dyn_static_rounds(ntiles, (int)a.grid.x, allpairs_nst(K, i8)) > 0)) {
     a.dyn = (uint32_t*)((char*)state + off);
     hipLaunchKernelGGL(zero_u32_kernel, dim3(1), dim3(64), 0, st, a.dyn, kDynSlot0);
@@ -1389,6 +1494,14 @@ static int launch_allpairs(bool i8, const void* As, const int32_t* Ae,
   a.fix.bs = Bsum;
   a.fix.off = i8 ? (uint32_t)i8_offset(rho) : 0u;
   a.fix.kpo2 = (uint32_t)((uint64_t)(a.nst * kChunkBytes) * a.fix.off * a.fix.off);
+  if (pipe == OZK_PIPE_HOST) {
+    if (!launch_ap_host(nhi, order, a)) {
+      set_error("host schedule of %d slices has no all-pairs instantiation", nhi);
+      return OZK_ERR_UNSUPPORTED;
+    }
+    OZK_LAUNCH_CHECK();
+    return OZK_OK;
+  }
   // the presets and the smallest custom schedules here, the others in the
   // parts (gemm_parts.h)
   bool done = true;
@@ -1427,7 +1540,7 @@ int launch_gram_sym(const void* S, const int32_t* E, int64_t n, int64_t K, int n
     set_error("symmetric gram needs the high or medium preset");
     return OZK_ERR_UNSUPPORTED;
   }
-  return launch_allpairs(i8, S, E, S, E, n, n, K, rho, nhi, nlo, OZK_ORDER_2SUM, G, ldg,
+  return launch_allpairs(i8, OZK_PIPE_ONDEVICE, S, E, S, E, n, n, K, rho, nhi, nlo, OZK_ORDER_2SUM, G, ldg,
                          nullptr, 0, ws, ws_bytes, st, Ssum, Ssum, true);
 }
 
@@ -1436,8 +1549,8 @@ int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
                 void* ws, size_t ws_bytes, hipStream_t st, bool i8, int rho,
                 const int32_t* Asum, const int32_t* Bsum) {
-  if (allpairs_schedule(pipe, nhi, nlo) && allpairs_order(nhi, nlo, order))
-    return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, order,
+  if (allpairs_schedule(pipe, nhi, nlo) && allpairs_order(pipe, nhi, nlo, order))
+    return launch_allpairs(i8, pipe, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, order,
                            C, ldc, nullptr, 0, ws, ws_bytes, st, Asum, Bsum);
   if (i8) {
     set_error("int8 slice planes need an all-pairs on-device schedule");
@@ -1473,7 +1586,7 @@ int launch_gemm_pair(const void* As, const int32_t* Ae, const void* Bs,
                      size_t ws_bytes, hipStream_t st, bool i8, int rho,
                      const int32_t* Asum, const int32_t* Bsum) {
   if (allpairs_schedule(OZK_PIPE_ONDEVICE, nhi, nlo))
-    return launch_allpairs(i8, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, kOrderPair,
+    return launch_allpairs(i8, OZK_PIPE_ONDEVICE, As, Ae, Bs, Be, N, M, K, rho, nhi, nlo, kOrderPair,
                            (double*)C_lo, ldc, C_hi, ldc, ws, ws_bytes, st, Asum, Bsum);
   if (i8) {
     set_error("int8 slice planes need an all-pairs on-device schedule");
@@ -1497,7 +1610,7 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t ldp, hipStream_t st, bool i8, int rho, const int32_t* Asum,
                     const int32_t* Bsum) {
   if (allpairs_schedule(pipe, nhi, nlo))
-    return launch_allpairs(i8, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
+    return launch_allpairs(i8, pipe, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
                            kOrderProducts, nullptr, 0, P, ldp, nullptr, 0, st, Asum, Bsum);
   if (i8) {
     set_error("int8 slice planes need an all-pairs on-device schedule");

@@ -133,7 +133,12 @@ def test_gemm_workspace_bytes(lib):
 
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 4, 1, 0) == dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 3, 1, 1) == dyn
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 8, 0, 3) == 0
+    # host schedules of up to 8 slices: all-pairs sweeps over groups of A
+    # planes (one for up to 5 slices; 8 slices take three, with the FP64
+    # running sum kept between them); more slices run the pairwise kernel
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 8, 0, 3) == up(100 * 70 * 8) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 5, 0, 2) == dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 9, 0, 3) == 0
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 0) == up(100 * 70 * 20) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == up(100 * 70 * 8) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == dyn

@@ -243,11 +243,14 @@ def test_extract_i8_rejects_coarse_grid(ll):
 
 # (2, 3), (1, 2), (2, 1), (1, 1): one-sweep custom schedules on the
 # all-pairs kernel; (4, 2), (1, 5): two sweeps of it; (5, 1): three;
-# (6, 1) and the host schedule: the pairwise kernel
+# (6, 1): the pairwise kernel.  Host schedules of 1 to 8 slices run on the
+# all-pairs kernel in sweeps over groups of A planes (one sweep up to 5
+# slices, two for 6 and 7, three for 8); 9 slices on the pairwise kernel.
 SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
              ("ondevice", 2, 3), ("ondevice", 1, 2), ("ondevice", 2, 1),
              ("ondevice", 1, 1), ("ondevice", 4, 2), ("ondevice", 5, 1), ("ondevice", 1, 5),
-             ("ondevice", 6, 1), ("host", 8, 0)]
+             ("ondevice", 6, 1), ("host", 1, 0), ("host", 4, 0), ("host", 5, 0),
+             ("host", 6, 0), ("host", 7, 0), ("host", 8, 0), ("host", 9, 0)]
 
 
 def _slices(ll, A, B, pipe, nh, nl):
@@ -464,6 +467,19 @@ def test_matmul_numpy_bit_exact(ozk):
     case("matmul host (70,200,50)")
     assert np.array_equal(ozk.matmul(A, B), OP.matmul_host_a2(A, B))
     assert np.array_equal(ozk.matmul(A, B, n_slices=9), OP.matmul_host_a2(A, B, n_slices=9))
+
+
+@pytest.mark.parametrize("n_slices", [8, 9])
+def test_matmul_host_tiles_bit_exact(ozk, n_slices):
+    """The host pipeline on several tiles with partial edges: 8 slices run
+    the all-pairs kernel's three sweeps, 9 the pairwise kernel; A2 through
+    matmul, A1 through matmul_numpy."""
+    A, B = gen("wide2", (300, 1000), 33), gen("wide2", (1000, 260), 34)
+    case(f"matmul host (300,1000,260) n_slices={n_slices}")
+    assert np.array_equal(ozk.matmul(A, B, n_slices=n_slices),
+                          OP.matmul_host_a2(A, B, n_slices=n_slices))
+    assert np.array_equal(ozk.matmul_numpy(A, B, n_slices=n_slices),
+                          O.matmul_numpy(A, B, n_slices=n_slices))
 
 
 def _digest(a):
