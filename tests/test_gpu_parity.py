@@ -445,6 +445,23 @@ def test_matmul_tail_split_bit_exact(ozk, N, K, M, precision):
         assert np.array_equal(C[rows], ref)
 
 
+def test_host_schedule_tail_split_bit_exact(ll):
+    """The host triangle of 5 slices runs in one all-pairs sweep, which
+    splits its tail along K: 17 x 17 = 289 tiles leave 33 tail tiles, each
+    in 2 pieces of 16 stages (K = 1024 on BF16 planes).  Orders A2 and A1
+    against the oracle on the tail rows and others."""
+    N, K, M = 1088, 1024, 1088
+    assert _tail_split(17 * 17, K, False) == 2
+    A, B = gen("wide2", (N, K), 41), gen("randn", (K, M), 42)
+    a, b, (oa, oae, ob, obe), sched, code = _slices(ll, A, B, "host", 5, 0)
+    rows = np.r_[0:16, 500:520, N - 48:N]
+    Pref = O.slice_products(oa[:, rows], ob, sched)
+    for name, code_o, acc in (("A2", 2, O.accumulate_a2), ("A1", 3, O.accumulate_a1)):
+        case(f"ozk_gemm host 5 slices order {name} N,K,M={(N, K, M)} (K-split tail)")
+        C = to_np(ll.gemm(a, b, code, 5, 0, code_o))
+        assert np.array_equal(C[rows], acc(Pref, sched, oae[:, rows], obe)), name
+
+
 @pytest.mark.parametrize("precision", ["high", "medium"])
 def test_gram_tail_split_bit_exact(ozk, precision):
     # 640 columns: 55 upper tiles of K = 8192 stages split 4 ways each
