@@ -89,6 +89,29 @@ def test_column_extraction_gives_up_then_repeats_without_gangs(ozk, set_polls):
     assert retries() == n0 + 3
 
 
+def test_long_column_gangs_give_up_then_repeat_without_gangs(ozk, set_polls):
+    """Columns of 40000 rows: gangs of 79 workgroups, whose members combine
+    the exchange words in batches; after giving up, the repeat transposes."""
+    from ozaki_jax_amd import lowlevel as ll
+    rng = np.random.RandomState(6)
+    X = rng.randn(40000, 48)
+    rho = O.rho_f32(40000)
+    cols = np.r_[0:5, 40:48]
+    set_polls(1)
+    case("ozk_extract_f32_i8 by columns (40000, 48), one poll per wait")
+    n0 = retries()
+    check_cols(ll.extract(X, 1, rho, 4, 1, i8=True), X, rho, cols)
+    assert retries() == n0 + 1
+    case("gram 40000 x 48, one poll per wait")
+    G = ozk.gram(X, mode="ozaki")
+    assert retries() == n0 + 2
+    set_polls(0)
+    case("the same calls with the built-in limit")
+    check_cols(ll.extract(X, 1, rho, 4, 1, i8=True), X, rho, cols)
+    assert np.array_equal(ozk.gram(X, mode="ozaki"), G)
+    assert retries() == n0 + 2
+
+
 def test_row_extraction_gives_up_then_repeats_without_gangs(ozk, set_polls):
     from ozaki_jax_amd import lowlevel as ll
     rng = np.random.RandomState(4)
