@@ -184,18 +184,20 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * The drivers below use INT8 planes (ozk_gemm_i8) instead when the
  * contraction length gives rho >= 19 and the schedule is an all-pairs one.
  *
- * All-pairs schedules: the on-device presets high (4,1) and medium (3,1),
- * which run in one K sweep, max (5,4), which runs its hh, hl and lh blocks
- * (matmul.py:670-674) as three sweeps and keeps the fold state between them
- * in the workspace, and the custom schedules (1,2), (1,3), (1,4), (2,1),
- * (2,2), (2,3) and (3,2), which fit one sweep.  Other schedules, and the host
- * pipeline, run one pair at a time on BF16 planes.
- * Workspace: ozk_gemm_workspace_bytes is the fold state (max and the
- * two-sweep schedules only) plus 4352 bytes of tile counters, with which
- * the last rounds of output tiles are handed out at run time to the
- * workgroups that finish first.  Any workspace from the fold state up (none
- * for one-sweep schedules) is accepted; below the full size the tiles run in
- * a static order. */
+ * All-pairs schedules: every on-device (n_hi, n_lo) with both counts in
+ * 1 .. 5, in one K sweep when n_hi + n_lo <= 5 (high (4,1), medium (3,1)),
+ * else in two (hh + hl, then lh) or three (hh, hl, lh, as max (5,4);
+ * matmul.py:670-674), keeping the fold state between the sweeps in the
+ * workspace; and the host pipeline's triangle of up to 8 slices in the FP64
+ * orders (HOST_JAX, HOST_NP, BLOCK64), in sweeps over groups of A planes
+ * that keep each element's FP64 running sum between them.  Other schedules
+ * run one pair at a time on BF16 planes.
+ * Workspace: ozk_gemm_workspace_bytes is the fold state (multi-sweep
+ * schedules only) plus 4352 bytes of tile counters, with which the last
+ * rounds of output tiles are handed out at run time to the workgroups that
+ * finish first.  Any workspace from the fold state up (none for one-sweep
+ * schedules) is accepted; below the full size the tiles run in a static
+ * order. */
 size_t ozk_gemm_workspace_bytes(int64_t N, int64_t M, int pipeline, int n_hi,
                                 int n_lo, int order);
 int ozk_gemm(const uint16_t* a_slices, const int32_t* a_exps,
