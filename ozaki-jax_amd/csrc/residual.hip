@@ -418,8 +418,8 @@ __global__ __launch_bounds__(64 * kResWaves) void residual_rows_kernel(
 // a row (global_load_lds_dwordx4, EPL / 2 loads of 1 KiB) and reads only
 // those, so its own vmcnt orders the copy before the reads.  Needs 16-byte
 // aligned rows and even K.
-template <int EPL, bool FULL, int W, int NHI, int NLO, int D = 0>
-__global__ __launch_bounds__(64 * W) void residual_split_kernel(
+template <int EPL, bool FULL, int W, int NHI, int NLO, int D = 0, int WPE = 1>
+__global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) void residual_split_kernel(
     const double* __restrict__ A, int64_t N, int64_t K, int64_t lda,
     const double* __restrict__ x, int64_t ldx, const double* __restrict__ b,
     int64_t ldb, double* __restrict__ r, int64_t ldr, int rho,
@@ -482,6 +482,7 @@ __global__ __launch_bounds__(64 * W) void residual_split_kernel(
     }
   };
   int trow = 0;  // this workgroup's row counter
+  int rslot = 0;  // the ring buffer of the row at hand
   if constexpr (D > 0) {  // the first D rows load while x is extracted
 #pragma unroll
     for (int i = 0; i < D; ++i)
@@ -562,16 +563,7 @@ __global__ __launch_bounds__(64 * W) void residual_split_kernel(
       if (later >= D - 1) wait_vm<(D - 1) * kDmaPerRow>();
       else if (later == 1) wait_vm<kDmaPerRow>();
       else wait_vm<0>();
-#pragma unroll
-      for (int j = 0; j < EPL; ++j) {
-        const int k = kw0 + j * 64 + lane;
-        const double v = ring[slot][wave][j * 64 + lane];
-        nx[j] = (FULL || k < Ki) ? v : 0.0;
-      }
-      // the reads complete before the buffer is refilled with row trow + D
-      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-      if (cur + (int64_t)D * G < N) dma_row(cur + (int64_t)D * G, slot);
-      ++trow;
+      rslot = slot;
     } else if constexpr (!PF) {
       load_row(cur);
     }
@@ -581,17 +573,35 @@ __global__ __launch_bounds__(64 * W) void residual_split_kernel(
     float Rh[EPL], Rl[EPL];
     bool bad = false;
     float mh = 0.0f, ml = 0.0f;
+    // element j of the row: from the ring (read as it is split, so the row
+    // is never held as doubles) or from the register prefetch
+    auto elem = [&](int j) -> double {
+      if constexpr (D > 0) {
+        const int k = kw0 + j * 64 + lane;
+        const double v = ring[rslot][wave][j * 64 + lane];
+        return (FULL || k < Ki) ? v : 0.0;
+      } else {
+        return nx[j];
+      }
+    };
 #pragma unroll
     for (int j = 0; j < EPL; ++j) {
-      bad |= !isfinite(nx[j]);
+      const double v = elem(j);
+      bad |= !isfinite(v);
       float pr[2];
-      split<float>(nx[j], pr);
+      split<float>(v, pr);
       Rh[j] = pr[0];
       Rl[j] = pr[1];
       if (j & 1) {
         mh = max3_abs(mh, Rh[j - 1], Rh[j]);
         ml = max3_abs(ml, Rl[j - 1], Rl[j]);
       }
+    }
+    if constexpr (D > 0) {
+      // the reads complete before the buffer is refilled with row trow + D
+      asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+      if (cur + (int64_t)D * G < N) dma_row(cur + (int64_t)D * G, rslot);
+      ++trow;
     }
     if (bad) atomicOr(flags, OZK_FLAG_NONFINITE);
 
@@ -778,45 +788,49 @@ static void launch_rows_1(const double* A, int64_t N, int64_t K, int64_t lda,
 
 // One right-hand side on the split-row kernel (2048 < K <= kResMaxK): W = 4
 // waves of 1024 elements up to K = 4096, else 8 waves of 1024 or 2048.
-// Rows longer than 4096 elements come through an LDS ring (D = 2 rows of
-// 8192, one of 16384 elements: 128 KiB) when they are 16-byte aligned and K
-// is even, else through the register prefetch.
+// 16-byte aligned rows of even K come through an LDS ring of one row buffer
+// per workgroup, others through the register prefetch.
 static void launch_rows_split(const double* A, int64_t N, int64_t K, int64_t lda,
                               const double* x, int64_t ldx, const double* b, int64_t ldb,
                               double* r, int64_t ldr, int rho, int nhi, uint32_t* flags,
                               hipStream_t st) {
-  // persistent grid: 8 / W workgroups per CU
+  // persistent grid: PER_CU workgroups per CU
   const int64_t cus = cu_count();
   const bool ring = (uintptr_t)A % 16 == 0 && lda % 2 == 0 && K % 2 == 0;
-#define OZK_SPLIT_D(E, W, H, D)                                                      \
+#define OZK_SPLIT_D(E, W, H, D, WPE, PER_CU)                                         \
   do {                                                                               \
-    const int64_t g = cus * (8 / (W));                                               \
+    const int64_t g = cus * (PER_CU);                                                \
     const dim3 grid((unsigned)(N < g ? N : g));                                      \
     if (K == 64 * (E) * (W))                                                         \
-      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, 1, D>), grid,         \
+      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, 1, D, WPE>), grid,    \
                          dim3(64 * (W)), 0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, \
                          rho, flags);                                                \
     else                                                                             \
-      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, 1, D>), grid,        \
+      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, 1, D, WPE>), grid,   \
                          dim3(64 * (W)), 0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, \
                          rho, flags);                                                \
   } while (0)
-#define OZK_SPLIT(E, W, H, D)          \
-  do {                                 \
-    if (ring) OZK_SPLIT_D(E, W, H, D); \
-    else OZK_SPLIT_D(E, W, H, 0);      \
-  } while (0)
-#define OZK_SPLIT_K(H)                                 \
-  if (K <= 64 * 16 * 4) OZK_SPLIT_D(16, 4, H, 0);      \
-  else if (K <= 64 * 16 * 8) OZK_SPLIT(16, 8, H, 2);   \
-  else OZK_SPLIT(32, 8, H, 1);
+  // Rows of up to 8192 elements that come through the ring keep one row
+  // buffer per workgroup and at most 128 VGPRs, so that 16 waves share a CU
+  // (4 workgroups of 4 waves, or 2 of 8): while one workgroup's waves wait
+  // at a row-maximum barrier, another's run.  Others: 8 waves per CU.
+#define OZK_SPLIT_K(H)                                                      \
+  if (K <= 64 * 16 * 4) {                                                   \
+    if (ring) OZK_SPLIT_D(16, 4, H, 1, 4, 4);                               \
+    else OZK_SPLIT_D(16, 4, H, 0, 1, 2);                                    \
+  } else if (K <= 64 * 16 * 8) {                                            \
+    if (ring) OZK_SPLIT_D(16, 8, H, 1, 4, 2);                               \
+    else OZK_SPLIT_D(16, 8, H, 0, 1, 1);                                    \
+  } else {                                                                  \
+    if (ring) OZK_SPLIT_D(32, 8, H, 1, 1, 1);                               \
+    else OZK_SPLIT_D(32, 8, H, 0, 1, 1);                                    \
+  }
   if (nhi == 4) {
     OZK_SPLIT_K(4);
   } else {
     OZK_SPLIT_K(3);
   }
 #undef OZK_SPLIT_K
-#undef OZK_SPLIT
 #undef OZK_SPLIT_D
 }
 
