@@ -279,8 +279,10 @@ def suite(args):
                 emit(d)
     # custom (n_hi, n_lo) schedules at 8192^3, N(0,1), all on the all-pairs
     # kernel (INT8 planes): (2, 2), (3, 2) in one sweep, (4, 2), (2, 4) in
-    # two, (4, 4), (5, 1) in three
-    for prec in ((2, 2), (3, 2), (4, 2), (2, 4), (4, 4), (5, 1)) if want("custom") else ():
+    # two, (4, 4), (5, 1) in three; (6, 1), (6, 5), (7, 6) in rectangle
+    # sweeps (4, 6 and 7)
+    for prec in ((2, 2), (3, 2), (4, 2), (2, 4), (4, 4), (5, 1), (6, 1), (6, 5),
+                 (7, 6)) if want("custom") else ():
         rs = np.random.RandomState(0)
         A, B = rs.randn(n, n), rs.randn(n, n)
         emit(ondevice(f"matmul ondevice fused custom {prec} 8192^3 N(0,1)", A, B, prec, rows))

@@ -57,6 +57,7 @@ int launch_fill_u32(uint32_t* p, uint32_t v, hipStream_t st);
 int launch_check_finite(const double* X, int64_t rows, int64_t cols,
                         int64_t ld, uint32_t* flags, hipStream_t st);
 bool allpairs_supported(int pipe, int nhi, int nlo);
+bool allpairs_products_supported(int pipe, int nhi, int nlo);
 int launch_gemm(const void* As, const int32_t* Ae, const void* Bs,
                 const int32_t* Be, int64_t N, int64_t M, int64_t K, int pipe,
                 int nhi, int nlo, int order, double* C, int64_t ldc,
@@ -407,8 +408,8 @@ int ozk_slice_products_i8(const int8_t* a_slices, const int32_t* a_sums,
   if (rc) return rc;
   OZK_CHECK_ARG(N >= 0 && M >= 0 && K >= 1, "invalid shape");
   OZK_CHECK_ARG(ldp >= M, "ldp < M");
-  if (rho < 19 || rho > 24 || !allpairs_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
-    set_error("int8 planes need 19 <= rho <= 24 and an all-pairs schedule");
+  if (rho < 19 || rho > 24 || !allpairs_products_supported(OZK_PIPE_ONDEVICE, n_hi, n_lo)) {
+    set_error("int8 per-pair products need 19 <= rho <= 24 and a fixed all-pairs schedule");
     return OZK_ERR_UNSUPPORTED;
   }
   if (N == 0 || M == 0) return OZK_OK;

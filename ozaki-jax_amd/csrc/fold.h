@@ -101,14 +101,13 @@ struct Fold2Sum {
       else twosum(bt, bl, ht);
       twosum(bt, bl, hl);
       if (q.be) {
-        if (q.blk == 0) {
-          twosum_from_zero(ct, cl, bt);
-          p0 = bl;
-        } else {
-          twosum(ct, cl, bt);
-          if (q.blk == 1) p1 = bl;
-          else p2 = bl;
-        }
+        if (q.blk == 0) twosum_from_zero(ct, cl, bt);
+        else twosum(ct, cl, bt);
+        // value selects, not a store through a selected field: the block id
+        // may be a run-time value, and the fold must stay in registers
+        p0 = q.blk == 0 ? bl : p0;
+        p1 = q.blk == 1 ? bl : p1;
+        p2 = q.blk == 2 ? bl : p2;
       }
     }
   }

@@ -198,9 +198,10 @@ __device__ __forceinline__ void k_sweep(const uint16_t* const (&a_ptr)[NA],
 
 constexpr int kThreads16 = 512;
 constexpr int kRing = 4;       // stage buffers (kRing - 1 stages in flight)
-// Dynamic-tail words (gemm_allpairs): kXcds counters per sweep, then one
-// word per workgroup (at most kDynMaxGrid) that passes a claimed tile on.
-constexpr int kDynSlot0 = 64, kDynMaxGrid = 1024;
+// Dynamic-tail words (gemm_allpairs): kXcds counters per sweep (at most
+// kDynSlot0 / kXcds sweeps), then one word per workgroup (at most
+// kDynMaxGrid) that passes a claimed tile on.
+constexpr int kDynSlot0 = 128, kDynMaxGrid = 1024;
 
 typedef int int32x4 __attribute__((ext_vector_type(4)));
 typedef int int32x16 __attribute__((ext_vector_type(16)));
@@ -266,7 +267,8 @@ constexpr int ap_rb(int nhi, int nlo, int b0, int b1, bool sym) {
 template <int PIPE, int NHI, int NLO, int B0, int B1, bool SYM = false>
 struct Sweep {
   static_assert(PIPE == OZK_PIPE_ONDEVICE, "sweeps cover the on-device schedule");
-  static constexpr bool kFirst = B0 == 0, kLast = B1 == 2;
+  static constexpr bool kRect = false, kFirst = B0 == 0, kLast = B1 == 2;
+  static constexpr bool kMid0 = false, kMid1 = false;
   static constexpr int kNBlk = 3, kDone0 = B0, kDone1 = B1 + 1;
   static constexpr int A0 = B0 == 2 ? NHI : 0;                    // first A plane
   static constexpr int NA = (B1 == 2 ? NHI + NLO : NHI) - A0;     // A planes
@@ -300,7 +302,8 @@ struct Sweep {
 // sum alone.
 template <int N, int G0, int G1>
 struct Sweep<OZK_PIPE_HOST, N, 0, G0, G1, false> {
-  static constexpr bool kFirst = G0 == 0, kLast = G1 == N - 1;
+  static constexpr bool kRect = false, kFirst = G0 == 0, kLast = G1 == N - 1;
+  static constexpr bool kMid0 = false, kMid1 = false;
   static constexpr int kNBlk = 1, kDone0 = 0, kDone1 = 0;
   static constexpr int A0 = G0, NA = G1 - G0 + 1, BB = 0, NB = N - G0;
   static constexpr int P0 = G0 * N - G0 * (G0 - 1) / 2;
@@ -331,6 +334,51 @@ constexpr int host_nsweeps(int n) {
   for (int g = 0; g < n; g = host_sweep_end(n, g) + 1) ++k;
   return k;
 }
+
+// Rectangle sweeps: the on-device schedules beyond the fixed ones (a count
+// of 6 to 8) run as sweeps over rectangles of one block: NA consecutive
+// groups of the block (A planes) times all NB B planes of its pairs, the
+// NA x NB pairs i-major, as the block orders them.  The kernel is the same
+// for every schedule and block with that shape: the host offsets the plane,
+// exponent and line-sum pointers to the rectangle's first A and B plane,
+// and the fold's block id, block-boundary flags and state boundaries come
+// in a run-time word (kRf*).  Sweep<kPipeRect, NA, NB, 0, 0>.
+constexpr int kPipeRect = 16;
+constexpr int kRfBlk = 3;           // bits 0-1: block id
+constexpr int kRfGFirst = 1 << 2;   // the rectangle starts its block
+constexpr int kRfGLast = 1 << 3;    // ... and ends it
+constexpr int kRfFirst = 1 << 4;    // starts the schedule: no state to load
+constexpr int kRfLast = 1 << 5;     // ends it: C is written
+constexpr int kRfPair = 1 << 6;     // 2Sum order: write the (hi, lo) pair
+constexpr int kRfDone0 = 7;         // bits 7-8: blocks folded before it
+constexpr int kRfDone1 = 9;         // bits 9-10: ... and after it
+
+template <int NA_, int NB_>
+struct Sweep<kPipeRect, NA_, NB_, 0, 0, false> {
+  static constexpr bool kRect = true, kFirst = false, kLast = false;
+  static constexpr bool kMid0 = false, kMid1 = false;
+  static constexpr int kNBlk = 3, kDone0 = 0, kDone1 = 0;
+  static constexpr int A0 = 0, NA = NA_, BB = 0, NB = NB_, P0 = 0;
+  static constexpr int NP = NA * NB;
+  static constexpr int S = NA + NB;
+  static constexpr int RB = ap_rb_of(NP, NA, NB, false);
+  static constexpr int TM = 32 * RB;
+  static constexpr int FA = 2 * RB;
+  static constexpr int NFRAG = NA * FA + NB * 4;
+  // fg and be hold inside the rectangle; the run-time word says whether the
+  // rectangle's first group and last pair are also its block's
+  static constexpr PairInfo pair(int k) {
+    return PairInfo{k / NB, k % NB, 0, k % NB == 0, k % NB == NB - 1, k == 0, k == NP - 1,
+                    k / NB == 0};
+  }
+  static constexpr int la(int k) { return k / NB; }
+  static constexpr int lb(int k) { return k % NB; }
+  static constexpr int tpair(int) { return -1; }
+};
+
+// Most planes (A + B) and pairs of one sweep: the 160 KiB ring holds 10
+// planes' fragments per stage, the registers 25 pairs' accumulators.
+constexpr int kSweepPlanes = 10, kSweepPairs = 25;
 
 template <class Op, class SW>
 struct AllPairsMMA {
@@ -490,47 +538,56 @@ __device__ __forceinline__ void wait_stage(int64_t later) {
 // Fold state at a block boundary, kept in a workspace between the sweeps of
 // one product: 2Sum order (ct, cl, p0, p1, p2) as FP32 fields, the FP64
 // block order the running sum c.  Field f of element (row, col) lies at
-// state[f * N * M + row * M + col].  DONE = the blocks folded before the
-// boundary: block lo parts p_DONE.. are still zero there, so they are
+// state[f * N * M + row * M + col].  `done` = the blocks folded before the
+// boundary: block lo parts p_done.. are still zero there, so they are
 // neither stored nor loaded.
+// MID: the boundary lies inside a block, between two of its groups; the
+// 2Sum order then also carries the block's running sum (bt, bl).  The FP64
+// orders' running sum covers every group folded so far either way.  `done`
+// and `mid` are compile-time constants for the sweeps of the fixed
+// schedules and run-time values for the rectangle sweeps.
 template <int ORDER> struct FoldState {  // the FP64 orders: the running sum
-  static constexpr int kBytes = 8;
-  template <int DONE>
+  static constexpr int kBytes = 8, kBytesMid = 8;
   static __device__ __forceinline__ void load(Fold64<ORDER>& f, const char* st, int64_t e,
-                                              int64_t) {
+                                              int64_t, int, bool) {
     f.c = ((const double*)st)[e];
   }
-  template <int DONE>
   static __device__ __forceinline__ void store(const Fold64<ORDER>& f, char* st, int64_t e,
-                                               int64_t) {
+                                               int64_t, int, bool) {
     ((double*)st)[e] = f.c;
   }
 };
 
 template <> struct FoldState<OZK_ORDER_2SUM> {
-  static constexpr int kBytes = 5 * 4;
-  template <int DONE>
+  static constexpr int kBytes = 5 * 4, kBytesMid = 7 * 4;
   static __device__ __forceinline__ void load(Fold2Sum& f, const char* st, int64_t e,
-                                              int64_t nm) {
+                                              int64_t nm, int done, bool mid) {
     const float* s = (const float*)st;
     f.ct = s[e];
     f.cl = s[nm + e];
-    if constexpr (DONE > 0) f.p0 = s[2 * nm + e];
-    if constexpr (DONE > 1) f.p1 = s[3 * nm + e];
-    if constexpr (DONE > 2) f.p2 = s[4 * nm + e];
+    if (done > 0) f.p0 = s[2 * nm + e];
+    if (done > 1) f.p1 = s[3 * nm + e];
+    if (done > 2) f.p2 = s[4 * nm + e];
+    if (mid) {
+      f.bt = s[5 * nm + e];
+      f.bl = s[6 * nm + e];
+    }
   }
-  template <int DONE>
   static __device__ __forceinline__ void store(const Fold2Sum& f, char* st, int64_t e,
-                                               int64_t nm) {
+                                               int64_t nm, int done, bool mid) {
     float* s = (float*)st;
     s[e] = f.ct;
     s[nm + e] = f.cl;
-    if constexpr (DONE > 0) s[2 * nm + e] = f.p0;
-    if constexpr (DONE > 1) s[3 * nm + e] = f.p1;
-    if constexpr (DONE > 2) s[4 * nm + e] = f.p2;
+    if (done > 0) s[2 * nm + e] = f.p0;
+    if (done > 1) s[3 * nm + e] = f.p1;
+    if (done > 2) s[4 * nm + e] = f.p2;
+    if (mid) {
+      s[5 * nm + e] = f.bt;
+      s[6 * nm + e] = f.bl;
+    }
   }
 };
-// ORDER value of the test hook that writes the per-pair products P.
+
 constexpr int kOrderProducts = -1;
 // ORDER value of the 2Sum order written as its double-float pair (C_hi,
 // C_lo) (pallas_gemm_accum.py:181-186) instead of their FP64 sum: C_hi goes
@@ -578,9 +635,17 @@ __device__ __forceinline__ void tile_epilogue(
     int lane, const int32_t* __restrict__ Ae, const int32_t* __restrict__ Be,
     int64_t N, int64_t M, int64_t a_lines, int64_t b_lines, float unit2,
     double* __restrict__ C, int64_t ldc, float* __restrict__ P, int64_t ldp,
-    char* __restrict__ state) {
+    char* __restrict__ state, int rflags) {
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP, RB = SW::RB;
   constexpr int NBLK = SW::kNBlk;
+  // where the sweep lies in its schedule: compile-time for the fixed
+  // schedules, the run-time word (kRf*) for a rectangle
+  const bool first = SW::kRect ? (rflags & kRfFirst) != 0 : SW::kFirst;
+  const bool last = SW::kRect ? (rflags & kRfLast) != 0 : SW::kLast;
+  const int done0 = SW::kRect ? (rflags >> kRfDone0) & 3 : SW::kDone0;
+  const int done1 = SW::kRect ? (rflags >> kRfDone1) & 3 : SW::kDone1;
+  const bool mid0 = SW::kRect ? (rflags & kRfGFirst) == 0 : SW::kMid0;
+  const bool mid1 = SW::kRect ? (rflags & kRfGLast) == 0 : SW::kMid1;
   const int64_t row0 = (int64_t)tm * SW::TM, col0 = (int64_t)tn * kBN;
 
   // Accumulator register r of lane l of a 16x16 block holds row
@@ -625,10 +690,10 @@ __device__ __forceinline__ void tile_epilogue(
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         fr[r].init();
-        if constexpr (!SW::kFirst) {
+        if (!first) {
           const int64_t row = rbase + 16 * h + r;
           if (row < N && col < M)
-            FoldState<ORDER>::template load<SW::kDone0>(fr[r], state, row * M + col, nm);
+            FoldState<ORDER>::load(fr[r], state, row * M + col, nm, done0, mid0);
         }
       }
       // One wait for all of them here: the folds below sit in branches on
@@ -645,7 +710,12 @@ __device__ __forceinline__ void tile_epilogue(
         typename FoldOf<ORDER>::type& f = fr[r];
 #pragma unroll
         for (int k = 0; k < NP; ++k) {
-          const PairInfo q = SW::pair(k);
+          PairInfo q = SW::pair(k);
+          if constexpr (SW::kRect) {
+            q.blk = rflags & kRfBlk;
+            q.fg = q.fg && (rflags & kRfGFirst);
+            q.be = q.be && (rflags & kRfGLast);
+          }
           const int ia = ea[SW::la(k)], ib = eb[SW::lb(k)];
           f.pair(q, Op::product(acc[k][h][r], unit2), scale32(ib), scale32(ia),
                  scale64(ib), scale64(ia));
@@ -670,14 +740,17 @@ __device__ __forceinline__ void tile_epilogue(
             C[row * ldc + col] = out;
             if (tm != tn) C[col * ldc + row] = out;
           }
-        } else if constexpr (!SW::kLast) {
-          if (live) FoldState<ORDER>::template store<SW::kDone1>(f, state, row * M + col, nm);
-        } else if constexpr (ORDER == kOrderPair) {
-          float hi, lo;
-          f.finish_pair(NBLK, hi, lo);
-          if (live) {
-            P[row * ldp + col] = hi;
-            ((float*)C)[row * ldp + col] = lo;
+        } else if (!last) {
+          if (live) FoldState<ORDER>::store(f, state, row * M + col, nm, done1, mid1);
+        } else if (ORDER == kOrderPair ||
+                   (ORDER == OZK_ORDER_2SUM && SW::kRect && (rflags & kRfPair))) {
+          if constexpr (std::is_same<typename FoldOf<ORDER>::type, Fold2Sum>::value) {
+            float hi, lo;
+            f.finish_pair(NBLK, hi, lo);
+            if (live) {
+              P[row * ldp + col] = hi;
+              ((float*)C)[row * ldp + col] = lo;
+            }
           }
         } else {
           const double out = f.finish(NBLK);
@@ -707,7 +780,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
     int64_t N, int64_t M, int64_t nst, int64_t a_lines, int64_t b_lines,
     float unit2, double* __restrict__ C, int64_t ldc, float* __restrict__ P,
     int64_t ldp, char* __restrict__ state, int tail_P, uint32_t* __restrict__ part,
-    I8Fix fix, uint32_t* __restrict__ dyn, int dyn_nstat) {
+    I8Fix fix, uint32_t* __restrict__ dyn, int dyn_nstat, int rflags) {
   typedef Sweep<PIPE, NHI, NLO, B0, B1, SYM> SW;
   constexpr int NA = SW::NA, NB = SW::NB, NP = SW::NP, RB = SW::RB, FA = SW::FA;
   constexpr int kBuf = SW::NFRAG * 64;  // uint4 per stage buffer
@@ -898,7 +971,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_allpairs(
       coords(item_tile(j), tm, tn);
       tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(mma.acc, tm, tn, mma.wr, mma.wc, lane, Ae,
                                                 Be, N, M, a_lines, b_lines, unit2, C, ldc,
-                                                P, ldp, state);
+                                                P, ldp, state, rflags);
     } else {
       // part[bid][thread][k][h]: each thread's sums are contiguous, so the
       // 16-byte stores take immediate offsets
@@ -980,7 +1053,7 @@ __global__ __launch_bounds__(kThreads16) void gemm_tail_fixup(
     for (int h = 0; h < RB; ++h) acc[k][h] = sum[RB * k + h][lane];
   }
   tile_epilogue<Op, SW, ORDER, B0, B1, SYM>(acc, tm, tn, w >> 2, w & 3, lane, Ae, Be, N, M,
-                                            a_lines, b_lines, unit2, C, ldc, P, ldp, state);
+                                            a_lines, b_lines, unit2, C, ldc, P, ldp, state, 0);
 }
 
 struct OnePairMMA {
@@ -1196,7 +1269,7 @@ static void launch_sweep_of(const ApArgs& a) {
   hipLaunchKernelGGL((gemm_allpairs<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>),
                      grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
                      a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
-                     split ? a.tail_P : 0, a.part, a.fix, dyn, nstat);
+                     split ? a.tail_P : 0, a.part, a.fix, dyn, nstat, 0);
   if constexpr (SW::kFirst && SW::kLast) {
     if (split)
       hipLaunchKernelGGL((gemm_tail_fixup<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>),
@@ -1231,6 +1304,40 @@ static void launch_host_order(int order, const ApArgs& a) {
     case OZK_ORDER_HOST_NP: launch_host_sweeps<N, OZK_ORDER_HOST_NP, 0>(a); break;
     default: launch_host_sweeps<N, kOrderProducts, 0>(a); break;
   }
+}
+
+// One rectangle sweep: planes a0.. of A and bb.. of B, the `ordinal`-th
+// sweep of its schedule (its dynamic-tail counters), flags kRf*.
+struct RectSweep {
+  int na, nb, a0, bb, ordinal, rflags;
+};
+
+template <class Op, int NA, int NB, int ORDER>
+static void launch_rect(const ApArgs& a, const RectSweep& r) {
+  typedef Sweep<kPipeRect, NA, NB, 0, 0> SW;
+  const int64_t nt = allpairs_ntiles(a.N, a.M, false, SW::TM);
+  const dim3 grid((unsigned)(nt < a.cus ? nt : a.cus));
+  const int nstat = a.dyn ? dyn_static_rounds(nt, (int)grid.x, a.nst) : 0;
+  uint32_t* dyn = nstat > 0 ? a.dyn + kXcds * r.ordinal : nullptr;
+  // the rectangle's first planes: slice planes, exponents and line sums
+  const int64_t aplane = a.al * kChunkBytes * a.nst, bplane = a.bl * kChunkBytes * a.nst;
+  I8Fix fix = a.fix;
+  if (fix.as) {
+    fix.as += (int64_t)r.a0 * a.al;
+    fix.bs += (int64_t)r.bb * a.bl;
+  }
+  hipLaunchKernelGGL((gemm_allpairs<Op, kPipeRect, NA, NB, ORDER, 0, 0, false>), grid,
+                     dim3(kThreads16), 0, a.st, a.As + r.a0 * aplane, a.Ae + r.a0 * a.al,
+                     a.Bs + r.bb * bplane, a.Be + r.bb * a.bl, a.N, a.M, a.nst, a.al, a.bl,
+                     a.unit2, a.C, a.ldc, a.P, a.ldp, a.state, 0, (uint32_t*)nullptr, fix, dyn,
+                     nstat, r.rflags);
+}
+
+// The 2Sum order and its pair form share the 2Sum kernels (kRfPair).
+template <class Op, int NA, int NB>
+static void launch_rect_order(int order, const ApArgs& a, const RectSweep& r) {
+  if (order == OZK_ORDER_BLOCK64) launch_rect<Op, NA, NB, OZK_ORDER_BLOCK64>(a, r);
+  else launch_rect<Op, NA, NB, OZK_ORDER_2SUM>(a, r);
 }
 
 template <class Op, int NHI, int NLO, int ORDER>
@@ -1290,6 +1397,20 @@ bool launch_ap_host(int n, int order, const ApArgs& a) {
     default: return false;
   }
 }
+#elif defined(OZK_GEMM_PART_RECT)
+// A part of the rectangle sweeps' instantiations: OZK_GEMM_RECT_SHAPES(X)
+// names its (NA, NB).  Returns false for a shape of another part.
+bool OZK_GEMM_PART_FN(bool i8, int order, const ApArgs& a, const RectSweep& r) {
+#define OZK_RECT_CASE(A, B)                                 \
+  if (r.na == A && r.nb == B) {                             \
+    if (i8) launch_rect_order<OpI8, A, B>(order, a, r);     \
+    else launch_rect_order<OpBf16, A, B>(order, a, r);      \
+    return true;                                            \
+  }
+  OZK_GEMM_RECT_SHAPES(OZK_RECT_CASE)
+#undef OZK_RECT_CASE
+  return false;
+}
 #elif defined(OZK_GEMM_PART)
 // A part of the schedules' instantiations, compiled as a translation unit
 // of its own so that the parts build in parallel: OZK_GEMM_PART_TUPLES(X)
@@ -1311,38 +1432,103 @@ bool launch_ap_part2(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 bool launch_ap_part3(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 bool launch_ap_part4(bool i8, int nhi, int nlo, int order, const ApArgs& a);
 bool launch_ap_host(int n, int order, const ApArgs& a);
+bool launch_ap_rect1(bool i8, int order, const ApArgs& a, const RectSweep& r);
+bool launch_ap_rect2(bool i8, int order, const ApArgs& a, const RectSweep& r);
+
+// The on-device schedules beyond the fixed ones, both counts up to
+// kRectMaxSlices, as rectangle sweeps: each block (hh, hl, lh) is cut into
+// as few rectangles of consecutive groups as fit a sweep (kSweepPlanes,
+// kSweepPairs), the groups spread evenly over them.  rect_plan fills `out`
+// (if given) and returns the number of sweeps; *mid says whether some
+// block is cut (its running sum then crosses a sweep boundary).
+constexpr int kRectMaxSlices = 8;
+constexpr int kRectMaxSweeps = kDynSlot0 / kXcds;
+
+static bool rect_tuple(int nhi, int nlo) {
+  return allpairs_nsweeps(nhi, nlo) == 0 && nhi >= 1 && nlo >= 1 && nhi <= kRectMaxSlices &&
+         nlo <= kRectMaxSlices;
+}
+
+static int rect_plan(int nhi, int nlo, bool pair_out, RectSweep* out, bool* mid) {
+  int n = 0;
+  if (mid) *mid = false;
+  for (int blk = 0; blk < 3; ++blk) {
+    const int ng = blk == 2 ? nlo : nhi;       // groups: the block's A planes
+    const int nb = blk == 1 ? nlo : nhi;       // B planes of every group
+    const int a_base = blk == 2 ? nhi : 0, b_base = blk == 1 ? nhi : 0;
+    int na = ng;
+    while (na > 1 && (na + nb > kSweepPlanes || na * nb > kSweepPairs)) --na;
+    const int nsw = (ng + na - 1) / na;
+    if (nsw > 1 && mid) *mid = true;
+    for (int sw = 0, g0 = 0; sw < nsw; ++sw) {
+      const int cnt = ng / nsw + (sw < ng % nsw ? 1 : 0);
+      const int g1 = g0 + cnt - 1;
+      if (out) {
+        RectSweep& r = out[n];
+        r.na = cnt;
+        r.nb = nb;
+        r.a0 = a_base + g0;
+        r.bb = b_base;
+        r.ordinal = n;
+        r.rflags = blk | (g0 == 0 ? kRfGFirst : 0) | (g1 == ng - 1 ? kRfGLast : 0) |
+                   (blk == 0 && g0 == 0 ? kRfFirst : 0) |
+                   (blk == 2 && g1 == ng - 1 ? kRfLast : 0) | (pair_out ? kRfPair : 0) |
+                   (blk << kRfDone0) | ((g1 == ng - 1 ? blk + 1 : blk) << kRfDone1);
+      }
+      ++n;
+      g0 = g1 + 1;
+    }
+  }
+  return n;
+}
 
 // Host schedules (FP64 extraction, BF16 planes) of up to this many slices
 // run on the all-pairs kernel, in sweeps over groups of A planes.
 constexpr int kHostMaxSlices = 8;
 
 // Orders the all-pairs kernel runs for schedule (nhi, nlo): every order for
-// the on-device presets, the on-device ones for the custom schedules, the
-// FP64 ones (and the per-product form) for the host schedules.
+// the on-device presets, the on-device ones for the custom schedules (the
+// rectangle sweeps: 2Sum, its pair form and the FP64 block order), the FP64
+// ones (and the per-product form) for the host schedules.
 static bool allpairs_order(int pipe, int nhi, int nlo, int order) {
   if (pipe == OZK_PIPE_HOST)
     return order == OZK_ORDER_BLOCK64 || order == OZK_ORDER_HOST_JAX ||
            order == OZK_ORDER_HOST_NP || order == kOrderProducts;
+  if (rect_tuple(nhi, nlo))
+    return order == OZK_ORDER_2SUM || order == OZK_ORDER_BLOCK64 || order == kOrderPair;
   return allpairs_preset(nhi, nlo) ||
          (order != OZK_ORDER_HOST_JAX && order != OZK_ORDER_HOST_NP);
 }
 
 static bool allpairs_schedule(int pipe, int nhi, int nlo) {
   if (pipe == OZK_PIPE_HOST) return nlo == 0 && nhi >= 1 && nhi <= kHostMaxSlices;
-  return pipe == OZK_PIPE_ONDEVICE && allpairs_nsweeps(nhi, nlo) > 0;
+  return pipe == OZK_PIPE_ONDEVICE && (allpairs_nsweeps(nhi, nlo) > 0 || rect_tuple(nhi, nlo));
 }
 
 static int allpairs_sweeps(int pipe, int nhi, int nlo) {
-  return pipe == OZK_PIPE_HOST ? host_nsweeps(nhi) : allpairs_nsweeps(nhi, nlo);
+  if (pipe == OZK_PIPE_HOST) return host_nsweeps(nhi);
+  return rect_tuple(nhi, nlo) ? rect_plan(nhi, nlo, false, nullptr, nullptr)
+                              : allpairs_nsweeps(nhi, nlo);
 }
 
 bool allpairs_supported(int pipe, int nhi, int nlo) {
   return allpairs_schedule(pipe, nhi, nlo);
 }
 
-static int fold_state_bytes(int order) {
-  return order == OZK_ORDER_2SUM ? FoldState<OZK_ORDER_2SUM>::kBytes
-                                 : FoldState<OZK_ORDER_BLOCK64>::kBytes;
+// The per-pair products (test hook) on the all-pairs kernel: the fixed
+// schedules only.
+bool allpairs_products_supported(int pipe, int nhi, int nlo) {
+  return allpairs_schedule(pipe, nhi, nlo) && allpairs_order(pipe, nhi, nlo, kOrderProducts);
+}
+
+// Bytes per element of the fold state between sweeps: the 2Sum order also
+// carries a block's running sum where a rectangle sweep cuts a block.
+static int fold_state_bytes(int pipe, int nhi, int nlo, int order) {
+  if (order != OZK_ORDER_2SUM) return FoldState<OZK_ORDER_BLOCK64>::kBytes;
+  bool mid = false;
+  if (pipe == OZK_PIPE_ONDEVICE && rect_tuple(nhi, nlo))
+    rect_plan(nhi, nlo, false, nullptr, &mid);
+  return mid ? FoldState<OZK_ORDER_2SUM>::kBytesMid : FoldState<OZK_ORDER_2SUM>::kBytes;
 }
 
 // Workspace an all-pairs product cannot run without: the fold state kept
@@ -1351,7 +1537,7 @@ size_t gemm_state_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo, int or
   if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(pipe, nhi, nlo, order) ||
       allpairs_sweeps(pipe, nhi, nlo) == 1 || order < 0)
     return 0;
-  return (size_t)N * (size_t)M * (size_t)fold_state_bytes(order);
+  return (size_t)N * (size_t)M * (size_t)fold_state_bytes(pipe, nhi, nlo, order);
 }
 
 // K-split of the tail.  With R = ntiles / cus whole rounds of one tile per
@@ -1494,6 +1680,19 @@ static int launch_allpairs(bool i8, int pipe, const void* As, const int32_t* Ae,
   a.fix.bs = Bsum;
   a.fix.off = i8 ? (uint32_t)i8_offset(rho) : 0u;
   a.fix.kpo2 = (uint32_t)((uint64_t)(a.nst * kChunkBytes) * a.fix.off * a.fix.off);
+  if (pipe == OZK_PIPE_ONDEVICE && rect_tuple(nhi, nlo)) {
+    RectSweep plan[kRectMaxSweeps];
+    const int n = rect_plan(nhi, nlo, order == kOrderPair, plan, nullptr);
+    const int ord = order == kOrderPair ? OZK_ORDER_2SUM : order;
+    for (int i = 0; i < n; ++i) {
+      if (!launch_ap_rect1(i8, ord, a, plan[i]) && !launch_ap_rect2(i8, ord, a, plan[i])) {
+        set_error("rectangle sweep %d x %d has no instantiation", plan[i].na, plan[i].nb);
+        return OZK_ERR_UNSUPPORTED;
+      }
+    }
+    OZK_LAUNCH_CHECK();
+    return OZK_OK;
+  }
   if (pipe == OZK_PIPE_HOST) {
     if (!launch_ap_host(nhi, order, a)) {
       set_error("host schedule of %d slices has no all-pairs instantiation", nhi);
@@ -1609,7 +1808,7 @@ int launch_products(const void* As, const void* Bs, int64_t N, int64_t M,
                     int64_t K, int pipe, int nhi, int nlo, float* P,
                     int64_t ldp, hipStream_t st, bool i8, int rho, const int32_t* Asum,
                     const int32_t* Bsum) {
-  if (allpairs_schedule(pipe, nhi, nlo))
+  if (allpairs_schedule(pipe, nhi, nlo) && allpairs_order(pipe, nhi, nlo, kOrderProducts))
     return launch_allpairs(i8, pipe, As, nullptr, Bs, nullptr, N, M, K, rho, nhi, nlo,
                            kOrderProducts, nullptr, 0, P, ldp, nullptr, 0, st, Asum, Bsum);
   if (i8) {

@@ -62,7 +62,7 @@ def test_host_functions(lib):
 
 # dynamic-tail words of an all-pairs product: 64 counters and one word per
 # workgroup (up to 1024)
-DYN = (64 + 1024) * 4
+DYN = (128 + 1024) * 4
 
 
 def r256(b):
@@ -124,8 +124,9 @@ def test_workspace_sizes(lib):
 
 def test_gemm_workspace_bytes(lib):
     # all-pairs schedules: the fold state the three-sweep max schedule keeps
-    # between launches (rounded to 256 B), then the dynamic-tail words (64
-    # counters and one word for each of up to 1024 workgroups)
+    # between launches (rounded to 256 B), then the dynamic-tail words (8
+    # counters for each of up to 16 sweeps and one word for each of up to
+    # 1024 workgroups)
     dyn = DYN
 
     def up(x):
@@ -142,6 +143,17 @@ def test_gemm_workspace_bytes(lib):
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 0) == up(100 * 70 * 20) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == up(100 * 70 * 8) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == dyn
+    # on-device schedules beyond (5, 5), both counts up to 8: rectangle
+    # sweeps; where one cuts a block the 2Sum state also carries the block's
+    # running sum (7 FP32 fields).  (6, 1): hh in two sweeps of 3 groups;
+    # (1, 6): one sweep per block.  Per-pair products and larger counts run
+    # the pairwise kernel.
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 6, 1, 0) == up(100 * 70 * 28) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 6, 1, 1) == up(100 * 70 * 8) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 1, 6, 0) == up(100 * 70 * 20) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 8, 8, 0) == up(100 * 70 * 28) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 6, 1, -1) == 0
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 9, 1, 0) == 0
     assert lib.ozk_extract_workspace_bytes(100, 50, 0) == 0
     assert lib.ozk_extract_workspace_bytes(100, 32768, 0) == 0
     # rows of 32769 to 262144 elements: row gangs; longer lines stream
@@ -164,8 +176,8 @@ def test_int8_entry_points_reject_before_device_work(lib):
     from ozaki_jax_amd import _lib
     # INT8 planes need 19 <= rho <= 24 (|q| <= 64, stored with an offset of
     # at most 63) and an all-pairs schedule: every (n_hi, n_lo) with both
-    # counts in 1 .. 5; others, such as (6,1), (1,6) and (6,6), run on BF16
-    # planes
+    # counts in 1 .. 8; others, such as (9,1), (1,9) and (9,9), run on BF16
+    # planes.  Per-pair products of INT8 planes: counts up to 5.
     for rho in (18, 25):
         rc = lib.ozk_extract_f32_i8(None, 4, 4, 4, 0, rho, 4, 1, None, None, None, None, None,
                                     0, None)
@@ -173,13 +185,17 @@ def test_int8_entry_points_reject_before_device_work(lib):
         rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, rho, 4, 1, 0,
                              None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED
-    for nh, nl in ((6, 1), (1, 6), (6, 6)):
+    for nh, nl in ((9, 1), (1, 9), (9, 9)):
         rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, nh, nl, 0,
                              None, 4, None, 0, None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED and b"all-pairs" in lib.ozk_last_error()
         rc = lib.ozk_slice_products_i8(None, None, None, None, 4, 4, 8192, 19, nh, nl, None, 4,
                                        None)
         assert rc == _lib.OZK_ERR_UNSUPPORTED
+    for nh, nl in ((6, 1), (8, 8)):
+        rc = lib.ozk_slice_products_i8(None, None, None, None, 4, 4, 8192, 19, nh, nl, None, 4,
+                                       None)
+        assert rc == _lib.OZK_ERR_UNSUPPORTED and b"fixed all-pairs" in lib.ozk_last_error()
     rc = lib.ozk_gemm_i8(None, None, None, None, None, None, 4, 4, 8192, 19, 4, 1, 7, None, 4,
                          None, 0, None)
     assert rc == _lib.OZK_ERR_INVALID

@@ -25,11 +25,14 @@ def _oracle_pair(A, B, rho, nh, nl):
     return (a, ae, b, be), OP.accumulate_a4(OP.slice_products(a, b, sched), sched, ae, be)
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 3), (4, 2), (5, 1)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 3), (4, 2), (5, 1), (6, 1),
+                                   (7, 6), (9, 1)])
 def test_fused_gemm_accum_pair(ozk, nh, nl):
     """Caller-held slices (the oracle's) through the NumPy family: all-pairs
-    kernel for the presets, (2, 3) (one sweep) and (4, 2) (two sweeps; the
-    fold state crosses the workspace), pairwise kernel for (5, 1)."""
+    kernel for the presets, (2, 3) (one sweep), (4, 2) (two sweeps; the fold
+    state crosses the workspace) and (5, 1) (three); rectangle sweeps for
+    (6, 1) and (7, 6) (the block sums cross the workspace too); pairwise
+    kernel for (9, 1)."""
     from ozaki_jax_amd.pallas_gemm_accum import fused_gemm_accum
     rng = np.random.RandomState(nh * 10 + nl)
     A = (rng.rand(96, 200) - 0.5) * np.exp(2 * rng.randn(96, 200))
@@ -44,7 +47,7 @@ def test_fused_gemm_accum_pair(ozk, nh, nl):
                           O.matmul_ondevice_a4(A, B, "raise", nh, nl))
 
 
-@pytest.mark.parametrize("nh,nl", [(4, 1), (5, 4), (4, 2)])
+@pytest.mark.parametrize("nh,nl", [(4, 1), (5, 4), (4, 2), (6, 1), (8, 8)])
 def test_gemm_pair_int8_planes(ozk, nh, nl):
     """INT8 planes (K = 5000 and 4200, rho = 19), 16 and 324 tiles."""
     import torch

@@ -243,13 +243,17 @@ def test_extract_i8_rejects_coarse_grid(ll):
 
 # (2, 3), (1, 2), (2, 1), (1, 1): one-sweep custom schedules on the
 # all-pairs kernel; (4, 2), (1, 5): two sweeps of it; (5, 1): three;
-# (6, 1): the pairwise kernel.  Host schedules of 1 to 8 slices run on the
-# all-pairs kernel in sweeps over groups of A planes (one sweep up to 5
-# slices, two for 6 and 7, three for 8); 9 slices on the pairwise kernel.
+# (6, 1), (1, 6), (7, 6), (8, 8): rectangle sweeps (4, 3, 7 and 12 of them;
+# (6, 1), (7, 6) and (8, 8) cut blocks between groups); (9, 1): the
+# pairwise kernel.  Host schedules of 1 to 8 slices run on the all-pairs
+# kernel in sweeps over groups of A planes (one sweep up to 5 slices, two
+# for 6 and 7, three for 8); 9 slices on the pairwise kernel.  Per-pair
+# products of the rectangle schedules come from the pairwise kernel.
 SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
              ("ondevice", 2, 3), ("ondevice", 1, 2), ("ondevice", 2, 1),
              ("ondevice", 1, 1), ("ondevice", 4, 2), ("ondevice", 5, 1), ("ondevice", 1, 5),
-             ("ondevice", 6, 1), ("host", 1, 0), ("host", 4, 0), ("host", 5, 0),
+             ("ondevice", 6, 1), ("ondevice", 1, 6), ("ondevice", 7, 6), ("ondevice", 8, 8),
+             ("ondevice", 9, 1), ("host", 1, 0), ("host", 4, 0), ("host", 5, 0),
              ("host", 6, 0), ("host", 7, 0), ("host", 8, 0), ("host", 9, 0)]
 
 
@@ -315,7 +319,8 @@ def test_slice_products_i8_bit_exact(ll, nh, nl, shape, rho_fixed):
 
 
 @pytest.mark.parametrize("nh,nl", [(4, 1), (3, 1), (5, 4), (2, 2), (1, 4), (3, 2), (1, 1), (4, 2),
-                                   (3, 3), (5, 1), (1, 5), (5, 5), (3, 4)])
+                                   (3, 3), (5, 1), (1, 5), (5, 5), (3, 4), (6, 1), (1, 6),
+                                   (6, 5), (7, 6), (8, 8), (8, 3), (3, 8)])
 @pytest.mark.parametrize("shape,rho_fixed", I8_SHAPES)
 def test_gemm_i8_orders_bit_exact(ll, nh, nl, shape, rho_fixed):
     N, K, M = shape
@@ -357,7 +362,8 @@ def test_gemm_orders_bit_exact(ll, pipe, nh, nl, shape):
 @pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (2, 2), (1, 1), (1, 2),
                                        (1, 4), (2, 1), (2, 3), (3, 2), (3, 3), (2, 4), (4, 4),
                                        (5, 1), (5, 2), (5, 3), (5, 5), (4, 3), (4, 5), (3, 4),
-                                       (3, 5), (2, 5), (1, 5), (6, 1)])
+                                       (3, 5), (2, 5), (1, 5), (6, 1), (1, 6), (6, 5),
+                                       (7, 6), (8, 8), (2, 7), (9, 1)])
 @pytest.mark.parametrize("accumulation", ["fused", "bf16_interleaved", "ondevice", "host"])
 def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
     A, B = gen("randn", (150, 300), 21), gen("randn", (300, 90), 22)
@@ -377,11 +383,12 @@ def test_matmul_ondevice_bit_exact(ozk, precision, accumulation):
 @pytest.mark.parametrize("precision", ["high", "medium", "max", (1, 1), (1, 2), (1, 3), (2, 1),
                                        (2, 2), (2, 3), (3, 2), (3, 3), (4, 2), (2, 4), (4, 4),
                                        (5, 1), (5, 2), (5, 3), (5, 5), (4, 3), (4, 5), (3, 4),
-                                       (3, 5), (2, 5), (1, 5), (6, 1)])
+                                       (3, 5), (2, 5), (1, 5), (6, 1), (1, 6), (6, 5),
+                                       (7, 6), (8, 8), (8, 2), (9, 1)])
 def test_matmul_long_contraction_bit_exact(ozk, precision):
-    # K > 4096: rho >= 19, every schedule with both counts in 1 .. 5 runs on
-    # INT8 planes in the all-pairs kernel (one, two or three sweeps); (6, 1)
-    # on BF16 planes in the pairwise kernel
+    # K > 4096: rho >= 19, every schedule with both counts in 1 .. 8 runs on
+    # INT8 planes in the all-pairs kernel (one, two or three sweeps up to 5,
+    # rectangle sweeps beyond); (9, 1) on BF16 planes in the pairwise kernel
     A, B = gen("randn", (40, 6000), 23), gen("wide2", (6000, 70), 24)
     nh, nl = OP.resolve_precision(precision)
     for acc, ref in [("fused", lambda: O.matmul_ondevice_a4(A, B, "raise", nh, nl)),
@@ -460,6 +467,24 @@ def test_host_schedule_tail_split_bit_exact(ll):
         case(f"ozk_gemm host 5 slices order {name} N,K,M={(N, K, M)} (K-split tail)")
         C = to_np(ll.gemm(a, b, code, 5, 0, code_o))
         assert np.array_equal(C[rows], acc(Pref, sched, oae[:, rows], obe)), name
+
+
+# Rectangle sweeps over many tiles: 2112 x 2112 gives 1089 tiles of 64 rows
+# (four whole rounds and a dynamic tail on 256 CUs) and 726 of 96 rows (no
+# dynamic tail), sweep by sweep; INT8 planes (K = 5000) and BF16 (K = 3000).
+@pytest.mark.parametrize("precision", [(6, 1), (7, 6)])
+@pytest.mark.parametrize("K", [5000, 3000])
+def test_matmul_rectangle_sweeps_many_tiles_bit_exact(ozk, precision, K):
+    N = M = 2112
+    A, B = gen("randn", (N, K), 81), gen("wide2", (K, M), 82)
+    nh, nl = precision
+    rows = np.r_[0:4, 95:97, 1055:1059, N - 6:N]  # 64- and 96-row tile edges
+    for acc in ("fused", "host"):
+        case(f"matmul rectangle sweeps {precision} {acc} ({N},{K},{M})")
+        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=precision)
+        ref = (O.matmul_ondevice_a3(A[rows], B, "raise", nh, nl) if acc == "host"
+               else O.matmul_ondevice_a4(A[rows], B, "raise", nh, nl))
+        assert np.array_equal(C[rows], ref)
 
 
 @pytest.mark.parametrize("precision", ["high", "medium"])
