@@ -188,12 +188,16 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * 1 .. 5, in one K sweep when n_hi + n_lo <= 5 (high (4,1), medium (3,1)),
  * else in two (hh + hl, then lh) or three (hh, hl, lh, as max (5,4);
  * matmul.py:670-674), keeping the fold state between the sweeps in the
- * workspace; and the host pipeline's triangle of up to 8 slices in the FP64
- * orders (HOST_JAX, HOST_NP, BLOCK64), in sweeps over groups of A planes
- * that keep each element's FP64 running sum between them.  Other schedules
- * run one pair at a time on BF16 planes.
+ * workspace; every other on-device (n_hi, n_lo) with both counts up to 8
+ * in the 2SUM and BLOCK64 orders (and ozk_gemm_2sum_pair), in sweeps over
+ * rectangles of one block (consecutive groups x the block's B planes; a
+ * block cut between groups carries its running sum in the fold state too);
+ * and the host pipeline's triangle of up to 8 slices in the FP64 orders
+ * (HOST_JAX, HOST_NP, BLOCK64), in sweeps over groups of A planes that keep
+ * each element's FP64 running sum between them.  Other schedules run one
+ * pair at a time on BF16 planes.
  * Workspace: ozk_gemm_workspace_bytes is the fold state (multi-sweep
- * schedules only) plus 4352 bytes of tile counters, with which the last
+ * schedules only) plus 4608 bytes of tile counters, with which the last
  * rounds of output tiles are handed out at run time to the workgroups that
  * finish first.  Any workspace from the fold state up (none for one-sweep
  * schedules) is accepted; below the full size the tiles run in a static
