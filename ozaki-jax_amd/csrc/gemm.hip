@@ -1533,11 +1533,13 @@ static int fold_state_bytes(int pipe, int nhi, int nlo, int order) {
 
 // Workspace an all-pairs product cannot run without: the fold state kept
 // between the sweeps of a multi-sweep schedule (0 for one sweep).
+// The per-product form keeps no state; the pair form keeps the 2Sum state.
 size_t gemm_state_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo, int order) {
   if (!allpairs_schedule(pipe, nhi, nlo) || !allpairs_order(pipe, nhi, nlo, order) ||
-      allpairs_sweeps(pipe, nhi, nlo) == 1 || order < 0)
+      allpairs_sweeps(pipe, nhi, nlo) == 1 || order == kOrderProducts)
     return 0;
-  return (size_t)N * (size_t)M * (size_t)fold_state_bytes(pipe, nhi, nlo, order);
+  const int fold = order == kOrderPair ? OZK_ORDER_2SUM : order;
+  return (size_t)N * (size_t)M * (size_t)fold_state_bytes(pipe, nhi, nlo, fold);
 }
 
 // K-split of the tail.  With R = ntiles / cus whole rounds of one tile per

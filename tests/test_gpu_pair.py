@@ -69,6 +69,26 @@ def test_gemm_pair_int8_planes(ozk, nh, nl):
         assert isinstance(hi, torch.Tensor)
 
 
+@pytest.mark.parametrize("nh,nl", [(4, 2), (6, 1)])
+def test_gemm_pair_int8_planes_dynamic_tail(ozk, nh, nl):
+    """A multi-sweep schedule over 33 x 33 tiles (four whole rounds on 256
+    CUs, then the dynamic tail): the pair form keeps the 2Sum fold state in
+    the workspace ahead of the tile counters, as the FP64 form does."""
+    from ozaki_jax_amd import lowlevel as ll
+    rng = np.random.RandomState(40 + nh)
+    N, K, M = 2112, 4200, 2112
+    A, B = rng.randn(N, K), (rng.rand(K, M) - 0.5) * np.exp(2 * rng.randn(K, M))
+    rho = O.rho_f32(K)
+    pa = ll.extract(A, 0, rho, nh, nl, i8=True)
+    pb = ll.extract(B, 1, rho, nh, nl, i8=True)
+    case(f"ozk_gemm_2sum_pair int8 ({nh},{nl}) ({N},{K},{M}) dynamic tail")
+    hi, lo = ll.gemm_pair(pa, pb, nh, nl)
+    rows = np.r_[0:4, 1055:1059, N - 4:N]
+    _, (ch, cl) = _oracle_pair(A[rows], B, rho, nh, nl)
+    assert np.array_equal(hi.cpu().numpy()[rows], ch)
+    assert np.array_equal(lo.cpu().numpy()[rows], cl)
+
+
 def test_fused_ozaki_matmul_given_rho(ozk):
     from ozaki_jax_amd.pallas_gemm_accum import fused_ozaki_matmul
     rng = np.random.RandomState(9)
