@@ -226,34 +226,37 @@ def suite(args):
         del At, Bt, C
         return d
 
-    # the host pipeline (FP64 extraction, 8 slices, 36 pairs on BF16 planes,
-    # order A2) on device tensors: 4096 x 1024 x 4096, N(0,1)
-    if want("host"):
+    # the host pipeline (FP64 extraction, BF16 planes) on device tensors, order
+    # A2: 8 slices (36 pairs) at 4096 x 1024 x 4096, and 9 slices (45 pairs,
+    # the safety budget's count at K = 4096, where rho = 47 leaves 6 bits per
+    # slice) at 2048 x 4096 x 2048; N(0,1)
+    for ns, (hn, hk, hm) in ((8, (4096, 1024, 4096)), (9, (2048, 4096, 2048))) if want("host") else ():
         rs = np.random.RandomState(0)
-        A, B = rs.randn(4096, 1024), rs.randn(1024, 4096)
+        A, B = rs.randn(hn, hk), rs.randn(hk, hm)
         At, Bt = torch.from_numpy(A).to(dev), torch.from_numpy(B).to(dev)
-        name = "matmul host n_slices=8 4096x1024x4096 N(0,1)"
+        name = f"matmul host n_slices={ns} {hn}x{hk}x{hm} N(0,1)"
         log(f"suite: {name}")
         # the call returns NumPy (as the reference's host pipeline does), so
         # it includes C's copy to the host; the device part is timed from the
         # extractions and the GEMM of the library's entry points
         from ozaki_jax_amd import lowlevel as ll
-        t = _timeit(lambda: ozk.matmul(At, Bt, n_slices=8), 5, sync)
-        rho = ozk.rho_f64(1024)
+        t = _timeit(lambda: ozk.matmul(At, Bt, n_slices=ns), 5, sync)
+        rho = ozk.rho_f64(hk)
 
         def device_part():
-            pa = ll.extract(At, 0, rho, 8, f64=True)
-            pb = ll.extract(Bt, 1, rho, 8, f64=True)
-            return ll.gemm(pa, pb, ll.PIPE_HOST, 8, 0, ll.ORDER_HOST_JAX)
+            pa = ll.extract(At, 0, rho, ns, f64=True)
+            pb = ll.extract(Bt, 1, rho, ns, f64=True)
+            return ll.gemm(pa, pb, ll.PIPE_HOST, ns, 0, ll.ORDER_HOST_JAX)
         t_dev = _timeit(device_part, 5, sync)
-        rows = np.array([0, 2047, 4095])
-        Cr = ozk.matmul(At, Bt, n_slices=8)[rows]
-        ref = OP.matmul_host_a2(A[rows], B, n_slices=8)
+        rows = np.array([0, hn // 2 - 1, hn - 1])
+        Cr = ozk.matmul(At, Bt, n_slices=ns)[rows]
+        ref = OP.matmul_host_a2(A[rows], B, n_slices=ns)
         t_dg = _timeit(lambda: torch.matmul(At, Bt), 3, sync)
-        flops = 2.0 * 4096 * 1024 * 4096
+        flops = 2.0 * hn * hk * hm
+        pairs = ns * (ns + 1) // 2
         emit({"config": name, "ms": t * 1e3, "device_ms": t_dev * 1e3,
               "fp64_eq_tflops_device": flops / t_dev / 1e12, "slice_format": "bf16",
-              "pair_rate_frac_of_mfma_peak": 36 * flops / t_dev / 1e12 / PEAK_BF16_TFLOPS,
+              "pair_rate_frac_of_mfma_peak": pairs * flops / t_dev / 1e12 / PEAK_BF16_TFLOPS,
               "rocblas_dgemm_ms": t_dg * 1e3,
               "max_scaled_err_vs_oracle": scaled_err(Cr, ref, A[rows], B),
               "max_scaled_err_vs_fp64": scaled_err(Cr, A[rows] @ B, A[rows], B),

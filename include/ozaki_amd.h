@@ -192,7 +192,7 @@ int ozk_pair_count(int pipeline, int n_hi, int n_lo);
  * in the 2SUM and BLOCK64 orders (and ozk_gemm_2sum_pair), in sweeps over
  * rectangles of one block (consecutive groups x the block's B planes; a
  * block cut between groups carries its running sum in the fold state too);
- * and the host pipeline's triangle of up to 8 slices in the FP64 orders
+ * and the host pipeline's triangle of up to 9 slices in the FP64 orders
  * (HOST_JAX, HOST_NP, BLOCK64), in sweeps over groups of A planes that keep
  * each element's FP64 running sum between them.  Other schedules run one
  * pair at a time on BF16 planes.

@@ -1382,7 +1382,7 @@ static void launch_ap_order(int order, const ApArgs& a) {
 
 
 #if defined(OZK_GEMM_PART_HOST)
-// The host schedules with 1 .. 8 slices (BF16 planes): false for any
+// The host schedules with 1 .. 9 slices (BF16 planes): false for any
 // other count.
 bool launch_ap_host(int n, int order, const ApArgs& a) {
   switch (n) {
@@ -1394,6 +1394,7 @@ bool launch_ap_host(int n, int order, const ApArgs& a) {
     case 6: launch_host_order<6>(order, a); return true;
     case 7: launch_host_order<7>(order, a); return true;
     case 8: launch_host_order<8>(order, a); return true;
+    case 9: launch_host_order<9>(order, a); return true;
     default: return false;
   }
 }
@@ -1483,8 +1484,11 @@ static int rect_plan(int nhi, int nlo, bool pair_out, RectSweep* out, bool* mid)
 }
 
 // Host schedules (FP64 extraction, BF16 planes) of up to this many slices
-// run on the all-pairs kernel, in sweeps over groups of A planes.
-constexpr int kHostMaxSlices = 8;
+// run on the all-pairs kernel, in sweeps over groups of A planes: group 0
+// pairs A plane 0 with all n B planes, which fit one stage beside it for
+// n <= 9.  (Nine slices of 6 bits are what the host pipeline needs for
+// 2048 < K <= 4226, where rho = 47.)
+constexpr int kHostMaxSlices = 9;
 
 // Orders the all-pairs kernel runs for schedule (nhi, nlo): every order for
 // the on-device presets, the on-device ones for the custom schedules (the

@@ -134,12 +134,13 @@ def test_gemm_workspace_bytes(lib):
 
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 4, 1, 0) == dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 3, 1, 1) == dyn
-    # host schedules of up to 8 slices: all-pairs sweeps over groups of A
-    # planes (one for up to 5 slices; 8 slices take three, with the FP64
-    # running sum kept between them); more slices run the pairwise kernel
+    # host schedules of up to 9 slices: all-pairs sweeps over groups of A
+    # planes (one for up to 5 slices; 8 slices take three, 9 four, with the
+    # FP64 running sum kept between them); more slices run the pairwise kernel
     assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 8, 0, 3) == up(100 * 70 * 8) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 5, 0, 2) == dyn
-    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 9, 0, 3) == 0
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 9, 0, 3) == up(100 * 70 * 8) + dyn
+    assert lib.ozk_gemm_workspace_bytes(100, 70, 1, 10, 0, 3) == 0
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 0) == up(100 * 70 * 20) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, 1) == up(100 * 70 * 8) + dyn
     assert lib.ozk_gemm_workspace_bytes(100, 70, 0, 5, 4, -1) == dyn

@@ -245,16 +245,17 @@ def test_extract_i8_rejects_coarse_grid(ll):
 # all-pairs kernel; (4, 2), (1, 5): two sweeps of it; (5, 1): three;
 # (6, 1), (1, 6), (7, 6), (8, 8): rectangle sweeps (4, 3, 7 and 12 of them;
 # (6, 1), (7, 6) and (8, 8) cut blocks between groups); (9, 1): the
-# pairwise kernel.  Host schedules of 1 to 8 slices run on the all-pairs
+# pairwise kernel.  Host schedules of 1 to 9 slices run on the all-pairs
 # kernel in sweeps over groups of A planes (one sweep up to 5 slices, two
-# for 6 and 7, three for 8); 9 slices on the pairwise kernel.  Per-pair
-# products of the rectangle schedules come from the pairwise kernel.
+# for 6 and 7, three for 8, four for 9); 10 slices on the pairwise kernel.
+# Per-pair products of the rectangle schedules come from the pairwise
+# kernel.
 SCHEDULES = [("ondevice", 4, 1), ("ondevice", 3, 1), ("ondevice", 5, 4),
              ("ondevice", 2, 3), ("ondevice", 1, 2), ("ondevice", 2, 1),
              ("ondevice", 1, 1), ("ondevice", 4, 2), ("ondevice", 5, 1), ("ondevice", 1, 5),
              ("ondevice", 6, 1), ("ondevice", 1, 6), ("ondevice", 7, 6), ("ondevice", 8, 8),
              ("ondevice", 9, 1), ("host", 1, 0), ("host", 4, 0), ("host", 5, 0),
-             ("host", 6, 0), ("host", 7, 0), ("host", 8, 0), ("host", 9, 0)]
+             ("host", 6, 0), ("host", 7, 0), ("host", 8, 0), ("host", 9, 0), ("host", 10, 0)]
 
 
 def _slices(ll, A, B, pipe, nh, nl):
@@ -511,11 +512,25 @@ def test_matmul_numpy_bit_exact(ozk):
     assert np.array_equal(ozk.matmul(A, B, n_slices=9), OP.matmul_host_a2(A, B, n_slices=9))
 
 
-@pytest.mark.parametrize("n_slices", [8, 9])
+def test_matmul_host_nine_slices_k4096_bit_exact(ozk):
+    """K = 4096: rho = 47 leaves 6 bits per slice, so the host pipeline's
+    safety budget (matmul.py:102-106) needs 9 slices; they run in the
+    all-pairs kernel's four sweeps (45 pairs).  Rows across the 64-row
+    tiles, A2 and A1."""
+    A, B = gen("randn", (200, 4096), 35), gen("wide2", (4096, 150), 36)
+    rows = np.r_[0:3, 63:66, 197:200]
+    case("matmul host (200,4096,150) n_slices=9")
+    C = ozk.matmul(A, B, n_slices=9)
+    assert np.array_equal(C[rows], OP.matmul_host_a2(A[rows], B, n_slices=9))
+    C = ozk.matmul_numpy(A, B, n_slices=9)
+    assert np.array_equal(C[rows], O.matmul_numpy(A[rows], B, n_slices=9))
+
+
+@pytest.mark.parametrize("n_slices", [8, 9, 10])
 def test_matmul_host_tiles_bit_exact(ozk, n_slices):
     """The host pipeline on several tiles with partial edges: 8 slices run
-    the all-pairs kernel's three sweeps, 9 the pairwise kernel; A2 through
-    matmul, A1 through matmul_numpy."""
+    the all-pairs kernel's three sweeps, 9 its four, 10 the pairwise kernel;
+    A2 through matmul, A1 through matmul_numpy."""
     A, B = gen("wide2", (300, 1000), 33), gen("wide2", (1000, 260), 34)
     case(f"matmul host (300,1000,260) n_slices={n_slices}")
     assert np.array_equal(ozk.matmul(A, B, n_slices=n_slices),
