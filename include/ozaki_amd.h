@@ -348,9 +348,10 @@ int ozk_gram_early_flags(const double* A, int64_t lda, int64_t rows,
 /* residual(A, x, b, mode="ozaki"): r = b - Ozaki(A, x) in order 2SUM with
  * rho = ozk_rho_f32(K); x is K x ncols, b and r are N x ncols
  * (solve.py:38-53, :78-82, :91-151).  Up to 4 columns with K <= 16384 and
- * (n_hi, n_lo) = (4, 1) or (3, 1) run fused row kernels that read A once per
- * column and need no workspace (ozk_residual_workspace_bytes returns 0);
- * other shapes extract A's slice planes and run the slice GEMM. */
+ * (n_hi, n_lo) = (4, 1) or (3, 1), or K <= 8192 and (5, 4), run fused row
+ * kernels that read A once per column and need no workspace
+ * (ozk_residual_workspace_bytes returns 0); other shapes extract A's slice
+ * planes and run the slice GEMM. */
 size_t ozk_residual_workspace_bytes(int64_t N, int64_t K, int64_t ncols,
                                     int n_hi, int n_lo);
 int ozk_residual(const double* A, int64_t lda, const double* x, int64_t ldx,

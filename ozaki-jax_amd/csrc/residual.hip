@@ -428,7 +428,7 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
   constexpr int NP = pair_count(OZK_PIPE_ONDEVICE, NHI, NLO);
   constexpr int NR = (NP + 3) / 4 * 4;  // pair sums padded for the reduce-scatter
   constexpr int KW = 64 * EPL, H = EPL / 2;
-  static_assert(EPL % 2 == 0 && NP <= 64, "elements are paired; one lane per pair");
+  static_assert(EPL % 2 == 0 && NP <= 128, "elements are paired; one or two pairs per lane");
   __shared__ ResRow<NP, NT> rows[kResBatch];
   __shared__ uint32_t gm[2][W][2];  // the waves' maxima, alternating buffers
   __shared__ float part[W][NR];     // the waves' pair sums of the row
@@ -546,7 +546,8 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
       }
     }
   };
-  constexpr bool PF = EPL <= 16 && D == 0;  // the next row's prefetch fits in registers
+  // the next row's prefetch fits in registers (not beside max's 65 pair sums)
+  constexpr bool PF = EPL <= 16 && D == 0 && NP <= 64;
   const int64_t G = gridDim.x;
   int64_t cur = blockIdx.x;
   if (PF && cur < N) load_row(cur);
@@ -685,11 +686,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
     __syncthreads();
     if (wave == 0) {
       ResRow<NP, NT>& rr = rows[nb];
-      if (lane < NP) {
-        float s = part[0][lane];
 #pragma unroll
-        for (int w = 1; w < W; ++w) s += part[w][lane];
-        rr.p[lane] = s;
+      for (int i = 0; i < (NP + 63) / 64; ++i) {
+        const int p = lane + 64 * i;
+        if (p < NP) {
+          float s = part[0][p];
+#pragma unroll
+          for (int w = 1; w < W; ++w) s += part[w][p];
+          rr.p[p] = s;
+        }
       }
       if (lane == 0) {
         rr.b = bv;
@@ -730,9 +735,15 @@ __global__ __launch_bounds__(64 * W) __attribute__((amdgpu_waves_per_eu(WPE))) v
 constexpr int64_t kResMaxCols = 4;
 constexpr int64_t kResMaxK = 64 * 32 * 8;
 
+// The max preset (5, 4): 65 pair sums and 9 slices of x per lane need the
+// registers of two waves per SIMD, so its rows run up to kResMaxKMax
+// elements (eight waves of 1024).
+constexpr int64_t kResMaxKMax = 64 * 16 * 8;
+
 bool residual_rows_supported(int64_t K, int64_t ncols, int nhi, int nlo) {
-  return ncols >= 1 && ncols <= kResMaxCols && K >= 1 && K <= kResMaxK &&
-         ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1));
+  if (ncols < 1 || ncols > kResMaxCols || K < 1) return false;
+  if (nhi == 5 && nlo == 4) return K <= kResMaxKMax;
+  return K <= kResMaxK && ((nhi == 4 && nlo == 1) || (nhi == 3 && nlo == 1));
 }
 
 // Values per lane (EPL): rows (and x) of up to 64 EPL elements.
@@ -777,7 +788,10 @@ static void launch_rows_1(const double* A, int64_t N, int64_t K, int64_t lda,
     case 16: OZK_RES(16, H, L); break; \
     default: OZK_RES(32, H, L); break; \
   }
-  if (nhi == 4) {
+  if (nhi == 5) {  // max (5, 4): rows of up to 1024 elements
+    if (epl == 8) OZK_RES(8, 5, 4);
+    else OZK_RES(16, 5, 4);
+  } else if (nhi == 4) {
     OZK_RES_E(4, 1);
   } else {
     OZK_RES_E(3, 1);
@@ -797,19 +811,20 @@ static void launch_rows_split(const double* A, int64_t N, int64_t K, int64_t lda
   // persistent grid: PER_CU workgroups per CU
   const int64_t cus = cu_count();
   const bool ring = (uintptr_t)A % 16 == 0 && lda % 2 == 0 && K % 2 == 0;
-#define OZK_SPLIT_D(E, W, H, D, WPE, PER_CU)                                         \
+#define OZK_SPLIT_DL(E, W, H, L, D, WPE, PER_CU)                                     \
   do {                                                                               \
     const int64_t g = cus * (PER_CU);                                                \
     const dim3 grid((unsigned)(N < g ? N : g));                                      \
     if (K == 64 * (E) * (W))                                                         \
-      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, 1, D, WPE>), grid,    \
+      hipLaunchKernelGGL((residual_split_kernel<E, true, W, H, L, D, WPE>), grid,    \
                          dim3(64 * (W)), 0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, \
                          rho, flags);                                                \
     else                                                                             \
-      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, 1, D, WPE>), grid,   \
+      hipLaunchKernelGGL((residual_split_kernel<E, false, W, H, L, D, WPE>), grid,   \
                          dim3(64 * (W)), 0, st, A, N, K, lda, x, ldx, b, ldb, r, ldr, \
                          rho, flags);                                                \
   } while (0)
+#define OZK_SPLIT_D(E, W, H, D, WPE, PER_CU) OZK_SPLIT_DL(E, W, H, 1, D, WPE, PER_CU)
   // Rows of up to 8192 elements that come through the ring keep one row
   // buffer per workgroup and at most 128 VGPRs, so that 16 waves share a CU
   // (4 workgroups of 4 waves, or 2 of 8): while one workgroup's waves wait
@@ -825,13 +840,28 @@ static void launch_rows_split(const double* A, int64_t N, int64_t K, int64_t lda
     if (ring) OZK_SPLIT_D(32, 8, H, 1, 1, 1);                               \
     else OZK_SPLIT_D(32, 8, H, 0, 1, 1);                                    \
   }
-  if (nhi == 4) {
+  // max (5, 4): two waves per SIMD (its pair sums and x slices take about
+  // 200 VGPRs), 1024 elements per wave
+#define OZK_SPLIT_MAX(W, PER_CU)                       \
+  if (ring) OZK_SPLIT_DL(16, W, 5, 4, 1, 2, PER_CU);   \
+  else OZK_SPLIT_DL(16, W, 5, 4, 0, 2, PER_CU);
+  if (nhi == 5) {
+    if (K <= 64 * 16 * 2) {
+      OZK_SPLIT_MAX(2, 4);
+    } else if (K <= 64 * 16 * 4) {
+      OZK_SPLIT_MAX(4, 2);
+    } else {
+      OZK_SPLIT_MAX(8, 1);
+    }
+  } else if (nhi == 4) {
     OZK_SPLIT_K(4);
   } else {
     OZK_SPLIT_K(3);
   }
+#undef OZK_SPLIT_MAX
 #undef OZK_SPLIT_K
 #undef OZK_SPLIT_D
+#undef OZK_SPLIT_DL
 }
 
 // r = b - Ozaki(A, x) for up to kResMaxCols right-hand sides (column j of x,
@@ -845,8 +875,10 @@ int launch_residual_rows(const double* A, int64_t N, int64_t K, int64_t lda,
   (void)nlo;
   const int rc = launch_fill_u32(flags, 0u, st);
   if (rc) return rc;
+  // one wave per row up to 2048 elements (max: 1024), else the split rows
+  const int64_t k1 = nhi == 5 ? 64 * 16 : 64 * 32;
   for (int64_t j = 0; j < ncols; ++j) {
-    if (K <= 64 * 32)
+    if (K <= k1)
       launch_rows_1(A, N, K, lda, x + j, ldx, b + j, ldb, r + j, ldr, rho, nhi, flags, st);
     else
       launch_rows_split(A, N, K, lda, x + j, ldx, b + j, ldb, r + j, ldr, rho, nhi, flags,

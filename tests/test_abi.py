@@ -122,6 +122,19 @@ def test_workspace_sizes(lib):
     assert ws >= 8 * 1000 * 64
 
 
+def test_residual_workspace_bytes(lib):
+    # the fused row kernels need no workspace: high / medium up to K = 16384,
+    # max up to 8192, up to 4 right-hand sides; other cases take the
+    # slice-GEMM route and its workspace
+    for nh, nl, kmax in ((4, 1, 16384), (3, 1, 16384), (5, 4, 8192)):
+        for K in (1, 700, 1024, 1025, 2049, kmax):
+            assert lib.ozk_residual_workspace_bytes(300, K, 1, nh, nl) == 0, (nh, nl, K)
+        assert lib.ozk_residual_workspace_bytes(300, kmax, 4, nh, nl) == 0
+        assert lib.ozk_residual_workspace_bytes(300, kmax + 1, 1, nh, nl) > 0
+        assert lib.ozk_residual_workspace_bytes(300, 700, 5, nh, nl) > 0
+    assert lib.ozk_residual_workspace_bytes(300, 700, 1, 4, 2) > 0
+
+
 def test_gemm_workspace_bytes(lib):
     # all-pairs schedules: the fold state the three-sweep max schedule keeps
     # between launches (rounded to 256 B), then the dynamic-tail words (8

@@ -675,8 +675,10 @@ def test_residual_fused_rows_bit_exact(ozk, N, K, precision):
     # high / medium: K <= 2048 runs the one-wave-per-row kernel, K <= 16384
     # the split-row kernel (4 waves of 1024 elements up to K = 4096, then 8
     # waves of 1024 or 2048, their rows through an LDS ring when K is even,
-    # else the register prefetch: 5001, 9999); K = 16385 and max take the
-    # slice-GEMM route
+    # else the register prefetch: 5001, 9999); K = 16385 takes the
+    # slice-GEMM route.  max: one wave per row up to K = 1024, then 2, 4 or
+    # 8 waves of 1024 elements up to K = 8192 (5001 without the ring), the
+    # slice-GEMM route beyond
     rng = np.random.RandomState(N + K)
     A = (rng.rand(N, K) - 0.5) * np.exp(2.0 * rng.randn(N, K))
     x, b = rng.randn(K), rng.randn(N)
@@ -700,7 +702,7 @@ def test_residual_fused_columns_bit_exact(ozk, K, ncols):
 
 
 @pytest.mark.parametrize("K", [2048, 1500, 1024, 700, 4096, 6000, 16384])
-@pytest.mark.parametrize("precision", ["high", "medium"])
+@pytest.mark.parametrize("precision", ["high", "medium", "max"])
 def test_residual_rows_batches_and_edge_rows(ozk, K, precision):
     """40000 rows (fewer for K > 2048, about 80 M elements): every wave of
     the one-wave-per-row kernel's persistent grid (one workgroup of 8 waves
@@ -715,7 +717,7 @@ def test_residual_rows_batches_and_edge_rows(ozk, K, precision):
     2^-103 row's last slices do too); the kernel must give NaN there too.  Rows are independent, so three row ranges are
     checked against the oracle on those rows alone."""
     N = 40000 if K <= 2048 else 80_000_000 // K
-    rng = np.random.RandomState(K + (7 if precision == "high" else 11))
+    rng = np.random.RandomState(K + {"high": 7, "medium": 11, "max": 13}[precision])
     A = rng.randn(N, K)
     A[3] = 0.0
     A[5] = 0.0
