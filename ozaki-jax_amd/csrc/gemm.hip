@@ -1445,6 +1445,26 @@ bool launch_ap_rect2(bool i8, int order, const ApArgs& a, const RectSweep& r);
 constexpr int kRectMaxSlices = 8;
 constexpr int kRectMaxSweeps = kDynSlot0 / kXcds;
 
+// Sweeps of a rectangle schedule (as rect_plan cuts it), and a check that
+// every schedule's sweeps fit the plan array and the dynamic-tail words.
+constexpr int rect_nsweeps(int nhi, int nlo) {
+  int n = 0;
+  for (int blk = 0; blk < 3; ++blk) {
+    const int ng = blk == 2 ? nlo : nhi, nb = blk == 1 ? nlo : nhi;
+    int na = ng;
+    while (na > 1 && (na + nb > kSweepPlanes || na * nb > kSweepPairs)) --na;
+    n += (ng + na - 1) / na;
+  }
+  return n;
+}
+constexpr bool rect_sweeps_fit() {
+  for (int h = 1; h <= kRectMaxSlices; ++h)
+    for (int l = 1; l <= kRectMaxSlices; ++l)
+      if (rect_nsweeps(h, l) > kRectMaxSweeps) return false;
+  return true;
+}
+static_assert(rect_sweeps_fit(), "a rectangle schedule has more sweeps than the plan holds");
+
 static bool rect_tuple(int nhi, int nlo) {
   return allpairs_nsweeps(nhi, nlo) == 0 && nhi >= 1 && nlo >= 1 && nhi <= kRectMaxSlices &&
          nlo <= kRectMaxSlices;
