@@ -642,9 +642,10 @@ def test_preflight_and_families(ozk):
 
 # (4500, 600): 10 x 10 tiles of 64 (two tile-row groups of the upper-triangle
 # order, a ragged last tile), INT8 planes; max takes the full product and a
-# separate symmetrisation.
+# separate symmetrisation, and so do the custom schedules: (4, 2) in two
+# fixed sweeps, (6, 1) and (7, 6) in rectangle sweeps over one plane set.
 @pytest.mark.parametrize("shape", [(64, 64), (300, 40), (33, 130), (5000, 24), (4500, 600)])
-@pytest.mark.parametrize("precision", ["high", "medium", "max"])
+@pytest.mark.parametrize("precision", ["high", "medium", "max", (4, 2), (6, 1), (7, 6)])
 def test_gram_bit_exact(ozk, shape, precision):
     A = gen("randn", shape, 51)
     case(f"gram ozaki {shape} {precision}")
