@@ -332,22 +332,23 @@ def suite_gram(emit, ozk, oracle, dev, sync):
 def suite_residual(emit, ozk, oracle, dev, sync):
     import torch
     # residual rows longer than one wave holds (split-row kernel) and several
-    # right-hand sides, N(0,1); sampled rows checked (rows are independent)
-    for n, nc in ((8192, 1), (4096, 4)):
+    # right-hand sides, N(0,1), high and max; sampled rows checked (rows are
+    # independent)
+    for prec, n, nc in (("high", 8192, 1), ("high", 4096, 4), ("max", 8192, 1)):
         rs = np.random.RandomState(5)
         A = rs.randn(n, n)
         x, b = rs.randn(n, nc), rs.randn(n, nc)
         At = torch.from_numpy(A).to(dev)
         xt, bt = torch.from_numpy(x).to(dev), torch.from_numpy(b).to(dev)
-        log(f"suite: residual {n}x{n}, {nc} right-hand side(s)")
-        t = _timeit(lambda: ozk.residual(At, xt, bt, mode="ozaki"), 10, sync)
-        r = ozk.residual(At, xt, bt, mode="ozaki").cpu().numpy()
+        log(f"suite: residual {prec} {n}x{n}, {nc} right-hand side(s)")
+        t = _timeit(lambda: ozk.residual(At, xt, bt, mode="ozaki", precision=prec), 10, sync)
+        r = ozk.residual(At, xt, bt, mode="ozaki", precision=prec).cpu().numpy()
         rows = np.array([0, n // 2, n - 1])
-        emit({"config": f"residual ozaki high {n}x{n} N(0,1), {nc} right-hand side(s)",
+        emit({"config": f"residual ozaki {prec} {n}x{n} N(0,1), {nc} right-hand side(s)",
               "ms": t * 1e3, "GB_per_s_of_A": A.nbytes * nc / t / 1e9,
               "frac_of_hbm_peak": A.nbytes * nc / t / 1e9 / PEAK_HBM_GBS,
               "bit_exact_vs_oracle": bool(np.array_equal(
-                  r[rows], oracle.residual_ozaki(A[rows], x, b[rows])))})
+                  r[rows], oracle.residual_ozaki(A[rows], x, b[rows], prec)))})
         del At, xt, bt
 
 
