@@ -51,6 +51,7 @@ SEQUENCES = [
     ("INT8 planes, max, block order", 0, 5, 4, 1, (300, 6000, 280), (70, 4500, 33)),
     ("BF16 planes, high, 2Sum", 0, 4, 1, 0, (1100, 2048, 1000), (96, 300, 64)),
     ("host pipeline, n_slices=8", 1, 8, 0, 3, (256, 256, 256), (40, 100, 30)),
+    ("INT8 planes, (6, 1) rectangle sweeps, 2Sum", 0, 6, 1, 0, (600, 5000, 576), (130, 4200, 90)),
 ]
 
 
