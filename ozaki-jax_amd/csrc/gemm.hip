@@ -1250,33 +1250,57 @@ struct ApArgs {
   I8Fix fix;
 };
 
-// One sweep.  Its grid (one workgroup per CU, at most one per tile) and
-// dynamic tail follow its own tile rows; a K-split tail (single sweeps
-// only) keeps the grid the tail plan chose.
-template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
-static void launch_sweep_of(const ApArgs& a) {
+// One sweep's kernel on operands As .. fix (the rectangle sweeps pass them
+// offset to their first planes); `ordinal` picks the sweep's dynamic-tail
+// counters.  Its grid (one workgroup per CU, at most one per tile) and
+// dynamic tail follow its own tile rows.  A single sweep may split its tail
+// along K instead, on the grid the plan of launch_allpairs chose, and then
+// runs the fixup.  (Sweeps of multi-sweep schedules do not split: there the
+// fixups cost about what the split saves.)
+template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM>
+static void launch_sweep_kernel(const ApArgs& a, const char* As, const int32_t* Ae,
+                                const char* Bs, const int32_t* Be, const I8Fix& fix,
+                                int ordinal, int rflags) {
   typedef Sweep<PIPE, NHI, NLO, B0, B1, SYM> SW;
-  const bool split = a.tail_P > 1 && SW::kFirst && SW::kLast;
-  dim3 grid = a.grid;
+  const int64_t nt = allpairs_ntiles(a.N, a.M, SYM, SW::TM);
+  dim3 grid((unsigned)(nt < a.cus ? nt : a.cus));
+  int tail_P = 0, tile0 = 0;
+  int64_t tail_T = 0;
+  uint32_t* part = nullptr;
+  if constexpr (SW::kFirst && SW::kLast) {
+    if (a.tail_P > 1) {
+      grid = a.grid;
+      tail_P = a.tail_P;
+      tail_T = a.tail_T;
+      tile0 = a.tile0;
+      part = a.part;
+    }
+  }
   uint32_t* dyn = nullptr;
   int nstat = 0;
-  if (!split) {
-    const int64_t nt = allpairs_ntiles(a.N, a.M, SYM, SW::TM);
-    grid = dim3((unsigned)(nt < a.cus ? nt : a.cus));
-    nstat = a.dyn ? dyn_static_rounds(nt, (int)grid.x, a.nst) : 0;
-    if (nstat > 0) dyn = a.dyn + kXcds * B0;
+  if (tail_P == 0 && a.dyn) {
+    nstat = dyn_static_rounds(nt, (int)grid.x, a.nst);
+    if (nstat > 0) dyn = a.dyn + kXcds * ordinal;
   }
-  hipLaunchKernelGGL((gemm_allpairs<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>),
-                     grid, dim3(kThreads16), 0, a.st, a.As, a.Ae, a.Bs, a.Be, a.N,
-                     a.M, a.nst, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp, a.state,
-                     split ? a.tail_P : 0, a.part, a.fix, dyn, nstat, 0);
+  hipLaunchKernelGGL((gemm_allpairs<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>), grid,
+                     dim3(kThreads16), 0, a.st, As, Ae, Bs, Be, a.N, a.M, a.nst, a.al, a.bl,
+                     a.unit2, a.C, a.ldc, a.P, a.ldp, a.state, tail_P, part, fix, dyn, nstat,
+                     rflags);
   if constexpr (SW::kFirst && SW::kLast) {
-    if (split)
+    if (tail_P > 1)
       hipLaunchKernelGGL((gemm_tail_fixup<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>),
-                         dim3((unsigned)(a.tail_T * 8)), dim3(kThreads16), 0, a.st, a.part, a.tail_P,
-                         a.tile0, a.Ae, a.Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P,
-                         a.ldp, a.state, a.fix);
+                         dim3((unsigned)(tail_T * 8)), dim3(kThreads16), 0, a.st, part, tail_P,
+                         tile0, Ae, Be, a.N, a.M, a.al, a.bl, a.unit2, a.C, a.ldc, a.P, a.ldp,
+                         a.state, fix);
   }
+}
+
+// One sweep of a fixed schedule (its dynamic-tail counters: those of its
+// first block or group).
+template <class Op, int PIPE, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
+static void launch_sweep_of(const ApArgs& a) {
+  launch_sweep_kernel<Op, PIPE, NHI, NLO, ORDER, B0, B1, SYM>(a, a.As, a.Ae, a.Bs, a.Be, a.fix,
+                                                              B0, 0);
 }
 
 template <class Op, int NHI, int NLO, int ORDER, int B0, int B1, bool SYM = false>
@@ -1314,11 +1338,6 @@ struct RectSweep {
 
 template <class Op, int NA, int NB, int ORDER>
 static void launch_rect(const ApArgs& a, const RectSweep& r) {
-  typedef Sweep<kPipeRect, NA, NB, 0, 0> SW;
-  const int64_t nt = allpairs_ntiles(a.N, a.M, false, SW::TM);
-  const dim3 grid((unsigned)(nt < a.cus ? nt : a.cus));
-  const int nstat = a.dyn ? dyn_static_rounds(nt, (int)grid.x, a.nst) : 0;
-  uint32_t* dyn = nstat > 0 ? a.dyn + kXcds * r.ordinal : nullptr;
   // the rectangle's first planes: slice planes, exponents and line sums
   const int64_t aplane = a.al * kChunkBytes * a.nst, bplane = a.bl * kChunkBytes * a.nst;
   I8Fix fix = a.fix;
@@ -1326,11 +1345,9 @@ static void launch_rect(const ApArgs& a, const RectSweep& r) {
     fix.as += (int64_t)r.a0 * a.al;
     fix.bs += (int64_t)r.bb * a.bl;
   }
-  hipLaunchKernelGGL((gemm_allpairs<Op, kPipeRect, NA, NB, ORDER, 0, 0, false>), grid,
-                     dim3(kThreads16), 0, a.st, a.As + r.a0 * aplane, a.Ae + r.a0 * a.al,
-                     a.Bs + r.bb * bplane, a.Be + r.bb * a.bl, a.N, a.M, a.nst, a.al, a.bl,
-                     a.unit2, a.C, a.ldc, a.P, a.ldp, a.state, 0, (uint32_t*)nullptr, fix, dyn,
-                     nstat, r.rflags);
+  launch_sweep_kernel<Op, kPipeRect, NA, NB, ORDER, 0, 0, false>(
+      a, a.As + r.a0 * aplane, a.Ae + r.a0 * a.al, a.Bs + r.bb * bplane, a.Be + r.bb * a.bl,
+      fix, r.ordinal, r.rflags);
 }
 
 // The 2Sum order and its pair form share the 2Sum kernels (kRfPair).
@@ -1571,7 +1588,7 @@ size_t gemm_state_bytes(int64_t N, int64_t M, int pipe, int nhi, int nlo, int or
 // CUs busy while the others idle.  Instead each tail tile is split along K
 // into P = min(cus / T, nst / kMinPieceStages) pieces, one per workgroup,
 // whose raw sums gemm_tail_fixup adds up and folds.  Single-sweep schedules
-// only; needs T * P * NP * 8 * kThreads16 * 4 bytes of workspace.
+// only; needs T * P * NP * RB * 4 * kThreads16 * 4 bytes of workspace.
 constexpr int kMinPieceStages = 16;
 
 struct TailPlan {
@@ -1619,7 +1636,7 @@ static int64_t allpairs_nst(int64_t K, bool i8) {
 }
 
 // Workspace of the K-split tail of an N x M (x K) all-pairs product: zero
-// when the product does not split.
+// when the product does not split (multi-sweep schedules never do).
 size_t gemm_tail_bytes(int64_t N, int64_t M, int64_t K, int pipe, int nhi, int nlo,
                        bool sym, bool i8) {
   if (!allpairs_schedule(pipe, nhi, nlo) || allpairs_sweeps(pipe, nhi, nlo) != 1) return 0;
@@ -1678,7 +1695,7 @@ static int launch_allpairs(bool i8, int pipe, const void* As, const int32_t* Ae,
     }
   }
   // the dynamic tail's counters, when some sweep will use them (each sweep
-  // decides for its own tiles in launch_sweep)
+  // decides for its own tiles in launch_sweep_kernel)
   if (!a.part && state && state_bytes >= off + kDynBytes &&
       (allpairs_sweeps(pipe, nhi, nlo) > 1 ||
        dyn_static_rounds(ntiles, (int)a.grid.x, allpairs_nst(K, i8)) > 0)) {

@@ -131,13 +131,17 @@ def extract(X, by_cols, rho, n0, n1=0, f64=False, i8=False):
     return Planes(s, e, lines, length, flags, rho if i8 else None, sums)
 
 
-def gemm(a, b, pipeline, n_hi, n_lo, order):
-    """ozk_gemm on two Planes (a: rows of A, b: columns of B) -> C (N, M)."""
+def gemm(a, b, pipeline, n_hi, n_lo, order, workspace_bytes=None):
+    """ozk_gemm on two Planes (a: rows of A, b: columns of B) -> C (N, M).
+    workspace_bytes: at least ozk_gemm_workspace_bytes (the default); what
+    lies beyond it holds the partial sums of a K-split tail."""
     lib = _lib.load()
     dev = a.s.device
     N, M, K = a.lines, b.lines, a.length
     C = D.torch.empty((N, M), dtype=D.torch.float64, device=dev)
     wsb = lib.ozk_gemm_workspace_bytes(N, M, pipeline, n_hi, n_lo, order)
+    if workspace_bytes is not None:
+        wsb = max(wsb, int(workspace_bytes))
     ws = D.workspace(wsb, dev)
     if a.i8:
         rc = lib.ozk_gemm_i8(a.s.data_ptr(), a.e.data_ptr(), a._sums_ptr(), b.s.data_ptr(),

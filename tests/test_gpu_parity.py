@@ -453,11 +453,47 @@ def test_matmul_tail_split_bit_exact(ozk, N, K, M, precision):
         assert np.array_equal(C[rows], ref)
 
 
+# Multi-sweep schedules on a partial last round (their sweeps do not split
+# the tail along K; the fold state crosses sweeps): 1100 x 1100 gives 324
+# tiles of 64 rows (one round and 68 tiles on 256 CUs) and 216 of 96 rows.
+# max (three sweeps), (4, 2) (two), (6, 1) and (7, 6) (rectangle sweeps);
+# INT8 planes (K = 6000) and BF16 (K = 3000); orders A4 and A3.
+@pytest.mark.parametrize("precision", ["max", (4, 2), (6, 1), (7, 6)])
+@pytest.mark.parametrize("K", [6000, 3000])
+def test_matmul_multisweep_partial_round_bit_exact(ozk, precision, K):
+    N = M = 1100
+    A, B = gen("wide2", (N, K), 91), gen("randn", (K, M), 92)
+    nh, nl = OP.resolve_precision(precision)
+    rows = np.r_[0:8, N // 2:N // 2 + 8, N - 16:N]
+    for acc in ("fused", "host"):
+        case(f"matmul multi-sweep partial round {precision} {acc} ({N},{K},{M})")
+        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=precision)
+        ref = (O.matmul_ondevice_a3(A[rows], B, "raise", nh, nl) if acc == "host"
+               else O.matmul_ondevice_a4(A[rows], B, "raise", nh, nl))
+        assert np.array_equal(C[rows], ref)
+
+
+def test_host_multisweep_partial_round_bit_exact(ozk):
+    """The host triangle of 8 slices in its three sweeps on a partial last
+    round: 1100 x 1100 (324 tiles of 64 rows), K = 1024 on BF16 planes.  A2
+    through matmul, A1 through matmul_numpy."""
+    N, K, M = 1100, 1024, 1100
+    A, B = gen("wide2", (N, K), 93), gen("randn", (K, M), 94)
+    rows = np.r_[0:16, 540:556, N - 24:N]
+    case(f"matmul host 8 slices {(N, K, M)} (multi-sweep, partial round)")
+    C = ozk.matmul(A, B, n_slices=8)
+    assert np.array_equal(C[rows], OP.matmul_host_a2(A[rows], B, n_slices=8))
+    C = ozk.matmul_numpy(A, B, n_slices=8)
+    assert np.array_equal(C[rows], O.matmul_numpy(A[rows], B, n_slices=8))
+
+
 def test_host_schedule_tail_split_bit_exact(ll):
     """The host triangle of 5 slices runs in one all-pairs sweep, which
-    splits its tail along K: 17 x 17 = 289 tiles leave 33 tail tiles, each
-    in 2 pieces of 16 stages (K = 1024 on BF16 planes).  Orders A2 and A1
-    against the oracle on the tail rows and others."""
+    splits its tail along K when the workspace has room for the partial
+    sums: 17 x 17 = 289 tiles leave 33 tail tiles, each in 2 pieces of 16
+    stages (K = 1024 on BF16 planes).  Orders A2 and A1 against the oracle
+    on the tail rows and others, split and in the static order (the
+    workspace ozk_gemm_workspace_bytes gives, which has no K)."""
     N, K, M = 1088, 1024, 1088
     assert _tail_split(17 * 17, K, False) == 2
     A, B = gen("wide2", (N, K), 41), gen("randn", (K, M), 42)
@@ -465,27 +501,10 @@ def test_host_schedule_tail_split_bit_exact(ll):
     rows = np.r_[0:16, 500:520, N - 48:N]
     Pref = O.slice_products(oa[:, rows], ob, sched)
     for name, code_o, acc in (("A2", 2, O.accumulate_a2), ("A1", 3, O.accumulate_a1)):
-        case(f"ozk_gemm host 5 slices order {name} N,K,M={(N, K, M)} (K-split tail)")
-        C = to_np(ll.gemm(a, b, code, 5, 0, code_o))
-        assert np.array_equal(C[rows], acc(Pref, sched, oae[:, rows], obe)), name
-
-
-# Rectangle sweeps over many tiles: 2112 x 2112 gives 1089 tiles of 64 rows
-# (four whole rounds and a dynamic tail on 256 CUs) and 726 of 96 rows (no
-# dynamic tail), sweep by sweep; INT8 planes (K = 5000) and BF16 (K = 3000).
-@pytest.mark.parametrize("precision", [(6, 1), (7, 6)])
-@pytest.mark.parametrize("K", [5000, 3000])
-def test_matmul_rectangle_sweeps_many_tiles_bit_exact(ozk, precision, K):
-    N = M = 2112
-    A, B = gen("randn", (N, K), 81), gen("wide2", (K, M), 82)
-    nh, nl = precision
-    rows = np.r_[0:4, 95:97, 1055:1059, N - 6:N]  # 64- and 96-row tile edges
-    for acc in ("fused", "host"):
-        case(f"matmul rectangle sweeps {precision} {acc} ({N},{K},{M})")
-        C = ozk.matmul(A, B, pipeline="ondevice", accumulation=acc, precision=precision)
-        ref = (O.matmul_ondevice_a3(A[rows], B, "raise", nh, nl) if acc == "host"
-               else O.matmul_ondevice_a4(A[rows], B, "raise", nh, nl))
-        assert np.array_equal(C[rows], ref)
+        for ws, how in ((64 << 20, "K-split tail"), (None, "static order")):
+            case(f"ozk_gemm host 5 slices order {name} N,K,M={(N, K, M)} ({how})")
+            C = to_np(ll.gemm(a, b, code, 5, 0, code_o, workspace_bytes=ws))
+            assert np.array_equal(C[rows], acc(Pref, sched, oae[:, rows], obe)), name
 
 
 @pytest.mark.parametrize("precision", ["high", "medium"])
